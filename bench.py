@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Decode benchmark: Llama-3.2-1B-shaped bf16 decoder, batch 1, on one MI355X.
+
+Workload (one "step" = one decode token through the whole forward pass):
+random-init bf16 weights (seed 0, N(0, 0.02), RMSNorm weights 1) in the
+Llama-3.2-1B shape (16 layers, hidden 2048, 32/8 heads, hd 64, SwiGLU 8192,
+vocab 128256, tied, interleaved RoPE theta 5e5), a 512-token random prompt
+(seed 1), then greedy decode of --steps tokens with a 4096-position f32 KV
+cache. Timing follows generateGreedyMeasured (src/generator.zig:221-293):
+decode tok/s = generated tokens / decode time; prefill tok/s = prompt tokens /
+prefill time.
+
+Prints one JSON line with the headline metric, the roofline of the dominant
+kernel (HIP events on the model's stream) and a CPU baseline (the oracle, a
+C restatement of the reference CPU path, on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+KERNELS = ("qkv", "attention", "o_proj", "gate_up", "down")
+
+
+def kernel_bytes(cfg, pos: int) -> dict:
+    """Algorithmic HBM bytes per launch of each decode kernel at position pos
+    (weights read once, activations read/written once)."""
+    H, I, V, kv = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.kv_dim()
+    T = pos + 1
+    bias = (H + 2 * kv) * 2 if cfg.qkv_bias else 0
+    return {
+        "qkv": (H * H + 2 * kv * H) * 2 + bias + H * 2 + H * 4 + (H + 2 * kv) * 4,
+        "attention": 2 * T * kv * 4 + 2 * kv * 4 + (H + 2 * kv) * 4 + H * 4,
+        "o_proj": H * H * 2 + H * 4 + 2 * H * 4,
+        "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
+        "down": H * I * 2 + I * 4 + 2 * H * 4,
+        "logits": V * H * 2 + H * 2 + H * 4 + V * 4,
+    }
+
+
+def token_bytes(cfg, pos: int) -> int:
+    """B(pos): weight bytes of one decode token plus f32 KV read (0..pos) and
+    write (pos), the roofline numerator of the headline target."""
+    kb = kernel_bytes(cfg, pos)
+    L = cfg.num_hidden_layers
+    return L * sum(kb[k] for k in KERNELS) + kb["logits"] + cfg.hidden_size * 2
+
+
+def profile_kernels(runner, cfg, token: int, pos: int, reps: int = 3) -> dict:
+    import ctypes
+
+    from vvli_amd import _lib
+
+    L = cfg.num_hidden_layers
+    n = 1 + 5 * L + 2
+    buf = (ctypes.c_float * n)()
+    got = ctypes.c_uint32()
+    acc = np.zeros(n)
+    for _ in range(reps):
+        _lib.check(_lib.lib().vvli_gpu_profile_step(runner._h, token, pos, buf, n, ctypes.byref(got)))
+        acc += np.frombuffer(buf, dtype=np.float32)[: got.value]
+    ms = acc / reps
+    out = {"embed": [ms[0]], "logits": [ms[1 + 5 * L]], "argmax": [ms[2 + 5 * L]]}
+    for i, k in enumerate(KERNELS):
+        out[k] = [ms[1 + 5 * l + i] for l in range(L)]
+    return out
+
+
+def cpu_baseline(cfg, blob, budget_s: float, max_tokens: int) -> dict:
+    """Decode tok/s of the oracle (C restatement of the reference CPU path:
+    per-call thread fan-out over rows, single-threaded attention) on this host."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = oracle.cpu_count()
+    r = oracle.OracleRunner(cfg, blob, max_tokens + 16, threads=threads, lanes=16)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=8)
+    for pos, t in enumerate(prompt):
+        logits = r.forward_token(int(t), pos)
+    tokens = []
+    t0 = time.perf_counter()
+    pos = len(prompt)
+    while len(tokens) < max_tokens and (time.perf_counter() - t0) < budget_s:
+        nxt = oracle.argmax(logits)
+        tokens.append(nxt)
+        logits = r.forward_token(nxt, pos)
+        pos += 1
+    dt = time.perf_counter() - t0
+    r.close()
+    return {"tokens": tokens, "seconds": dt, "threads": threads, "prompt": prompt}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128, help="decode tokens timed")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens before the timed run")
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (multi-GPU sharding is not built)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from vvli_amd import config as C
+    from vvli_amd import runtime as R
+
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    torch.cuda.set_device(0)
+    cfg = C.llama32_1b()
+    t = time.perf_counter()
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02)
+    print(f"[bench] synthetic blob {blob.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f}s", file=sys.stderr,
+          flush=True)
+    runner = R.Runner(cfg, blob, args.ctx)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
+
+    # Warmup: graph capture, clocks, caches.
+    runner.generate_greedy_measured(prompt[:16], max(1, args.warmup))
+    runner.kv_clear()
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tokens, stats = runner.generate_greedy_measured(prompt, args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    assert stats.generated_tokens == args.steps
+    decode_s = stats.decode_nanoseconds / 1e9
+    tok_s = args.steps / decode_s
+    prefill_tok_s = stats.prefill_tokens_per_second()
+    print(f"[bench] decode {tok_s:.1f} tok/s, prefill {prefill_tok_s:.1f} tok/s (wall {wall:.2f}s)", file=sys.stderr,
+          flush=True)
+
+    # Whole-token roofline: sum of B(pos) over the decode positions / decode time.
+    positions = range(args.prompt, args.prompt + args.steps)
+    step_bytes = sum(token_bytes(cfg, p) for p in positions)
+    step_gbs = step_bytes / decode_s / 1e9
+
+    # Per-kernel durations from HIP events on the model's stream, mid-decode.
+    mid = args.prompt + args.steps // 2
+    prof = profile_kernels(runner, cfg, int(tokens[args.steps // 2]), mid)
+    kb = kernel_bytes(cfg, mid)
+    kernels = {}
+    for k in list(KERNELS) + ["logits"]:
+        avg_ms = float(np.mean(prof[k]))
+        total_ms = float(np.sum(prof[k]))
+        kernels[k] = {"avg_us": avg_ms * 1e3, "total_us": total_ms * 1e3, "bytes": kb[k],
+                      "gbs": kb[k] / (avg_ms * 1e-3) / 1e9}
+    dom = max(kernels, key=lambda k: kernels[k]["total_us"])
+    d = kernels[dom]
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": d["bytes"], "avg_launch_us": round(d["avg_us"], 2)}
+    print("[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f}us {v['gbs']:.0f}GB/s" for k, v in kernels.items()),
+          file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(cfg, blob, args.cpu_budget, 512)
+        # Parity spot check: the GPU's greedy continuation of the same 8-token prompt.
+        runner.kv_clear()
+        g_tokens, _ = runner.generate_greedy_measured(cb["prompt"].astype(np.uint32), len(cb["tokens"]))
+        same = bool(np.array_equal(g_tokens, np.array(cb["tokens"], dtype=np.uint32)))
+        cpu = {"value": round(len(cb["tokens"]) / cb["seconds"], 3), "unit": "tok/s", "cores": cb["threads"],
+               "kind": "port",
+               "sample": f"oracle (C restatement of the reference CPU path, {cb['threads']} threads, 16-lane f32 "
+                         f"accumulators) greedy decode of {len(cb['tokens'])} tokens after an 8-token prompt, "
+                         f"same weights; GPU tokens identical: {same}"}
+        print(f"[bench] cpu baseline {cpu['value']} tok/s on {cb['threads']} threads; tokens identical: {same}",
+              file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "decode tok/s @bs1 + GEMV HBM GB/s (% of peak), Llama-3.2-1B bf16",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(decode_s * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "llama-3.2-1b bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
+                   "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32",
+                   "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": round(prefill_tok_s, 2),
+        "step_roofline": {"bytes_per_token_avg": step_bytes // args.steps, "achieved": round(step_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kernels.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    runner.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,174 @@
+/*
+ * vvli_gpu.h -- C ABI of the MI355X (gfx950) dense-decoder forward pass.
+ *
+ * This is the drop-in boundary for VVLI's CPU runner. A Zig host binds it with
+ * @cImport and keeps its runner/generator API; the
+ * library holds the weights, the KV cache and all activations in HBM and runs
+ * hand-written HIP kernels.
+ *
+ * Conventions (after src/gpu/metal_smoke.zig:5-11 and src/gpu/metal_smoke.m:23-29):
+ *   - every entry point returns int: 0 on success, a VVLI_* code otherwise;
+ *   - outputs go through caller-owned pointers; NULL required args -> VVLI_NULL_ARG;
+ *   - vvli_gpu_last_error() gives a thread-local message for the last failure.
+ * Threading: one model handle owns one HIP stream and admits one call at a
+ * time; separate handles may be used from separate threads. Every call is
+ * synchronous on return unless it says otherwise. The library starts no
+ * host threads.
+ */
+#ifndef VVLI_GPU_H
+#define VVLI_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VVLI_GPU_ABI_VERSION 1u
+
+/* Return codes. Each maps one member of the reference's error sets
+ * (src/llm.zig:17-27, src/generator.zig:8-12, src/gguf.zig:7-12). */
+enum {
+    VVLI_OK = 0,
+    VVLI_INVALID_CONFIG = 1,        /* llm.Error.InvalidConfig */
+    VVLI_INVALID_WEIGHT = 2,        /* llm.Error.InvalidWeight */
+    VVLI_INVALID_TOKEN = 3,         /* llm.Error.InvalidToken */
+    VVLI_CONTEXT_FULL = 4,          /* llm.Error.ContextFull */
+    VVLI_UNSUPPORTED_DTYPE = 5,     /* llm.Error.UnsupportedDType */
+    VVLI_UNSUPPORTED_ARCH = 6,      /* llm.Error.UnsupportedModelArchitecture */
+    VVLI_OUT_OF_MEMORY = 7,         /* error.OutOfMemory (hipMalloc / host alloc) */
+    VVLI_HIP_ERROR = 8,             /* HIP runtime failure (no reference counterpart) */
+    VVLI_MISSING_FIELD = 9,         /* llm.Error.MissingJsonField */
+    VVLI_EMPTY_PROMPT = 10,         /* generator.Error.EmptyPrompt */
+    VVLI_MISSING_TENSOR = 11,       /* llm.Error.MissingSafetensorsTensor */
+    VVLI_INVALID_FILE = 12,         /* gguf.Error.InvalidGguf / bad safetensors header / IO */
+    VVLI_UNSUPPORTED_VERSION = 13,  /* gguf.Error.UnsupportedGgufVersion */
+    VVLI_OUTPUT_TOO_SMALL = 14,     /* generator.Error.OutputTooSmall */
+    VVLI_INVALID_SAMPLING = 15,     /* generator.Error.InvalidSamplingOptions */
+    VVLI_NULL_ARG = 100             /* NULL required argument (metal_smoke.m:24) */
+};
+
+/* Enumerations (src/llm.zig:29-58). */
+enum { VVLI_ARCH_LLAMA = 0, VVLI_ARCH_MISTRAL = 1, VVLI_ARCH_OLMOE = 2, VVLI_ARCH_QWEN2 = 3 };
+enum { VVLI_ROPE_INTERLEAVED = 0, VVLI_ROPE_SPLIT_HALF = 1 };
+enum { VVLI_WEIGHT_F32 = 0, VVLI_WEIGHT_BF16 = 1 };
+
+/* Model shape contract: the fields of llm.Config (src/llm.zig:77-97). */
+typedef struct vvli_gpu_config {
+    uint32_t abi_version;     /* must be VVLI_GPU_ABI_VERSION */
+    uint32_t arch;            /* VVLI_ARCH_* */
+    uint32_t vocab, hidden, inter, layers, heads, kv_heads, max_pos;
+    uint32_t rope_layout;     /* VVLI_ROPE_* */
+    uint32_t weight_kind;     /* VVLI_WEIGHT_*: dtype of the blob */
+    uint32_t num_experts, experts_per_tok; /* 0 for dense models */
+    float rope_theta, rms_eps;
+    uint8_t tie, qkv_bias, qk_norm, _pad;
+    uint32_t eos_token_id, pad_token_id;
+} vvli_gpu_config;
+
+typedef struct vvli_gpu_model vvli_gpu_model;
+
+/* Generation statistics: generator.Stats (src/generator.zig:25-43). */
+typedef struct vvli_gpu_stats {
+    uint64_t prompt_tokens, generated_tokens;
+    int64_t prefill_ns, decode_ns, total_ns;
+} vvli_gpu_stats;
+
+/* ---------------------------------------------------------------------- */
+/* Library                                                                 */
+/* ---------------------------------------------------------------------- */
+uint32_t vvli_gpu_abi_version(void);
+/* Thread-local text for the last non-zero return on this thread. */
+const char* vvli_gpu_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* Shape contract (host only; no GPU needed)                               */
+/* ---------------------------------------------------------------------- */
+/* Config.validate, src/llm.zig:195-216. */
+int vvli_gpu_config_validate(const vvli_gpu_config* cfg);
+/* Config.parameterCount, src/llm.zig:241-276. */
+uint64_t vvli_gpu_parameter_count(const vvli_gpu_config* cfg);
+/* storageElementCount, src/llm.zig:814-837: elements of the contiguous blob
+ * (dtype = cfg->weight_kind), every slice starting on a 64-byte boundary. */
+uint64_t vvli_gpu_storage_element_count(const vvli_gpu_config* cfg);
+
+/* ---------------------------------------------------------------------- */
+/* Model: weights + KV cache + scratch in HBM                              */
+/* ---------------------------------------------------------------------- */
+/* Replaces OwnedModel + KVCache.init + Scratch.init + Runner.init
+ * (src/llm.zig:424-446, 545-563, 626-662, 694-700). host_blob is the
+ * contiguous blob in the order of OwnedModel.assignSlices (src/llm.zig:488-522);
+ * it is copied to the device before the call returns, so the caller may free
+ * it afterwards. The KV cache is cleared (KVCache.clear). Dense llama /
+ * mistral / qwen2 only: MoE configs return VVLI_UNSUPPORTED_ARCH like
+ * OwnedModel.init (src/llm.zig:426). max_seq_len must be in 1..max_pos. */
+int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,
+                          size_t blob_elems, vvli_gpu_model** out);
+int vvli_gpu_model_destroy(vvli_gpu_model* model);
+/* KVCache.clear, src/llm.zig:576-579. */
+int vvli_gpu_kv_clear(vvli_gpu_model* model);
+/* Replace the RoPE inverse-frequency table (n = head_dim/2). NULL restores
+ * the reference formula inv_freq[i] = 1/pow(theta, 2i/head_dim)
+ * (src/llm.zig:1360-1363). Used for llama3-scaled frequencies. */
+int vvli_gpu_set_rope_table(vvli_gpu_model* model, const float* inv_freq, uint32_t n);
+
+/* Runner.forwardToken, src/llm.zig:702-709. token >= vocab -> VVLI_INVALID_TOKEN,
+ * pos >= max_seq_len -> VVLI_CONTEXT_FULL. logits_out (vocab floats) and
+ * argmax_out (llm.argmax of the logits, src/llm.zig:778-789) are optional. */
+int vvli_gpu_forward_token(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* logits_out,
+                           uint32_t* argmax_out);
+/* Runner.forwardEmbedding, src/llm.zig:711-718: embedding = hidden floats (host). */
+int vvli_gpu_forward_embedding(vvli_gpu_model* model, const float* embedding, uint32_t pos, float* logits_out,
+                               uint32_t* argmax_out);
+/* forwardToken that also returns the residual stream after every layer
+ * (hidden_out: layers*hidden floats, layer-major) for per-layer parity. */
+int vvli_gpu_forward_token_debug(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* logits_out,
+                                 float* hidden_out);
+/* Read back one KV-cache row (kv_heads*head_dim floats each; either output
+ * may be NULL): KVCache.keySlice / valueSlice, src/llm.zig:581-589. */
+int vvli_gpu_kv_read(vvli_gpu_model* model, uint32_t layer, uint32_t pos, float* k_out, float* v_out);
+
+/* Batched prompt processing: the prompt loop of src/generator.zig:243-251 run
+ * as MFMA GEMMs plus causal attention. Writes K/V for positions
+ * start_pos..start_pos+n-1 and returns the logits / argmax of the last one,
+ * the same state the token loop leaves. */
+int vvli_gpu_prefill(vvli_gpu_model* model, const uint32_t* tokens, uint32_t n, uint32_t start_pos,
+                     float* last_logits, uint32_t* argmax_out);
+
+/* Greedy generation: generateGreedyMeasured* (src/generator.zig:221-293) with
+ * temperature 0 and no repeat penalty. Prefill runs the prompt (flags bit 0:
+ * batched vvli_gpu_prefill, else one forward per token), then decode takes the
+ * on-device argmax, emits it, stops on EOS (eos < 0: never), else forwards it.
+ * Without EOS the decode steps run back to back with no host round trip.
+ * out_tokens must hold max_new entries; *n_out receives the count. */
+#define VVLI_GEN_BATCHED_PREFILL 1u
+int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                             int64_t eos, uint32_t flags, uint32_t* out_tokens, uint32_t* n_out,
+                             vvli_gpu_stats* stats);
+
+/* ---------------------------------------------------------------------- */
+/* Measurement (no reference counterpart: the reference has no profiler)   */
+/* ---------------------------------------------------------------------- */
+/* Runs one token step (like forward_token) with a HIP event recorded on the
+ * model's stream between consecutive kernels and returns each kernel's time
+ * in milliseconds, in launch order: embed, then per layer {qkv, attention,
+ * o_proj, gate_up, down}, then logits, argmax. *n_out = kernels timed. */
+int vvli_gpu_profile_step(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* ms_out, uint32_t cap,
+                          uint32_t* n_out);
+
+/* ---------------------------------------------------------------------- */
+/* Isolated matmul op (device pointers)                                    */
+/* ---------------------------------------------------------------------- */
+/* linearInto (src/llm.zig:1228-1275) generalised to M rows of activations:
+ * Y[m,n] = sum_k bf16 W[n,k] * X[m,k] (+ bias[n]) with f32 accumulation.
+ * dW: N*K bf16, dX: M*K f32, dBias: N bf16 or NULL, dY: M*N f32, all device
+ * pointers; K must be a multiple of 8. stream: hipStream_t or NULL for the
+ * null stream. Asynchronous: returns after the launch. */
+int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
+                    uint32_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VVLI_GPU_H */

@@ -1,0 +1,164 @@
+"""GPU parity of the token step against the oracle (CPU restatement of the
+reference forward pass, oracle/vvli_oracle.c), through the C ABI.
+
+Bar: per-layer residual stream and logits within 2e-3 max relative error
+(max |gpu - ref| / max |ref|, f32 accumulation on both sides), K/V cache rows
+within the same bound, greedy token sequences identical.
+"""
+import numpy as np
+import pytest
+
+from vvli_amd import config as C
+from vvli_amd import runtime as R
+from vvli_amd._lib import VvliError
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def rel_err(got, ref) -> float:
+    ref = np.asarray(ref, dtype=np.float64)
+    got = np.asarray(got, dtype=np.float64)
+    return float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+
+
+def cfg_small(**kw) -> C.Config:
+    base = dict(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                num_key_value_heads=2, max_position_embeddings=4096, rope_theta=1e6, rms_norm_eps=1e-6,
+                tie_word_embeddings=True, architecture="qwen2", qkv_bias=True, rope_layout=C.ROPE_SPLIT_HALF)
+    base.update(kw)
+    return C.Config(**base)
+
+
+# name -> (config, weight kind, blob maker, positions to step through)
+CASES = {
+    # The reference's own tiny runner test (src/llm.zig:1743-1782), f32 and bf16 blobs.
+    "tiny_f32": (C.tiny_test(), C.WEIGHT_F32, "det", 8),
+    "tiny_bf16": (C.tiny_test(), C.WEIGHT_BF16, "det", 8),
+    # Qwen2-style: split-half RoPE, qkv bias, tied, hd 64, GQA group 2.
+    "qwen_small": (cfg_small(), C.WEIGHT_BF16, "synth", 70),
+    # Llama-from-GGUF style: interleaved RoPE, no bias, untied, GQA group 4.
+    "llama_small": (cfg_small(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_attention_heads=8,
+                              num_key_value_heads=2, qkv_bias=False, tie_word_embeddings=False,
+                              architecture="llama", rope_layout=C.ROPE_INTERLEAVED, rope_theta=5e5,
+                              rms_norm_eps=1e-5), C.WEIGHT_BF16, "synth", 40),
+    # hd 128, group 7 (the Qwen2.5-7B head shape).
+    "hd128_g7": (cfg_small(vocab_size=640, hidden_size=896, intermediate_size=1024, num_attention_heads=7,
+                           num_key_value_heads=1, tie_word_embeddings=False), C.WEIGHT_BF16, "synth", 40),
+    # Qwen2.5-0.5B head shape: hidden 896, 14/2 heads, K = 896 and 4864.
+    "qwen05_heads": (cfg_small(vocab_size=2000, hidden_size=896, intermediate_size=4864, num_attention_heads=14,
+                               num_key_value_heads=2), C.WEIGHT_BF16, "synth", 24),
+    # f32 weights through the f32 kernel variants.
+    "qwen_small_f32": (cfg_small(), C.WEIGHT_F32, "synth", 20),
+}
+
+
+def make_blob(cfg, kind, how):
+    if how == "det":
+        return R.deterministic_blob(cfg, kind)
+    return R.synthetic_blob(cfg, kind, seed=0, stddev=0.02)
+
+
+@pytest.fixture(scope="module")
+def built():
+    R._lib.lib()
+    return True
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_token_steps_match_oracle(name, built, oracle_mod, host_threads):
+    cfg, kind, how, steps = CASES[name]
+    max_seq = min(cfg.max_position_embeddings, 128)
+    blob = make_blob(cfg, kind, how)
+    orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
+    rng = np.random.default_rng(1)
+    toks = rng.integers(0, cfg.vocab_size, size=steps)
+    print(f"case={name} steps={steps}", flush=True)
+    with R.Runner(cfg, blob, max_seq) as gpu:
+        for pos, tok in enumerate(toks):
+            ref_logits, ref_hidden = orc.forward_token(int(tok), pos, want_hidden=True)
+            logits, hidden = gpu.forward_token_debug(int(tok), pos)
+            for layer in range(cfg.num_hidden_layers):
+                e = rel_err(hidden[layer], ref_hidden[layer])
+                assert e <= TOL, f"{name} pos {pos} layer {layer}: hidden rel err {e:.3e}"
+            e = rel_err(logits, ref_logits)
+            assert e <= TOL, f"{name} pos {pos}: logits rel err {e:.3e}"
+        for layer in range(cfg.num_hidden_layers):
+            for pos in (0, steps // 2, steps - 1):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"{name} kv layer {layer} pos {pos}"
+
+
+@pytest.mark.parametrize("name", ["tiny_f32", "qwen_small", "llama_small"])
+def test_graph_step_equals_debug_step(name, built):
+    """The graph-replayed step (forward_token) gives the same logits and
+    argmax as the eagerly launched one (forward_token_debug)."""
+    cfg, kind, how, steps = CASES[name]
+    blob = make_blob(cfg, kind, how)
+    max_seq = min(cfg.max_position_embeddings, 64)
+    toks = np.random.default_rng(2).integers(0, cfg.vocab_size, size=min(steps, 12))
+    with R.Runner(cfg, blob, max_seq) as a, R.Runner(cfg, blob, max_seq) as b:
+        for pos, tok in enumerate(toks):
+            la = a.forward_token(int(tok), pos).copy()
+            am = a.last_argmax
+            lb, _ = b.forward_token_debug(int(tok), pos)
+            np.testing.assert_array_equal(la, lb)
+            assert am == R.argmax(la)
+
+
+@pytest.mark.parametrize("name", ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7"])
+def test_greedy_generation_matches_oracle(name, built, oracle_mod, host_threads):
+    cfg, kind, how, _ = CASES[name]
+    blob = make_blob(cfg, kind, how)
+    max_seq = min(cfg.max_position_embeddings, 96)
+    n_prompt = min(8, max_seq // 2)
+    n_new = max_seq - n_prompt
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, size=n_prompt).astype(np.uint32)
+    orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
+    ref, _ = orc.generate_greedy(prompt, n_new)
+    with R.Runner(cfg, blob, max_seq) as gpu:
+        got, stats = gpu.generate_greedy_measured(prompt, n_new)
+        assert stats.generated_tokens == n_new and stats.prompt_tokens == n_prompt
+        np.testing.assert_array_equal(got, ref)
+        # Same run with EOS = a token that appears mid-sequence stops right after it.
+        gpu.kv_clear()
+        eos = int(ref[n_new // 2])
+        first = int(np.argmax(ref == eos))
+        got2, stats2 = gpu.generate_greedy_measured(prompt, n_new, eos_token_id=eos)
+        np.testing.assert_array_equal(got2, ref[: first + 1])
+
+
+def test_forward_embedding_matches_oracle(built, oracle_mod):
+    cfg, kind, how, _ = CASES["qwen_small"]
+    blob = make_blob(cfg, kind, how)
+    orc = oracle_mod.OracleRunner(cfg, blob, 16, threads=2)
+    emb = np.full(cfg.hidden_size, 0.01, dtype=np.float32)  # src/llm.zig:1777-1778
+    with R.Runner(cfg, blob, 16) as gpu:
+        gpu.forward_token(3, 0)
+        orc.forward_token(3, 0)
+        got = gpu.forward_embedding(emb, 1).copy()
+        ref = orc.forward_embedding(emb, 1)
+        assert rel_err(got, ref) <= TOL
+        assert np.isfinite(got).all()
+
+
+def test_runner_errors(built):
+    cfg = C.tiny_test()
+    blob = R.deterministic_blob(cfg, C.WEIGHT_F32)
+    with R.Runner(cfg, blob, 8) as gpu:
+        with pytest.raises(VvliError) as e:
+            gpu.forward_token(cfg.vocab_size, 0)  # src/llm.zig:704
+        assert e.value.name == "InvalidToken"
+        with pytest.raises(VvliError) as e:
+            gpu.forward_token(1, 8)  # src/llm.zig:705
+        assert e.value.name == "ContextFull"
+        with pytest.raises(VvliError) as e:
+            gpu.generate_greedy_measured(np.zeros(0, dtype=np.uint32), 4)  # src/generator.zig:230
+        assert e.value.name == "EmptyPrompt"
+        with pytest.raises(VvliError) as e:
+            gpu.generate_greedy_measured(np.zeros(4, dtype=np.uint32), 8)  # 4 + 8 > 8 positions
+        assert e.value.name == "ContextFull"
+        # The runner still works after the errors.
+        assert np.isfinite(gpu.forward_token(3, 0)).all()

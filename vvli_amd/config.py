@@ -1,0 +1,240 @@
+"""Model shape contract: a Python mirror of VVLI's ``llm.Config``.
+
+Fields and defaults follow ``Config`` (src/llm.zig:77-97); the derived sizes
+follow ``headDim`` / ``kvDim`` / ``kvGroupSize`` (src/llm.zig:229-239). The
+named constructors are the decoder shapes the benchmarks and parity tests run.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import json
+
+from . import _lib
+
+ARCH = {"llama": 0, "mistral": 1, "olmoe": 2, "qwen2": 3}
+ROPE_INTERLEAVED, ROPE_SPLIT_HALF = 0, 1
+WEIGHT_F32, WEIGHT_BF16 = 0, 1
+
+
+@dataclasses.dataclass
+class Config:
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    max_position_embeddings: int
+    rope_theta: float
+    rms_norm_eps: float
+    tie_word_embeddings: bool
+    architecture: str = "qwen2"  # src/llm.zig:78 default
+    qkv_bias: bool = True  # src/llm.zig:94 default
+    rope_layout: int = ROPE_SPLIT_HALF  # src/llm.zig:89 default
+    num_experts: int = 0
+    num_experts_per_token: int = 0
+    qk_norm: bool = False
+    eos_token_id: int = 0
+    pad_token_id: int = 0
+
+    # ---- derived sizes (src/llm.zig:229-239) ----
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    def kv_dim(self) -> int:
+        return self.num_key_value_heads * self.head_dim()
+
+    def kv_group_size(self) -> int:
+        return self.num_attention_heads // self.num_key_value_heads
+
+    # ---- C ABI ----
+    def to_c(self, weight_kind: int = WEIGHT_BF16) -> _lib.CConfig:
+        c = _lib.CConfig()
+        c.abi_version = _lib.ABI_VERSION
+        c.arch = ARCH[self.architecture]
+        c.vocab = self.vocab_size
+        c.hidden = self.hidden_size
+        c.inter = self.intermediate_size
+        c.layers = self.num_hidden_layers
+        c.heads = self.num_attention_heads
+        c.kv_heads = self.num_key_value_heads
+        c.max_pos = self.max_position_embeddings
+        c.rope_layout = self.rope_layout
+        c.weight_kind = weight_kind
+        c.num_experts = self.num_experts
+        c.experts_per_tok = self.num_experts_per_token
+        c.rope_theta = self.rope_theta
+        c.rms_eps = self.rms_norm_eps
+        c.tie = int(self.tie_word_embeddings)
+        c.qkv_bias = int(self.qkv_bias)
+        c.qk_norm = int(self.qk_norm)
+        c.eos_token_id = self.eos_token_id
+        c.pad_token_id = self.pad_token_id
+        return c
+
+    def validate(self) -> None:
+        """Config.validate (src/llm.zig:195-216), run by the library."""
+        _lib.check(_lib.lib().vvli_gpu_config_validate(ctypes.byref(self.to_c())))
+
+    def parameter_count(self) -> int:
+        return int(_lib.lib().vvli_gpu_parameter_count(ctypes.byref(self.to_c())))
+
+    def storage_element_count(self, weight_kind: int = WEIGHT_BF16) -> int:
+        return int(_lib.lib().vvli_gpu_storage_element_count(ctypes.byref(self.to_c(weight_kind))))
+
+    @classmethod
+    def from_json(cls, text: str) -> "Config":
+        """Config.fromJson (src/llm.zig:99-147): HF config.json keys."""
+        o = json.loads(text)
+        if not isinstance(o, dict):
+            raise _lib.VvliError(1, "config is not a JSON object")
+        mt = o.get("model_type")
+        if not isinstance(mt, str):
+            raise _lib.VvliError(9, "model_type")
+        if mt not in ARCH:
+            raise _lib.VvliError(6, f"model_type {mt}")
+
+        def req(key):
+            v = o.get(key)
+            if v is None:
+                raise _lib.VvliError(9, key)
+            if not isinstance(v, int) or isinstance(v, bool) or v < 0:
+                raise _lib.VvliError(1, key)
+            return v
+
+        def opt_int(key):
+            v = o.get(key)
+            return v if isinstance(v, int) and not isinstance(v, bool) and v >= 0 else None
+
+        def opt_float(key, default):
+            v = o.get(key)
+            return float(v) if isinstance(v, (int, float)) and not isinstance(v, bool) else default
+
+        def opt_bool(key, default):
+            v = o.get(key)
+            return v if isinstance(v, bool) else default
+
+        def token_id(key):
+            v = o.get(key)
+            if isinstance(v, list):
+                v = v[0] if v else None
+            return v if isinstance(v, int) and not isinstance(v, bool) and v >= 0 else 0
+
+        heads = req("num_attention_heads")
+        experts = opt_int("num_experts") or 0
+        cfg = cls(
+            architecture=mt,
+            vocab_size=req("vocab_size"),
+            hidden_size=req("hidden_size"),
+            intermediate_size=req("intermediate_size"),
+            num_hidden_layers=req("num_hidden_layers"),
+            num_attention_heads=heads,
+            num_key_value_heads=opt_int("num_key_value_heads") or heads,
+            num_experts=experts,
+            num_experts_per_token=opt_int("num_experts_per_tok") or 0,
+            qk_norm=mt == "olmoe",
+            rope_layout=ROPE_SPLIT_HALF,
+            max_position_embeddings=req("max_position_embeddings"),
+            rope_theta=opt_float("rope_theta", 10_000.0),
+            rms_norm_eps=opt_float("rms_norm_eps", 0.000001),
+            tie_word_embeddings=opt_bool("tie_word_embeddings", False),
+            qkv_bias=opt_bool("attention_bias", mt == "qwen2"),
+            eos_token_id=token_id("eos_token_id"),
+            pad_token_id=token_id("pad_token_id"),
+        )
+        cfg.validate()
+        return cfg
+
+
+# ---------------------------------------------------------------------------
+# Named shapes.
+# ---------------------------------------------------------------------------
+def tiny_test() -> Config:
+    """The reference's tiny runner test (src/llm.zig:1743-1782)."""
+    return Config(
+        vocab_size=24,
+        hidden_size=16,
+        intermediate_size=32,
+        num_hidden_layers=2,
+        num_attention_heads=4,
+        num_key_value_heads=2,
+        max_position_embeddings=16,
+        rope_theta=10_000.0,
+        rms_norm_eps=0.000001,
+        tie_word_embeddings=True,
+        eos_token_id=2,
+        pad_token_id=0,
+    )
+
+
+def qwen25_05b() -> Config:
+    """Qwen2.5-0.5B: 24 layers, hidden 896, 14/2 heads, inter 4864, vocab 151936, tied, qkv bias."""
+    return Config(
+        architecture="qwen2",
+        vocab_size=151936,
+        hidden_size=896,
+        intermediate_size=4864,
+        num_hidden_layers=24,
+        num_attention_heads=14,
+        num_key_value_heads=2,
+        max_position_embeddings=32768,
+        rope_theta=1_000_000.0,
+        rms_norm_eps=1e-6,
+        tie_word_embeddings=True,
+        qkv_bias=True,
+        rope_layout=ROPE_SPLIT_HALF,
+        eos_token_id=151645,
+        pad_token_id=151654,
+    )
+
+
+def llama32_1b() -> Config:
+    """Llama-3.2-1B as read from a GGUF (Config.fromGguf, src/llm.zig:153-193):
+    interleaved RoPE, no qkv bias, tied (no output.weight)."""
+    return Config(
+        architecture="llama",
+        vocab_size=128256,
+        hidden_size=2048,
+        intermediate_size=8192,
+        num_hidden_layers=16,
+        num_attention_heads=32,
+        num_key_value_heads=8,
+        max_position_embeddings=131072,
+        rope_theta=500_000.0,
+        rms_norm_eps=1e-5,
+        tie_word_embeddings=True,
+        qkv_bias=False,
+        rope_layout=ROPE_INTERLEAVED,
+        eos_token_id=128009,
+        pad_token_id=128004,
+    )
+
+
+def qwen25_7b() -> Config:
+    """Qwen2.5-7B: 28 layers, hidden 3584, 28/4 heads, hd 128, inter 18944, untied, qkv bias."""
+    return Config(
+        architecture="qwen2",
+        vocab_size=152064,
+        hidden_size=3584,
+        intermediate_size=18944,
+        num_hidden_layers=28,
+        num_attention_heads=28,
+        num_key_value_heads=4,
+        max_position_embeddings=32768,
+        rope_theta=1_000_000.0,
+        rms_norm_eps=1e-6,
+        tie_word_embeddings=False,
+        qkv_bias=True,
+        rope_layout=ROPE_SPLIT_HALF,
+        eos_token_id=151645,
+        pad_token_id=151643,
+    )
+
+
+NAMED = {
+    "tiny": tiny_test,
+    "qwen2.5-0.5b": qwen25_05b,
+    "llama-3.2-1b": llama32_1b,
+    "qwen2.5-7b": qwen25_7b,
+}

@@ -1,0 +1,234 @@
+// attention.hip -- batch-1 GQA decode attention over the f32 KV cache.
+//
+// Reference: Runner.forwardLayer (src/llm.zig:742-755) -> applyRoPE on q and
+// k (:1337-1371), K/V append at `pos` (:744-745), computeAttentionInto
+// (:1302-1335): per q head, s_t = (q.K_t)/sqrt(hd) for t <= pos, softmax,
+// out = sum_t p_t V_t.
+//
+// Design: grid = (nsplit, kv_heads). Block (s, h) takes a contiguous range of
+// positions of kv head h for all `group` q heads that share it (GQA), walks
+// it in LDS tiles with an online softmax, and writes (m, l, acc) partials.
+// The block whose range holds `pos` rotates the new k, appends k/v to the
+// cache and uses them straight from LDS. The last block of each kv head
+// (atomic ticket) merges the partials. The position is read from device
+// memory, so the launch can be replayed from a graph.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace vvli {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxGroup = 16;
+constexpr uint32_t kMinChunk = 16;
+
+__device__ inline void rope_pair(const float* src, float* dst, int first, int second, float c, float s) {
+    // rotatePair, src/llm.zig:1360-1371 (kept unfused: x0*c - x1*s, x0*s + x1*c)
+    const float x0 = src[first], x1 = src[second];
+    dst[first] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    dst[second] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+__device__ inline void pair_index(uint32_t layout, int i, int hd, int& first, int& second) {
+    if (layout == 0) {  // interleaved: (2i, 2i+1)
+        first = 2 * i;
+        second = 2 * i + 1;
+    } else {  // split_half: (i, i + hd/2)
+        first = i;
+        second = i + hd / 2;
+    }
+}
+
+template <int HDMAX>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
+    constexpr int TILE = 4096 / HDMAX;                      // 64 rows at hd 64, 32 at hd 128
+    constexpr int NP = (kMaxGroup * HDMAX + kThreads - 1) / kThreads;  // (g,d) pairs per thread
+
+    __shared__ float qs[kMaxGroup][HDMAX];
+    __shared__ float ks[TILE][HDMAX + 1];
+    __shared__ float vs[TILE][HDMAX];
+    __shared__ float ps[kMaxGroup][TILE];
+    __shared__ float knew[HDMAX], vnew[HDMAX];
+    __shared__ float m_s[kMaxGroup], l_s[kMaxGroup], c_s[kMaxGroup];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int hd = (int)a.hd;
+    const int half = hd / 2;
+    const uint32_t h = blockIdx.y;
+    const uint32_t s = blockIdx.x;
+    const int G = (int)(a.heads / a.kv_heads);
+    const uint32_t kvw = a.kv_heads * a.hd;
+    const uint32_t pos = *a.pos;
+    const uint32_t T = pos + 1;
+    uint32_t chunk = (T + a.nsplit - 1) / a.nsplit;
+    if (chunk < kMinChunk) chunk = kMinChunk;
+    const uint32_t t0 = s * chunk;
+    const uint32_t t1 = min(t0 + chunk, T);
+    const float* cs = a.rope_cs + (size_t)pos * hd;  // [hd/2][2]
+
+    if (t0 < t1) {
+        // RoPE'd q for the group's heads.
+        for (int idx = tid; idx < G * half; idx += kThreads) {
+            const int g = idx / half, i = idx - g * half;
+            int f, sc;
+            pair_index(a.rope_layout, i, hd, f, sc);
+            rope_pair(a.q + (size_t)(h * G + g) * hd, qs[g], f, sc, cs[2 * i], cs[2 * i + 1]);
+        }
+        const bool owns_pos = pos >= t0 && pos < t1;
+        if (owns_pos) {
+            const float* kn = a.k_new + (size_t)h * hd;
+            for (int i = tid; i < half; i += kThreads) {
+                int f, sc;
+                pair_index(a.rope_layout, i, hd, f, sc);
+                rope_pair(kn, knew, f, sc, cs[2 * i], cs[2 * i + 1]);
+            }
+            for (int d = tid; d < hd; d += kThreads) vnew[d] = a.v_new[(size_t)h * hd + d];
+        }
+        if (tid < kMaxGroup) {
+            m_s[tid] = -INFINITY;
+            l_s[tid] = 0.f;
+        }
+        __syncthreads();
+        if (owns_pos) {
+            float* kd = a.kcache + (size_t)pos * kvw + (size_t)h * hd;
+            float* vd = a.vcache + (size_t)pos * kvw + (size_t)h * hd;
+            for (int d = tid; d < hd; d += kThreads) {
+                kd[d] = knew[d];
+                vd[d] = vnew[d];
+            }
+        }
+
+        float acc[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) acc[i] = 0.f;
+
+        for (uint32_t ta = t0; ta < t1; ta += TILE) {
+            const int tlen = (int)min((uint32_t)TILE, t1 - ta);
+            // Stage K/V rows of this kv head (row `pos` comes from LDS).
+            const int vec_per_row = hd / 4;
+            for (int idx = tid; idx < tlen * vec_per_row; idx += kThreads) {
+                const int j = idx / vec_per_row, c4 = (idx - j * vec_per_row) * 4;
+                const uint32_t t = ta + j;
+                float4 kv4, vv4;
+                if (t == pos) {
+                    kv4 = make_float4(knew[c4], knew[c4 + 1], knew[c4 + 2], knew[c4 + 3]);
+                    vv4 = make_float4(vnew[c4], vnew[c4 + 1], vnew[c4 + 2], vnew[c4 + 3]);
+                } else {
+                    const size_t off = (size_t)t * kvw + (size_t)h * hd + c4;
+                    kv4 = *reinterpret_cast<const float4*>(a.kcache + off);
+                    vv4 = *reinterpret_cast<const float4*>(a.vcache + off);
+                }
+                ks[j][c4] = kv4.x;
+                ks[j][c4 + 1] = kv4.y;
+                ks[j][c4 + 2] = kv4.z;
+                ks[j][c4 + 3] = kv4.w;
+                *reinterpret_cast<float4*>(&vs[j][c4]) = vv4;
+            }
+            __syncthreads();
+            // Scores s[g][j] = (q_g . K_j) * scale.
+            for (int idx = tid; idx < G * TILE; idx += kThreads) {
+                const int g = idx / TILE, j = idx - g * TILE;
+                float d0 = 0.f;
+                if (j < tlen) {
+                    for (int d = 0; d < hd; ++d) d0 = fmaf(qs[g][d], ks[j][d], d0);
+                    d0 *= a.scale;
+                } else {
+                    d0 = -INFINITY;
+                }
+                ps[g][j] = d0;
+            }
+            __syncthreads();
+            // Online softmax update, one wave per q head.
+            for (int g = wave; g < G; g += kThreads / kWave) {
+                const float sc = lane < TILE ? ps[g][lane] : -INFINITY;
+                const float m_old = m_s[g];
+                const float m_new = fmaxf(m_old, wave_max(sc));
+                const float corr = expf(m_old - m_new);
+                const float e = lane < tlen ? expf(sc - m_new) : 0.f;
+                if (lane < TILE) ps[g][lane] = e;
+                const float lsum = wave_sum(e);
+                if (lane == 0) {
+                    l_s[g] = l_s[g] * corr + lsum;
+                    m_s[g] = m_new;
+                    c_s[g] = corr;
+                }
+            }
+            __syncthreads();
+            // acc[g][d] = acc * corr + sum_j p[g][j] V[j][d]
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int idx = tid + i * kThreads;
+                if (idx < G * hd) {
+                    const int g = idx / hd, d = idx - g * hd;
+                    float v = acc[i] * c_s[g];
+                    for (int j = 0; j < tlen; ++j) v = fmaf(ps[g][j], vs[j][d], v);
+                    acc[i] = v;
+                }
+            }
+            __syncthreads();
+        }
+        // Partials: [h][s][g][2 + hd] = (m, l, acc[hd]).
+        const size_t stride = (size_t)2 + hd;
+        float* pbase = a.part + ((size_t)h * a.nsplit + s) * G * stride;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int idx = tid + i * kThreads;
+            if (idx < G * hd) {
+                const int g = idx / hd, d = idx - g * hd;
+                pbase[g * stride + 2 + d] = acc[i];
+            }
+        }
+        if (tid < G) {
+            pbase[tid * stride] = m_s[tid];
+            pbase[tid * stride + 1] = l_s[tid];
+        }
+    }
+
+    // Ticket: the last block of this kv head merges the partials.
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = atomicAdd(&a.counters[h], 1u);
+        last_flag = prev == a.nsplit - 1;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    const uint32_t ns = min(a.nsplit, (T + chunk - 1) / chunk);
+    const size_t stride = (size_t)2 + hd;
+    const float* hbase = a.part + (size_t)h * a.nsplit * G * stride;
+    for (int idx = tid; idx < G * hd; idx += kThreads) {
+        const int g = idx / hd, d = idx - g * hd;
+        float M = -INFINITY;
+        for (uint32_t sp = 0; sp < ns; ++sp) M = fmaxf(M, hbase[(sp * G + g) * stride]);
+        float L = 0.f, O = 0.f;
+        for (uint32_t sp = 0; sp < ns; ++sp) {
+            const float* p = hbase + (sp * G + g) * stride;
+            const float w = expf(p[0] - M);
+            L = fmaf(p[1], w, L);
+            O = fmaf(p[2 + d], w, O);
+        }
+        a.out[(size_t)(h * G + g) * hd + d] = O / L;
+    }
+    if (tid == 0) a.counters[h] = 0;
+}
+
+}  // namespace
+
+size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t nsplit) {
+    return (size_t)kv_heads * nsplit * (heads / kv_heads) * (2 + hd);
+}
+
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s) {
+    dim3 grid(a.nsplit, a.kv_heads);
+    if (a.hd <= 64)
+        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace vvli

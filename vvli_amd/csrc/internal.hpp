@@ -1,0 +1,52 @@
+// internal.hpp -- declarations shared by the host-side sources of libvvli_gpu.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "vvli_gpu.h"
+
+namespace vvli {
+
+// Thread-local error text; every failing entry point sets it and returns rc.
+int set_error(int rc, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+constexpr size_t kNone = static_cast<size_t>(-1);
+constexpr size_t kAlignBytes = 64;  // src/tensor.zig:8 data_alignment_bytes
+
+inline uint32_t head_dim(const vvli_gpu_config& c) { return c.hidden / c.heads; }     // src/llm.zig:229-231
+inline uint32_t kv_dim(const vvli_gpu_config& c) { return c.kv_heads * head_dim(c); }  // src/llm.zig:233-235
+inline uint32_t kv_group(const vvli_gpu_config& c) { return c.heads / c.kv_heads; }    // src/llm.zig:237-239
+inline size_t elem_bytes(const vvli_gpu_config& c) { return c.weight_kind == VVLI_WEIGHT_BF16 ? 2 : 4; }
+
+// Offsets (elements) of every slice of the blob; OwnedModel.assignSlices
+// order (src/llm.zig:488-522), each slice aligned to 64 bytes.
+struct LayerSlices {
+    size_t input_norm, q, q_bias, k, k_bias, v, v_bias, o, post_norm, gate, up, down;
+};
+struct BlobLayout {
+    size_t embed = 0, final_norm = 0, lm_head = kNone, total = 0;
+    std::vector<LayerSlices> layers;
+};
+
+int validate_config(const vvli_gpu_config& c, bool require_dense);
+uint64_t parameter_count(const vvli_gpu_config& c);
+BlobLayout compute_layout(const vvli_gpu_config& c);
+
+// bf16 <-> f32 (src/llm.zig:791-803).
+inline float bf16_to_f32(uint16_t b) {
+    uint32_t u = static_cast<uint32_t>(b) << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+}
+inline uint16_t f32_to_bf16(float v) {
+    uint32_t b;
+    __builtin_memcpy(&b, &v, 4);
+    return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+}  // namespace vvli

@@ -1,0 +1,90 @@
+// kernels.hpp -- host-side launch interface of the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vvli {
+
+// ---------------------------------------------------------------------------
+// GEMV (batch-1 linearInto, src/llm.zig:1228-1275) with fused prologue /
+// epilogues. Weights are row-major [rows][K] in the blob dtype.
+// ---------------------------------------------------------------------------
+enum GemvMode {
+    kGemvPlain = 0,   // out[r] = W.x (+ bias[r]); up to 3 stacked segments (q|k|v)
+    kGemvResid = 1,   // out[r] += W.x            (o_proj / down_proj + residual add)
+    kGemvGateUp = 2,  // out[r] = silu(Wg.x) * (Wu.x)   (gate/up + siluMulInto)
+    kGemvLogits = 3,  // out[r] = W.x; per-block argmax key -> block_keys[block]
+};
+
+struct GemvArgs {
+    const void* w[3] = {nullptr, nullptr, nullptr};
+    const void* bias[3] = {nullptr, nullptr, nullptr};
+    float* out[3] = {nullptr, nullptr, nullptr};
+    uint32_t rows[3] = {0, 0, 0};
+    const void* w_up = nullptr;      // gate/up mode: the up matrix (rows of w[0])
+    const float* x = nullptr;        // input vector, K floats
+    const void* norm_w = nullptr;    // RMSNorm weight applied to x first (nullable)
+    float eps = 0.f;
+    uint32_t K = 0;
+    unsigned long long* block_keys = nullptr;  // logits mode
+};
+
+// Rows per block for a mode (host uses it to size block_keys and to check
+// that stacked segments split on block boundaries).
+uint32_t gemv_rows_per_block(int mode);
+uint32_t gemv_grid(int mode, uint32_t total_rows);
+hipError_t launch_gemv(int weight_kind, int mode, const GemvArgs& a, hipStream_t s);
+hipError_t gemv_init_attributes();
+
+// ---------------------------------------------------------------------------
+// Decode attention (computeAttentionInto, src/llm.zig:1302-1335) with RoPE of
+// q / new k (applyRoPE, :1337-1371) and the KV append (:744-745) fused in.
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+    const float* q = nullptr;      // raw q (after bias), heads*hd
+    const float* k_new = nullptr;  // raw k of this position, kv floats
+    const float* v_new = nullptr;
+    float* kcache = nullptr;       // this layer's [max_seq][kv] keys
+    float* vcache = nullptr;
+    const uint32_t* pos = nullptr;  // device: current position
+    const float* rope_cs = nullptr;  // [max_seq][hd/2][2] (cos, sin)
+    float* part = nullptr;           // [kv_heads][nsplit][group][hd+2]
+    uint32_t* counters = nullptr;    // [kv_heads], zero between launches
+    float* out = nullptr;            // heads*hd
+    uint32_t heads = 0, kv_heads = 0, hd = 0, nsplit = 0, rope_layout = 0;
+    float scale = 0.f;               // 1/sqrt(hd)
+};
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s);
+size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t nsplit);
+
+// ---------------------------------------------------------------------------
+// Small kernels.
+// ---------------------------------------------------------------------------
+// Device step state read and advanced by the graph-replayable token step.
+// A step embeds `token` at `pos`; the finish kernel then sets pos + 1 and
+// picks the next token: prompt[pos + 1] while inside the prompt, else the
+// argmax, which it appends to out_tokens when `counting` is set.
+struct StepState {
+    uint32_t token;       // token to embed
+    uint32_t pos;         // position of this step
+    uint32_t n_out;       // tokens appended to out_tokens so far
+    uint32_t counting;    // 1: append post-prompt argmaxes to out_tokens
+    uint32_t argmax;      // argmax of the last logits
+    uint32_t prompt_len;  // tokens of `prompt` still to be fed, counted from pos 0
+    uint32_t pad[2];
+};
+
+// copyEmbeddingToken (src/llm.zig:1373-1380): x = embed[token] as f32.
+hipError_t launch_embed(int weight_kind, const void* embed, const StepState* st, float* x, uint32_t hidden,
+                        hipStream_t s);
+// Reduce block argmax keys, then advance the step state (see StepState).
+hipError_t launch_argmax_finish(const unsigned long long* keys, uint32_t nkeys, const float* logits,
+                                StepState* st, const uint32_t* prompt, uint32_t* out_tokens, uint32_t out_cap,
+                                hipStream_t s);
+// Host-free state reset (a kernel, so it is safe to capture and to enqueue
+// back to back without a pinned staging buffer).
+hipError_t launch_set_state(StepState* st, uint32_t token, uint32_t pos, uint32_t prompt_len, uint32_t counting,
+                            hipStream_t s);
+
+}  // namespace vvli

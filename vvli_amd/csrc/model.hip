@@ -1,0 +1,593 @@
+// model.hip -- the C ABI of include/vvli_gpu.h: device-resident model, the
+// token step, and the greedy generation loop.
+//
+// Device memory of one model (one HIP stream per model):
+//   blob      weights, byte-identical to the host blob (OwnedModel layout)
+//   k, v      f32 KV cache [layer][max_seq][kv_dim] (KVCache, src/llm.zig:539-606)
+//   rope_cs   (cos, sin) of pos * inv_freq for every position, f32
+//   x, qkv, attn, ff, logits   f32 activations (Scratch, src/llm.zig:608-686)
+//   part, counters             decode-attention split partials
+//   keys, state, prompt, out   argmax keys and the device-side step state
+// One token step = embed, per layer {qkv GEMV, attention, o GEMV + residual,
+// gate/up GEMV + SwiGLU, down GEMV + residual}, logits GEMV, argmax. It reads
+// the token and position from `state`, so it is captured once into a HIP
+// graph and replayed; generation chains the steps on the device.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "internal.hpp"
+#include "kernels.hpp"
+
+using namespace vvli;
+
+struct vvli_gpu_model {
+    vvli_gpu_config cfg{};
+    uint32_t max_seq = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    BlobLayout layout;
+    size_t ebytes = 2;
+    char* blob = nullptr;
+    float* kcache = nullptr;
+    float* vcache = nullptr;
+    float* rope_cs = nullptr;
+    float* x = nullptr;
+    float* qkv = nullptr;
+    float* attn = nullptr;
+    float* ff = nullptr;
+    float* logits = nullptr;
+    float* hidden = nullptr;
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
+    unsigned long long* keys = nullptr;
+    uint32_t nkeys = 0;
+    StepState* state = nullptr;
+    uint32_t* prompt = nullptr;
+    uint32_t* out_tokens = nullptr;
+    uint32_t out_cap = 0;
+    StepState* h_state = nullptr;  // pinned
+    uint32_t nsplit = 1;
+    hipGraphExec_t graph = nullptr;
+    std::vector<float> inv_freq;
+    std::vector<hipEvent_t>* prof = nullptr;  // set while profiling: one event per launch boundary
+};
+
+namespace {
+
+#define HIP_TRY(expr)                                                                                   \
+    do {                                                                                                \
+        hipError_t e_ = (expr);                                                                         \
+        if (e_ != hipSuccess)                                                                           \
+            return set_error(e_ == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR, "%s: %s", \
+                             #expr, hipGetErrorString(e_));                                             \
+    } while (0)
+
+// Records a launch boundary when the step is being profiled.
+int mark(vvli_gpu_model* m, hipStream_t s) {
+    if (!m->prof) return VVLI_OK;
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    m->prof->push_back(e);
+    HIP_TRY(hipEventRecord(e, s));
+    return VVLI_OK;
+}
+
+#define LAUNCH(expr)                  \
+    do {                              \
+        HIP_TRY(expr);                \
+        int mrc_ = mark(m, s);        \
+        if (mrc_) return mrc_;        \
+    } while (0)
+
+const void* wslice(const vvli_gpu_model* m, size_t off) {
+    return off == kNone ? nullptr : static_cast<const void*>(m->blob + off * m->ebytes);
+}
+
+int init_once() {
+    static std::once_flag flag;
+    static hipError_t err = hipSuccess;
+    std::call_once(flag, [] { err = gemv_init_attributes(); });
+    HIP_TRY(err);
+    return VVLI_OK;
+}
+
+// inv_freq[i] = 1 / pow(theta, 2i / hd) in f32 (rotatePair, src/llm.zig:1360-1363),
+// then (cos, sin) of the f32 angle pos * inv_freq for every position.
+int upload_rope(vvli_gpu_model* m) {
+    const uint32_t hd = head_dim(m->cfg), half = hd / 2;
+    if (m->inv_freq.empty()) {
+        m->inv_freq.resize(half);
+        for (uint32_t i = 0; i < half; ++i) {
+            const float exponent = static_cast<float>(2 * i) / static_cast<float>(hd);
+            m->inv_freq[i] = 1.0f / powf(m->cfg.rope_theta, exponent);
+        }
+    }
+    std::vector<float> cs(static_cast<size_t>(m->max_seq) * hd);
+    for (uint32_t p = 0; p < m->max_seq; ++p) {
+        const float pos_f = static_cast<float>(p);
+        for (uint32_t i = 0; i < half; ++i) {
+            const float angle = pos_f * m->inv_freq[i];
+            cs[(static_cast<size_t>(p) * half + i) * 2] = cosf(angle);
+            cs[(static_cast<size_t>(p) * half + i) * 2 + 1] = sinf(angle);
+        }
+    }
+    HIP_TRY(hipMemcpy(m->rope_cs, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+    return VVLI_OK;
+}
+
+int check_kernel_shapes(const vvli_gpu_config& c) {
+    const uint32_t hd = head_dim(c), e = c.weight_kind == VVLI_WEIGHT_BF16 ? 8 : 4;
+    if (hd % 4 != 0 || hd > 128)
+        return set_error(VVLI_INVALID_CONFIG, "head_dim %u: GPU kernels need a multiple of 4 up to 128", hd);
+    if (kv_group(c) > 16) return set_error(VVLI_INVALID_CONFIG, "GQA group %u > 16", kv_group(c));
+    if (c.hidden % e != 0 || c.inter % e != 0)
+        return set_error(VVLI_INVALID_CONFIG, "hidden/intermediate must be multiples of %u", e);
+    return VVLI_OK;
+}
+
+// The layers, final norm and logits of one step (embedding already in x).
+int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+    const vvli_gpu_config& c = m->cfg;
+    const int kind = static_cast<int>(c.weight_kind);
+    const uint32_t H = c.hidden, kv = kv_dim(c), I = c.inter, hd = head_dim(c);
+    float* q = m->qkv;
+    float* kn = m->qkv + H;
+    float* vn = m->qkv + H + kv;
+    const uint32_t rplain = gemv_rows_per_block(kGemvPlain);
+    const bool stack = (H % rplain == 0) && (kv % rplain == 0);
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const LayerSlices& L = m->layout.layers[l];
+        // 1. input RMSNorm + q/k/v projections (+ bias).
+        GemvArgs g;
+        g.x = m->x;
+        g.norm_w = wslice(m, L.input_norm);
+        g.eps = c.rms_eps;
+        g.K = H;
+        if (stack) {
+            g.w[0] = wslice(m, L.q);
+            g.w[1] = wslice(m, L.k);
+            g.w[2] = wslice(m, L.v);
+            g.bias[0] = wslice(m, L.q_bias);
+            g.bias[1] = wslice(m, L.k_bias);
+            g.bias[2] = wslice(m, L.v_bias);
+            g.out[0] = q;
+            g.out[1] = kn;
+            g.out[2] = vn;
+            g.rows[0] = H;
+            g.rows[1] = kv;
+            g.rows[2] = kv;
+            LAUNCH(launch_gemv(kind, kGemvPlain, g, s));
+        } else {
+            const size_t wo[3] = {L.q, L.k, L.v}, bo[3] = {L.q_bias, L.k_bias, L.v_bias};
+            float* outs[3] = {q, kn, vn};
+            const uint32_t rows[3] = {H, kv, kv};
+            for (int i = 0; i < 3; ++i) {
+                GemvArgs gi = g;
+                gi.w[0] = wslice(m, wo[i]);
+                gi.bias[0] = wslice(m, bo[i]);
+                gi.out[0] = outs[i];
+                gi.rows[0] = rows[i];
+                LAUNCH(launch_gemv(kind, kGemvPlain, gi, s));
+            }
+        }
+        // 2. RoPE + KV append + attention.
+        AttnArgs a;
+        a.q = q;
+        a.k_new = kn;
+        a.v_new = vn;
+        a.kcache = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
+        a.vcache = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
+        a.pos = &m->state->pos;
+        a.rope_cs = m->rope_cs;
+        a.part = m->part;
+        a.counters = m->counters;
+        a.out = m->attn;
+        a.heads = c.heads;
+        a.kv_heads = c.kv_heads;
+        a.hd = hd;
+        a.nsplit = m->nsplit;
+        a.rope_layout = c.rope_layout;
+        a.scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/llm.zig:1313
+        LAUNCH(launch_attn_decode(a, s));
+        // 3. x += Wo . attn
+        GemvArgs go;
+        go.w[0] = wslice(m, L.o);
+        go.out[0] = m->x;
+        go.rows[0] = H;
+        go.x = m->attn;
+        go.K = H;
+        LAUNCH(launch_gemv(kind, kGemvResid, go, s));
+        // 4. post-attention RMSNorm + gate/up + SwiGLU.
+        GemvArgs gu;
+        gu.w[0] = wslice(m, L.gate);
+        gu.w_up = wslice(m, L.up);
+        gu.out[0] = m->ff;
+        gu.rows[0] = I;
+        gu.x = m->x;
+        gu.norm_w = wslice(m, L.post_norm);
+        gu.eps = c.rms_eps;
+        gu.K = H;
+        LAUNCH(launch_gemv(kind, kGemvGateUp, gu, s));
+        // 5. x += Wd . ff
+        GemvArgs gd;
+        gd.w[0] = wslice(m, L.down);
+        gd.out[0] = m->x;
+        gd.rows[0] = H;
+        gd.x = m->ff;
+        gd.K = I;
+        LAUNCH(launch_gemv(kind, kGemvResid, gd, s));
+        if (hidden_dbg)
+            HIP_TRY(hipMemcpyAsync(hidden_dbg + static_cast<size_t>(l) * H, m->x, H * sizeof(float),
+                                   hipMemcpyDeviceToDevice, s));
+    }
+    // Final RMSNorm + logits (lm_head, or the embedding when tied: logitsMatrix, src/llm.zig:410-412).
+    GemvArgs gl;
+    gl.w[0] = wslice(m, c.tie ? m->layout.embed : m->layout.lm_head);
+    gl.out[0] = m->logits;
+    gl.rows[0] = c.vocab;
+    gl.x = m->x;
+    gl.norm_w = wslice(m, m->layout.final_norm);
+    gl.eps = c.rms_eps;
+    gl.K = H;
+    gl.block_keys = m->keys;
+    LAUNCH(launch_gemv(kind, kGemvLogits, gl, s));
+    LAUNCH(launch_argmax_finish(m->keys, m->nkeys, m->logits, m->state, m->prompt, m->out_tokens, m->out_cap, s));
+    return VVLI_OK;
+}
+
+int enqueue_step(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+    int rc = mark(m, s);
+    if (rc) return rc;
+    LAUNCH(launch_embed(static_cast<int>(m->cfg.weight_kind), wslice(m, m->layout.embed), m->state, m->x,
+                        m->cfg.hidden, s));
+    return enqueue_body(m, s, hidden_dbg);
+}
+
+int ensure_graph(vvli_gpu_model* m) {
+    if (m->graph) return VVLI_OK;
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, m->stream, nullptr);
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc != VVLI_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    HIP_TRY(e);
+    e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_TRY(e);
+    return VVLI_OK;
+}
+
+int read_outputs(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
+    if (logits_out)
+        HIP_TRY(hipMemcpyAsync(logits_out, m->logits, static_cast<size_t>(m->cfg.vocab) * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (argmax_out) *argmax_out = m->h_state->argmax;
+    return VVLI_OK;
+}
+
+void free_model(vvli_gpu_model* m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
+                    m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->h_state) (void)hipHostFree(m->h_state);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+template <typename T>
+int dmalloc(T** p, size_t count) {
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(p), (count ? count : 1) * sizeof(T)));
+    return VVLI_OK;
+}
+
+int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob, size_t blob_elems,
+                vvli_gpu_model** out) {
+    if (!cfg || !host_blob || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create");
+    *out = nullptr;
+    int rc = validate_config(*cfg, true);
+    if (rc) return rc;
+    if ((rc = check_kernel_shapes(*cfg))) return rc;
+    if (max_seq_len == 0 || max_seq_len > cfg->max_pos)  // KVCache.init, src/llm.zig:548
+        return set_error(VVLI_INVALID_CONFIG, "max_seq_len %u not in 1..%u", max_seq_len, cfg->max_pos);
+    if ((rc = init_once())) return rc;
+
+    auto* m = new vvli_gpu_model();
+    m->cfg = *cfg;
+    m->max_seq = max_seq_len;
+    m->layout = compute_layout(*cfg);
+    m->ebytes = elem_bytes(*cfg);
+    if (blob_elems < m->layout.total) {
+        free_model(m);
+        return set_error(VVLI_INVALID_WEIGHT, "blob has %zu elements, layout needs %zu", blob_elems, m->layout.total);
+    }
+    (void)hipGetDevice(&m->device);
+    const uint32_t H = cfg->hidden, kv = kv_dim(*cfg), hd = head_dim(*cfg);
+    const size_t kvlen = static_cast<size_t>(cfg->layers) * max_seq_len * kv;
+    m->nsplit = std::max<uint32_t>(1, std::min<uint32_t>((256 + cfg->kv_heads - 1) / cfg->kv_heads,
+                                                        (max_seq_len + 15) / 16));
+    m->nkeys = gemv_grid(kGemvLogits, cfg->vocab);
+    m->out_cap = max_seq_len + 1;
+#define TRY_ALLOC(expr)         \
+    if ((rc = (expr)) != 0) {   \
+        free_model(m);          \
+        return rc;              \
+    }
+    TRY_ALLOC(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) == hipSuccess
+                  ? 0
+                  : set_error(VVLI_HIP_ERROR, "hipStreamCreate failed"));
+    TRY_ALLOC(dmalloc(&m->blob, m->layout.total * m->ebytes));
+    TRY_ALLOC(dmalloc(&m->kcache, kvlen));
+    TRY_ALLOC(dmalloc(&m->vcache, kvlen));
+    TRY_ALLOC(dmalloc(&m->rope_cs, static_cast<size_t>(max_seq_len) * hd));
+    TRY_ALLOC(dmalloc(&m->x, H));
+    TRY_ALLOC(dmalloc(&m->qkv, H + 2 * kv));
+    TRY_ALLOC(dmalloc(&m->attn, H));
+    TRY_ALLOC(dmalloc(&m->ff, cfg->inter));
+    TRY_ALLOC(dmalloc(&m->logits, cfg->vocab));
+    TRY_ALLOC(dmalloc(&m->hidden, static_cast<size_t>(cfg->layers) * H));
+    TRY_ALLOC(dmalloc(&m->part, attn_part_floats(cfg->heads, cfg->kv_heads, hd, m->nsplit)));
+    TRY_ALLOC(dmalloc(&m->counters, cfg->kv_heads));
+    TRY_ALLOC(dmalloc(&m->keys, m->nkeys));
+    TRY_ALLOC(dmalloc(&m->state, 1));
+    TRY_ALLOC(dmalloc(&m->prompt, max_seq_len));
+    TRY_ALLOC(dmalloc(&m->out_tokens, m->out_cap));
+    TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_state), sizeof(StepState), hipHostMallocDefault) ==
+                      hipSuccess
+                  ? 0
+                  : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
+    auto fail_hip = [&](hipError_t e, const char* what) {
+        return e == hipSuccess ? 0 : set_error(VVLI_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+    };
+    TRY_ALLOC(fail_hip(hipMemcpy(m->blob, host_blob, m->layout.total * m->ebytes, hipMemcpyHostToDevice),
+                       "blob upload"));
+    TRY_ALLOC(fail_hip(hipMemset(m->kcache, 0, kvlen * sizeof(float)), "kv clear"));
+    TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
+    TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
+    TRY_ALLOC(fail_hip(hipMemset(m->state, 0, sizeof(StepState)), "state"));
+    TRY_ALLOC(upload_rope(m));
+    TRY_ALLOC(fail_hip(hipDeviceSynchronize(), "create sync"));
+#undef TRY_ALLOC
+    *out = m;
+    return VVLI_OK;
+}
+
+int64_t now_ns() {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+}  // namespace
+
+extern "C" {
+
+int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob, size_t blob_elems,
+                          vvli_gpu_model** out) {
+    clear_error();
+    return create_impl(cfg, max_seq_len, host_blob, blob_elems, out);
+}
+
+int vvli_gpu_model_destroy(vvli_gpu_model* model) {
+    if (!model) return set_error(VVLI_NULL_ARG, "model is NULL");
+    (void)hipSetDevice(model->device);
+    (void)hipStreamSynchronize(model->stream);
+    free_model(model);
+    return VVLI_OK;
+}
+
+int vvli_gpu_kv_clear(vvli_gpu_model* m) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    HIP_TRY(hipSetDevice(m->device));
+    const size_t kvlen = static_cast<size_t>(m->cfg.layers) * m->max_seq * kv_dim(m->cfg);
+    HIP_TRY(hipMemsetAsync(m->kcache, 0, kvlen * sizeof(float), m->stream));
+    HIP_TRY(hipMemsetAsync(m->vcache, 0, kvlen * sizeof(float), m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return VVLI_OK;
+}
+
+int vvli_gpu_set_rope_table(vvli_gpu_model* m, const float* inv_freq, uint32_t n) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    HIP_TRY(hipSetDevice(m->device));
+    const uint32_t half = head_dim(m->cfg) / 2;
+    if (inv_freq && n != half) return set_error(VVLI_INVALID_CONFIG, "rope table needs %u entries, got %u", half, n);
+    if (inv_freq)
+        m->inv_freq.assign(inv_freq, inv_freq + n);
+    else
+        m->inv_freq.clear();
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return upload_rope(m);
+}
+
+int vvli_gpu_forward_token(vvli_gpu_model* m, uint32_t token, uint32_t pos, float* logits_out, uint32_t* argmax_out) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
+    if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = ensure_graph(m);
+    if (rc) return rc;
+    HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
+    HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    return read_outputs(m, logits_out, argmax_out);
+}
+
+int vvli_gpu_forward_embedding(vvli_gpu_model* m, const float* embedding, uint32_t pos, float* logits_out,
+                               uint32_t* argmax_out) {
+    if (!m || !embedding) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_forward_embedding");
+    if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipMemcpyAsync(m->x, embedding, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_set_state(m->state, 0, pos, 0, 0, m->stream));
+    int rc = enqueue_body(m, m->stream, nullptr);
+    if (rc) return rc;
+    return read_outputs(m, logits_out, argmax_out);
+}
+
+int vvli_gpu_forward_token_debug(vvli_gpu_model* m, uint32_t token, uint32_t pos, float* logits_out,
+                                 float* hidden_out) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
+    if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
+    int rc = enqueue_step(m, m->stream, m->hidden);
+    if (rc) return rc;
+    if (hidden_out)
+        HIP_TRY(hipMemcpyAsync(hidden_out, m->hidden, static_cast<size_t>(m->cfg.layers) * m->cfg.hidden * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    return read_outputs(m, logits_out, nullptr);
+}
+
+int vvli_gpu_profile_step(vvli_gpu_model* m, uint32_t token, uint32_t pos, float* ms_out, uint32_t cap,
+                          uint32_t* n_out) {
+    if (!m || !ms_out || !n_out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_profile_step");
+    if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
+    if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
+    std::vector<hipEvent_t> evs;
+    m->prof = &evs;
+    int rc = enqueue_step(m, m->stream, nullptr);
+    m->prof = nullptr;
+    hipError_t e = hipStreamSynchronize(m->stream);
+    uint32_t n = 0;
+    if (rc == VVLI_OK && e == hipSuccess) {
+        for (size_t i = 1; i < evs.size() && n < cap; ++i, ++n) {
+            float ms = 0.f;
+            e = hipEventElapsedTime(&ms, evs[i - 1], evs[i]);
+            if (e != hipSuccess) break;
+            ms_out[n] = ms;
+        }
+    }
+    for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
+    if (rc) return rc;
+    HIP_TRY(e);
+    *n_out = n;
+    return VVLI_OK;
+}
+
+int vvli_gpu_kv_read(vvli_gpu_model* m, uint32_t layer, uint32_t pos, float* k_out, float* v_out) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (layer >= m->cfg.layers || pos >= m->max_seq)
+        return set_error(VVLI_INVALID_CONFIG, "layer %u / pos %u out of range", layer, pos);
+    HIP_TRY(hipSetDevice(m->device));
+    const size_t kv = kv_dim(m->cfg);
+    const size_t off = (static_cast<size_t>(layer) * m->max_seq + pos) * kv;
+    if (k_out)
+        HIP_TRY(hipMemcpyAsync(k_out, m->kcache + off, kv * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+    if (v_out)
+        HIP_TRY(hipMemcpyAsync(v_out, m->vcache + off, kv * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return VVLI_OK;
+}
+
+int vvli_gpu_prefill(vvli_gpu_model* m, const uint32_t* tokens, uint32_t n, uint32_t start_pos, float* last_logits,
+                     uint32_t* argmax_out) {
+    if (!m || !tokens) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_prefill");
+    if (n == 0) return set_error(VVLI_EMPTY_PROMPT, "empty prompt");
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab", tokens[i]);
+    if (static_cast<uint64_t>(start_pos) + n > m->max_seq)
+        return set_error(VVLI_CONTEXT_FULL, "prefill end %u > max_seq_len %u", start_pos + n, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = ensure_graph(m);
+    if (rc) return rc;
+    // Prompt tokens live at their absolute positions in `prompt`.
+    HIP_TRY(hipMemcpyAsync(m->prompt + start_pos, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_set_state(m->state, tokens[0], start_pos, start_pos + n, 0, m->stream));
+    for (uint32_t i = 0; i < n; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    return read_outputs(m, last_logits, argmax_out);
+}
+
+int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                             int64_t eos, uint32_t flags, uint32_t* out_tokens, uint32_t* n_out,
+                             vvli_gpu_stats* stats) {
+    if (!m || !out_tokens || !n_out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_generate_greedy");
+    if (n_prompt == 0 || !prompt) return set_error(VVLI_EMPTY_PROMPT, "empty prompt");  // generator.zig:230
+    for (uint32_t i = 0; i < n_prompt; ++i)
+        if (prompt[i] >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "prompt token %u >= vocab", prompt[i]);
+    if (n_prompt > m->max_seq)
+        return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
+    (void)flags;
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = ensure_graph(m);
+    if (rc) return rc;
+    const int64_t t0 = now_ns();
+    // Prefill: one step per prompt token, chained on the device.
+    HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
+    for (uint32_t i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    const int64_t t1 = now_ns();
+    // Decode: out[0] is the argmax of the last prompt step. Each step
+    // forwards the last emitted token (the last one too, generator.zig:272).
+    uint32_t produced = 0;
+    if (max_new > 0) {
+        if (eos < 0) {
+            if (static_cast<uint64_t>(n_prompt) + max_new > m->max_seq)
+                return set_error(VVLI_CONTEXT_FULL, "prompt %u + %u new tokens > max_seq_len %u", n_prompt, max_new,
+                                 m->max_seq);
+            for (uint32_t i = 0; i < max_new; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+            produced = max_new;
+        } else {
+            uint32_t pos = n_prompt;
+            while (produced < max_new) {
+                HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+                HIP_TRY(hipStreamSynchronize(m->stream));
+                const uint32_t next = m->h_state->argmax;
+                ++produced;
+                if (static_cast<int64_t>(next) == eos) break;
+                if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len", pos);
+                HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+                ++pos;
+            }
+        }
+        HIP_TRY(hipMemcpyAsync(out_tokens, m->out_tokens, produced * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                               m->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    const int64_t t2 = now_ns();
+    *n_out = produced;
+    if (stats) {
+        stats->prompt_tokens = n_prompt;
+        stats->generated_tokens = produced;
+        stats->prefill_ns = t1 - t0;
+        stats->decode_ns = t2 - t1;
+        stats->total_ns = t2 - t0;
+    }
+    return VVLI_OK;
+}
+
+int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
+                    uint32_t K, void* stream) {
+    if (!dW || !dX || !dY) return set_error(VVLI_NULL_ARG, "NULL device pointer to vvli_gpu_linear");
+    if (M == 0 || N == 0 || K == 0 || K % 8 != 0)
+        return set_error(VVLI_INVALID_CONFIG, "bad linear shape M=%u N=%u K=%u (K %% 8 == 0 required)", M, N, K);
+    int rc = init_once();
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (uint32_t mi = 0; mi < M; ++mi) {
+        GemvArgs g;
+        g.w[0] = dW;
+        g.bias[0] = dBias;
+        g.out[0] = dY + static_cast<size_t>(mi) * N;
+        g.rows[0] = N;
+        g.x = dX + static_cast<size_t>(mi) * K;
+        g.K = K;
+        HIP_TRY(launch_gemv(VVLI_WEIGHT_BF16, kGemvPlain, g, s));
+    }
+    return VVLI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,192 @@
+"""Python host over the C ABI, named after VVLI's runner API.
+
+``Runner`` mirrors ``llm.Runner`` (src/llm.zig:688-776): ``forward_token``,
+``forward_embedding`` and ``argmax``; ``generate_greedy_measured`` mirrors
+``generator.generateGreedyMeasured`` (src/generator.zig:177-293). Every call
+goes through libvvli_gpu.so; nothing here computes model math.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from ctypes import byref, c_uint32, c_void_p
+
+import numpy as np
+
+from . import _lib
+from .config import WEIGHT_BF16, WEIGHT_F32, Config
+
+_DTYPE = {WEIGHT_BF16: np.uint16, WEIGHT_F32: np.float32}
+
+
+def _ptr(a: np.ndarray | None) -> c_void_p | None:
+    return None if a is None else c_void_p(a.ctypes.data)
+
+
+def empty_blob(cfg: Config, weight_kind: int = WEIGHT_BF16) -> np.ndarray:
+    n = cfg.storage_element_count(weight_kind)
+    return np.empty(n, dtype=_DTYPE[weight_kind])
+
+
+def synthetic_blob(cfg: Config, weight_kind: int = WEIGHT_BF16, seed: int = 0, stddev: float = 0.02,
+                   threads: int = 0) -> np.ndarray:
+    """Seeded N(0, stddev) weights, RMSNorm weights 1 (vvli_host_fill_synthetic)."""
+    blob = empty_blob(cfg, weight_kind)
+    c = cfg.to_c(weight_kind)
+    _lib.check(_lib.lib().vvli_host_fill_synthetic(byref(c), seed, stddev, _ptr(blob), blob.size, threads))
+    return blob
+
+
+def deterministic_blob(cfg: Config, weight_kind: int = WEIGHT_F32) -> np.ndarray:
+    """OwnedModel.fillDeterministicForTesting (src/llm.zig:466-477)."""
+    blob = empty_blob(cfg, weight_kind)
+    _lib.lib().vvli_host_fill_deterministic(_ptr(blob), blob.size, weight_kind)
+    return blob
+
+
+def argmax(logits: np.ndarray) -> int:
+    """llm.argmax (src/llm.zig:778-789): first index of the strict maximum."""
+    best, bv = 0, logits[0]
+    for i in range(1, len(logits)):
+        if logits[i] > bv:
+            best, bv = i, logits[i]
+    return best
+
+
+@dataclasses.dataclass
+class Stats:
+    """generator.Stats (src/generator.zig:25-43)."""
+
+    prompt_tokens: int
+    generated_tokens: int
+    prefill_nanoseconds: int
+    decode_nanoseconds: int
+    total_nanoseconds: int
+
+    def decode_tokens_per_second(self) -> float:
+        return _tps(self.generated_tokens, self.decode_nanoseconds)
+
+    def prefill_tokens_per_second(self) -> float:
+        return _tps(self.prompt_tokens, self.prefill_nanoseconds)
+
+    def total_tokens_per_second(self) -> float:
+        return _tps(self.prompt_tokens + self.generated_tokens, self.total_nanoseconds)
+
+
+def _tps(tokens: int, ns: int) -> float:
+    # tokensPerSecond, src/generator.zig:326-330
+    return 0.0 if tokens == 0 or ns <= 0 else tokens * 1e9 / ns
+
+
+class Runner:
+    """Device-resident model + KV cache + scratch on the current HIP device.
+
+    Owns one ``vvli_gpu_model`` handle (weights, f32 KV cache of
+    ``max_seq_len`` positions, activations). The host blob is copied to the
+    device by the constructor and may be dropped afterwards.
+    """
+
+    def __init__(self, cfg: Config, blob: np.ndarray, max_seq_len: int, weight_kind: int | None = None):
+        if weight_kind is None:
+            weight_kind = WEIGHT_BF16 if blob.dtype == np.uint16 else WEIGHT_F32
+        if blob.dtype != _DTYPE[weight_kind]:
+            raise TypeError("blob dtype does not match weight_kind")
+        self.cfg = cfg
+        self.weight_kind = weight_kind
+        self.max_seq_len = max_seq_len
+        self._c = cfg.to_c(weight_kind)
+        handle = c_void_p()
+        blob = np.ascontiguousarray(blob)
+        _lib.check(_lib.lib().vvli_gpu_model_create(byref(self._c), max_seq_len, _ptr(blob), blob.size, byref(handle)))
+        self._h = handle
+        self.logits = np.zeros(cfg.vocab_size, dtype=np.float32)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.check(_lib.lib().vvli_gpu_model_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- llm.Runner ----
+    def forward_token(self, token_id: int, position: int) -> np.ndarray:
+        """Runner.forwardToken (src/llm.zig:702-709); returns the logits."""
+        am = c_uint32()
+        _lib.check(_lib.lib().vvli_gpu_forward_token(self._h, token_id, position, _ptr(self.logits), byref(am)))
+        self.last_argmax = am.value
+        return self.logits
+
+    def forward_token_argmax(self, token_id: int, position: int) -> int:
+        am = c_uint32()
+        _lib.check(_lib.lib().vvli_gpu_forward_token(self._h, token_id, position, None, byref(am)))
+        return am.value
+
+    def forward_embedding(self, embedding: np.ndarray, position: int) -> np.ndarray:
+        """Runner.forwardEmbedding (src/llm.zig:711-718)."""
+        emb = np.ascontiguousarray(embedding, dtype=np.float32)
+        if emb.size != self.cfg.hidden_size:
+            raise _lib.VvliError(2, "embedding length != hidden_size")
+        am = c_uint32()
+        _lib.check(_lib.lib().vvli_gpu_forward_embedding(self._h, _ptr(emb), position, _ptr(self.logits), byref(am)))
+        self.last_argmax = am.value
+        return self.logits
+
+    def forward_token_debug(self, token_id: int, position: int) -> tuple[np.ndarray, np.ndarray]:
+        """forwardToken plus the residual stream after every layer ([layers, hidden])."""
+        hidden = np.zeros((self.cfg.num_hidden_layers, self.cfg.hidden_size), dtype=np.float32)
+        _lib.check(_lib.lib().vvli_gpu_forward_token_debug(self._h, token_id, position, _ptr(self.logits), _ptr(hidden)))
+        return self.logits.copy(), hidden
+
+    def kv_read(self, layer: int, position: int) -> tuple[np.ndarray, np.ndarray]:
+        kv = self.cfg.kv_dim()
+        k = np.zeros(kv, dtype=np.float32)
+        v = np.zeros(kv, dtype=np.float32)
+        _lib.check(_lib.lib().vvli_gpu_kv_read(self._h, layer, position, _ptr(k), _ptr(v)))
+        return k, v
+
+    def kv_clear(self) -> None:
+        _lib.check(_lib.lib().vvli_gpu_kv_clear(self._h))
+
+    def set_rope_table(self, inv_freq: np.ndarray | None) -> None:
+        if inv_freq is None:
+            _lib.check(_lib.lib().vvli_gpu_set_rope_table(self._h, None, 0))
+        else:
+            t = np.ascontiguousarray(inv_freq, dtype=np.float32)
+            _lib.check(_lib.lib().vvli_gpu_set_rope_table(self._h, _ptr(t), t.size))
+
+    def prefill(self, tokens, start_pos: int = 0) -> tuple[np.ndarray, int]:
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        am = c_uint32()
+        _lib.check(_lib.lib().vvli_gpu_prefill(self._h, _ptr(toks), toks.size, start_pos, _ptr(self.logits), byref(am)))
+        return self.logits, am.value
+
+    # ---- generator ----
+    def generate_greedy_measured(self, prompt, max_new_tokens: int, eos_token_id: int | None = None,
+                                 batched_prefill: bool = False) -> tuple[np.ndarray, Stats]:
+        """generateGreedyMeasured (src/generator.zig:177-293), greedy sampler."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(1, max_new_tokens), dtype=np.uint32)
+        n = c_uint32()
+        st = _lib.CStats()
+        eos = -1 if eos_token_id is None else int(eos_token_id)
+        flags = 1 if batched_prefill else 0
+        _lib.check(_lib.lib().vvli_gpu_generate_greedy(self._h, _ptr(p), p.size, max_new_tokens, eos, flags, _ptr(out),
+                                                       byref(n), byref(st)))
+        stats = Stats(st.prompt_tokens, st.generated_tokens, st.prefill_ns, st.decode_ns, st.total_ns)
+        return out[: n.value].copy(), stats
+
+
+def linear(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None = None, stream: int | None = None) -> None:
+    """vvli_gpu_linear on raw device pointers (e.g. torch ``tensor.data_ptr()``)."""
+    _lib.check(_lib.lib().vvli_gpu_linear(c_void_p(dW), c_void_p(dX), None if dBias is None else c_void_p(dBias),
+                                          c_void_p(dY), M, N, K, None if stream is None else c_void_p(stream)))
