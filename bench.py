@@ -109,6 +109,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
+                    help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -129,6 +131,7 @@ def main() -> int:
     print(f"[bench] synthetic blob {blob.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f}s", file=sys.stderr,
           flush=True)
     runner = R.Runner(cfg, blob, args.ctx)
+    runner.set_decode_path(args.path)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
 
     # Warmup: graph capture, clocks, caches.

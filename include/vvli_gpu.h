@@ -156,6 +156,18 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint
  * o_proj, gate_up, down}, then logits, argmax. *n_out = kernels timed. */
 int vvli_gpu_profile_step(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* ms_out, uint32_t cap,
                           uint32_t* n_out);
+/* Which implementation runs forward_token / prefill / generate:
+ * 0 = auto (currently the per-kernel graph, the faster one on the Llama-1B
+ * decode benchmark), 1 = per-kernel HIP graph, 2 = persistent one-launch step
+ * (bf16 weights only; VVLI_INVALID_CONFIG if unavailable). For A/B
+ * measurement and for checking both against the same reference. */
+int vvli_gpu_set_decode_path(vvli_gpu_model* model, uint32_t path);
+/* One persistent step with phase timestamps (100 MHz ticks): ticks_out holds
+ * (n_blocks + 1) * stride values; row b < n_blocks = block b's arrival at
+ * barrier k (k >= 1), the last row = the release of barrier k (k = 0: start).
+ * *n_blocks = blocks of the persistent launch. */
+int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t pos, uint64_t* ticks_out,
+                                uint32_t stride, uint32_t* n_blocks);
 
 /* ---------------------------------------------------------------------- */
 /* Isolated matmul op (device pointers)                                    */

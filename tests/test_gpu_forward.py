@@ -93,13 +93,15 @@ def test_token_steps_match_oracle(name, built, oracle_mod, host_threads):
 
 @pytest.mark.parametrize("name", ["tiny_f32", "qwen_small", "llama_small"])
 def test_graph_step_equals_debug_step(name, built):
-    """The graph-replayed step (forward_token) gives the same logits and
-    argmax as the eagerly launched one (forward_token_debug)."""
+    """The graph-replayed per-kernel step (forward_token on the 'graph' path)
+    gives the same logits and argmax as the eagerly launched one
+    (forward_token_debug): same kernels, same order."""
     cfg, kind, how, steps = CASES[name]
     blob = make_blob(cfg, kind, how)
     max_seq = min(cfg.max_position_embeddings, 64)
     toks = np.random.default_rng(2).integers(0, cfg.vocab_size, size=min(steps, 12))
     with R.Runner(cfg, blob, max_seq) as a, R.Runner(cfg, blob, max_seq) as b:
+        a.set_decode_path("graph")
         for pos, tok in enumerate(toks):
             la = a.forward_token(int(tok), pos).copy()
             am = a.last_argmax
@@ -108,8 +110,38 @@ def test_graph_step_equals_debug_step(name, built):
             assert am == R.argmax(la)
 
 
+BF16_CASES = ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7", "qwen05_heads"]
+
+
+@pytest.mark.parametrize("name", BF16_CASES)
+def test_persistent_steps_match_oracle(name, built, oracle_mod, host_threads):
+    """The one-launch persistent step (forward_token on the 'persistent'
+    path): logits, argmax and K/V rows against the oracle, token by token."""
+    cfg, kind, how, steps = CASES[name]
+    steps = {"llama_small": 300}.get(name, steps)  # > 2 attention splits of 128 positions
+    max_seq = min(cfg.max_position_embeddings, 512)
+    blob = make_blob(cfg, kind, how)
+    orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
+    toks = np.random.default_rng(1).integers(0, cfg.vocab_size, size=steps)
+    print(f"case={name} steps={steps} persistent", flush=True)
+    with R.Runner(cfg, blob, max_seq) as gpu:
+        gpu.set_decode_path("persistent")
+        for pos, tok in enumerate(toks):
+            ref = orc.forward_token(int(tok), pos)
+            got = gpu.forward_token(int(tok), pos)
+            e = rel_err(got, ref)
+            assert e <= TOL, f"{name} pos {pos}: logits rel err {e:.3e}"
+            assert gpu.last_argmax == oracle_mod.argmax(ref), f"{name} pos {pos}: argmax"
+        for layer in range(cfg.num_hidden_layers):
+            for pos in (0, steps - 1):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"{name} kv layer {layer} pos {pos}"
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7"])
-def test_greedy_generation_matches_oracle(name, built, oracle_mod, host_threads):
+def test_greedy_generation_matches_oracle(name, path, built, oracle_mod, host_threads):
     cfg, kind, how, _ = CASES[name]
     blob = make_blob(cfg, kind, how)
     max_seq = min(cfg.max_position_embeddings, 96)
@@ -118,7 +150,9 @@ def test_greedy_generation_matches_oracle(name, built, oracle_mod, host_threads)
     prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, size=n_prompt).astype(np.uint32)
     orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
     ref, _ = orc.generate_greedy(prompt, n_new)
+    print(f"case={name} path={path}", flush=True)
     with R.Runner(cfg, blob, max_seq) as gpu:
+        gpu.set_decode_path(path)
         got, stats = gpu.generate_greedy_measured(prompt, n_new)
         assert stats.generated_tokens == n_new and stats.prompt_tokens == n_prompt
         np.testing.assert_array_equal(got, ref)

@@ -21,13 +21,18 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxGroup = 16;
-constexpr uint32_t kMinChunk = 16;
+constexpr uint32_t kMinChunk = 64;  // positions per block before another split is used
+constexpr int kMaxSplit = 64;
 
 __device__ inline void rope_pair(const float* src, float* dst, int first, int second, float c, float s) {
     // rotatePair, src/llm.zig:1360-1371 (kept unfused: x0*c - x1*s, x0*s + x1*c)
     const float x0 = src[first], x1 = src[second];
     dst[first] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     dst[second] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+__device__ inline float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ inline void pair_index(uint32_t layout, int i, int hd, int& first, int& second) {
@@ -51,6 +56,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     __shared__ float ps[kMaxGroup][TILE];
     __shared__ float knew[HDMAX], vnew[HDMAX];
     __shared__ float m_s[kMaxGroup], l_s[kMaxGroup], c_s[kMaxGroup];
+    __shared__ float wsplit[kMaxSplit][kMaxGroup];  // combine weights exp(m_s - M) / L
     __shared__ int last_flag;
 
     const int tid = threadIdx.x;
@@ -170,7 +176,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
             }
             __syncthreads();
         }
-        // Partials: [h][s][g][2 + hd] = (m, l, acc[hd]).
+        // Partials: [h][s][g][2 + hd] = (m, l, acc[hd]). Agent-scope stores
+        // write through to the coherence point, so the merging block (on any
+        // XCD) reads them without an L2 writeback/invalidate.
         const size_t stride = (size_t)2 + hd;
         float* pbase = a.part + ((size_t)h * a.nsplit + s) * G * stride;
 #pragma unroll
@@ -178,45 +186,66 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
             const int idx = tid + i * kThreads;
             if (idx < G * hd) {
                 const int g = idx / hd, d = idx - g * hd;
-                pbase[g * stride + 2 + d] = acc[i];
+                __hip_atomic_store(pbase + g * stride + 2 + d, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         if (tid < G) {
-            pbase[tid * stride] = m_s[tid];
-            pbase[tid * stride + 1] = l_s[tid];
+            __hip_atomic_store(pbase + tid * stride, m_s[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pbase + tid * stride + 1, l_s[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-
-    // Ticket: the last block of this kv head merges the partials.
-    __threadfence();
+    // Ticket among the non-empty splits: the last one to finish merges. Every
+    // thread waits for its partial stores to complete before the ticket.
+    const uint32_t ns = min(a.nsplit, (T + chunk - 1) / chunk);
+    if (t0 >= t1) return;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[h], 1u);
-        last_flag = prev == a.nsplit - 1;
+        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == ns - 1;
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
-    const uint32_t ns = min(a.nsplit, (T + chunk - 1) / chunk);
     const size_t stride = (size_t)2 + hd;
     const float* hbase = a.part + (size_t)h * a.nsplit * G * stride;
+    // Split weights: w[s][g] = exp(m_s - M) / sum_s' l_s' exp(m_s' - M).
+    for (int g = wave; g < G; g += kThreads / kWave) {
+        float mv = -INFINITY, lv = 0.f;
+        if ((uint32_t)lane < ns) {
+            mv = __hip_atomic_load(hbase + (lane * G + g) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lv = __hip_atomic_load(hbase + (lane * G + g) * stride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const float M = wave_max(mv);
+        const float e = (uint32_t)lane < ns ? expf(mv - M) : 0.f;
+        const float L = wave_sum(lv * e);
+        if ((uint32_t)lane < ns) wsplit[lane][g] = e / L;
+    }
+    __syncthreads();
     for (int idx = tid; idx < G * hd; idx += kThreads) {
         const int g = idx / hd, d = idx - g * hd;
-        float M = -INFINITY;
-        for (uint32_t sp = 0; sp < ns; ++sp) M = fmaxf(M, hbase[(sp * G + g) * stride]);
-        float L = 0.f, O = 0.f;
-        for (uint32_t sp = 0; sp < ns; ++sp) {
-            const float* p = hbase + (sp * G + g) * stride;
-            const float w = expf(p[0] - M);
-            L = fmaf(p[1], w, L);
-            O = fmaf(p[2 + d], w, O);
+        const float* p = hbase + (size_t)g * stride + 2 + d;
+        float o = 0.f;
+        uint32_t sp = 0;
+        for (; sp + 4 <= ns; sp += 4) {
+            const float a0 = ld_agent(p + (size_t)(sp + 0) * G * stride), a1 = ld_agent(p + (size_t)(sp + 1) * G * stride);
+            const float a2 = ld_agent(p + (size_t)(sp + 2) * G * stride), a3 = ld_agent(p + (size_t)(sp + 3) * G * stride);
+            o = fmaf(a0, wsplit[sp][g], o);
+            o = fmaf(a1, wsplit[sp + 1][g], o);
+            o = fmaf(a2, wsplit[sp + 2][g], o);
+            o = fmaf(a3, wsplit[sp + 3][g], o);
         }
-        a.out[(size_t)(h * G + g) * hd + d] = O / L;
+        for (; sp < ns; ++sp) o = fmaf(ld_agent(p + (size_t)sp * G * stride), wsplit[sp][g], o);
+        a.out[(size_t)(h * G + g) * hd + d] = o;
     }
-    if (tid == 0) a.counters[h] = 0;
+    if (tid == 0) __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
+
+uint32_t attn_nsplit(uint32_t max_seq) {
+    const uint32_t n = (max_seq + kMinChunk - 1) / kMinChunk;
+    return n < 1 ? 1 : (n > (uint32_t)kMaxSplit ? (uint32_t)kMaxSplit : n);
+}
 
 size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t nsplit) {
     return (size_t)kv_heads * nsplit * (heads / kv_heads) * (2 + hd);

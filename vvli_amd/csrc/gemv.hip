@@ -4,14 +4,20 @@
 // 1445-1466): out[r] = sum_k W[r,k] * x[k] (+ bias[r]), bf16 widened exactly
 // by <<16, f32 accumulation.
 //
-// Design: a 256-thread block owns R consecutive rows (R*K*2 contiguous bytes
-// of HBM). The K dimension is cut into 16-byte units (8 bf16); thread t takes
-// units t, t+256, ... of every row, so each wave load is 1 KiB contiguous and
-// every thread reuses its x values across the R rows. Weight loads for the
-// first batch are issued before x is staged (x and the RMSNorm scale come from
-// LDS), so the x round trip hides under the weight latency. Per-thread partial
-// sums are reduced with DPP inside the wave and through LDS across waves.
+// Design (HBM-bound streaming):
+//   * The block stages x in LDS once (optionally RMS-normalised:
+//     x * w * (1/sqrt(mean(x^2) + eps)), rmsNormInto src/llm.zig:1287-1300).
+//   * Work unit = a wave-tile of R rows (R gate rows + R up rows in the
+//     SwiGLU mode). A row is cut into 16-byte units (8 bf16); lane l takes
+//     units l, l+64, ... so every wave load is 1 KiB contiguous. A tile is
+//     walked in "items" of NJC units per lane per row.
+//   * Waves take tiles grid-stride. Items are double-buffered in registers:
+//     the loads of item i+1 are in flight while item i is multiplied, and the
+//     first item's loads are issued before x is staged.
+//   * A row's partial sums are reduced inside the wave with DPP; lane 0
+//     applies the fused epilogue (bias, residual add, SiLU*up, argmax key).
 #include "device_common.hpp"
+#include "gemv_tile.hpp"
 #include "kernels.hpp"
 
 namespace vvli {
@@ -19,16 +25,9 @@ namespace vvli {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
+constexpr int kWavesPerBlock = kThreads / kWave;
+constexpr uint32_t kMaxBlocks = 1024;
 
-template <int MODE> struct ModeCfg;
-template <> struct ModeCfg<kGemvPlain> { static constexpr int R = 8, UB = 2; };
-template <> struct ModeCfg<kGemvResid> { static constexpr int R = 4, UB = 2; };
-template <> struct ModeCfg<kGemvGateUp> { static constexpr int R = 4, UB = 2; };
-template <> struct ModeCfg<kGemvLogits> { static constexpr int R = 8, UB = 2; };
-
-// Stage x (optionally RMS-normalised: out = x * w * s, s = 1/sqrt(mean(x^2)+eps),
-// rmsNormInto src/llm.zig:1287-1300) into LDS.
 template <typename WT>
 __device__ inline void stage_x(float* xs, float* red, const float* __restrict__ x, const WT* __restrict__ norm_w,
                                float eps, uint32_t K) {
@@ -43,8 +42,10 @@ __device__ inline void stage_x(float* xs, float* red, const float* __restrict__ 
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
-        float total = (red[0] + red[1]) + (red[2] + red[3]);
-        float scale = 1.0f / sqrtf(total / (float)K + eps);
+        float total = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) total += red[w];
+        const float scale = 1.0f / sqrtf(total / (float)K + eps);
         for (uint32_t k = tid; k < K; k += kThreads) xs[k] = xs[k] * WeightTraits<WT>::at(norm_w, k) * scale;
     }
     __syncthreads();
@@ -52,138 +53,99 @@ __device__ inline void stage_x(float* xs, float* red, const float* __restrict__ 
 
 template <typename WT, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-    using T = WeightTraits<WT>;
-    constexpr int E = T::kPerUnit;
     constexpr int R = ModeCfg<MODE>::R;
-    constexpr int UB = ModeCfg<MODE>::UB;
-    constexpr int NR = (MODE == kGemvGateUp) ? 2 * R : R;
+    constexpr int NR = (MODE == kGemvGateUp ? 2 : 1) * R;
+    constexpr int E = WeightTraits<WT>::kPerUnit;
+    using TileT = Tile<WT, MODE, NR>;
 
     extern __shared__ float smem[];
     const uint32_t K = a.K;
     float* xs = smem;
-    float* red = smem + K;  // kWaves * NR floats
-
-    const int tid = threadIdx.x;
-    const uint32_t row0 = blockIdx.x * R;
-    int seg = 0;
-    uint32_t base = 0;
-    if (row0 >= a.rows[0]) {
-        base = a.rows[0];
-        seg = 1;
-        if (row0 >= a.rows[0] + a.rows[1]) {
-            base += a.rows[1];
-            seg = 2;
-        }
-    }
-    const uint32_t srow = row0 - base;
-    const uint32_t seg_rows = a.rows[seg];
-
-    const WT* rowp[NR];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        uint32_t rr = srow + r < seg_rows ? srow + r : seg_rows - 1;
-        rowp[r] = static_cast<const WT*>(a.w[seg]) + (size_t)rr * K;
-        if constexpr (MODE == kGemvGateUp) rowp[R + r] = static_cast<const WT*>(a.w_up) + (size_t)rr * K;
-    }
-
+    float* red = smem + K;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * kWavesPerBlock;
     const uint32_t U = K / E;
+    const uint32_t per_item = kNJC * kWave;
+    const uint32_t nchunk = (U + per_item - 1) / per_item;
+    const uint32_t total = a.rows[0] + a.rows[1] + a.rows[2];
+    const uint32_t ntiles = (total + R - 1) / R;
+    // Items of this wave: (tile, chunk) for tile = wid, wid + nwaves, ...
+    const uint32_t my_tiles = wid < ntiles ? (ntiles - 1 - wid) / nwaves + 1 : 0;
+    const uint32_t n_items = my_tiles * nchunk;
+
+    uint4 bufA[NR][kNJC], bufB[NR][kNJC];
+    TileT tA, tB;
+    uint32_t item = 0;
+    if (n_items > 0) {
+        make_tile<WT, MODE>(a, wid, K, tA);
+        issue<WT, NR>(bufA, tA.p, 0, U, lane);
+    }
+    stage_x<WT>(xs, red, a.x, static_cast<const WT*>(a.norm_w), a.eps, K);
+
     float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+    unsigned long long best = 0ull;
 
-    // First batch of weight loads goes out before x is staged.
-    uint4 wv[UB][NR];
-    uint32_t u = tid;
+    // Process item `it` held in `cur`/`tc`; prefetch item it+1 into `nxt`/`tn`.
+    auto step = [&](uint4(&cur)[NR][kNJC], TileT& tc, uint4(&nxt)[NR][kNJC], TileT& tn, uint32_t it) {
+        const uint32_t chunk = it % nchunk;
+        if (it + 1 < n_items) {
+            const uint32_t nit = it + 1, nch = nit % nchunk;
+            if (nch == 0) make_tile<WT, MODE>(a, wid + (nit / nchunk) * nwaves, K, tn);
+            else tn = tc;
+            issue<WT, NR>(nxt, tn.p, nch * per_item, U, lane);
+        }
+        consume<WT, NR>(cur, xs, chunk * per_item, U, lane, acc);
+        if (chunk == nchunk - 1) {
+            float s[NR];
 #pragma unroll
-    for (int b = 0; b < UB; ++b) {
-        const uint32_t ub = u + b * kThreads;
+            for (int r = 0; r < NR; ++r) {
+                s[r] = wave_sum(acc[r]);
+                acc[r] = 0.f;
+            }
+            if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < NR; ++r) wv[b][r] = ub < U ? load_unit(rowp[r] + (size_t)ub * E) : make_uint4(0, 0, 0, 0);
-    }
-
-    stage_x<WT>(xs, red, a.x, static_cast<const WT*>(a.norm_w), a.eps, K);
-
-    while (true) {
-#pragma unroll
-        for (int b = 0; b < UB; ++b) {
-            const uint32_t ub = u + b * kThreads;
-            if (ub < U) {
-                float xv[E];
-#pragma unroll
-                for (int e = 0; e < E; e += 4) {
-                    float4 t = *reinterpret_cast<const float4*>(xs + (size_t)ub * E + e);
-                    xv[e] = t.x;
-                    xv[e + 1] = t.y;
-                    xv[e + 2] = t.z;
-                    xv[e + 3] = t.w;
-                }
-#pragma unroll
-                for (int r = 0; r < NR; ++r) {
-                    float wf[E];
-                    T::expand(wv[b][r], wf);
-#pragma unroll
-                    for (int e = 0; e < E; ++e) acc[r] = fmaf(wf[e], xv[e], acc[r]);
+                for (int r = 0; r < R; ++r) {
+                    if (!tc.valid[r]) continue;
+                    const uint32_t row = tc.row[r];
+                    if constexpr (MODE == kGemvPlain) {
+                        const WT* bias = static_cast<const WT*>(a.bias[tc.seg[r]]);
+                        a.out[tc.seg[r]][row] = s[r] + (bias ? WeightTraits<WT>::at(bias, row) : 0.0f);
+                    } else if constexpr (MODE == kGemvResid) {
+                        a.out[0][row] = a.out[0][row] + s[r];
+                    } else if constexpr (MODE == kGemvGateUp) {
+                        // siluMulInto, src/llm.zig:1382-1387
+                        const float g = s[r], u = s[R + r];
+                        a.out[0][row] = (g / (1.0f + expf(-g))) * u;
+                    } else {
+                        a.out[0][row] = s[r];
+                        const unsigned long long key = argmax_key(s[r], row);
+                        best = key > best ? key : best;
+                    }
                 }
             }
         }
-        u += UB * kThreads;
-        if (u >= U) break;
-#pragma unroll
-        for (int b = 0; b < UB; ++b) {
-            const uint32_t ub = u + b * kThreads;
-#pragma unroll
-            for (int r = 0; r < NR; ++r)
-                wv[b][r] = ub < U ? load_unit(rowp[r] + (size_t)ub * E) : make_uint4(0, 0, 0, 0);
-        }
-    }
+    };
 
-    // Block reduction: DPP within each wave, LDS across the 4 waves.
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        float s = wave_sum(acc[r]);
-        if ((tid & 63) == 0) red[(tid >> 6) * NR + r] = s;
+    while (item < n_items) {
+        step(bufA, tA, bufB, tB, item);
+        ++item;
+        if (item >= n_items) break;
+        step(bufB, tB, bufA, tA, item);
+        ++item;
     }
-    __syncthreads();
     if constexpr (MODE == kGemvLogits) {
-        // Whole wave 0 takes part so the shuffle reduction has every lane.
-        if (tid < kWave) {
-            const uint32_t row = srow + tid;
-            const bool valid = tid < R && row < seg_rows;
-            unsigned long long key = 0ull;
-            if (valid) {
-                float s = (red[tid] + red[NR + tid]) + (red[2 * NR + tid] + red[3 * NR + tid]);
-                a.out[0][row] = s;
-                key = argmax_key(s, row);
-            }
-            key = wave_max_u64(key);
-            if (tid == 0) a.block_keys[blockIdx.x] = key;
-        }
-    } else if (tid < R) {
-        const int r = tid;
-        const uint32_t row = srow + r;
-        const bool valid = row < seg_rows;
-        float s = (red[r] + red[NR + r]) + (red[2 * NR + r] + red[3 * NR + r]);
-        if constexpr (MODE == kGemvPlain) {
-            if (valid) {
-                const WT* bias = static_cast<const WT*>(a.bias[seg]);
-                a.out[seg][row] = s + (bias ? T::at(bias, row) : 0.0f);
-            }
-        } else if constexpr (MODE == kGemvResid) {
-            if (valid) a.out[0][row] = a.out[0][row] + s;
-        } else {  // gate/up: siluMulInto, src/llm.zig:1382-1387
-            float u_ = (red[R + r] + red[NR + R + r]) + (red[2 * NR + R + r] + red[3 * NR + R + r]);
-            if (valid) a.out[0][row] = (s / (1.0f + expf(-s))) * u_;
-        }
+        if (lane == 0) a.block_keys[wid] = best;
     }
 }
 
 template <typename WT, int MODE>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
-    constexpr int R = ModeCfg<MODE>::R;
-    constexpr int NR = (MODE == kGemvGateUp) ? 2 * R : R;
     const uint32_t total = a.rows[0] + a.rows[1] + a.rows[2];
-    const uint32_t grid = (total + R - 1) / R;
-    const size_t lds = (size_t)a.K * sizeof(float) + kWaves * NR * sizeof(float);
+    const uint32_t grid = gemv_grid(MODE, total);
+    const size_t lds = (size_t)a.K * sizeof(float) + kWavesPerBlock * sizeof(float);
     hipLaunchKernelGGL((gemv_kernel<WT, MODE>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
@@ -197,18 +159,18 @@ hipError_t set_attr() {
 }  // namespace
 
 uint32_t gemv_rows_per_block(int mode) {
-    switch (mode) {
-        case kGemvPlain: return ModeCfg<kGemvPlain>::R;
-        case kGemvResid: return ModeCfg<kGemvResid>::R;
-        case kGemvGateUp: return ModeCfg<kGemvGateUp>::R;
-        default: return ModeCfg<kGemvLogits>::R;
-    }
+    // Rows per wave-tile; stacked q|k|v segments must split on tile boundaries.
+    return mode == kGemvGateUp ? ModeCfg<kGemvGateUp>::R : ModeCfg<kGemvPlain>::R;
 }
 
 uint32_t gemv_grid(int mode, uint32_t total_rows) {
-    uint32_t r = gemv_rows_per_block(mode);
-    return (total_rows + r - 1) / r;
+    const uint32_t r = gemv_rows_per_block(mode);
+    const uint32_t tiles = (total_rows + r - 1) / r;
+    uint32_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+    return blocks > kMaxBlocks ? kMaxBlocks : blocks;
 }
+
+uint32_t gemv_num_keys(uint32_t total_rows) { return gemv_grid(kGemvLogits, total_rows) * kWavesPerBlock; }
 
 hipError_t gemv_init_attributes() {
     hipError_t e = hipSuccess;

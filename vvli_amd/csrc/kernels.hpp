@@ -34,6 +34,8 @@ struct GemvArgs {
 // that stacked segments split on block boundaries).
 uint32_t gemv_rows_per_block(int mode);
 uint32_t gemv_grid(int mode, uint32_t total_rows);
+// Argmax keys written by a logits-mode launch over total_rows rows (one per wave).
+uint32_t gemv_num_keys(uint32_t total_rows);
 hipError_t launch_gemv(int weight_kind, int mode, const GemvArgs& a, hipStream_t s);
 hipError_t gemv_init_attributes();
 
@@ -57,6 +59,9 @@ struct AttnArgs {
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s);
 size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t nsplit);
+// Split count for a cache of max_seq positions (grid = nsplit x kv_heads; a
+// step at position pos uses ceil((pos+1)/chunk) of them, chunk >= 64).
+uint32_t attn_nsplit(uint32_t max_seq);
 
 // ---------------------------------------------------------------------------
 // Small kernels.
@@ -72,7 +77,8 @@ struct StepState {
     uint32_t counting;    // 1: append post-prompt argmaxes to out_tokens
     uint32_t argmax;      // argmax of the last logits
     uint32_t prompt_len;  // tokens of `prompt` still to be fed, counted from pos 0
-    uint32_t pad[2];
+    uint32_t stop;        // set by the persistent step: EOS emitted or cache full
+    uint32_t pad;
 };
 
 // copyEmbeddingToken (src/llm.zig:1373-1380): x = embed[token] as f32.
@@ -86,5 +92,67 @@ hipError_t launch_argmax_finish(const unsigned long long* keys, uint32_t nkeys, 
 // back to back without a pinned staging buffer).
 hipError_t launch_set_state(StepState* st, uint32_t token, uint32_t pos, uint32_t prompt_len, uint32_t counting,
                             hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Persistent decode step (decode_step.hip): bf16 weights only.
+// ---------------------------------------------------------------------------
+struct DecodeLayer {
+    const uint16_t *input_norm, *q, *q_bias, *k, *k_bias, *v, *v_bias, *o, *post_norm, *gate, *up, *down;
+};
+
+// One GEMV phase of the persistent step: up to three stacked row segments
+// (q | k | v; each of an even row count) or a gate and an up matrix. Built by
+// the host in device memory, so the kernel reads it with scalar loads instead
+// of keeping a local copy (a run-time segment index into a local struct puts
+// it in scratch memory).
+struct DecodeGemv {
+    const uint16_t *w0, *w1, *w2;
+    const uint16_t *b0, *b1, *b2;
+    float *o0, *o1, *o2;
+    uint32_t r0, r1, r2;
+    const uint16_t* w_up;
+    uint32_t K;
+};
+
+struct DecodeStepParams {
+    uint32_t vocab, hidden, inter, layers, heads, kv_heads, hd, kvdim, rope_layout, max_seq;
+    float eps, scale;
+    const uint16_t* embed;
+    const uint16_t* final_norm;
+    const uint16_t* lm_head;  // the embedding when tied
+    const DecodeLayer* layer;  // device array [layers]
+    const DecodeGemv* gemv;    // device array [layers * 4 + 1]: per layer qkv, o, gate_up, down; then logits
+    float* kcache;
+    float* vcache;
+    const float* rope_cs;
+    float* x;       // residual stream [hidden]
+    float* qkv;     // q | k | v
+    float* ff;      // [inter]
+    float* logits;  // [vocab]
+    float* part_ml;   // attention partials: (max, sum) [kv_heads][nsplit][group][2]
+    float* part_acc;  // attention partials: unnormalised out [kv_heads][nsplit][group][hd]
+    uint32_t* counters;  // [kv_heads] merge tickets, zero between phases
+    float* attn;      // merged attention output [heads * hd]
+    unsigned long long* keys;  // one argmax key per wave
+    StepState* state;
+    const uint32_t* prompt;
+    uint32_t* out_tokens;
+    uint32_t out_cap;
+    uint32_t* flags;    // [blocks * 32] barrier generations
+    uint32_t* release;  // barrier release word
+    uint32_t* error;    // non-zero: a barrier timed out (all blocks leave)
+    uint32_t nsplit, min_chunk;
+    uint32_t n_steps;
+    int64_t eos;  // < 0: none
+    // Optional phase timing (100 MHz s_memrealtime ticks): block b's arrival
+    // at barrier k in timing[b * timing_stride + k], block 0's release of
+    // barrier k in timing[gridDim * timing_stride + k]; index 0 is the start.
+    unsigned long long* timing;
+    uint32_t timing_stride;
+};
+
+size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t heads, uint32_t hd);
+hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu);
+hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s);
 
 }  // namespace vvli

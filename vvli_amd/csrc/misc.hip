@@ -77,6 +77,7 @@ __global__ void set_state_kernel(StepState* st, uint32_t token, uint32_t pos, ui
         st->counting = counting;
         st->argmax = 0;
         st->prompt_len = prompt_len;
+        st->stop = 0;
     }
 }
 }  // namespace

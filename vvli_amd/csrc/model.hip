@@ -54,6 +54,19 @@ struct vvli_gpu_model {
     hipGraphExec_t graph = nullptr;
     std::vector<float> inv_freq;
     std::vector<hipEvent_t>* prof = nullptr;  // set while profiling: one event per launch boundary
+    // Persistent decode step (bf16 only).
+    bool mk_ok = false;
+    uint32_t path = 0;  // 0 auto, 1 per-kernel graph, 2 persistent
+    uint32_t mk_blocks = 0;
+    size_t mk_lds = 0;
+    uint32_t mk_nsplit = 1;
+    DecodeLayer* mk_layers = nullptr;
+    DecodeGemv* mk_gemv = nullptr;  // [layers * 4 + 1] phase descriptors
+    float* mk_part = nullptr;       // persistent attention partials: (m, l) block then acc block
+    uint32_t* mk_sync = nullptr;  // flags [blocks*32] | release [32] | error [32]
+    size_t mk_sync_words = 0;
+    uint32_t* h_err = nullptr;    // pinned
+    bool mk_pending = false;      // a persistent launch ran since the last error check
 };
 
 namespace {
@@ -264,12 +277,83 @@ int ensure_graph(vvli_gpu_model* m) {
     return VVLI_OK;
 }
 
+// Auto picks the per-kernel graph: on the Llama-3.2-1B decode benchmark it
+// currently measures faster than the persistent step (926 vs 872 tok/s).
+bool use_persistent(const vvli_gpu_model* m) { return m->mk_ok && m->path == 2; }
+
+int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned long long* timing = nullptr,
+                   uint32_t timing_stride = 0) {
+    const vvli_gpu_config& c = m->cfg;
+    DecodeStepParams p{};
+    p.vocab = c.vocab;
+    p.hidden = c.hidden;
+    p.inter = c.inter;
+    p.layers = c.layers;
+    p.heads = c.heads;
+    p.kv_heads = c.kv_heads;
+    p.hd = head_dim(c);
+    p.kvdim = kv_dim(c);
+    p.rope_layout = c.rope_layout;
+    p.max_seq = m->max_seq;
+    p.eps = c.rms_eps;
+    p.scale = 1.0f / sqrtf(static_cast<float>(p.hd));
+    p.embed = static_cast<const uint16_t*>(wslice(m, m->layout.embed));
+    p.final_norm = static_cast<const uint16_t*>(wslice(m, m->layout.final_norm));
+    p.lm_head = static_cast<const uint16_t*>(wslice(m, c.tie ? m->layout.embed : m->layout.lm_head));
+    p.layer = m->mk_layers;
+    p.gemv = m->mk_gemv;
+    p.kcache = m->kcache;
+    p.vcache = m->vcache;
+    p.rope_cs = m->rope_cs;
+    p.x = m->x;
+    p.qkv = m->qkv;
+    p.ff = m->ff;
+    p.logits = m->logits;
+    const uint32_t G = c.heads / c.kv_heads;
+    p.part_ml = m->mk_part;
+    p.part_acc = m->mk_part + static_cast<size_t>(c.kv_heads) * m->mk_nsplit * G * 2;
+    p.counters = m->counters;
+    p.attn = m->attn;
+    p.keys = m->keys;
+    p.state = m->state;
+    p.prompt = m->prompt;
+    p.out_tokens = m->out_tokens;
+    p.out_cap = m->out_cap;
+    p.flags = m->mk_sync;
+    p.release = m->mk_sync + static_cast<size_t>(m->mk_blocks) * 32;
+    p.error = p.release + 32;
+    p.nsplit = m->mk_nsplit;
+    p.min_chunk = 64;
+    p.n_steps = n_steps;
+    p.eos = eos;
+    p.timing = timing;
+    p.timing_stride = timing_stride;
+    HIP_TRY(hipMemsetAsync(m->mk_sync, 0, m->mk_sync_words * sizeof(uint32_t), m->stream));
+    HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
+    m->mk_pending = true;
+    return VVLI_OK;
+}
+
+int check_persistent_error(vvli_gpu_model* m) {
+    if (!m->mk_pending) return VVLI_OK;
+    m->mk_pending = false;
+    HIP_TRY(hipMemcpyAsync(m->h_err, m->mk_sync + static_cast<size_t>(m->mk_blocks) * 32 + 32, sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (*m->h_err != 0)
+        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (barrier timeout)",
+                         *m->h_err);
+    return VVLI_OK;
+}
+
 int read_outputs(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
     if (logits_out)
         HIP_TRY(hipMemcpyAsync(logits_out, m->logits, static_cast<size_t>(m->cfg.vocab) * sizeof(float),
                                hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
+    int rc = check_persistent_error(m);
+    if (rc) return rc;
     if (argmax_out) *argmax_out = m->h_state->argmax;
     return VVLI_OK;
 }
@@ -279,10 +363,12 @@ void free_model(vvli_gpu_model* m) {
     (void)hipSetDevice(m->device);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
-                    m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens};
+                    m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
+                    m->mk_layers, m->mk_gemv, m->mk_sync, m->mk_part};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
+    if (m->h_err) (void)hipHostFree(m->h_err);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -316,9 +402,25 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     (void)hipGetDevice(&m->device);
     const uint32_t H = cfg->hidden, kv = kv_dim(*cfg), hd = head_dim(*cfg);
     const size_t kvlen = static_cast<size_t>(cfg->layers) * max_seq_len * kv;
-    m->nsplit = std::max<uint32_t>(1, std::min<uint32_t>((256 + cfg->kv_heads - 1) / cfg->kv_heads,
-                                                        (max_seq_len + 15) / 16));
-    m->nkeys = gemv_grid(kGemvLogits, cfg->vocab);
+    m->nsplit = attn_nsplit(max_seq_len);
+    m->nkeys = gemv_num_keys(cfg->vocab);
+    // Persistent step: bf16 only, one 512-thread block per CU if it fits.
+    if (cfg->weight_kind == VVLI_WEIGHT_BF16) {
+        int cus = 0, bpc = 0;
+        m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->heads, hd);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
+            m->mk_lds <= 160 * 1024 && decode_step_max_blocks(hd, m->mk_lds, &bpc) == hipSuccess && bpc >= 1 &&
+            cus > 0) {
+            m->mk_ok = true;
+            m->mk_blocks = static_cast<uint32_t>(cus);
+            m->mk_nsplit = std::max<uint32_t>(1, std::min<uint32_t>(16, (max_seq_len + 63) / 64));  // <= kMaxSplitMk
+        }
+        (void)hipGetLastError();
+    }
+    const uint32_t G = cfg->heads / cfg->kv_heads;
+    const size_t part_floats = attn_part_floats(cfg->heads, cfg->kv_heads, hd, m->nsplit);
+    const size_t mk_part_floats = static_cast<size_t>(cfg->kv_heads) * m->mk_nsplit * G * (2 + hd);
+    const uint32_t nkeys_alloc = std::max<uint32_t>(m->nkeys, m->mk_blocks * 8);
     m->out_cap = max_seq_len + 1;
 #define TRY_ALLOC(expr)         \
     if ((rc = (expr)) != 0) {   \
@@ -338,9 +440,20 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(dmalloc(&m->ff, cfg->inter));
     TRY_ALLOC(dmalloc(&m->logits, cfg->vocab));
     TRY_ALLOC(dmalloc(&m->hidden, static_cast<size_t>(cfg->layers) * H));
-    TRY_ALLOC(dmalloc(&m->part, attn_part_floats(cfg->heads, cfg->kv_heads, hd, m->nsplit)));
+    TRY_ALLOC(dmalloc(&m->part, part_floats));
     TRY_ALLOC(dmalloc(&m->counters, cfg->kv_heads));
-    TRY_ALLOC(dmalloc(&m->keys, m->nkeys));
+    TRY_ALLOC(dmalloc(&m->keys, nkeys_alloc));
+    if (m->mk_ok) {
+        m->mk_sync_words = static_cast<size_t>(m->mk_blocks) * 32 + 64;
+        TRY_ALLOC(dmalloc(&m->mk_sync, m->mk_sync_words));
+        TRY_ALLOC(dmalloc(&m->mk_layers, cfg->layers));
+        TRY_ALLOC(dmalloc(&m->mk_gemv, static_cast<size_t>(cfg->layers) * 4 + 1));
+        TRY_ALLOC(dmalloc(&m->mk_part, mk_part_floats));
+        TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_err), sizeof(uint32_t), hipHostMallocDefault) ==
+                          hipSuccess
+                      ? 0
+                      : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
+    }
     TRY_ALLOC(dmalloc(&m->state, 1));
     TRY_ALLOC(dmalloc(&m->prompt, max_seq_len));
     TRY_ALLOC(dmalloc(&m->out_tokens, m->out_cap));
@@ -357,10 +470,97 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
     TRY_ALLOC(fail_hip(hipMemset(m->state, 0, sizeof(StepState)), "state"));
+    if (m->mk_sync)
+        TRY_ALLOC(fail_hip(hipMemset(m->mk_sync, 0, m->mk_sync_words * sizeof(uint32_t)), "sync clear"));
     TRY_ALLOC(upload_rope(m));
+    if (m->mk_ok) {
+        std::vector<DecodeLayer> dl(cfg->layers);
+        for (uint32_t l = 0; l < cfg->layers; ++l) {
+            const LayerSlices& L = m->layout.layers[l];
+            auto w = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+            dl[l] = DecodeLayer{w(L.input_norm), w(L.q), w(L.q_bias), w(L.k), w(L.k_bias), w(L.v), w(L.v_bias),
+                                w(L.o),          w(L.post_norm), w(L.gate), w(L.up), w(L.down)};
+        }
+        TRY_ALLOC(fail_hip(hipMemcpy(m->mk_layers, dl.data(), dl.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice),
+                           "layer table"));
+        // GEMV phase descriptors: per layer qkv, o (+residual), gate/up, down (+residual); then logits.
+        std::vector<DecodeGemv> dg(static_cast<size_t>(cfg->layers) * 4 + 1, DecodeGemv{});
+        float* q = m->qkv;
+        float* kn = m->qkv + H;
+        float* vn = m->qkv + H + kv;
+        for (uint32_t l = 0; l < cfg->layers; ++l) {
+            const DecodeLayer& L = dl[l];
+            DecodeGemv& gq = dg[l * 4 + 0];
+            gq.w0 = L.q, gq.w1 = L.k, gq.w2 = L.v;
+            gq.b0 = L.q_bias, gq.b1 = L.k_bias, gq.b2 = L.v_bias;
+            gq.o0 = q, gq.o1 = kn, gq.o2 = vn;
+            gq.r0 = H, gq.r1 = kv, gq.r2 = kv;
+            gq.K = H;
+            DecodeGemv& go = dg[l * 4 + 1];
+            go.w0 = L.o, go.o0 = m->x, go.r0 = H, go.K = H;
+            DecodeGemv& gg = dg[l * 4 + 2];
+            gg.w0 = L.gate, gg.w_up = L.up, gg.o0 = m->ff, gg.r0 = cfg->inter, gg.K = H;
+            DecodeGemv& gd = dg[l * 4 + 3];
+            gd.w0 = L.down, gd.o0 = m->x, gd.r0 = H, gd.K = cfg->inter;
+        }
+        DecodeGemv& gl = dg[static_cast<size_t>(cfg->layers) * 4];
+        gl.w0 = static_cast<const uint16_t*>(wslice(m, cfg->tie ? m->layout.embed : m->layout.lm_head));
+        gl.o0 = m->logits, gl.r0 = cfg->vocab, gl.K = H;
+        TRY_ALLOC(fail_hip(hipMemcpy(m->mk_gemv, dg.data(), dg.size() * sizeof(DecodeGemv), hipMemcpyHostToDevice),
+                           "gemv table"));
+    }
     TRY_ALLOC(fail_hip(hipDeviceSynchronize(), "create sync"));
 #undef TRY_ALLOC
     *out = m;
+    return VVLI_OK;
+}
+
+int64_t now_ns();
+
+// generateGreedyMeasured on the persistent step: one launch for the prompt
+// (token-at-a-time, as the reference), one for the decode steps; the device
+// feeds each argmax back as the next token and stops on EOS.
+int generate_persistent(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
+                        uint32_t* out_tokens, uint32_t* n_out, vvli_gpu_stats* stats) {
+    const uint32_t avail = m->max_seq - n_prompt;  // positions left for decode forwards
+    if (eos < 0 && static_cast<uint64_t>(n_prompt) + max_new > m->max_seq)
+        return set_error(VVLI_CONTEXT_FULL, "prompt %u + %u new tokens > max_seq_len %u", n_prompt, max_new, m->max_seq);
+    const int64_t t0 = now_ns();
+    HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
+    int rc = run_persistent(m, n_prompt, eos);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if ((rc = check_persistent_error(m))) return rc;
+    const int64_t t1 = now_ns();
+    uint32_t produced = 0;
+    if (max_new > 0) {
+        const bool first_is_eos = eos >= 0 && static_cast<int64_t>(m->h_state->argmax) == eos;
+        const uint32_t steps = std::min(max_new, avail);
+        if (!first_is_eos && steps > 0) {
+            if ((rc = run_persistent(m, steps, eos))) return rc;
+        }
+        HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+        if ((rc = check_persistent_error(m))) return rc;
+        produced = std::min(m->h_state->n_out, max_new);
+        HIP_TRY(hipMemcpyAsync(out_tokens, m->out_tokens, produced * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                               m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+        const bool hit_eos = eos >= 0 && produced > 0 && static_cast<int64_t>(out_tokens[produced - 1]) == eos;
+        if (produced < max_new && !hit_eos)
+            return set_error(VVLI_CONTEXT_FULL, "decode reached max_seq_len %u after %u tokens", m->max_seq, produced);
+    }
+    const int64_t t2 = now_ns();
+    *n_out = produced;
+    if (stats) {
+        stats->prompt_tokens = n_prompt;
+        stats->generated_tokens = produced;
+        stats->prefill_ns = t1 - t0;
+        stats->decode_ns = t2 - t1;
+        stats->total_ns = t2 - t0;
+    }
     return VVLI_OK;
 }
 
@@ -415,11 +615,26 @@ int vvli_gpu_forward_token(vvli_gpu_model* m, uint32_t token, uint32_t pos, floa
     if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    if (use_persistent(m)) {
+        HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
+        int rc = run_persistent(m, 1, -1);
+        if (rc) return rc;
+        return read_outputs(m, logits_out, argmax_out);
+    }
     int rc = ensure_graph(m);
     if (rc) return rc;
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
     HIP_TRY(hipGraphLaunch(m->graph, m->stream));
     return read_outputs(m, logits_out, argmax_out);
+}
+
+int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (path > 2) return set_error(VVLI_INVALID_CONFIG, "decode path %u not in 0..2", path);
+    if (path == 2 && !m->mk_ok)
+        return set_error(VVLI_INVALID_CONFIG, "persistent decode step unavailable (bf16 weights, fits one CU)");
+    m->path = path;
+    return VVLI_OK;
 }
 
 int vvli_gpu_forward_embedding(vvli_gpu_model* m, const float* embedding, uint32_t pos, float* logits_out,
@@ -477,6 +692,33 @@ int vvli_gpu_profile_step(vvli_gpu_model* m, uint32_t token, uint32_t pos, float
     return VVLI_OK;
 }
 
+int vvli_gpu_profile_persistent(vvli_gpu_model* m, uint32_t token, uint32_t pos, uint64_t* ticks_out,
+                                uint32_t stride, uint32_t* n_blocks) {
+    if (!m || !ticks_out || !n_blocks) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_profile_persistent");
+    if (!m->mk_ok) return set_error(VVLI_INVALID_CONFIG, "persistent decode step unavailable for this model");
+    if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
+    if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    const size_t n = static_cast<size_t>(m->mk_blocks + 1) * stride;
+    unsigned long long* d = nullptr;
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&d), n * sizeof(unsigned long long)));
+    hipError_t e = hipMemsetAsync(d, 0, n * sizeof(unsigned long long), m->stream);
+    int rc = e == hipSuccess ? VVLI_OK : set_error(VVLI_HIP_ERROR, "memset: %s", hipGetErrorString(e));
+    if (!rc) rc = launch_set_state(m->state, token, pos, 0, 0, m->stream) == hipSuccess ? VVLI_OK
+                                                                                       : set_error(VVLI_HIP_ERROR, "set_state");
+    if (!rc) rc = run_persistent(m, 1, -1, d, stride);
+    if (!rc) {
+        e = hipMemcpyAsync(ticks_out, d, n * sizeof(unsigned long long), hipMemcpyDeviceToHost, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) rc = set_error(VVLI_HIP_ERROR, "profile readback: %s", hipGetErrorString(e));
+    }
+    if (!rc) rc = check_persistent_error(m);
+    (void)hipFree(d);
+    if (rc) return rc;
+    *n_blocks = m->mk_blocks;
+    return VVLI_OK;
+}
+
 int vvli_gpu_kv_read(vvli_gpu_model* m, uint32_t layer, uint32_t pos, float* k_out, float* v_out) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     if (layer >= m->cfg.layers || pos >= m->max_seq)
@@ -501,11 +743,16 @@ int vvli_gpu_prefill(vvli_gpu_model* m, const uint32_t* tokens, uint32_t n, uint
     if (static_cast<uint64_t>(start_pos) + n > m->max_seq)
         return set_error(VVLI_CONTEXT_FULL, "prefill end %u > max_seq_len %u", start_pos + n, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
-    int rc = ensure_graph(m);
-    if (rc) return rc;
     // Prompt tokens live at their absolute positions in `prompt`.
     HIP_TRY(hipMemcpyAsync(m->prompt + start_pos, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(launch_set_state(m->state, tokens[0], start_pos, start_pos + n, 0, m->stream));
+    if (use_persistent(m)) {
+        int rc = run_persistent(m, n, -1);
+        if (rc) return rc;
+        return read_outputs(m, last_logits, argmax_out);
+    }
+    int rc = ensure_graph(m);
+    if (rc) return rc;
     for (uint32_t i = 0; i < n; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
     return read_outputs(m, last_logits, argmax_out);
 }
@@ -521,6 +768,7 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
         return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
     (void)flags;
     HIP_TRY(hipSetDevice(m->device));
+    if (use_persistent(m)) return generate_persistent(m, prompt, n_prompt, max_new, eos, out_tokens, n_out, stats);
     int rc = ensure_graph(m);
     if (rc) return rc;
     const int64_t t0 = now_ns();

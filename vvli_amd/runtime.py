@@ -164,6 +164,10 @@ class Runner:
             t = np.ascontiguousarray(inv_freq, dtype=np.float32)
             _lib.check(_lib.lib().vvli_gpu_set_rope_table(self._h, _ptr(t), t.size))
 
+    def set_decode_path(self, path: str) -> None:
+        """'auto', 'graph' (per-kernel HIP graph) or 'persistent' (one launch per step)."""
+        _lib.check(_lib.lib().vvli_gpu_set_decode_path(self._h, {"auto": 0, "graph": 1, "persistent": 2}[path]))
+
     def prefill(self, tokens, start_pos: int = 0) -> tuple[np.ndarray, int]:
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
         am = c_uint32()
