@@ -76,6 +76,19 @@ def profile_kernels(runner, cfg, token: int, pos: int, reps: int = 3) -> dict:
     return out
 
 
+def measured_traffic(symbol: str):
+    """HBM bytes per launch of `symbol` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 256 MiB copy)."""
+    path = ROOT / "profiles" / "pmc_traffic_llama1b_decode.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.strip().split("\t")
+        if len(parts) == 3 and parts[0] == "traffic" and parts[1] == symbol:
+            return int(parts[2])
+    return None
+
+
 def cpu_baseline(cfg, blob, budget_s: float, max_tokens: int) -> dict:
     """Decode tok/s of the oracle (C restatement of the reference CPU path:
     per-call thread fan-out over rows, single-threaded attention) on this host."""
@@ -109,6 +122,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
@@ -155,23 +170,43 @@ def main() -> int:
     step_bytes = sum(token_bytes(cfg, p) for p in positions)
     step_gbs = step_bytes / decode_s / 1e9
 
-    # Per-kernel durations from HIP events on the model's stream, mid-decode.
+    # Per-kernel durations, mid-decode: start/stop events at each kernel's own
+    # dispatch boundaries on the model's stream (vvli_gpu_profile_step), the
+    # same interval a kernel trace reports. Grouped by kernel symbol.
     mid = args.prompt + args.steps // 2
     prof = profile_kernels(runner, cfg, int(tokens[args.steps // 2]), mid)
     kb = kernel_bytes(cfg, mid)
+    L = cfg.num_hidden_layers
+    groups = {  # kernel symbol -> (step kernels it runs, launches per step)
+        "gemv_kernel<bf16, 0> (qkv)": (["qkv"], L),
+        "attn_decode_kernel<64> (attention)": (["attention"], L),
+        "gemv_kernel<bf16, 1> (o_proj + down)": (["o_proj", "down"], 2 * L),
+        "gemv_kernel<bf16, 2> (gate_up)": (["gate_up"], L),
+        "gemv_kernel<bf16, 3> (logits)": (["logits"], 1),
+    }
     kernels = {}
-    for k in list(KERNELS) + ["logits"]:
-        avg_ms = float(np.mean(prof[k]))
-        total_ms = float(np.sum(prof[k]))
-        kernels[k] = {"avg_us": avg_ms * 1e3, "total_us": total_ms * 1e3, "bytes": kb[k],
-                      "gbs": kb[k] / (avg_ms * 1e-3) / 1e9}
+    for sym, (parts, launches) in groups.items():
+        total_ms = float(sum(np.sum(prof[k]) for k in parts))
+        nbytes = sum(kb[k] * len(prof[k]) for k in parts)
+        kernels[sym] = {"launches": launches, "total_us": total_ms * 1e3, "avg_us": total_ms * 1e3 / launches,
+                        "bytes_per_launch": nbytes // launches, "gbs": nbytes / (total_ms * 1e-3) / 1e9}
     dom = max(kernels, key=lambda k: kernels[k]["total_us"])
     d = kernels[dom]
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": d["bytes"], "avg_launch_us": round(d["avg_us"], 2)}
+    traffic = measured_traffic(dom.split(" (")[0])
+    roofline = {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
+                "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 2),
+                "launches_per_step": d["launches"]}
     print("[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f}us {v['gbs']:.0f}GB/s" for k, v in kernels.items()),
           file=sys.stderr, flush=True)
+
+    if args.copy_calibration:
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1.0)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -208,7 +243,7 @@ def main() -> int:
         "step_roofline": {"bytes_per_token_avg": step_bytes // args.steps, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
-        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kernels.items()},
+        "kernels": {k: {"avg_us": round(v["avg_us"], 2), "gbs": round(v["gbs"], 1)} for k, v in kernels.items()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

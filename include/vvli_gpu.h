@@ -150,10 +150,11 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint
 /* ---------------------------------------------------------------------- */
 /* Measurement (no reference counterpart: the reference has no profiler)   */
 /* ---------------------------------------------------------------------- */
-/* Runs one token step (like forward_token) with a HIP event recorded on the
- * model's stream between consecutive kernels and returns each kernel's time
- * in milliseconds, in launch order: embed, then per layer {qkv, attention,
- * o_proj, gate_up, down}, then logits, argmax. *n_out = kernels timed. */
+/* Runs one token step of the per-kernel path (like forward_token) with every
+ * kernel launched between its own start/stop HIP events on the model's
+ * stream (hipExtLaunchKernel: the kernel's dispatch interval) and returns each
+ * kernel's time in milliseconds, in launch order: embed, then per layer {qkv,
+ * attention, o_proj, gate_up, down}, then logits, argmax. *n_out = kernels timed. */
 int vvli_gpu_profile_step(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* ms_out, uint32_t cap,
                           uint32_t* n_out);
 /* Which implementation runs forward_token / prefill / generate:

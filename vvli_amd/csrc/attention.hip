@@ -253,11 +253,8 @@ size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t
 
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s) {
     dim3 grid(a.nsplit, a.kv_heads);
-    if (a.hd <= 64)
-        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kThreads), 0, s, a);
-    return hipGetLastError();
+    if (a.hd <= 64) return vlaunch(attn_decode_kernel<64>, grid, dim3(kThreads), 0, s, a);
+    return vlaunch(attn_decode_kernel<128>, grid, dim3(kThreads), 0, s, a);
 }
 
 }  // namespace vvli

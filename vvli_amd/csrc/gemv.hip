@@ -146,8 +146,7 @@ hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
     const uint32_t total = a.rows[0] + a.rows[1] + a.rows[2];
     const uint32_t grid = gemv_grid(MODE, total);
     const size_t lds = (size_t)a.K * sizeof(float) + kWavesPerBlock * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<WT, MODE>), dim3(grid), dim3(kThreads), lds, s, a);
-    return hipGetLastError();
+    return vlaunch(gemv_kernel<WT, MODE>, dim3(grid), dim3(kThreads), lds, s, a);
 }
 
 template <typename WT, int MODE>

@@ -1,10 +1,34 @@
 // kernels.hpp -- host-side launch interface of the HIP kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+#include <vector>
+
 namespace vvli {
+
+// While non-null (vvli_gpu_profile_step), every kernel launch records a
+// start/stop event pair at its own dispatch boundaries (hipExtLaunchKernel),
+// which times the kernel alone, as a kernel trace does.
+extern thread_local std::vector<std::pair<hipEvent_t, hipEvent_t>>* g_launch_events;
+
+template <typename... Args, typename F>
+inline hipError_t vlaunch(F kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s, Args... args) {
+    if (g_launch_events) {
+        hipEvent_t a = nullptr, b = nullptr;
+        hipError_t e = hipEventCreate(&a);
+        if (e == hipSuccess) e = hipEventCreate(&b);
+        if (e != hipSuccess) return e;
+        g_launch_events->push_back({a, b});
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<std::uint32_t>(shmem), s, a, b, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+    }
+    return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // GEMV (batch-1 linearInto, src/llm.zig:1228-1275) with fused prologue /

@@ -4,6 +4,8 @@
 
 namespace vvli {
 
+thread_local std::vector<std::pair<hipEvent_t, hipEvent_t>>* g_launch_events = nullptr;
+
 namespace {
 
 template <typename WT>
@@ -54,18 +56,15 @@ hipError_t launch_embed(int weight_kind, const void* embed, const StepState* st,
                         hipStream_t s) {
     const dim3 grid((hidden + 255) / 256);
     if (weight_kind == 1)
-        hipLaunchKernelGGL(embed_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(embed), st, x,
-                           hidden);
-    else
-        hipLaunchKernelGGL(embed_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(embed), st, x, hidden);
-    return hipGetLastError();
+        return vlaunch(embed_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(embed), st, x,
+                       hidden);
+    return vlaunch(embed_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(embed), st, x, hidden);
 }
 
 hipError_t launch_argmax_finish(const unsigned long long* keys, uint32_t nkeys, const float* logits, StepState* st,
                                 const uint32_t* prompt, uint32_t* out_tokens, uint32_t out_cap, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kFinishThreads), 0, s, keys, nkeys, logits, st, prompt,
-                       out_tokens, out_cap);
-    return hipGetLastError();
+    return vlaunch(argmax_finish_kernel, dim3(1), dim3(kFinishThreads), 0, s, keys, nkeys, logits, st, prompt,
+                   out_tokens, out_cap);
 }
 
 namespace {
@@ -84,8 +83,7 @@ __global__ void set_state_kernel(StepState* st, uint32_t token, uint32_t pos, ui
 
 hipError_t launch_set_state(StepState* st, uint32_t token, uint32_t pos, uint32_t prompt_len, uint32_t counting,
                             hipStream_t s) {
-    hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(64), 0, s, st, token, pos, prompt_len, counting);
-    return hipGetLastError();
+    return vlaunch(set_state_kernel, dim3(1), dim3(64), 0, s, st, token, pos, prompt_len, counting);
 }
 
 }  // namespace vvli

@@ -53,7 +53,6 @@ struct vvli_gpu_model {
     uint32_t nsplit = 1;
     hipGraphExec_t graph = nullptr;
     std::vector<float> inv_freq;
-    std::vector<hipEvent_t>* prof = nullptr;  // set while profiling: one event per launch boundary
     // Persistent decode step (bf16 only).
     bool mk_ok = false;
     uint32_t path = 0;  // 0 auto, 1 per-kernel graph, 2 persistent
@@ -79,22 +78,7 @@ namespace {
                              #expr, hipGetErrorString(e_));                                             \
     } while (0)
 
-// Records a launch boundary when the step is being profiled.
-int mark(vvli_gpu_model* m, hipStream_t s) {
-    if (!m->prof) return VVLI_OK;
-    hipEvent_t e;
-    HIP_TRY(hipEventCreate(&e));
-    m->prof->push_back(e);
-    HIP_TRY(hipEventRecord(e, s));
-    return VVLI_OK;
-}
-
-#define LAUNCH(expr)                  \
-    do {                              \
-        HIP_TRY(expr);                \
-        int mrc_ = mark(m, s);        \
-        if (mrc_) return mrc_;        \
-    } while (0)
+#define LAUNCH(expr) HIP_TRY(expr)
 
 const void* wslice(const vvli_gpu_model* m, size_t off) {
     return off == kNone ? nullptr : static_cast<const void*>(m->blob + off * m->ebytes);
@@ -253,8 +237,6 @@ int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
 }
 
 int enqueue_step(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
-    int rc = mark(m, s);
-    if (rc) return rc;
     LAUNCH(launch_embed(static_cast<int>(m->cfg.weight_kind), wslice(m, m->layout.embed), m->state, m->x,
                         m->cfg.hidden, s));
     return enqueue_body(m, s, hidden_dbg);
@@ -671,21 +653,24 @@ int vvli_gpu_profile_step(vvli_gpu_model* m, uint32_t token, uint32_t pos, float
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
-    std::vector<hipEvent_t> evs;
-    m->prof = &evs;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
+    g_launch_events = &evs;
     int rc = enqueue_step(m, m->stream, nullptr);
-    m->prof = nullptr;
+    g_launch_events = nullptr;
     hipError_t e = hipStreamSynchronize(m->stream);
     uint32_t n = 0;
     if (rc == VVLI_OK && e == hipSuccess) {
-        for (size_t i = 1; i < evs.size() && n < cap; ++i, ++n) {
+        for (size_t i = 0; i < evs.size() && n < cap; ++i, ++n) {
             float ms = 0.f;
-            e = hipEventElapsedTime(&ms, evs[i - 1], evs[i]);
+            e = hipEventElapsedTime(&ms, evs[i].first, evs[i].second);
             if (e != hipSuccess) break;
             ms_out[n] = ms;
         }
     }
-    for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
+    for (auto& ev : evs) {
+        (void)hipEventDestroy(ev.first);
+        (void)hipEventDestroy(ev.second);
+    }
     if (rc) return rc;
     HIP_TRY(e);
     *n_out = n;
