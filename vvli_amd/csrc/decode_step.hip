@@ -38,19 +38,23 @@ constexpr int kMaxSplitMk = 16;  // attention splits per kv head (merged by ever
 constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of polling: phases take <= ~0.2 ms
 constexpr uint32_t kFlagStride = 32;  // words between per-block flags (128 B)
 
-__device__ __forceinline__ float ld_a(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_a(const float* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t ld_a(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned long long ld_a(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_a(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_a(float* p, float v) {
+    __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void st_a(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_a(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
@@ -79,8 +83,9 @@ __device__ __forceinline__ bool mk_barrier(const DecodeStepParams& p, uint32_t* 
     if (tid == 0) *s_gen = gen;
     if (tid == 0) {
         *s_ok = 1;
-        if (p.timing && gen < p.timing_stride)
-            p.timing[blockIdx.x * p.timing_stride + gen] = __builtin_amdgcn_s_memrealtime();
+        if (p.timing && (gen + 1) * p.timing_slots <= p.timing_stride)
+            p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots + p.timing_slots - 1] =
+                __builtin_amdgcn_s_memrealtime();
         st_a(p.flags + blockIdx.x * kFlagStride, gen);
     }
     if (blockIdx.x == 0) {
@@ -97,8 +102,9 @@ __device__ __forceinline__ bool mk_barrier(const DecodeStepParams& p, uint32_t* 
         }
         __syncthreads();
         if (tid == 0) {
-            if (p.timing && gen < p.timing_stride)
-                p.timing[(size_t)gridDim.x * p.timing_stride + gen] = __builtin_amdgcn_s_memrealtime();
+            if (p.timing && (gen + 1) * p.timing_slots <= p.timing_stride)
+                p.timing[(size_t)gridDim.x * p.timing_stride + gen * p.timing_slots + p.timing_slots - 1] =
+                    __builtin_amdgcn_s_memrealtime();
             st_a(p.release, *s_ok ? gen : 0xffffffffu);
         }
     } else if (tid == 0) {
@@ -113,7 +119,15 @@ __device__ __forceinline__ bool mk_barrier(const DecodeStepParams& p, uint32_t* 
         if (ld_a(p.error) != 0) *s_ok = 0;
     }
     __syncthreads();
+    if (tid == 0 && p.timing && p.timing_slots > 1 && (gen + 1) * p.timing_slots <= p.timing_stride)
+        p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots] = __builtin_amdgcn_s_memrealtime();
     return *s_ok != 0;
+}
+
+// Detail timing mark of the current phase (16-slot timing only).
+__device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t gen, int slot) {
+    if (p.timing && p.timing_slots > 1 && (gen + 1) * p.timing_slots <= p.timing_stride)
+        p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
 }
 
 // ---------------------------------------------------------------------------
@@ -131,31 +145,32 @@ __device__ __forceinline__ const uint16_t* seg_bias(const MkGemv& g, int seg) {
 __device__ __forceinline__ float* seg_out(const MkGemv& g, int seg) { return seg == 0 ? g.o0 : (seg == 1 ? g.o1 : g.o2); }
 
 struct MkTile {
-    const uint16_t* p[2];
-    uint32_t row[2];
-    int seg[2];
-    bool valid[2];
-    float resid[2];  // residual rows (residual mode, lane 0), loaded with the tile's first weights
+    const uint16_t* p[2];  // weight rows streamed by this tile
+    uint32_t row[2];       // output rows (row[1] unused in the SwiGLU mode)
+    int seg;               // segment of both rows (q | k | v in the plain mode)
+    bool valid[2];         // output row exists
 };
 
-template <int MODE>
-__device__ __forceinline__ uint32_t mk_tiles(const MkGemv& g) {
+__device__ __forceinline__ uint32_t mk_tiles(const MkGemv& g, int mode) {
     const uint32_t total = g.r0 + g.r1 + g.r2;
-    return MODE == kGemvGateUp ? total : (total + 1) / 2;
+    return mode == kGemvGateUp ? total : (total + 1) / 2;
 }
 
-template <int MODE>
-__device__ __forceinline__ void mk_make_tile(const MkGemv& g, uint32_t tile, MkTile& t, int lane) {
+// Tile `tile`: gate row t and up row t (SwiGLU), else rows 2t, 2t+1 of the
+// stacked segments (segments hold an even number of rows, so a tile never
+// straddles two; an odd last row re-reads its own row as the second).
+__device__ __forceinline__ void mk_make_tile(const MkGemv& g, int mode, uint32_t tile, MkTile& t) {
     const uint32_t K = g.K;
-    if constexpr (MODE == kGemvGateUp) {
-        t.valid[0] = t.valid[1] = tile < g.r0;
-        const uint32_t r = t.valid[0] ? tile : 0;
+    if (mode == kGemvGateUp) {
+        const bool v = tile < g.r0;
+        const uint32_t r = v ? tile : 0;
         t.p[0] = g.w0 + (size_t)r * K;
         t.p[1] = g.w_up + (size_t)r * K;
         t.row[0] = t.row[1] = r;
-        t.seg[0] = t.seg[1] = 0;
+        t.seg = 0;
+        t.valid[0] = v;
+        t.valid[1] = false;
     } else {
-        // Segments hold an even number of rows, so a tile never straddles two.
         const uint32_t total = g.r0 + g.r1 + g.r2;
         uint32_t first = tile * 2;
         int seg = 0;
@@ -168,111 +183,156 @@ __device__ __forceinline__ void mk_make_tile(const MkGemv& g, uint32_t tile, MkT
             }
         }
         const uint16_t* wb = seg_w(g, seg);
+        t.seg = seg;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             t.valid[r] = tile * 2 + r < total;
             const uint32_t gr = t.valid[r] ? first + r : first;
             t.p[r] = wb + (size_t)gr * K;
             t.row[r] = gr;
-            t.seg[r] = seg;
-            if constexpr (MODE == kGemvResid) t.resid[r] = (lane == 0 && t.valid[r]) ? ld_a(g.o0 + gr) : 0.f;
         }
     }
 }
 
 struct MkWave {
-    uint32_t wid, nw;
+    uint32_t wid;    // wave (t mod blocks) ... : spreads a short phase over every CU
+    uint32_t wid_c;  // block-contiguous wave index: long phases sweep memory together
+    uint32_t nw;
     int lane;
 };
 
+// Wave index that owns tiles wid, wid + nw, ... of a phase with `ntiles` tiles.
+__device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
+    return ntiles > w.nw ? w.wid_c : w.wid;
+}
+
 // Issue the first item of this wave's first tile (weights only: may run
 // before the phase input exists).
-template <int MODE>
-__device__ __forceinline__ bool mk_prefetch(const MkGemv& g, const MkWave& w, uint4 (&buf)[2][kNJC], MkTile& t) {
-    if (w.wid >= mk_tiles<MODE>(g)) return false;
-    mk_make_tile<MODE>(g, w.wid, t, w.lane);
+__device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkWave& w, uint4 (&buf)[2][kNJC],
+                                            MkTile& t) {
+    const uint32_t ntiles = mk_tiles(g, mode);
+    const uint32_t me = mk_owner(w, ntiles);
+    if (me >= ntiles) return false;
+    mk_make_tile(g, mode, me, t);
     issue<uint16_t, 2>(buf, t.p, 0, g.K / 8, w.lane);
     return true;
 }
 
-template <int MODE>
-__device__ __forceinline__ void mk_epilogue(const MkGemv& g, const MkTile& t, const float (&s)[2],
-                                   unsigned long long& best) {
-    if constexpr (MODE == kGemvGateUp) {
-        if (t.valid[0]) {
-            const float gv = s[0], uv = s[1];  // siluMulInto, src/llm.zig:1382-1387
-            st_a(g.o0 + t.row[0], (gv / (1.0f + expf(-gv))) * uv);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (!t.valid[r]) continue;
-            const uint32_t row = t.row[r];
-            if constexpr (MODE == kGemvPlain) {
-                const uint16_t* bias = seg_bias(g, t.seg[r]);
-                st_a(seg_out(g, t.seg[r]) + row, s[r] + (bias ? WeightTraits<uint16_t>::at(bias, row) : 0.0f));
-            } else if constexpr (MODE == kGemvResid) {
-                st_a(g.o0 + row, s[r]);  // s already holds residual + projection
-            } else {
-                if (row == 0)
-                    st_a(g.o0, s[r]);  // read back by the argmax block (NaN rule)
-                else
-                    g.o0[row] = s[r];
-                const unsigned long long key = argmax_key(s[r], row);
-                best = key > best ? key : best;
-            }
-        }
-    }
-}
-
-// Run this wave's tiles of a GEMV phase; bufA/tA hold the prefetched first
-// item when `have` is set.
-template <int MODE>
-__device__ __forceinline__ void mk_gemv(const MkGemv& g, const float* xs, const MkWave& w, uint4 (&bufA)[2][kNJC], MkTile& tA,
-                        bool have, unsigned long long& best) {
+// Run this wave's tiles of a GEMV phase (`mode` is uniform over the grid);
+// bufA/tA hold the prefetched first item when `have` is set.
+//
+// Tile results are parked in lanes -- lane k holds the k-th tile of the
+// current batch of 64 -- and written with one vector store per batch: on gfx9
+// loads and stores share one completion counter, so a store per tile would
+// make every following weight wait for that store's acknowledgement. Each lane
+// also loads its tile's addend (residual row or bias) when the batch opens.
+__device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
+                                        uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best) {
+    const int lane = w.lane;
     const uint32_t U = g.K / 8;
     const uint32_t per_item = kNJC * kWave;
     const uint32_t nchunk = (U + per_item - 1) / per_item;
-    const uint32_t ntiles = mk_tiles<MODE>(g);
-    const uint32_t my_tiles = w.wid < ntiles ? (ntiles - 1 - w.wid) / w.nw + 1 : 0;
+    const uint32_t ntiles = mk_tiles(g, mode);
+    const uint32_t me = mk_owner(w, ntiles);
+    const uint32_t my_tiles = me < ntiles ? (ntiles - 1 - me) / w.nw + 1 : 0;
     const uint32_t n_items = my_tiles * nchunk;
     if (n_items == 0) return;
     if (!have) {
-        mk_make_tile<MODE>(g, w.wid, tA, w.lane);
-        issue<uint16_t, 2>(bufA, tA.p, 0, U, w.lane);
+        mk_make_tile(g, mode, me, tA);
+        issue<uint16_t, 2>(bufA, tA.p, 0, U, lane);
     }
-    uint4 bufB[2][kNJC];
-    MkTile tB;
-    float acc[2] = {0.f, 0.f};
-    auto step = [&](uint4(&cur)[2][kNJC], MkTile& tc, uint4(&nxt)[2][kNJC], MkTile& tn, uint32_t it) {
-        const uint32_t chunk = it % nchunk;
-        if (it + 1 < n_items) {
-            const uint32_t nit = it + 1, nch = nit % nchunk;
-            if (nch == 0) mk_make_tile<MODE>(g, w.wid + (nit / nchunk) * w.nw, tn, w.lane);
-            else tn = tc;
-            issue<uint16_t, 2>(nxt, tn.p, nch * per_item, U, w.lane);
-        }
-        consume<uint16_t, 2>(cur, xs, chunk * per_item, U, w.lane, acc);
-        if (chunk == nchunk - 1) {
-            float s[2];
-            s[0] = wave_sum(acc[0]);
-            s[1] = wave_sum(acc[1]);
-            acc[0] = acc[1] = 0.f;
-            if constexpr (MODE == kGemvResid) {
-                s[0] += tc.resid[0];  // x = residual + proj (addInto, src/llm.zig:1389-1396)
-                s[1] += tc.resid[1];
-            }
-            if (w.lane == 0) mk_epilogue<MODE>(g, tc, s, best);
+    // Lane state of the open batch: rows, segment, addends, parked results.
+    uint32_t ra = 0, rb = 0;
+    int sa = 0;
+    bool va = false, vb = false;
+    float ea = 0.f, eb = 0.f, oa = 0.f, ob = 0.f;
+    uint32_t base = 0, pending = 0;
+    auto open_batch = [&]() {
+        const uint32_t k = base + (uint32_t)lane;
+        const bool mine = k < my_tiles;
+        MkTile t;
+        mk_make_tile(g, mode, mine ? me + k * w.nw : me, t);
+        ra = t.row[0];
+        rb = t.row[1];
+        sa = t.seg;
+        va = mine && t.valid[0];
+        vb = mine && t.valid[1];
+        ea = eb = 0.f;
+        if (mode == kGemvResid) {  // x = residual + proj (addInto, src/llm.zig:1389-1396)
+            if (va) ea = ld_a(g.o0 + ra);
+            if (vb) eb = ld_a(g.o0 + rb);
+        } else if (mode == kGemvPlain) {  // linearRange: dot + bias (src/llm.zig:1273)
+            const uint16_t* bias = seg_bias(g, sa);
+            if (bias && va) ea = __uint_as_float((uint32_t)*as_global(bias + ra) << 16);
+            if (bias && vb) eb = __uint_as_float((uint32_t)*as_global(bias + rb) << 16);
         }
     };
-    uint32_t item = 0;
-    while (item < n_items) {
-        step(bufA, tA, bufB, tB, item);
-        ++item;
-        if (item >= n_items) break;
-        step(bufB, tB, bufA, tA, item);
-        ++item;
+    auto flush = [&]() {
+        if ((uint32_t)lane < pending) {
+            if (mode == kGemvLogits) {
+                if (va) {
+                    if (ra == 0)
+                        st_a(g.o0, oa);  // read back by the argmax block (NaN rule)
+                    else
+                        *as_global(g.o0 + ra) = oa;
+                }
+                if (vb) *as_global(g.o0 + rb) = ob;
+            } else {
+                float* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
+                if (va) st_a(o + ra, oa + ea);
+                if (vb) st_a(o + rb, ob + eb);
+            }
+        }
+        pending = 0;
+    };
+    open_batch();
+    uint4 bufB[2][kNJC];
+    MkTile tc = tA, tn = tA;  // tiles of the item being consumed / in flight
+    float acc0 = 0.f, acc1 = 0.f;
+    for (uint32_t it = 0; it < n_items; ++it) {
+        const uint32_t chunk = it % nchunk;
+        const bool more = it + 1 < n_items;
+        if (more && chunk == nchunk - 1) mk_make_tile(g, mode, me + ((it + 1) / nchunk) * w.nw, tn);
+        const uint32_t nbase = (chunk == nchunk - 1 ? 0 : chunk + 1) * per_item;
+        float acc[2] = {acc0, acc1};
+        if (it & 1) {
+            if (more) issue<uint16_t, 2>(bufA, tn.p, nbase, U, lane);
+            consume<uint16_t, 2>(bufB, xs, chunk * per_item, U, lane, acc);
+        } else {
+            if (more) issue<uint16_t, 2>(bufB, tn.p, nbase, U, lane);
+            consume<uint16_t, 2>(bufA, xs, chunk * per_item, U, lane, acc);
+        }
+        acc0 = acc[0];
+        acc1 = acc[1];
+        if (chunk == nchunk - 1) {
+            float v0 = wave_sum(acc0);
+            const float v1 = wave_sum(acc1);
+            acc0 = acc1 = 0.f;
+            if (mode == kGemvGateUp) {
+                v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
+            } else if (mode == kGemvLogits && lane == 0) {
+                if (tc.valid[0]) {
+                    const unsigned long long k0 = argmax_key(v0, tc.row[0]);
+                    best = k0 > best ? k0 : best;
+                }
+                if (tc.valid[1]) {
+                    const unsigned long long k1 = argmax_key(v1, tc.row[1]);
+                    best = k1 > best ? k1 : best;
+                }
+            }
+            if ((uint32_t)lane == pending) {
+                oa = v0;
+                ob = v1;
+            }
+            if (++pending == kWave) {
+                flush();
+                base += kWave;
+                open_batch();
+            }
+            tc = tn;
+        }
     }
+    flush();
 }
 
 // ---------------------------------------------------------------------------
@@ -282,15 +342,19 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, const float* xs, const 
 // (rmsNormInto, src/llm.zig:1287-1300). src is an f32 activation read with
 // agent-scope loads, or (src_bf16) a bf16 embedding row (copyEmbeddingToken,
 // :1373-1380), which block 0 also publishes as the residual stream x_out.
+// The norm weights are loaded in the same batch as the activation (into
+// nws = xs + n), so the phase waits for one memory round trip, not two.
 __device__ __forceinline__ void mk_stage(float* xs, float* red, const float* src, const uint16_t* src_bf16,
                                          float* x_out, const uint16_t* norm_w, float eps, uint32_t n) {
     const int tid = threadIdx.x;
     constexpr int B = 8;  // 16-byte loads issued before any is consumed
+    float* nws = xs + n;
     float ss = 0.f;
     if (src_bf16) {
         for (uint32_t k = tid; k < n; k += kMkThreads) {
             const float v = WeightTraits<uint16_t>::at(src_bf16, k);
             xs[k] = v;
+            if (norm_w) nws[k] = __uint_as_float((uint32_t)*as_global(norm_w + k) << 16);
             ss = fmaf(v, v, ss);
             if (x_out) st_a(x_out + k, v);
         }
@@ -299,13 +363,22 @@ __device__ __forceinline__ void mk_stage(float* xs, float* red, const float* src
         const uint32_t n4 = n / 4;
         for (uint32_t i0 = tid; i0 < n4; i0 += B * kMkThreads) {
             float4 v[B];
+            uint2 nv[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) v[b] = ld_coh4(r, (i0 + b * kMkThreads) * 16);
+            for (int b = 0; b < B; ++b) {
+                const uint32_t i = i0 + b * kMkThreads;
+                v[b] = ld_coh4(r, i * 16);
+                nv[b] = (norm_w && i < n4) ? load_u32x2(norm_w + 4 * i) : make_uint2(0, 0);
+            }
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 const uint32_t i = i0 + b * kMkThreads;
                 if (i < n4) {
                     *reinterpret_cast<float4*>(xs + 4 * i) = v[b];
+                    if (norm_w)
+                        *reinterpret_cast<float4*>(nws + 4 * i) =
+                            make_float4(__uint_as_float(nv[b].x << 16), __uint_as_float(nv[b].x & 0xffff0000u),
+                                        __uint_as_float(nv[b].y << 16), __uint_as_float(nv[b].y & 0xffff0000u));
                     ss = fmaf(v[b].x, v[b].x, ss);
                     ss = fmaf(v[b].y, v[b].y, ss);
                     ss = fmaf(v[b].z, v[b].z, ss);
@@ -322,7 +395,7 @@ __device__ __forceinline__ void mk_stage(float* xs, float* red, const float* src
 #pragma unroll
         for (int i = 0; i < kMkWaves; ++i) total += red[i];
         const float scale = 1.0f / sqrtf(total / (float)n + eps);
-        for (uint32_t k = tid; k < n; k += kMkThreads) xs[k] = xs[k] * WeightTraits<uint16_t>::at(norm_w, k) * scale;
+        for (uint32_t k = tid; k < n; k += kMkThreads) xs[k] = xs[k] * nws[k] * scale;
     }
     __syncthreads();
 }
@@ -438,8 +511,8 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
                     v4 = *reinterpret_cast<const float4*>(vnew + c4);
                 } else {
                     const size_t off = (size_t)t * kvw + (size_t)h * hd + c4;
-                    k4 = *reinterpret_cast<const float4*>(kc + off);
-                    v4 = *reinterpret_cast<const float4*>(vc + off);
+                    k4 = load_f32x4(kc + off);
+                    v4 = load_f32x4(vc + off);
                 }
                 *reinterpret_cast<float4*>(ks + j * KS + c4) = k4;
                 *reinterpret_cast<float4*>(vs + j * HDMAX + c4) = v4;
@@ -587,6 +660,60 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
+// Phases of one token step: per layer Q (input RMSNorm + q/k/v), A (RoPE, KV
+// append, attention), O (x += Wo.attn), G (post-attention RMSNorm, gate/up,
+// SwiGLU), D (x += Wd.ff); then the logits phase (final RMSNorm + lm_head).
+// All GEMV phases run through one code path with a grid-uniform mode, so the
+// whole step loop stays small enough for the instruction cache.
+enum : uint32_t { kPhQ = 0, kPhA = 1, kPhO = 2, kPhG = 3, kPhD = 4, kPhPerLayer = 5 };
+
+struct MkPhase {
+    uint32_t layer, kind;
+    bool logits;
+};
+
+__device__ __forceinline__ MkPhase mk_phase(uint32_t ph, uint32_t layers) {
+    MkPhase f;
+    f.layer = ph / kPhPerLayer;
+    f.kind = ph - f.layer * kPhPerLayer;
+    f.logits = f.layer == layers;
+    return f;
+}
+
+__device__ __forceinline__ int mk_mode(const MkPhase& f) {
+    if (f.logits) return kGemvLogits;
+    return f.kind == kPhQ ? kGemvPlain : (f.kind == kPhG ? kGemvGateUp : kGemvResid);
+}
+
+// The host-built tables (GEMV descriptors, norm weights per layer) are copied
+// into LDS when the kernel starts: read from global memory they would miss the
+// caches every phase (the weight stream evicts them) and put a memory round
+// trip in front of every phase.
+struct MkTables {
+    const MkGemv* gemv;         // [layers * 4 + 1]
+    const uint16_t* const* norm;  // [layers * 2]: input, post-attention
+};
+
+__device__ __forceinline__ MkTables mk_load_tables(const DecodeStepParams& p, char* lds) {
+    MkGemv* g = reinterpret_cast<MkGemv*>(lds);
+    const uint16_t** nrm = reinterpret_cast<const uint16_t**>(lds + (size_t)(p.layers * 4 + 1) * sizeof(MkGemv));
+    const uint32_t gw = (p.layers * 4 + 1) * sizeof(MkGemv) / 4;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p.gemv);
+    for (uint32_t i = threadIdx.x; i < gw; i += kMkThreads) reinterpret_cast<uint32_t*>(g)[i] = src[i];
+    for (uint32_t i = threadIdx.x; i < p.layers * 2; i += kMkThreads)
+        nrm[i] = (i & 1) ? p.layer[i >> 1].post_norm : p.layer[i >> 1].input_norm;
+    __syncthreads();
+    return MkTables{g, nrm};
+}
+
+__device__ __forceinline__ const MkGemv& mk_gemv_of(const DecodeStepParams& p, const MkTables& t, const MkPhase& f) {
+    return t.gemv[f.logits ? p.layers * 4 : f.layer * 4 + (f.kind == kPhQ ? 0 : f.kind - 1)];
+}
+__device__ __forceinline__ const uint16_t* mk_norm_of(const DecodeStepParams& p, const MkTables& t, const MkPhase& f) {
+    if (f.logits) return p.final_norm;
+    return f.kind == kPhQ ? t.norm[f.layer * 2] : (f.kind == kPhG ? t.norm[f.layer * 2 + 1] : nullptr);
+}
+
 template <int HDMAX, bool EXACT>
 __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParams p) {
     extern __shared__ float smem[];
@@ -599,17 +726,19 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     w.lane = tid & 63;
     // Tile t goes to wave (t mod blocks) of ... so consecutive tiles land on
     // different CUs and a phase with fewer tiles than waves still uses them all.
-    w.wid = (tid >> 6) * gridDim.x + blockIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
+    w.wid = wave * gridDim.x + blockIdx.x;
+    w.wid_c = blockIdx.x * kMkWaves + wave;
     w.nw = gridDim.x * kMkWaves;
     if (tid == 0) s_gen = 0;
     uint4 buf[2][kNJC];
     MkTile tile;
     unsigned long long best = 0ull;
-    const uint32_t H = p.hidden, kvw = p.kvdim;
-    float* q_out = p.qkv;
-    float* k_out = p.qkv + p.heads * p.hd;
-    float* v_out = k_out + kvw;
-    if (p.timing && tid == 0 && blockIdx.x == 0) p.timing[(size_t)gridDim.x * p.timing_stride] = __builtin_amdgcn_s_memrealtime();
+    const uint32_t H = p.hidden;
+    if (p.timing && tid == 0 && blockIdx.x == 0)
+        p.timing[(size_t)gridDim.x * p.timing_stride + p.timing_slots - 1] = __builtin_amdgcn_s_memrealtime();
+    const uint32_t nph = kPhPerLayer * p.layers + 1;
+    const MkTables tb = mk_load_tables(p, reinterpret_cast<char*>(smem) + p.table_lds_offset);
 
     for (uint32_t step = 0; step < p.n_steps; ++step) {
         // Step state (written by block 0 in the previous step's argmax phase).
@@ -628,67 +757,33 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
         uint32_t chunk = (T + p.nsplit - 1) / p.nsplit;
         if (chunk < p.min_chunk) chunk = p.min_chunk;
         const uint32_t ns = (T + chunk - 1) / chunk;
+        bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
 
-        for (uint32_t l = 0; l < p.layers; ++l) {
-            const DecodeLayer& L = p.layer[l];
-            // ---- Q: input RMSNorm + q/k/v (+ bias) ----
-            const MkGemv& gq = p.gemv[l * 4 + 0];
-            bool have = (l == 0) ? mk_prefetch<kGemvPlain>(gq, w, buf, tile) : true;
-            mk_stage(smem, red, p.x, l == 0 ? p.embed + (size_t)token * H : nullptr,
-                     (l == 0 && blockIdx.x == 0) ? p.x : nullptr, L.input_norm, p.eps, H);
-            // (Layer 0 reads the embedding row straight from the blob; block 0
-            // publishes it as the residual stream, first read two barriers on.)
-            mk_gemv<kGemvPlain>(gq, smem, w, buf, tile, have, best);
-            wait_all_mem();
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
-
-            // ---- A: RoPE + KV append + split attention ----
-            mk_attention<HDMAX, EXACT>(p, l, pos, chunk, ns, smem);
-            // Prefetch the O phase's first item.
-            const MkGemv& go = p.gemv[l * 4 + 1];
-            wait_all_mem();
-            have = mk_prefetch<kGemvResid>(go, w, buf, tile);
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
-
-            // ---- O: merge attention splits; x += Wo . attn ----
-            mk_stage(smem, red, p.attn, nullptr, nullptr, nullptr, 0.f, H);
-            mk_gemv<kGemvResid>(go, smem, w, buf, tile, have, best);
-            const MkGemv& gg = p.gemv[l * 4 + 2];
-            wait_all_mem();
-            have = mk_prefetch<kGemvGateUp>(gg, w, buf, tile);
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
-
-            // ---- G: post-attention RMSNorm + gate/up + SwiGLU ----
-            mk_stage(smem, red, p.x, nullptr, nullptr, L.post_norm, p.eps, H);
-            mk_gemv<kGemvGateUp>(gg, smem, w, buf, tile, have, best);
-            const MkGemv& gd = p.gemv[l * 4 + 3];
-            wait_all_mem();
-            have = mk_prefetch<kGemvResid>(gd, w, buf, tile);
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
-
-            // ---- D: x += Wd . ff ----
-            mk_stage(smem, red, p.ff, nullptr, nullptr, nullptr, 0.f, p.inter);
-            mk_gemv<kGemvResid>(gd, smem, w, buf, tile, have, best);
-            wait_all_mem();
-            if (l + 1 < p.layers) {
-                const DecodeLayer& N = p.layer[l + 1];
-                const MkGemv& gn = p.gemv[(l + 1) * 4 + 0];
-                (void)mk_prefetch<kGemvPlain>(gn, w, buf, tile);
+        for (uint32_t ph = 0; ph < nph; ++ph) {
+            const MkPhase f = mk_phase(ph, p.layers);
+            if (f.kind == kPhA && !f.logits) {
+                mk_attention<HDMAX, EXACT>(p, f.layer, pos, chunk, ns, smem);
             } else {
-                const MkGemv& gl = p.gemv[p.layers * 4];
-                (void)mk_prefetch<kGemvLogits>(gl, w, buf, tile);
+                const uint16_t* norm = mk_norm_of(p, tb, f);
+                const float* src = f.kind == kPhO ? p.attn : (f.kind == kPhD ? p.ff : p.x);
+                // Layer 0 reads the embedding row straight from the blob; block 0
+                // publishes it as the residual stream, first read two barriers on.
+                mk_stage(smem, red, src, ph == 0 ? p.embed + (size_t)token * H : nullptr,
+                         (ph == 0 && blockIdx.x == 0) ? p.x : nullptr, norm, p.eps, f.kind == kPhD ? p.inter : H);
+                if (tid == 0) mk_mark(p, s_gen, 1);
+                if (f.logits) best = 0ull;
+                mk_gemv(mk_gemv_of(p, tb, f), mk_mode(f), smem, w, buf, tile, have, best);
+                if (f.logits && w.lane == 0) st_a(p.keys + w.wid, best);
+            }
+            if (w.lane == 0) mk_mark(p, s_gen, 2 + (tid >> 6));
+            wait_all_mem();
+            // Issue the first weights of the next GEMV phase before the barrier.
+            if (ph + 1 < nph) {
+                const MkPhase nf = mk_phase(ph + 1, p.layers);
+                if (nf.kind != kPhA || nf.logits) have = mk_prefetch(mk_gemv_of(p, tb, nf), mk_mode(nf), w, buf, tile);
             }
             if (!mk_barrier(p, &s_gen, &s_ok)) return;
         }
-
-        // ---- logits: final RMSNorm + lm_head (or tied embedding) ----
-        const MkGemv& gl = p.gemv[p.layers * 4];
-        mk_stage(smem, red, p.x, nullptr, nullptr, p.final_norm, p.eps, H);
-        best = 0ull;
-        mk_gemv<kGemvLogits>(gl, smem, w, buf, tile, true, best);
-        if (w.lane == 0) st_a(p.keys + w.wid, best);
-        wait_all_mem();
-        if (!mk_barrier(p, &s_gen, &s_ok)) return;
 
         // ---- argmax + step advance (block 0) ----
         if (blockIdx.x == 0) {
@@ -735,12 +830,17 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
 
 }  // namespace
 
-size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t heads, uint32_t hd) {
+size_t decode_step_table_offset(uint32_t hidden, uint32_t inter, uint32_t hd) {
     const size_t attn = hd <= 64 ? (size_t)AttnLds<64>::kTotal : (size_t)AttnLds<128>::kTotal;
-    const size_t stage = (size_t)(hidden > inter ? hidden : inter);
-    (void)heads;
+    // Staged input plus the norm weights of hidden-sized inputs.
+    const size_t stage = (size_t)(2 * hidden > inter ? 2 * hidden : inter);
     const size_t need = attn > stage ? attn : stage;
-    return need * sizeof(float);
+    return (need * sizeof(float) + 15) / 16 * 16;
+}
+
+size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, uint32_t hd) {
+    return decode_step_table_offset(hidden, inter, hd) + (size_t)(layers * 4 + 1) * sizeof(DecodeGemv) +
+           (size_t)layers * 2 * sizeof(const uint16_t*);
 }
 
 static const void* decode_step_fn(uint32_t hd) {

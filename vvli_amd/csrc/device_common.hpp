@@ -37,7 +37,29 @@ template <> struct WeightTraits<float> {
     }
 };
 
-__device__ inline uint4 load_unit(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Device pointers handed around in structs (or read back from LDS) are
+// generic; the casts to the global address space make the compiler emit
+// global_* rather than flat_* memory instructions (flat ones also count
+// against the LDS counter and cost more to issue).
+#define VVLI_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ VVLI_GLOBAL T* as_global(T* p) {
+    return (VVLI_GLOBAL T*)p;
+}
+typedef unsigned int vvli_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vvli_u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint4 load_unit(const void* p) {
+    const vvli_u32x4 v = *as_global(reinterpret_cast<const vvli_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float4 load_f32x4(const float* p) {
+    const vvli_u32x4 v = *as_global(reinterpret_cast<const vvli_u32x4*>(p));
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ inline uint2 load_u32x2(const void* p) {
+    const vvli_u32x2 v = *as_global(reinterpret_cast<const vvli_u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
 
 // ---- wave reductions with DPP --------------------------------------------
 // quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_half_mirror =

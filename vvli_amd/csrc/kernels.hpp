@@ -168,14 +168,20 @@ struct DecodeStepParams {
     uint32_t nsplit, min_chunk;
     uint32_t n_steps;
     int64_t eos;  // < 0: none
-    // Optional phase timing (100 MHz s_memrealtime ticks): block b's arrival
-    // at barrier k in timing[b * timing_stride + k], block 0's release of
-    // barrier k in timing[gridDim * timing_stride + k]; index 0 is the start.
+    // Optional phase timing (100 MHz s_memrealtime ticks), timing_slots
+    // entries per barrier k: block b's arrival at barrier k in
+    // timing[b * timing_stride + k * slots + slots - 1], block 0's release of
+    // barrier k in timing[gridDim * timing_stride + k * slots + slots - 1];
+    // k = 0 is the start. With 16 slots, slot 0 is the release seen by the
+    // block, 1 its staged input, 2 + w wave w's last result of the phase.
     unsigned long long* timing;
     uint32_t timing_stride;
+    uint32_t timing_slots;
+    uint32_t table_lds_offset;  // bytes: where the kernel copies gemv[] / norms into LDS
 };
 
-size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t heads, uint32_t hd);
+size_t decode_step_table_offset(uint32_t hidden, uint32_t inter, uint32_t hd);
+size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, uint32_t hd);
 hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu);
 hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s);
 

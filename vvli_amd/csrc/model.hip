@@ -310,6 +310,8 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.eos = eos;
     p.timing = timing;
     p.timing_stride = timing_stride;
+    p.timing_slots = timing_stride >= 16u * (5u * c.layers + 4u) ? 16u : 1u;
+    p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, c.inter, p.hd));
     HIP_TRY(hipMemsetAsync(m->mk_sync, 0, m->mk_sync_words * sizeof(uint32_t), m->stream));
     HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
     m->mk_pending = true;
@@ -389,7 +391,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     // Persistent step: bf16 only, one 512-thread block per CU if it fits.
     if (cfg->weight_kind == VVLI_WEIGHT_BF16) {
         int cus = 0, bpc = 0;
-        m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->heads, hd);
+        m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->layers, hd);
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
             m->mk_lds <= 160 * 1024 && decode_step_max_blocks(hd, m->mk_lds, &bpc) == hipSuccess && bpc >= 1 &&
             cus > 0) {
