@@ -158,15 +158,18 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint
 int vvli_gpu_profile_step(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* ms_out, uint32_t cap,
                           uint32_t* n_out);
 /* Which implementation runs forward_token / prefill / generate:
- * 0 = auto (currently the per-kernel graph, the faster one on the Llama-1B
- * decode benchmark), 1 = per-kernel HIP graph, 2 = persistent one-launch step
- * (bf16 weights only; VVLI_INVALID_CONFIG if unavailable). For A/B
- * measurement and for checking both against the same reference. */
+ * 0 = auto (the persistent step where available, else the per-kernel graph),
+ * 1 = per-kernel HIP graph, 2 = persistent one-launch step (bf16 weights
+ * only; VVLI_INVALID_CONFIG if unavailable). For A/B measurement and for
+ * checking both against the same reference. */
 int vvli_gpu_set_decode_path(vvli_gpu_model* model, uint32_t path);
 /* One persistent step with phase timestamps (100 MHz ticks): ticks_out holds
- * (n_blocks + 1) * stride values; row b < n_blocks = block b's arrival at
- * barrier k (k >= 1), the last row = the release of barrier k (k = 0: start).
- * *n_blocks = blocks of the persistent launch. */
+ * (n_blocks + 1) * stride values. With stride >= 16 * (5 * layers + 2), phase
+ * k of the step (per layer q/k/v, attention, o, gate/up, down; then logits)
+ * fills ticks_out[b * stride + 16 k] with block b's staged input and
+ * [b * stride + 16 k + 1 + w] with wave w's end of the phase;
+ * ticks_out[n_blocks * stride] is the kernel start. *n_blocks = blocks of the
+ * persistent launch. */
 int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t pos, uint64_t* ticks_out,
                                 uint32_t stride, uint32_t* n_blocks);
 

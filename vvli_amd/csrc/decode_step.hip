@@ -3,26 +3,36 @@
 // llm.argmax, :778-789), optionally many in a row (the decode loop of
 // generateGreedyMeasured, src/generator.zig:243-281).
 //
-// Why: at batch 1 every layer is 5 dependent, HBM-bound GEMV/attention
-// phases. As separate kernels each pays ~4 us of launch/ramp/drain; here they
-// are phases of one kernel separated by a software grid barrier (~1.6 us:
-// each block publishes a generation flag, block 0 gathers and releases), and
-// every wave issues the weight loads of its first tile of the next phase
-// *before* it enters the barrier, so the barrier hides under the weight
-// stream.
+// Why: at batch 1 every layer is five dependent, HBM-bound phases (q/k/v
+// GEMV, attention, o GEMV, gate/up GEMV, down GEMV). As separate kernels each
+// pays launch, ramp and drain; here they are phases of one kernel, and every
+// wave issues the weight loads of its first tile of the next phase before it
+// waits for that phase's input.
 //
-// Memory model: activations (x, q/k/v, ff, attention partials, argmax keys,
-// step state) are exchanged across blocks on different XCDs through
-// agent-scope atomic loads/stores, which gfx950 executes with sc1 (coherent
-// across the per-XCD L2s), with no L2 writeback/invalidate fences. Each wave
-// waits for its own stores (s_waitcnt 0) before the block reaches the barrier.
-// New K/V rows are written the same way; older rows are read with plain loads
-// (a row is never read before it is written within a launch, and the launch
-// starts with clean caches).
+// Dataflow instead of grid barriers: every activation that crosses blocks is
+// an array of 64-bit tagged words, value bits in the low half and the epoch of
+// the phase that wrote it in the high half, stored and loaded with single
+// agent-scope 64-bit accesses (gfx950: sc1, coherent across the per-XCD L2s).
+// A consumer polls exactly the words it needs until each carries the epoch it
+// expects, so a phase boundary costs one store->load hop instead of a flag
+// barrier plus a separate load of the data, and nobody waits for a store
+// acknowledgement. Epochs grow monotonically over launches (the host passes
+// the first one), so buffers never need clearing between steps.
+//
+// Why a word is never overwritten before every reader has it: a phase only
+// reads inputs if it produces outputs, and the next write of any buffer lies
+// downstream (through the dependency chain of later phases) of every output of
+// the phases that read it. A block with no work in a phase skips its input.
+//
+// KV rows: the attention unit that owns position pos appends its K/V row with
+// agent-scope stores and waits for their acknowledgement before it publishes
+// the attention output; later steps read rows with plain loads (a row is never
+// read before it is written within a launch, and a launch starts with clean
+// caches).
 //
 // Deadlock safety: the launch is cooperative (all blocks co-resident or the
-// launch fails), every spin is bounded, and a timeout raises a device error
-// flag that makes every block leave at its next barrier; the host reports it.
+// launch fails), every poll is bounded, and a timeout raises a device error
+// flag that makes every block leave at its next poll; the host reports it.
 #include "device_common.hpp"
 #include "gemv_tile.hpp"
 #include "kernels.hpp"
@@ -34,17 +44,15 @@ namespace {
 constexpr int kMkThreads = 512;
 constexpr int kMkWaves = kMkThreads / kWave;
 constexpr int kMaxGroupMk = 16;
-constexpr int kMaxSplitMk = 16;  // attention splits per kv head (merged by every block)
-constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of polling: phases take <= ~0.2 ms
-constexpr uint32_t kFlagStride = 32;  // words between per-block flags (128 B)
+constexpr int kMaxSplitMk = 16;  // attention splits per kv head
+constexpr uint32_t kSpinLimit = 1u << 22;  // polls of one word (each after a short sleep): seconds
 
-__device__ __forceinline__ float ld_a(const float* p) {
-    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+typedef unsigned long long tword;
+
 __device__ __forceinline__ uint32_t ld_a(const uint32_t* p) {
     return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned long long ld_a(const unsigned long long* p) {
+__device__ __forceinline__ tword ld_a(const tword* p) {
     return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_a(float* p, float v) {
@@ -53,14 +61,21 @@ __device__ __forceinline__ void st_a(float* p, float v) {
 __device__ __forceinline__ void st_a(uint32_t* p, uint32_t v) {
     __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_a(unsigned long long* p, unsigned long long v) {
+__device__ __forceinline__ void st_a(tword* p, tword v) {
     __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
-// 16-byte loads that see other XCDs' agent-scope stores: buffer loads with
-// the sc1 cache policy (the bit the compiler uses for agent-scope atomic
-// loads), through a raw buffer resource (out-of-range reads return 0).
+__device__ __forceinline__ tword tw_make(float v, uint32_t tag) {
+    return ((tword)tag << 32) | (tword)__float_as_uint(v);
+}
+__device__ __forceinline__ tword tw_make_u(uint32_t v, uint32_t tag) { return ((tword)tag << 32) | (tword)v; }
+__device__ __forceinline__ float tw_val(tword w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ uint32_t tw_tag(tword w) { return (uint32_t)(w >> 32); }
+
+// 16-byte loads (two tagged words) that see other XCDs' agent-scope stores:
+// buffer loads with the sc1 cache policy, through a raw buffer resource
+// (out-of-range reads return 0).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kCpolSc1 = 16;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base, uint32_t bytes) {
@@ -70,64 +85,33 @@ __device__ __forceinline__ float4 ld_coh4(__amdgpu_buffer_rsrc_t r, uint32_t byt
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-
-// ---------------------------------------------------------------------------
-// Grid barrier: block b stores generation g in flags[b]; block 0 waits for all
-// flags, then stores g in `release`; the others wait for `release`.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool mk_barrier(const DecodeStepParams& p, uint32_t* s_gen, int* s_ok) {
-    __syncthreads();
-    const uint32_t gen = *s_gen + 1;
-    __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid == 0) *s_gen = gen;
-    if (tid == 0) {
-        *s_ok = 1;
-        if (p.timing && (gen + 1) * p.timing_slots <= p.timing_stride)
-            p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots + p.timing_slots - 1] =
-                __builtin_amdgcn_s_memrealtime();
-        st_a(p.flags + blockIdx.x * kFlagStride, gen);
-    }
-    if (blockIdx.x == 0) {
-        __syncthreads();
-        for (uint32_t b = tid; b < gridDim.x; b += kMkThreads) {
-            uint32_t spins = 0;
-            while (ld_a(p.flags + b * kFlagStride) < gen) {
-                if (++spins > kSpinLimit || ((spins & 255u) == 0 && ld_a(p.error) != 0)) {
-                    st_a(p.error, 1u);
-                    *s_ok = 0;
-                    break;
-                }
-            }
-        }
-        __syncthreads();
-        if (tid == 0) {
-            if (p.timing && (gen + 1) * p.timing_slots <= p.timing_stride)
-                p.timing[(size_t)gridDim.x * p.timing_stride + gen * p.timing_slots + p.timing_slots - 1] =
-                    __builtin_amdgcn_s_memrealtime();
-            st_a(p.release, *s_ok ? gen : 0xffffffffu);
-        }
-    } else if (tid == 0) {
-        uint32_t spins = 0;
-        while (ld_a(p.release) < gen) {
-            if (++spins > kSpinLimit || ((spins & 255u) == 0 && ld_a(p.error) != 0)) {
-                st_a(p.error, 1u);
-                *s_ok = 0;
-                break;
-            }
-        }
-        if (ld_a(p.error) != 0) *s_ok = 0;
-    }
-    __syncthreads();
-    if (tid == 0 && p.timing && p.timing_slots > 1 && (gen + 1) * p.timing_slots <= p.timing_stride)
-        p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots] = __builtin_amdgcn_s_memrealtime();
-    return *s_ok != 0;
+__device__ __forceinline__ void ld_coh_tw2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, tword& a, tword& b) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
+    a = ((tword)v.y << 32) | v.x;
+    b = ((tword)v.w << 32) | v.z;
 }
 
-// Detail timing mark of the current phase (16-slot timing only).
-__device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t gen, int slot) {
-    if (p.timing && p.timing_slots > 1 && (gen + 1) * p.timing_slots <= p.timing_stride)
-        p.timing[blockIdx.x * p.timing_stride + gen * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
+// Wait until *p carries `tag` (w holds a first load). False: the spin limit
+// passed (the error flag is raised) or another block raised it.
+__device__ __forceinline__ bool poll_tw(const tword* p, uint32_t tag, tword& w, uint32_t* err) {
+    uint32_t spins = 0;
+    while (tw_tag(w) != tag) {
+        if (++spins > kSpinLimit) {
+            st_a(err, 1u);
+            return false;
+        }
+        if ((spins & 63u) == 0 && ld_a(err) != 0) return false;
+        __builtin_amdgcn_s_sleep(1);
+        w = ld_a(p);
+    }
+    return true;
+}
+
+// Detail timing mark (16-slot timing only): slot 0 the block's staged input,
+// 1 + w wave w's end of the phase.
+__device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
+    if (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
+        p.timing[blockIdx.x * p.timing_stride + ph * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
 }
 
 // ---------------------------------------------------------------------------
@@ -142,7 +126,7 @@ __device__ __forceinline__ const uint16_t* seg_w(const MkGemv& g, int seg) {
 __device__ __forceinline__ const uint16_t* seg_bias(const MkGemv& g, int seg) {
     return seg == 0 ? g.b0 : (seg == 1 ? g.b1 : g.b2);
 }
-__device__ __forceinline__ float* seg_out(const MkGemv& g, int seg) { return seg == 0 ? g.o0 : (seg == 1 ? g.o1 : g.o2); }
+__device__ __forceinline__ tword* seg_out(const MkGemv& g, int seg) { return seg == 0 ? g.o0 : (seg == 1 ? g.o1 : g.o2); }
 
 struct MkTile {
     const uint16_t* p[2];  // weight rows streamed by this tile
@@ -202,32 +186,51 @@ struct MkWave {
 };
 
 // Wave index that owns tiles wid, wid + nw, ... of a phase with `ntiles` tiles.
+// Either way block b owns a tile of the phase iff b < ntiles.
 __device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
     return ntiles > w.nw ? w.wid_c : w.wid;
 }
 
 // Issue the first item of this wave's first tile (weights only: may run
-// before the phase input exists).
+// before the phase input exists). Defines buf and t on every path, so they are
+// dead between a phase's last item and the next prefetch.
 __device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkWave& w, uint4 (&buf)[2][kNJC],
                                             MkTile& t) {
     const uint32_t ntiles = mk_tiles(g, mode);
     const uint32_t me = mk_owner(w, ntiles);
-    if (me >= ntiles) return false;
-    mk_make_tile(g, mode, me, t);
+    mk_make_tile(g, mode, me < ntiles ? me : 0, t);
+    if (me >= ntiles) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int j = 0; j < kNJC; ++j) buf[r][j] = make_uint4(0, 0, 0, 0);
+        return false;
+    }
     issue<uint16_t, 2>(buf, t.p, 0, g.K / 8, w.lane);
     return true;
 }
 
+// Where a residual-mode phase takes its residual rows: tagged words of an
+// earlier phase, or (layer 0) the bf16 embedding row of the token.
+struct MkResid {
+    const tword* src;
+    uint32_t tag;
+    const uint16_t* bf16;
+};
+
 // Run this wave's tiles of a GEMV phase (`mode` is uniform over the grid);
-// bufA/tA hold the prefetched first item when `have` is set.
+// bufA/tA hold the prefetched first item when `have` is set. Outputs are
+// tagged with `tag` (logits: plain floats plus the argmax key in `best`).
 //
 // Tile results are parked in lanes -- lane k holds the k-th tile of the
 // current batch of 64 -- and written with one vector store per batch: on gfx9
 // loads and stores share one completion counter, so a store per tile would
 // make every following weight wait for that store's acknowledgement. Each lane
-// also loads its tile's addend (residual row or bias) when the batch opens.
-__device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
-                                        uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best) {
+// also loads its tile's addend (residual row or bias) when the batch opens and
+// checks the residual's tag only when it writes.
+__device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
+                                        uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
+                                        uint32_t tag, const MkResid& rs, uint32_t* err) {
     const int lane = w.lane;
     const uint32_t U = g.K / 8;
     const uint32_t per_item = kNJC * kWave;
@@ -236,7 +239,7 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
     const uint32_t me = mk_owner(w, ntiles);
     const uint32_t my_tiles = me < ntiles ? (ntiles - 1 - me) / w.nw + 1 : 0;
     const uint32_t n_items = my_tiles * nchunk;
-    if (n_items == 0) return;
+    if (n_items == 0) return true;
     if (!have) {
         mk_make_tile(g, mode, me, tA);
         issue<uint16_t, 2>(bufA, tA.p, 0, U, lane);
@@ -245,8 +248,10 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
     uint32_t ra = 0, rb = 0;
     int sa = 0;
     bool va = false, vb = false;
+    tword wa = 0, wb = 0;  // residual words (tag checked at write time)
     float ea = 0.f, eb = 0.f, oa = 0.f, ob = 0.f;
     uint32_t base = 0, pending = 0;
+    bool ok = true;
     auto open_batch = [&]() {
         const uint32_t k = base + (uint32_t)lane;
         const bool mine = k < my_tiles;
@@ -259,8 +264,13 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
         vb = mine && t.valid[1];
         ea = eb = 0.f;
         if (mode == kGemvResid) {  // x = residual + proj (addInto, src/llm.zig:1389-1396)
-            if (va) ea = ld_a(g.o0 + ra);
-            if (vb) eb = ld_a(g.o0 + rb);
+            if (rs.bf16) {
+                if (va) ea = __uint_as_float((uint32_t)*as_global(rs.bf16 + ra) << 16);
+                if (vb) eb = __uint_as_float((uint32_t)*as_global(rs.bf16 + rb) << 16);
+            } else {
+                wa = va ? ld_a(rs.src + ra) : tw_make_u(0, rs.tag);
+                wb = vb ? ld_a(rs.src + rb) : tw_make_u(0, rs.tag);
+            }
         } else if (mode == kGemvPlain) {  // linearRange: dot + bias (src/llm.zig:1273)
             const uint16_t* bias = seg_bias(g, sa);
             if (bias && va) ea = __uint_as_float((uint32_t)*as_global(bias + ra) << 16);
@@ -270,17 +280,17 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
     auto flush = [&]() {
         if ((uint32_t)lane < pending) {
             if (mode == kGemvLogits) {
-                if (va) {
-                    if (ra == 0)
-                        st_a(g.o0, oa);  // read back by the argmax block (NaN rule)
-                    else
-                        *as_global(g.o0 + ra) = oa;
-                }
-                if (vb) *as_global(g.o0 + rb) = ob;
+                if (va) *as_global(g.plain + ra) = oa;
+                if (vb) *as_global(g.plain + rb) = ob;
             } else {
-                float* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
-                if (va) st_a(o + ra, oa + ea);
-                if (vb) st_a(o + rb, ob + eb);
+                if (mode == kGemvResid && !rs.bf16) {
+                    ok = ok && poll_tw(rs.src + ra, rs.tag, wa, err) && poll_tw(rs.src + rb, rs.tag, wb, err);
+                    ea = tw_val(wa);
+                    eb = tw_val(wb);
+                }
+                tword* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
+                if (va) st_a(o + ra, tw_make(oa + ea, tag));
+                if (vb) st_a(o + rb, tw_make(ob + eb, tag));
             }
         }
         pending = 0;
@@ -311,8 +321,11 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
             if (mode == kGemvGateUp) {
                 v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
             } else if (mode == kGemvLogits && lane == 0) {
+                // llm.argmax (src/llm.zig:778-789): a NaN logit 0 makes the
+                // result 0 (every comparison with it fails): top key, index 0.
                 if (tc.valid[0]) {
-                    const unsigned long long k0 = argmax_key(v0, tc.row[0]);
+                    const unsigned long long k0 =
+                        (tc.row[0] == 0 && v0 != v0) ? ~0ull : argmax_key(v0, tc.row[0]);
                     best = k0 > best ? k0 : best;
                 }
                 if (tc.valid[1]) {
@@ -333,60 +346,61 @@ __device__ __forceinline__ void mk_gemv(const MkGemv& g, int mode, const float* 
         }
     }
     flush();
+    return ok;
 }
 
 // ---------------------------------------------------------------------------
 // Input staging into LDS.
 // ---------------------------------------------------------------------------
 // xs[k] = src[k] (* norm_w[k] * s) with s = 1/sqrt(mean(src^2) + eps)
-// (rmsNormInto, src/llm.zig:1287-1300). src is an f32 activation read with
-// agent-scope loads, or (src_bf16) a bf16 embedding row (copyEmbeddingToken,
-// :1373-1380), which block 0 also publishes as the residual stream x_out.
-// The norm weights are loaded in the same batch as the activation (into
-// nws = xs + n), so the phase waits for one memory round trip, not two.
-__device__ __forceinline__ void mk_stage(float* xs, float* red, const float* src, const uint16_t* src_bf16,
-                                         float* x_out, const uint16_t* norm_w, float eps, uint32_t n) {
+// (rmsNormInto, src/llm.zig:1287-1300). src is a tagged activation of phase
+// `tag` (polled until every word carries it) or (src_bf16) a bf16 embedding
+// row (copyEmbeddingToken, :1373-1380). The norm weights are loaded in the
+// same batch as the activation (into nws = xs + n). False: a poll failed.
+__device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src, uint32_t tag,
+                                         const uint16_t* src_bf16, const uint16_t* norm_w, float eps, uint32_t n,
+                                         uint32_t* err) {
     const int tid = threadIdx.x;
-    constexpr int B = 8;  // 16-byte loads issued before any is consumed
+    constexpr int B = 8;  // word pairs issued before any is consumed
     float* nws = xs + n;
     float ss = 0.f;
+    bool ok = true;
     if (src_bf16) {
         for (uint32_t k = tid; k < n; k += kMkThreads) {
-            const float v = WeightTraits<uint16_t>::at(src_bf16, k);
+            const float v = __uint_as_float((uint32_t)*as_global(src_bf16 + k) << 16);
             xs[k] = v;
             if (norm_w) nws[k] = __uint_as_float((uint32_t)*as_global(norm_w + k) << 16);
             ss = fmaf(v, v, ss);
-            if (x_out) st_a(x_out + k, v);
         }
     } else {
-        const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * 4);
-        const uint32_t n4 = n / 4;
-        for (uint32_t i0 = tid; i0 < n4; i0 += B * kMkThreads) {
-            float4 v[B];
-            uint2 nv[B];
+        const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * 8);
+        const uint32_t n2 = n / 2;
+        for (uint32_t i0 = tid; i0 < n2; i0 += B * kMkThreads) {
+            tword a[B], b[B];
+            uint32_t nv[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const uint32_t i = i0 + b * kMkThreads;
-                v[b] = ld_coh4(r, i * 16);
-                nv[b] = (norm_w && i < n4) ? load_u32x2(norm_w + 4 * i) : make_uint2(0, 0);
+            for (int k = 0; k < B; ++k) {
+                const uint32_t i = i0 + k * kMkThreads;
+                ld_coh_tw2(r, i * 16, a[k], b[k]);
+                nv[k] = (norm_w && i < n2) ? *as_global(reinterpret_cast<const uint32_t*>(norm_w + 2 * i)) : 0u;
             }
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const uint32_t i = i0 + b * kMkThreads;
-                if (i < n4) {
-                    *reinterpret_cast<float4*>(xs + 4 * i) = v[b];
+            for (int k = 0; k < B; ++k) {
+                const uint32_t i = i0 + k * kMkThreads;
+                if (i < n2) {
+                    ok = ok && poll_tw(src + 2 * i, tag, a[k], err) && poll_tw(src + 2 * i + 1, tag, b[k], err);
+                    const float v0 = tw_val(a[k]), v1 = tw_val(b[k]);
+                    *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(v0, v1);
                     if (norm_w)
-                        *reinterpret_cast<float4*>(nws + 4 * i) =
-                            make_float4(__uint_as_float(nv[b].x << 16), __uint_as_float(nv[b].x & 0xffff0000u),
-                                        __uint_as_float(nv[b].y << 16), __uint_as_float(nv[b].y & 0xffff0000u));
-                    ss = fmaf(v[b].x, v[b].x, ss);
-                    ss = fmaf(v[b].y, v[b].y, ss);
-                    ss = fmaf(v[b].z, v[b].z, ss);
-                    ss = fmaf(v[b].w, v[b].w, ss);
+                        *reinterpret_cast<float2*>(nws + 2 * i) =
+                            make_float2(__uint_as_float(nv[k] << 16), __uint_as_float(nv[k] & 0xffff0000u));
+                    ss = fmaf(v0, v0, ss);
+                    ss = fmaf(v1, v1, ss);
                 }
             }
         }
     }
+    if (__syncthreads_or(!ok)) return false;
     if (norm_w) {
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -396,22 +410,18 @@ __device__ __forceinline__ void mk_stage(float* xs, float* red, const float* src
         for (int i = 0; i < kMkWaves; ++i) total += red[i];
         const float scale = 1.0f / sqrtf(total / (float)n + eps);
         for (uint32_t k = tid; k < n; k += kMkThreads) xs[k] = xs[k] * nws[k] * scale;
+        __syncthreads();
     }
-    __syncthreads();
+    return true;
 }
 
 // ---------------------------------------------------------------------------
 // Attention phase: units (kv head h, split s) over blocks.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void rope_rot(const float* src, float* dst, int f, int sc, float c, float s) {
-    const float x0 = src[f], x1 = src[sc];
-    dst[f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-    dst[sc] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
-}
-
 // LDS layout of the attention phase (floats): q [16][HDMAX], K tile
 // [TILE][HDMAX+4] (16-byte aligned rows), V tile [TILE][HDMAX], probabilities
-// [16][TILE], new k / v rows, running max / sum / correction per q head.
+// [16][TILE] (also the split merge weights), new k / v rows, running max /
+// sum / correction per q head, split (m, l) for the merge.
 template <int HDMAX>
 struct AttnLds {
     static constexpr int TILE = 4096 / HDMAX;  // 64 rows at hd 64, 32 at hd 128
@@ -425,24 +435,30 @@ struct AttnLds {
     static constexpr int kM = kVnew + HDMAX;
     static constexpr int kL = kM + kMaxGroupMk;
     static constexpr int kC = kL + kMaxGroupMk;
-    static constexpr int kTotal = kC + kMaxGroupMk;
+    static constexpr int kPm = kC + kMaxGroupMk;
+    static constexpr int kPl = kPm + kMaxSplitMk * kMaxGroupMk;
+    static constexpr int kTotal = kPl + kMaxSplitMk * kMaxGroupMk;
 };
 
-// One (kv head, split) unit per block iteration: RoPE of q and of the new k
-// (applyRoPE, src/llm.zig:1337-1371), K/V append at pos (:744-745), and an
-// online-softmax pass over the split's positions for the `group` q heads
-// sharing the kv head (computeAttentionInto, :1302-1335). Partials (m, l,
-// acc) are merged by the split that finishes last into p.attn. EXACT: hd == HDMAX (loops
-// fully unrolled), else hd <= HDMAX at run time.
+// One (kv head, split) unit per block: RoPE of q and of the new k (applyRoPE,
+// src/llm.zig:1337-1371), K/V append at pos (:744-745), and an online-softmax
+// pass over the split's positions for the `group` q heads sharing the kv head
+// (computeAttentionInto, :1302-1335). The split holding pos (always the last)
+// merges the others' partials (m, l, acc) into the attention output
+// (flash-decoding: out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s).
+// The K/V rows of the first tile are loaded before q is waited for. EXACT:
+// hd == HDMAX (loops fully unrolled), else hd <= HDMAX at run time.
 template <int HDMAX, bool EXACT>
-__device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t layer, uint32_t pos, uint32_t chunk,
-                                          uint32_t ns, float* smem) {
+__device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t layer, uint32_t pos, uint32_t chunk,
+                                             uint32_t ns, float* smem, uint32_t tag_in, uint32_t tag_out) {
     using LY = AttnLds<HDMAX>;
     constexpr int TILE = LY::TILE, KS = LY::KS;
     constexpr int NP = (kMaxGroupMk * HDMAX + kMkThreads - 1) / kMkThreads;
+    constexpr int NT = (TILE * HDMAX / 4 + kMkThreads - 1) / kMkThreads;  // float4 of a K (V) tile per thread
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hd = EXACT ? HDMAX : (int)p.hd;
     const int half = hd / 2;
+    const int vpr = hd / 4;
     const int G = (int)(p.heads / p.kv_heads);
     const uint32_t kvw = p.kvdim;
     float* qs = smem + LY::kQ;
@@ -454,23 +470,63 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
     float* m_s = smem + LY::kM;
     float* l_s = smem + LY::kL;
     float* c_s = smem + LY::kC;
+    float* pm = smem + LY::kPm;
+    float* pl = smem + LY::kPl;
     const float* cs = p.rope_cs + (size_t)pos * hd;
     float* kc = p.kcache + (size_t)layer * p.max_seq * kvw;
     float* vc = p.vcache + (size_t)layer * p.max_seq * kvw;
-    const float* q = p.qkv;
-    const float* kn_all = p.qkv + p.heads * p.hd;
-    const float* vn_all = kn_all + kvw;
+    const __amdgpu_buffer_rsrc_t kr = coh_rsrc(kc, pos * kvw * 4u);  // rows [0, pos)
+    const __amdgpu_buffer_rsrc_t vr = coh_rsrc(vc, pos * kvw * 4u);
+    const tword* q = p.tqkv;
+    const tword* kn_all = p.tqkv + p.heads * p.hd;
+    const tword* vn_all = kn_all + kvw;
     const bool inter = p.rope_layout == 0;
+    bool ok = true;
 
     for (uint32_t unit = blockIdx.x; unit < p.kv_heads * ns; unit += gridDim.x) {
         const uint32_t h = unit / ns, s = unit - h * ns;
         const uint32_t t0 = s * chunk, t1 = min(t0 + chunk, pos + 1);
-        const bool owns = pos >= t0 && pos < t1;
+        const bool owns = s == ns - 1;  // the last split ends at pos
+        // K/V rows of a tile travel through registers (rk, rv) so the next
+        // tile's loads are in flight while the current one is computed. They
+        // are loaded coherently: a row written in this launch may share a
+        // cache line with one read earlier by another XCD. (Rows outside the
+        // tile and the new row, taken from LDS, load as zeros: out of range.)
+        float4 rk[NT], rv[NT];
+#define VVLI_TILE_LOAD(ta_, tlen_)                                                    \
+    _Pragma("unroll") for (int i = 0; i < NT; ++i) {                                  \
+        const int idx = tid + i * kMkThreads;                                         \
+        const int j = idx / vpr, c4 = (idx - j * vpr) * 4;                            \
+        const uint32_t t = (ta_) + j;                                                 \
+        const bool in = idx < (tlen_) * vpr && t != pos;                              \
+        const uint32_t off = in ? (t * kvw + (uint32_t)h * hd + c4) * 4u : 0xffffffffu; \
+        rk[i] = ld_coh4(kr, off);                                                     \
+        rv[i] = ld_coh4(vr, off);                                                     \
+    }
+#define VVLI_TILE_STORE(ta_, tlen_)                                                   \
+    _Pragma("unroll") for (int i = 0; i < NT; ++i) {                                  \
+        const int idx = tid + i * kMkThreads;                                         \
+        if (idx < (tlen_) * vpr) {                                                    \
+            const int j = idx / vpr, c4 = (idx - j * vpr) * 4;                        \
+            float4* kd = reinterpret_cast<float4*>(ks + j * KS + c4);                 \
+            float4* vd = reinterpret_cast<float4*>(vs + j * HDMAX + c4);              \
+            *kd = rk[i];                                                              \
+            *vd = rv[i];                                                              \
+            if ((ta_) + j == pos) { /* the new row comes from LDS, not the cache */  \
+                *kd = *reinterpret_cast<const float4*>(knew + c4);                    \
+                *vd = *reinterpret_cast<const float4*>(vnew + c4);                    \
+            }                                                                         \
+        }                                                                             \
+    }
+        VVLI_TILE_LOAD(t0, (int)min((uint32_t)TILE, t1 - t0));
+        // q (and the owner's new k / v) of this kv head, RoPE'd into LDS.
         for (int idx = tid; idx < G * half; idx += kMkThreads) {
             const int g = idx / half, i = idx - g * half;
             const int f = inter ? 2 * i : i, sc = inter ? 2 * i + 1 : i + half;
-            const float* src = q + (size_t)(h * G + g) * hd;
-            const float x0 = ld_a(src + f), x1 = ld_a(src + sc);
+            const tword* src = q + (size_t)(h * G + g) * hd;
+            tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
+            ok = ok && poll_tw(src + f, tag_in, w0, p.error) && poll_tw(src + sc, tag_in, w1, p.error);
+            const float x0 = tw_val(w0), x1 = tw_val(w1);
             const float c = cs[2 * i], sn = cs[2 * i + 1];
             qs[g * HDMAX + f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
             qs[g * HDMAX + sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
@@ -478,18 +534,26 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
         if (owns) {
             for (int i = tid; i < half; i += kMkThreads) {
                 const int f = inter ? 2 * i : i, sc = inter ? 2 * i + 1 : i + half;
-                const float x0 = ld_a(kn_all + (size_t)h * hd + f), x1 = ld_a(kn_all + (size_t)h * hd + sc);
+                const tword* src = kn_all + (size_t)h * hd;
+                tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
+                ok = ok && poll_tw(src + f, tag_in, w0, p.error) && poll_tw(src + sc, tag_in, w1, p.error);
+                const float x0 = tw_val(w0), x1 = tw_val(w1);
                 const float c = cs[2 * i], sn = cs[2 * i + 1];
                 knew[f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
                 knew[sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
             }
-            for (int d = tid; d < hd; d += kMkThreads) vnew[d] = ld_a(vn_all + (size_t)h * hd + d);
+            for (int d = tid; d < hd; d += kMkThreads) {
+                const tword* src = vn_all + (size_t)h * hd + d;
+                tword wv = ld_a(src);
+                ok = ok && poll_tw(src, tag_in, wv, p.error);
+                vnew[d] = tw_val(wv);
+            }
         }
         if (tid < kMaxGroupMk) {
             m_s[tid] = -INFINITY;
             l_s[tid] = 0.f;
         }
-        __syncthreads();
+        if (__syncthreads_or(!ok)) return false;
         if (owns) {
             for (int d = tid; d < hd; d += kMkThreads) {
                 st_a(kc + (size_t)pos * kvw + (size_t)h * hd + d, knew[d]);
@@ -501,21 +565,9 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
         for (int i = 0; i < NP; ++i) acc[i] = 0.f;
         for (uint32_t ta = t0; ta < t1; ta += TILE) {
             const int tlen = (int)min((uint32_t)TILE, t1 - ta);
-            const int vpr = hd / 4;
-            for (int idx = tid; idx < tlen * vpr; idx += kMkThreads) {
-                const int j = idx / vpr, c4 = (idx - j * vpr) * 4;
-                const uint32_t t = ta + j;
-                float4 k4, v4;
-                if (t == pos) {
-                    k4 = *reinterpret_cast<const float4*>(knew + c4);
-                    v4 = *reinterpret_cast<const float4*>(vnew + c4);
-                } else {
-                    const size_t off = (size_t)t * kvw + (size_t)h * hd + c4;
-                    k4 = load_f32x4(kc + off);
-                    v4 = load_f32x4(vc + off);
-                }
-                *reinterpret_cast<float4*>(ks + j * KS + c4) = k4;
-                *reinterpret_cast<float4*>(vs + j * HDMAX + c4) = v4;
+            VVLI_TILE_STORE(ta, tlen);
+            if (ta + TILE < t1) {
+                VVLI_TILE_LOAD(ta + TILE, (int)min((uint32_t)TILE, t1 - ta - TILE));
             }
             __syncthreads();
             // scores s[g][j] = (q_g . K_j) * scale, four independent chains
@@ -587,74 +639,77 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
             }
             __syncthreads();
         }
-        // Partials of this split: (m, l) per q head and the unnormalised output.
-        float* pml = p.part_ml + ((size_t)h * p.nsplit + s) * G * 2;
-        float* pacc = p.part_acc + ((size_t)h * p.nsplit + s) * G * hd;
+        const size_t pbase = (size_t)h * p.nsplit;
+        if (!owns) {
+            // Partials of this split: (m, l) per q head and the unnormalised output.
+            tword* pml = p.tpart_ml + (pbase + s) * G * 2;
+            tword* pacc = p.tpart_acc + (pbase + s) * G * hd;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int idx = tid + i * kMkThreads;
+                if (idx < G * hd) st_a(pacc + idx, tw_make(acc[i], tag_out));  // idx = g * hd + d
+            }
+            if (tid < G) {
+                st_a(pml + 2 * tid, tw_make(m_s[tid], tag_out));
+                st_a(pml + 2 * tid + 1, tw_make(l_s[tid], tag_out));
+            }
+            continue;
+        }
+        // Owner: merge weights from every split's (m, l), own split last.
+        if (tid < (int)(ns - 1) * G) {
+            const tword* src = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
+            tword wm = ld_a(src), wl = ld_a(src + 1);
+            ok = ok && poll_tw(src, tag_out, wm, p.error) && poll_tw(src + 1, tag_out, wl, p.error);
+            pm[tid] = tw_val(wm);
+            pl[tid] = tw_val(wl);
+        }
+        if (tid < G) {
+            pm[(ns - 1) * G + tid] = m_s[tid];
+            pl[(ns - 1) * G + tid] = l_s[tid];
+        }
+        if (__syncthreads_or(!ok)) return false;
+        float* wsp = ps;  // [split][group] merge weights
+        for (int g = wave; g < G; g += kMkWaves) {
+            const bool in = (uint32_t)lane < ns;
+            const float mv = in ? pm[lane * G + g] : -INFINITY;
+            const float lv = in ? pl[lane * G + g] : 0.f;
+            const float M = wave_max(mv);
+            const float e = in ? expf(mv - M) : 0.f;
+            const float L = wave_sum(lv * e);
+            if (in) wsp[lane * G + g] = e / L;
+        }
+        wait_all_mem();  // the K/V row stores (wave 0) land before any wave publishes the output
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             const int idx = tid + i * kMkThreads;
-            if (idx < G * hd) st_a(pacc + idx, acc[i]);  // idx = g * hd + d
-        }
-        if (tid < G) {
-            st_a(pml + 2 * tid, m_s[tid]);
-            st_a(pml + 2 * tid + 1, l_s[tid]);
-        }
-        // The last split of kv head h to finish merges all of them (flash-
-        // decoding merge): out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s.
-        wait_all_mem();
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(p.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *reinterpret_cast<uint32_t*>(m_s) = prev == ns - 1 ? 1u : 0u;  // m_s[0] is free now
-        }
-        __syncthreads();
-        const bool last = *reinterpret_cast<uint32_t*>(m_s) != 0;
-        __syncthreads();
-        if (last) {
-            float* wsp = ps;  // [split][group] merge weights
-            for (int g = wave; g < G; g += kMkWaves) {
-                float mv = -INFINITY, lv = 0.f;
-                if ((uint32_t)lane < ns) {
-                    const float* q2 = p.part_ml + (((size_t)h * p.nsplit + lane) * G + g) * 2;
-                    mv = ld_a(q2);
-                    lv = ld_a(q2 + 1);
-                }
-                const float M = wave_max(mv);
-                const float e = (uint32_t)lane < ns ? expf(mv - M) : 0.f;
-                const float L = wave_sum(lv * e);
-                if ((uint32_t)lane < ns) wsp[lane * G + g] = e / L;
-            }
-            __syncthreads();
-            const __amdgpu_buffer_rsrc_t r = coh_rsrc(p.part_acc + (size_t)h * p.nsplit * G * hd, ns * G * hd * 4);
-            const int n4 = G * hd / 4;
-            for (int i4 = tid; i4 < n4; i4 += kMkThreads) {
-                const int g = (4 * i4) / hd;
-                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-                for (uint32_t s0 = 0; s0 < ns; s0 += 8) {
-                    float4 v[8];
+            if (idx < G * hd) {
+                const int g = idx / hd;
+                const tword* src = p.tpart_acc + pbase * G * hd + idx;
+                constexpr int SB = 4;  // split partials loaded per batch
+                float o = 0.f;
+                for (int s0 = 0; s0 < (int)ns - 1; s0 += SB) {
+                    tword wv[SB];
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) v[b] = ld_coh4(r, ((s0 + b) * G * hd + 4 * i4) * 4);
+                    for (int b = 0; b < SB; ++b)
+                        if (s0 + b < (int)ns - 1) wv[b] = ld_a(src + (size_t)(s0 + b) * G * hd);
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) {
-                        if (s0 + b < ns) {
-                            const float w = wsp[(s0 + b) * G + g];
-                            o.x = fmaf(v[b].x, w, o.x);
-                            o.y = fmaf(v[b].y, w, o.y);
-                            o.z = fmaf(v[b].z, w, o.z);
-                            o.w = fmaf(v[b].w, w, o.w);
+                    for (int b = 0; b < SB; ++b) {
+                        if (s0 + b < (int)ns - 1) {
+                            ok = ok && poll_tw(src + (size_t)(s0 + b) * G * hd, tag_out, wv[b], p.error);
+                            o = fmaf(tw_val(wv[b]), wsp[(s0 + b) * G + g], o);
                         }
                     }
                 }
-                float* dst = p.attn + (size_t)h * G * hd + 4 * i4;
-                st_a(dst, o.x);
-                st_a(dst + 1, o.y);
-                st_a(dst + 2, o.z);
-                st_a(dst + 3, o.w);
+                o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
+                st_a(p.tattn + (size_t)h * G * hd + idx, tw_make(o, tag_out));
             }
-            if (tid == 0) st_a(p.counters + h, 0u);
         }
-        __syncthreads();
+        if (__syncthreads_or(!ok)) return false;
     }
+    return true;
+#undef VVLI_TILE_LOAD
+#undef VVLI_TILE_STORE
 }
 
 // ---------------------------------------------------------------------------
@@ -662,9 +717,10 @@ __device__ __forceinline__ void mk_attention(const DecodeStepParams& p, uint32_t
 // ---------------------------------------------------------------------------
 // Phases of one token step: per layer Q (input RMSNorm + q/k/v), A (RoPE, KV
 // append, attention), O (x += Wo.attn), G (post-attention RMSNorm, gate/up,
-// SwiGLU), D (x += Wd.ff); then the logits phase (final RMSNorm + lm_head).
-// All GEMV phases run through one code path with a grid-uniform mode, so the
-// whole step loop stays small enough for the instruction cache.
+// SwiGLU), D (x += Wd.ff); then the logits phase (final RMSNorm + lm_head) and
+// the argmax (block 0), which publishes the next token. All GEMV phases run
+// through one code path with a grid-uniform mode, so the whole step loop
+// stays small enough for the instruction cache.
 enum : uint32_t { kPhQ = 0, kPhA = 1, kPhO = 2, kPhG = 3, kPhD = 4, kPhPerLayer = 5 };
 
 struct MkPhase {
@@ -690,7 +746,7 @@ __device__ __forceinline__ int mk_mode(const MkPhase& f) {
 // caches every phase (the weight stream evicts them) and put a memory round
 // trip in front of every phase.
 struct MkTables {
-    const MkGemv* gemv;         // [layers * 4 + 1]
+    const MkGemv* gemv;           // [layers * 4 + 1]
     const uint16_t* const* norm;  // [layers * 2]: input, post-attention
 };
 
@@ -717,38 +773,49 @@ __device__ __forceinline__ const uint16_t* mk_norm_of(const DecodeStepParams& p,
 template <int HDMAX, bool EXACT>
 __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParams p) {
     extern __shared__ float smem[];
-    __shared__ int s_ok;
-    __shared__ uint32_t s_gen;
     __shared__ float red[kMkWaves];
+    __shared__ unsigned long long kred[kMkWaves];
     __shared__ uint32_t s_ctl[4];
     const int tid = threadIdx.x;
     MkWave w;
     w.lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
     // Tile t goes to wave (t mod blocks) of ... so consecutive tiles land on
     // different CUs and a phase with fewer tiles than waves still uses them all.
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
     w.wid = wave * gridDim.x + blockIdx.x;
     w.wid_c = blockIdx.x * kMkWaves + wave;
     w.nw = gridDim.x * kMkWaves;
-    if (tid == 0) s_gen = 0;
     uint4 buf[2][kNJC];
     MkTile tile;
     unsigned long long best = 0ull;
     const uint32_t H = p.hidden;
+    const uint32_t nps = kPhPerLayer * p.layers + 2;  // phases per step: layers, logits, argmax
+    const uint32_t logits_ph = kPhPerLayer * p.layers;
     if (p.timing && tid == 0 && blockIdx.x == 0)
-        p.timing[(size_t)gridDim.x * p.timing_stride + p.timing_slots - 1] = __builtin_amdgcn_s_memrealtime();
-    const uint32_t nph = kPhPerLayer * p.layers + 1;
+        p.timing[(size_t)gridDim.x * p.timing_stride] = __builtin_amdgcn_s_memrealtime();
     const MkTables tb = mk_load_tables(p, reinterpret_cast<char*>(smem) + p.table_lds_offset);
+    if (tid == 0) {
+        s_ctl[0] = ld_a(&p.state->token);
+        s_ctl[1] = ld_a(&p.state->pos);
+    }
+    __syncthreads();
+    uint32_t token = s_ctl[0];
+    const uint32_t pos0 = s_ctl[1];
+    bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
 
     for (uint32_t step = 0; step < p.n_steps; ++step) {
-        // Step state (written by block 0 in the previous step's argmax phase).
-        if (tid == 0) {
-            s_ctl[0] = ld_a(&p.state->token);
-            s_ctl[1] = ld_a(&p.state->pos);
+        const uint32_t e0 = p.epoch0 + step * nps;  // epoch of this step's phase 0
+        const uint32_t pos = pos0 + step;
+        if (step > 0) {  // next token from the previous step's argmax
+            __syncthreads();
+            if (tid == 0) {
+                tword wv = ld_a(p.step_word);
+                s_ctl[2] = poll_tw(p.step_word, e0 - 1, wv, p.error) ? (uint32_t)wv : 0xfffffffeu;
+            }
+            __syncthreads();
+            token = s_ctl[2];
+            if (token >= 0xfffffffeu) break;  // stop (EOS / context full) or error
         }
-        __syncthreads();
-        const uint32_t token = s_ctl[0], pos = s_ctl[1];
-        __syncthreads();
         if (pos >= p.max_seq || token >= p.vocab) {  // host validated; defensive stop
             if (blockIdx.x == 0 && tid == 0) st_a(p.error, 2u);
             return;
@@ -757,49 +824,67 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
         uint32_t chunk = (T + p.nsplit - 1) / p.nsplit;
         if (chunk < p.min_chunk) chunk = p.min_chunk;
         const uint32_t ns = (T + chunk - 1) / chunk;
-        bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
+        const uint16_t* emb = p.embed + (size_t)token * H;
 
-        for (uint32_t ph = 0; ph < nph; ++ph) {
+        for (uint32_t ph = 0; ph <= logits_ph; ++ph) {
             const MkPhase f = mk_phase(ph, p.layers);
+            const uint32_t tag = e0 + ph;
+            bool ok = true;
             if (f.kind == kPhA && !f.logits) {
-                mk_attention<HDMAX, EXACT>(p, f.layer, pos, chunk, ns, smem);
+                ok = mk_attention<HDMAX, EXACT>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag);
             } else {
-                const uint16_t* norm = mk_norm_of(p, tb, f);
-                const float* src = f.kind == kPhO ? p.attn : (f.kind == kPhD ? p.ff : p.x);
-                // Layer 0 reads the embedding row straight from the blob; block 0
-                // publishes it as the residual stream, first read two barriers on.
-                mk_stage(smem, red, src, ph == 0 ? p.embed + (size_t)token * H : nullptr,
-                         (ph == 0 && blockIdx.x == 0) ? p.x : nullptr, norm, p.eps, f.kind == kPhD ? p.inter : H);
-                if (tid == 0) mk_mark(p, s_gen, 1);
+                const MkGemv& g = mk_gemv_of(p, tb, f);
+                const int mode = mk_mode(f);
                 if (f.logits) best = 0ull;
-                mk_gemv(mk_gemv_of(p, tb, f), mk_mode(f), smem, w, buf, tile, have, best);
-                if (f.logits && w.lane == 0) st_a(p.keys + w.wid, best);
+                if (blockIdx.x < mk_tiles(g, mode)) {  // the block has tiles: stage the input
+                    const tword* src = f.kind == kPhO ? p.tattn
+                                                      : (f.kind == kPhD ? p.tff : (f.kind == kPhG ? p.tx + H : p.tx));
+                    ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
+                                  f.kind == kPhD ? p.inter : H, p.error);
+                    if (tid == 0) mk_mark(p, ph, 0);
+                    // Residual rows: O reads x of the previous layer's D (or the
+                    // embedding), D reads x of this layer's O.
+                    MkResid rs;
+                    rs.src = f.kind == kPhO ? p.tx : p.tx + H;
+                    rs.tag = f.kind == kPhO ? tag - 3 : tag - 2;
+                    rs.bf16 = (f.kind == kPhO && f.layer == 0) ? emb : nullptr;
+                    ok = ok && mk_gemv(g, mode, smem, w, buf, tile, have, best, tag, rs, p.error);
+                }
+                if (f.logits && w.lane == 0) {
+                    st_a(p.tkeys + 2 * w.wid, tw_make_u((uint32_t)(best >> 32), tag));
+                    st_a(p.tkeys + 2 * w.wid + 1, tw_make_u((uint32_t)best, tag));
+                }
             }
-            if (w.lane == 0) mk_mark(p, s_gen, 2 + (tid >> 6));
-            wait_all_mem();
-            // Issue the first weights of the next GEMV phase before the barrier.
-            if (ph + 1 < nph) {
+            if (w.lane == 0) mk_mark(p, ph, 1 + (int)wave);
+            if (__syncthreads_or(!ok)) return;
+            // Issue the first weights of the next GEMV phase (the next step's
+            // first phase after the logits) before waiting for its input.
+            if (ph < logits_ph) {
                 const MkPhase nf = mk_phase(ph + 1, p.layers);
                 if (nf.kind != kPhA || nf.logits) have = mk_prefetch(mk_gemv_of(p, tb, nf), mk_mode(nf), w, buf, tile);
+            } else if (step + 1 < p.n_steps) {
+                have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
         }
 
         // ---- argmax + step advance (block 0) ----
         if (blockIdx.x == 0) {
-            __shared__ unsigned long long kred[kMkWaves];
+            const uint32_t ktag = e0 + logits_ph;
             unsigned long long b = 0ull;
+            bool ok = true;
             for (uint32_t i = tid; i < w.nw; i += kMkThreads) {
-                const unsigned long long k = ld_a(p.keys + i);
+                tword hi = ld_a(p.tkeys + 2 * i), lo = ld_a(p.tkeys + 2 * i + 1);
+                ok = ok && poll_tw(p.tkeys + 2 * i, ktag, hi, p.error) &&
+                     poll_tw(p.tkeys + 2 * i + 1, ktag, lo, p.error);
+                const unsigned long long k = ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
                 b = k > b ? k : b;
             }
             b = wave_max_u64(b);
             if (w.lane == 0) kred[tid >> 6] = b;
-            __syncthreads();
+            if (__syncthreads_or(!ok)) return;
             if (tid == 0) {
                 for (int i = 0; i < kMkWaves; ++i) b = kred[i] > b ? kred[i] : b;
-                const float l0 = ld_a(p.logits);
-                const uint32_t tok = (l0 != l0) ? 0u : argmax_key_index(b);  // llm.argmax, src/llm.zig:778-789
+                const uint32_t tok = argmax_key_index(b);  // llm.argmax, src/llm.zig:778-789
                 const uint32_t next_pos = pos + 1;
                 const uint32_t prompt_len = ld_a(&p.state->prompt_len);
                 uint32_t next_tok = tok, stop = 0;
@@ -816,14 +901,8 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 st_a(&p.state->token, next_tok);
                 st_a(&p.state->pos, next_pos);
                 st_a(&p.state->stop, stop);
+                if (step + 1 < p.n_steps) st_a(p.step_word, tw_make_u(stop ? 0xffffffffu : next_tok, e0 + nps - 1));
             }
-        }
-        if (step + 1 < p.n_steps) {
-            wait_all_mem();
-            if (!mk_barrier(p, &s_gen, &s_ok)) return;
-            if (tid == 0) s_ctl[2] = ld_a(&p.state->stop);
-            __syncthreads();
-            if (s_ctl[2]) return;
         }
     }
 }
@@ -842,6 +921,8 @@ size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, u
     return decode_step_table_offset(hidden, inter, hd) + (size_t)(layers * 4 + 1) * sizeof(DecodeGemv) +
            (size_t)layers * 2 * sizeof(const uint16_t*);
 }
+
+uint32_t decode_step_phases_per_step(uint32_t layers) { return kPhPerLayer * layers + 2; }
 
 static const void* decode_step_fn(uint32_t hd) {
     if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true>);

@@ -126,18 +126,20 @@ struct DecodeLayer {
 
 // One GEMV phase of the persistent step: up to three stacked row segments
 // (q | k | v; each of an even row count) or a gate and an up matrix. Built by
-// the host in device memory, so the kernel reads it with scalar loads instead
-// of keeping a local copy (a run-time segment index into a local struct puts
-// it in scratch memory).
+// the host in device memory; the kernel copies the table into LDS.
 struct DecodeGemv {
     const uint16_t *w0, *w1, *w2;
     const uint16_t *b0, *b1, *b2;
-    float *o0, *o1, *o2;
+    unsigned long long *o0, *o1, *o2;  // tagged outputs per segment (value bits | epoch << 32)
+    float* plain;                      // logits phase: plain f32 outputs
     uint32_t r0, r1, r2;
     const uint16_t* w_up;
     uint32_t K;
 };
 
+// Activations of the persistent step are arrays of tagged 64-bit words: the
+// f32 value (or u32) in the low half, the epoch of the phase that wrote it in
+// the high half.
 struct DecodeStepParams {
     uint32_t vocab, hidden, inter, layers, heads, kv_heads, hd, kvdim, rope_layout, max_seq;
     float eps, scale;
@@ -149,31 +151,28 @@ struct DecodeStepParams {
     float* kcache;
     float* vcache;
     const float* rope_cs;
-    float* x;       // residual stream [hidden]
-    float* qkv;     // q | k | v
-    float* ff;      // [inter]
-    float* logits;  // [vocab]
-    float* part_ml;   // attention partials: (max, sum) [kv_heads][nsplit][group][2]
-    float* part_acc;  // attention partials: unnormalised out [kv_heads][nsplit][group][hd]
-    uint32_t* counters;  // [kv_heads] merge tickets, zero between phases
-    float* attn;      // merged attention output [heads * hd]
-    unsigned long long* keys;  // one argmax key per wave
+    unsigned long long* tx;         // residual stream: [2][hidden] (layer input | after attention)
+    unsigned long long* tqkv;       // q | k | v
+    unsigned long long* tattn;      // merged attention output [heads * hd]
+    unsigned long long* tff;        // [inter]
+    unsigned long long* tpart_ml;   // attention partials: (max, sum) [kv_heads][nsplit][group][2]
+    unsigned long long* tpart_acc;  // attention partials: unnormalised out [kv_heads][nsplit][group][hd]
+    unsigned long long* tkeys;      // argmax key of every wave: [waves][2] (high, low half)
+    unsigned long long* step_word;  // next token (0xffffffff: stop) published by the argmax
+    float* logits;                  // [vocab]
     StepState* state;
     const uint32_t* prompt;
     uint32_t* out_tokens;
     uint32_t out_cap;
-    uint32_t* flags;    // [blocks * 32] barrier generations
-    uint32_t* release;  // barrier release word
-    uint32_t* error;    // non-zero: a barrier timed out (all blocks leave)
+    uint32_t* error;  // non-zero: a poll timed out (all blocks leave)
+    uint32_t epoch0;  // epoch of the first phase of this launch (>= 1)
     uint32_t nsplit, min_chunk;
     uint32_t n_steps;
     int64_t eos;  // < 0: none
-    // Optional phase timing (100 MHz s_memrealtime ticks), timing_slots
-    // entries per barrier k: block b's arrival at barrier k in
-    // timing[b * timing_stride + k * slots + slots - 1], block 0's release of
-    // barrier k in timing[gridDim * timing_stride + k * slots + slots - 1];
-    // k = 0 is the start. With 16 slots, slot 0 is the release seen by the
-    // block, 1 its staged input, 2 + w wave w's last result of the phase.
+    // Optional phase timing (100 MHz s_memrealtime ticks): kernel start in
+    // timing[gridDim * timing_stride]; with timing_slots = 16, phase k of the
+    // first step writes block b's staged input at timing[b * timing_stride +
+    // k * 16] and wave w's end of the phase at [... + 1 + w].
     unsigned long long* timing;
     uint32_t timing_stride;
     uint32_t timing_slots;
@@ -182,6 +181,7 @@ struct DecodeStepParams {
 
 size_t decode_step_table_offset(uint32_t hidden, uint32_t inter, uint32_t hd);
 size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, uint32_t hd);
+uint32_t decode_step_phases_per_step(uint32_t layers);
 hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu);
 hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s);
 

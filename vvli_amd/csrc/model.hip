@@ -61,9 +61,10 @@ struct vvli_gpu_model {
     uint32_t mk_nsplit = 1;
     DecodeLayer* mk_layers = nullptr;
     DecodeGemv* mk_gemv = nullptr;  // [layers * 4 + 1] phase descriptors
-    float* mk_part = nullptr;       // persistent attention partials: (m, l) block then acc block
-    uint32_t* mk_sync = nullptr;  // flags [blocks*32] | release [32] | error [32]
-    size_t mk_sync_words = 0;
+    unsigned long long* mk_tw = nullptr;  // tagged activations (DecodeStepParams tx .. step_word)
+    size_t mk_tw_words = 0;
+    uint32_t* mk_err = nullptr;           // device error word
+    uint32_t mk_epoch = 1;                // epoch of the next launch's first phase
     uint32_t* h_err = nullptr;    // pinned
     bool mk_pending = false;      // a persistent launch ran since the last error check
 };
@@ -259,13 +260,46 @@ int ensure_graph(vvli_gpu_model* m) {
     return VVLI_OK;
 }
 
-// Auto picks the per-kernel graph: on the Llama-3.2-1B decode benchmark it
-// currently measures faster than the persistent step (926 vs 872 tok/s).
-bool use_persistent(const vvli_gpu_model* m) { return m->mk_ok && m->path == 2; }
+// Auto picks the persistent step where it is available (bf16 weights): on the
+// Llama-3.2-1B decode benchmark it measures 1178 tok/s against the per-kernel
+// graph's 921.
+bool use_persistent(const vvli_gpu_model* m) { return m->mk_ok && m->path != 1; }
+
+// Offsets (in words) of the tagged activation arrays inside mk_tw.
+struct TaggedLayout {
+    size_t tx, tqkv, tattn, tff, ml, acc, keys, step, total;
+};
+TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t blocks) {
+    const size_t H = c.hidden, kv = kv_dim(c), G = c.heads / c.kv_heads, hd = head_dim(c);
+    TaggedLayout t{};
+    size_t cur = 0;
+    auto take = [&](size_t n) {
+        const size_t at = cur;
+        cur += (n + 15) / 16 * 16;  // 128-byte aligned arrays
+        return at;
+    };
+    t.tx = take(2 * H);
+    t.tqkv = take(H + 2 * kv);
+    t.tattn = take(H);
+    t.tff = take(c.inter);
+    t.ml = take(static_cast<size_t>(c.kv_heads) * nsplit * G * 2);
+    t.acc = take(static_cast<size_t>(c.kv_heads) * nsplit * G * hd);
+    t.keys = take(static_cast<size_t>(blocks) * 8 * 2);
+    t.step = take(1);
+    t.total = cur;
+    return t;
+}
 
 int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned long long* timing = nullptr,
                    uint32_t timing_stride = 0) {
     const vvli_gpu_config& c = m->cfg;
+    // Epochs only grow; before they would wrap, clear every tag (stale words
+    // then carry epoch 0, which no phase uses).
+    const uint64_t need = static_cast<uint64_t>(n_steps) * decode_step_phases_per_step(c.layers) + 1;
+    if (static_cast<uint64_t>(m->mk_epoch) + need >= 0xffffffffull) {
+        HIP_TRY(hipMemsetAsync(m->mk_tw, 0, m->mk_tw_words * sizeof(unsigned long long), m->stream));
+        m->mk_epoch = 1;
+    }
     DecodeStepParams p{};
     p.vocab = c.vocab;
     p.hidden = c.hidden;
@@ -287,32 +321,32 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.kcache = m->kcache;
     p.vcache = m->vcache;
     p.rope_cs = m->rope_cs;
-    p.x = m->x;
-    p.qkv = m->qkv;
-    p.ff = m->ff;
+    const TaggedLayout tl = tagged_layout(c, m->mk_nsplit, m->mk_blocks);
+    p.tx = m->mk_tw + tl.tx;
+    p.tqkv = m->mk_tw + tl.tqkv;
+    p.tattn = m->mk_tw + tl.tattn;
+    p.tff = m->mk_tw + tl.tff;
+    p.tpart_ml = m->mk_tw + tl.ml;
+    p.tpart_acc = m->mk_tw + tl.acc;
+    p.tkeys = m->mk_tw + tl.keys;
+    p.step_word = m->mk_tw + tl.step;
     p.logits = m->logits;
-    const uint32_t G = c.heads / c.kv_heads;
-    p.part_ml = m->mk_part;
-    p.part_acc = m->mk_part + static_cast<size_t>(c.kv_heads) * m->mk_nsplit * G * 2;
-    p.counters = m->counters;
-    p.attn = m->attn;
-    p.keys = m->keys;
     p.state = m->state;
     p.prompt = m->prompt;
     p.out_tokens = m->out_tokens;
     p.out_cap = m->out_cap;
-    p.flags = m->mk_sync;
-    p.release = m->mk_sync + static_cast<size_t>(m->mk_blocks) * 32;
-    p.error = p.release + 32;
+    p.error = m->mk_err;
+    p.epoch0 = m->mk_epoch;
     p.nsplit = m->mk_nsplit;
     p.min_chunk = 64;
     p.n_steps = n_steps;
     p.eos = eos;
     p.timing = timing;
     p.timing_stride = timing_stride;
-    p.timing_slots = timing_stride >= 16u * (5u * c.layers + 4u) ? 16u : 1u;
+    p.timing_slots = timing_stride >= 16u * decode_step_phases_per_step(c.layers) ? 16u : 1u;
     p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, c.inter, p.hd));
-    HIP_TRY(hipMemsetAsync(m->mk_sync, 0, m->mk_sync_words * sizeof(uint32_t), m->stream));
+    m->mk_epoch += static_cast<uint32_t>(need);
+    HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
     HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
     m->mk_pending = true;
     return VVLI_OK;
@@ -321,11 +355,11 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
 int check_persistent_error(vvli_gpu_model* m) {
     if (!m->mk_pending) return VVLI_OK;
     m->mk_pending = false;
-    HIP_TRY(hipMemcpyAsync(m->h_err, m->mk_sync + static_cast<size_t>(m->mk_blocks) * 32 + 32, sizeof(uint32_t),
+    HIP_TRY(hipMemcpyAsync(m->h_err, m->mk_err, sizeof(uint32_t),
                            hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
     if (*m->h_err != 0)
-        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (barrier timeout)",
+        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (input wait timed out)",
                          *m->h_err);
     return VVLI_OK;
 }
@@ -348,7 +382,7 @@ void free_model(vvli_gpu_model* m) {
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
-                    m->mk_layers, m->mk_gemv, m->mk_sync, m->mk_part};
+                    m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -394,7 +428,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
         m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->layers, hd);
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
             m->mk_lds <= 160 * 1024 && decode_step_max_blocks(hd, m->mk_lds, &bpc) == hipSuccess && bpc >= 1 &&
-            cus > 0) {
+            cus > 0 && static_cast<uint64_t>(max_seq_len) * kv * sizeof(float) < (1ull << 31)) {  // 32-bit KV offsets
             m->mk_ok = true;
             m->mk_blocks = static_cast<uint32_t>(cus);
             m->mk_nsplit = std::max<uint32_t>(1, std::min<uint32_t>(16, (max_seq_len + 63) / 64));  // <= kMaxSplitMk
@@ -403,7 +437,6 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     }
     const uint32_t G = cfg->heads / cfg->kv_heads;
     const size_t part_floats = attn_part_floats(cfg->heads, cfg->kv_heads, hd, m->nsplit);
-    const size_t mk_part_floats = static_cast<size_t>(cfg->kv_heads) * m->mk_nsplit * G * (2 + hd);
     const uint32_t nkeys_alloc = std::max<uint32_t>(m->nkeys, m->mk_blocks * 8);
     m->out_cap = max_seq_len + 1;
 #define TRY_ALLOC(expr)         \
@@ -428,11 +461,11 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(dmalloc(&m->counters, cfg->kv_heads));
     TRY_ALLOC(dmalloc(&m->keys, nkeys_alloc));
     if (m->mk_ok) {
-        m->mk_sync_words = static_cast<size_t>(m->mk_blocks) * 32 + 64;
-        TRY_ALLOC(dmalloc(&m->mk_sync, m->mk_sync_words));
+        m->mk_tw_words = tagged_layout(*cfg, m->mk_nsplit, m->mk_blocks).total;
+        TRY_ALLOC(dmalloc(&m->mk_tw, m->mk_tw_words));
+        TRY_ALLOC(dmalloc(&m->mk_err, 32));
         TRY_ALLOC(dmalloc(&m->mk_layers, cfg->layers));
         TRY_ALLOC(dmalloc(&m->mk_gemv, static_cast<size_t>(cfg->layers) * 4 + 1));
-        TRY_ALLOC(dmalloc(&m->mk_part, mk_part_floats));
         TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_err), sizeof(uint32_t), hipHostMallocDefault) ==
                           hipSuccess
                       ? 0
@@ -454,8 +487,10 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
     TRY_ALLOC(fail_hip(hipMemset(m->state, 0, sizeof(StepState)), "state"));
-    if (m->mk_sync)
-        TRY_ALLOC(fail_hip(hipMemset(m->mk_sync, 0, m->mk_sync_words * sizeof(uint32_t)), "sync clear"));
+    if (m->mk_tw) {
+        TRY_ALLOC(fail_hip(hipMemset(m->mk_tw, 0, m->mk_tw_words * sizeof(unsigned long long)), "tag clear"));
+        TRY_ALLOC(fail_hip(hipMemset(m->mk_err, 0, 32 * sizeof(uint32_t)), "error clear"));
+    }
     TRY_ALLOC(upload_rope(m));
     if (m->mk_ok) {
         std::vector<DecodeLayer> dl(cfg->layers);
@@ -469,27 +504,28 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
                            "layer table"));
         // GEMV phase descriptors: per layer qkv, o (+residual), gate/up, down (+residual); then logits.
         std::vector<DecodeGemv> dg(static_cast<size_t>(cfg->layers) * 4 + 1, DecodeGemv{});
-        float* q = m->qkv;
-        float* kn = m->qkv + H;
-        float* vn = m->qkv + H + kv;
+        const TaggedLayout tl = tagged_layout(*cfg, m->mk_nsplit, m->mk_blocks);
+        unsigned long long* q = m->mk_tw + tl.tqkv;
+        unsigned long long* x_in = m->mk_tw + tl.tx;       // layer input (written by D)
+        unsigned long long* x_mid = m->mk_tw + tl.tx + H;  // after attention (written by O)
         for (uint32_t l = 0; l < cfg->layers; ++l) {
             const DecodeLayer& L = dl[l];
             DecodeGemv& gq = dg[l * 4 + 0];
             gq.w0 = L.q, gq.w1 = L.k, gq.w2 = L.v;
             gq.b0 = L.q_bias, gq.b1 = L.k_bias, gq.b2 = L.v_bias;
-            gq.o0 = q, gq.o1 = kn, gq.o2 = vn;
+            gq.o0 = q, gq.o1 = q + H, gq.o2 = q + H + kv;
             gq.r0 = H, gq.r1 = kv, gq.r2 = kv;
             gq.K = H;
             DecodeGemv& go = dg[l * 4 + 1];
-            go.w0 = L.o, go.o0 = m->x, go.r0 = H, go.K = H;
+            go.w0 = L.o, go.o0 = x_mid, go.r0 = H, go.K = H;
             DecodeGemv& gg = dg[l * 4 + 2];
-            gg.w0 = L.gate, gg.w_up = L.up, gg.o0 = m->ff, gg.r0 = cfg->inter, gg.K = H;
+            gg.w0 = L.gate, gg.w_up = L.up, gg.o0 = m->mk_tw + tl.tff, gg.r0 = cfg->inter, gg.K = H;
             DecodeGemv& gd = dg[l * 4 + 3];
-            gd.w0 = L.down, gd.o0 = m->x, gd.r0 = H, gd.K = cfg->inter;
+            gd.w0 = L.down, gd.o0 = x_in, gd.r0 = H, gd.K = cfg->inter;
         }
         DecodeGemv& gl = dg[static_cast<size_t>(cfg->layers) * 4];
         gl.w0 = static_cast<const uint16_t*>(wslice(m, cfg->tie ? m->layout.embed : m->layout.lm_head));
-        gl.o0 = m->logits, gl.r0 = cfg->vocab, gl.K = H;
+        gl.plain = m->logits, gl.r0 = cfg->vocab, gl.K = H;
         TRY_ALLOC(fail_hip(hipMemcpy(m->mk_gemv, dg.data(), dg.size() * sizeof(DecodeGemv), hipMemcpyHostToDevice),
                            "gemv table"));
     }
