@@ -158,6 +158,8 @@ def main() -> int:
     tokens, stats = runner.generate_greedy_measured(prompt, args.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    persistent = args.path != "graph" and runner.persistent_available()
+    decode_launch_ms = runner.last_launch_ms() if persistent else None
     assert stats.generated_tokens == args.steps
     decode_s = stats.decode_nanoseconds / 1e9
     tok_s = args.steps / decode_s
@@ -170,9 +172,10 @@ def main() -> int:
     step_bytes = sum(token_bytes(cfg, p) for p in positions)
     step_gbs = step_bytes / decode_s / 1e9
 
-    # Per-kernel durations, mid-decode: start/stop events at each kernel's own
-    # dispatch boundaries on the model's stream (vvli_gpu_profile_step), the
-    # same interval a kernel trace reports. Grouped by kernel symbol.
+    # Per-kernel durations of the per-kernel path, mid-decode: start/stop
+    # events at each kernel's own dispatch boundaries on the model's stream
+    # (vvli_gpu_profile_step), the same interval a kernel trace reports.
+    # Grouped by kernel symbol.
     mid = args.prompt + args.steps // 2
     prof = profile_kernels(runner, cfg, int(tokens[args.steps // 2]), mid)
     kb = kernel_bytes(cfg, mid)
@@ -190,6 +193,14 @@ def main() -> int:
         nbytes = sum(kb[k] * len(prof[k]) for k in parts)
         kernels[sym] = {"launches": launches, "total_us": total_ms * 1e3, "avg_us": total_ms * 1e3 / launches,
                         "bytes_per_launch": nbytes // launches, "gbs": nbytes / (total_ms * 1e-3) / 1e9}
+    if persistent:
+        # The persistent decode step is the one kernel of the timed region: its
+        # decode launch runs all --steps tokens. Algorithmic bytes per launch =
+        # sum over the decode positions of B(pos); duration = HIP events around
+        # that launch on the model's stream.
+        sym = "decode_step_kernel<64, true> (persistent decode step)"
+        kernels = {sym: {"launches": 1, "total_us": decode_launch_ms * 1e3, "avg_us": decode_launch_ms * 1e3,
+                         "bytes_per_launch": step_bytes, "gbs": step_bytes / (decode_launch_ms * 1e-3) / 1e9}}
     dom = max(kernels, key=lambda k: kernels[k]["total_us"])
     d = kernels[dom]
     traffic = measured_traffic(dom.split(" (")[0])
@@ -197,6 +208,9 @@ def main() -> int:
                 "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 2),
                 "launches_per_step": d["launches"]}
+    if persistent:
+        roofline["tokens_per_launch"] = args.steps
+        roofline["us_per_token"] = round(d["avg_us"] / args.steps, 2)
     print("[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f}us {v['gbs']:.0f}GB/s" for k, v in kernels.items()),
           file=sys.stderr, flush=True)
 

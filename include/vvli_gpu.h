@@ -172,6 +172,12 @@ int vvli_gpu_set_decode_path(vvli_gpu_model* model, uint32_t path);
  * persistent launch. */
 int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t pos, uint64_t* ticks_out,
                                 uint32_t stride, uint32_t* n_blocks);
+/* Device time of the last persistent launch on this model (HIP events
+ * recorded on the model's stream right before and after the cooperative
+ * launch), in milliseconds; for generate_greedy that is its decode launch,
+ * for prefill its one launch. VVLI_INVALID_CONFIG if no persistent launch
+ * has run. Waits for the launch to finish. */
+int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
 
 /* ---------------------------------------------------------------------- */
 /* Isolated matmul op (device pointers)                                    */

@@ -33,6 +33,8 @@
 // Deadlock safety: the launch is cooperative (all blocks co-resident or the
 // launch fails), every poll is bounded, and a timeout raises a device error
 // flag that makes every block leave at its next poll; the host reports it.
+#include <cstdlib>
+
 #include "device_common.hpp"
 #include "gemv_tile.hpp"
 #include "kernels.hpp"
@@ -570,37 +572,39 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 VVLI_TILE_LOAD(ta + TILE, (int)min((uint32_t)TILE, t1 - ta - TILE));
             }
             __syncthreads();
-            // scores s[g][j] = (q_g . K_j) * scale, four independent chains
-            for (int idx = tid; idx < G * TILE; idx += kMkThreads) {
+            // scores s[g][j] = (q_g . K_j) * scale: thread pairs, each over half
+            // of the dimensions (two independent chains), summed across the pair.
+            for (int idx2 = tid; idx2 < 2 * G * TILE; idx2 += kMkThreads) {
+                const int idx = idx2 >> 1, half_d = idx2 & 1;
                 const int g = idx / TILE, j = idx - g * TILE;
-                float d0 = -INFINITY;
+                float a0 = 0.f, a1 = 0.f;
                 if (j < tlen) {
-                    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
                     const float* qr = qs + g * HDMAX;
                     const float* kr = ks + j * KS;
                     if constexpr (EXACT) {
 #pragma unroll
-                        for (int d = 0; d < HDMAX; d += 4) {
+                        for (int d = half_d * 4; d < HDMAX; d += 8) {  // float4 chunks alternate in the pair
                             const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
                             const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
                             a0 = fmaf(q4.x, k4.x, a0);
                             a1 = fmaf(q4.y, k4.y, a1);
-                            a2 = fmaf(q4.z, k4.z, a2);
-                            a3 = fmaf(q4.w, k4.w, a3);
+                            a0 = fmaf(q4.z, k4.z, a0);
+                            a1 = fmaf(q4.w, k4.w, a1);
                         }
                     } else {
-                        for (int d = 0; d < hd; d += 4) {
+                        for (int d = half_d * 4; d < hd; d += 8) {
                             const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
                             const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
                             a0 = fmaf(q4.x, k4.x, a0);
                             a1 = fmaf(q4.y, k4.y, a1);
-                            a2 = fmaf(q4.z, k4.z, a2);
-                            a3 = fmaf(q4.w, k4.w, a3);
+                            a0 = fmaf(q4.z, k4.z, a0);
+                            a1 = fmaf(q4.w, k4.w, a1);
                         }
                     }
-                    d0 = ((a0 + a1) + (a2 + a3)) * p.scale;
                 }
-                ps[g * TILE + j] = d0;
+                const float part = a0 + a1;
+                const float dot = part + __shfl_xor(part, 1, kWave);
+                if (half_d == 0) ps[g * TILE + j] = j < tlen ? dot * p.scale : -INFINITY;
             }
             __syncthreads();
             for (int g = wave; g < G; g += kMkWaves) {
@@ -655,14 +659,50 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             }
             continue;
         }
-        // Owner: merge weights from every split's (m, l), own split last.
-        if (tid < (int)(ns - 1) * G) {
-            const tword* src = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
-            tword wm = ld_a(src), wl = ld_a(src + 1);
-            ok = ok && poll_tw(src, tag_out, wm, p.error) && poll_tw(src + 1, tag_out, wl, p.error);
-            pm[tid] = tw_val(wm);
-            pl[tid] = tw_val(wl);
-        }
+        // Owner: fetch the other splits' partials -- (m, l) together with the
+        // first batch of outputs, re-polled as a whole until every word
+        // carries the tag (one memory round trip when they are there) -- then
+        // merge, own split last.
+        const int nml = (int)(ns - 1) * G;
+        const int npe = (G * hd + kMkThreads - 1) / kMkThreads;  // output batches in use
+        const tword* mls = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
+        const tword* accs = p.tpart_acc + pbase * G * hd;
+        tword wv[kMaxSplitMk - 1];
+#define VVLI_POLL_PARTIALS(i_, with_ml_)                                                                    \
+    {                                                                                                       \
+        const int idx_ = tid + (i_) * kMkThreads;                                                           \
+        const bool mine_ = idx_ < G * hd;                                                                   \
+        const bool ml_ = (with_ml_) && tid < nml;                                                           \
+        tword wm_ = 0, wl_ = 0;                                                                             \
+        for (uint32_t spins = 0;; ++spins) {                                                                \
+            bool good = true;                                                                               \
+            if (ml_) {                                                                                      \
+                wm_ = ld_a(mls);                                                                            \
+                wl_ = ld_a(mls + 1);                                                                        \
+            }                                                                                               \
+            _Pragma("unroll") for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) if (mine_ && s2 < (int)ns - 1)   \
+                wv[s2] = ld_a(accs + (size_t)s2 * G * hd + idx_);                                           \
+            if (ml_) good = tw_tag(wm_) == tag_out && tw_tag(wl_) == tag_out;                               \
+            _Pragma("unroll") for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) if (mine_ && s2 < (int)ns - 1)   \
+                good = good && tw_tag(wv[s2]) == tag_out;                                                   \
+            if (good) break;                                                                                \
+            if (spins > kSpinLimit) {                                                                       \
+                st_a(p.error, 1u);                                                                          \
+                ok = false;                                                                                 \
+                break;                                                                                      \
+            }                                                                                               \
+            if ((spins & 63u) == 63u && ld_a(p.error) != 0) {                                               \
+                ok = false;                                                                                 \
+                break;                                                                                      \
+            }                                                                                               \
+            __builtin_amdgcn_s_sleep(1);                                                                    \
+        }                                                                                                   \
+        if (ml_) {                                                                                          \
+            pm[tid] = tw_val(wm_);                                                                          \
+            pl[tid] = tw_val(wl_);                                                                          \
+        }                                                                                                   \
+    }
+        VVLI_POLL_PARTIALS(0, true)
         if (tid < G) {
             pm[(ns - 1) * G + tid] = m_s[tid];
             pl[(ns - 1) * G + tid] = l_s[tid];
@@ -682,29 +722,20 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
+            if (i >= npe) break;
+            if (i > 0) VVLI_POLL_PARTIALS(i, false)
             const int idx = tid + i * kMkThreads;
             if (idx < G * hd) {
                 const int g = idx / hd;
-                const tword* src = p.tpart_acc + pbase * G * hd + idx;
-                constexpr int SB = 4;  // split partials loaded per batch
                 float o = 0.f;
-                for (int s0 = 0; s0 < (int)ns - 1; s0 += SB) {
-                    tword wv[SB];
 #pragma unroll
-                    for (int b = 0; b < SB; ++b)
-                        if (s0 + b < (int)ns - 1) wv[b] = ld_a(src + (size_t)(s0 + b) * G * hd);
-#pragma unroll
-                    for (int b = 0; b < SB; ++b) {
-                        if (s0 + b < (int)ns - 1) {
-                            ok = ok && poll_tw(src + (size_t)(s0 + b) * G * hd, tag_out, wv[b], p.error);
-                            o = fmaf(tw_val(wv[b]), wsp[(s0 + b) * G + g], o);
-                        }
-                    }
-                }
+                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2)
+                    if (s2 < (int)ns - 1) o = fmaf(tw_val(wv[s2]), wsp[s2 * G + g], o);
                 o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
                 st_a(p.tattn + (size_t)h * G * hd + idx, tw_make(o, tag_out));
             }
         }
+#undef VVLI_POLL_PARTIALS
         if (__syncthreads_or(!ok)) return false;
     }
     return true;
@@ -938,9 +969,20 @@ hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu) {
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kMkThreads, lds);
 }
 
+// The launch is cooperative (the runtime guarantees that all blocks are
+// resident at once, which the inter-block polls rely on). With
+// VVLI_PLAIN_LAUNCH=1 it is an ordinary launch of the same grid -- one block
+// per CU, which the occupancy check at model creation showed fits -- for
+// tools that do not follow cooperative dispatches (rocprofv3 kernel traces).
+// Were a block not resident, the bounded polls would report a device error.
 hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s) {
     DecodeStepParams copy = p;
     void* args[] = {&copy};
+    static const bool plain = [] {
+        const char* e = getenv("VVLI_PLAIN_LAUNCH");
+        return e && e[0] == '1';
+    }();
+    if (plain) return hipLaunchKernel(decode_step_fn(p.hd), dim3(blocks), dim3(kMkThreads), args, lds, s);
     return hipLaunchCooperativeKernel(decode_step_fn(p.hd), dim3(blocks), dim3(kMkThreads), args, (unsigned)lds, s);
 }
 

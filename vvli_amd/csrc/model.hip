@@ -67,6 +67,8 @@ struct vvli_gpu_model {
     uint32_t mk_epoch = 1;                // epoch of the next launch's first phase
     uint32_t* h_err = nullptr;    // pinned
     bool mk_pending = false;      // a persistent launch ran since the last error check
+    hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last persistent launch
+    bool mk_timed = false;
 };
 
 namespace {
@@ -347,8 +349,11 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, c.inter, p.hd));
     m->mk_epoch += static_cast<uint32_t>(need);
     HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
+    HIP_TRY(hipEventRecord(m->mk_ev0, m->stream));
     HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
+    HIP_TRY(hipEventRecord(m->mk_ev1, m->stream));
     m->mk_pending = true;
+    m->mk_timed = true;
     return VVLI_OK;
 }
 
@@ -387,6 +392,8 @@ void free_model(vvli_gpu_model* m) {
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
     if (m->h_err) (void)hipHostFree(m->h_err);
+    if (m->mk_ev0) (void)hipEventDestroy(m->mk_ev0);
+    if (m->mk_ev1) (void)hipEventDestroy(m->mk_ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -466,6 +473,9 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
         TRY_ALLOC(dmalloc(&m->mk_err, 32));
         TRY_ALLOC(dmalloc(&m->mk_layers, cfg->layers));
         TRY_ALLOC(dmalloc(&m->mk_gemv, static_cast<size_t>(cfg->layers) * 4 + 1));
+        TRY_ALLOC(hipEventCreate(&m->mk_ev0) == hipSuccess && hipEventCreate(&m->mk_ev1) == hipSuccess
+                      ? 0
+                      : set_error(VVLI_HIP_ERROR, "hipEventCreate failed"));
         TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_err), sizeof(uint32_t), hipHostMallocDefault) ==
                           hipSuccess
                       ? 0
@@ -739,6 +749,15 @@ int vvli_gpu_profile_persistent(vvli_gpu_model* m, uint32_t token, uint32_t pos,
     (void)hipFree(d);
     if (rc) return rc;
     *n_blocks = m->mk_blocks;
+    return VVLI_OK;
+}
+
+int vvli_gpu_last_launch_time(vvli_gpu_model* m, float* ms_out) {
+    if (!m || !ms_out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_last_launch_time");
+    if (!m->mk_timed) return set_error(VVLI_INVALID_CONFIG, "no persistent launch has run on this model");
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipEventSynchronize(m->mk_ev1));
+    HIP_TRY(hipEventElapsedTime(ms_out, m->mk_ev0, m->mk_ev1));
     return VVLI_OK;
 }
 

@@ -99,6 +99,7 @@ class Runner:
         blob = np.ascontiguousarray(blob)
         _lib.check(_lib.lib().vvli_gpu_model_create(byref(self._c), max_seq_len, _ptr(blob), blob.size, byref(handle)))
         self._h = handle
+        self._path = "auto"
         self.logits = np.zeros(cfg.vocab_size, dtype=np.float32)
 
     def close(self) -> None:
@@ -164,9 +165,28 @@ class Runner:
             t = np.ascontiguousarray(inv_freq, dtype=np.float32)
             _lib.check(_lib.lib().vvli_gpu_set_rope_table(self._h, _ptr(t), t.size))
 
+    def persistent_available(self) -> bool:
+        """True when this model can run the persistent one-launch step (the
+        default decode path then)."""
+        try:
+            self.set_decode_path("persistent")
+        except _lib.VvliError:
+            return False
+        finally:
+            self.set_decode_path(self._path)
+        return True
+
+    def last_launch_ms(self) -> float:
+        """Device time (HIP events) of the last persistent launch: the decode
+        launch of generate_greedy_measured, or a prefill / token step."""
+        ms = ctypes.c_float()
+        _lib.check(_lib.lib().vvli_gpu_last_launch_time(self._h, ctypes.byref(ms)))
+        return float(ms.value)
+
     def set_decode_path(self, path: str) -> None:
         """'auto', 'graph' (per-kernel HIP graph) or 'persistent' (one launch per step)."""
         _lib.check(_lib.lib().vvli_gpu_set_decode_path(self._h, {"auto": 0, "graph": 1, "persistent": 2}[path]))
+        self._path = path
 
     def prefill(self, tokens, start_pos: int = 0) -> tuple[np.ndarray, int]:
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
