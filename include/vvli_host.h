@@ -37,6 +37,19 @@ int vvli_host_fill_synthetic(const vvli_gpu_config* cfg, uint64_t seed, float st
  * tensors that live outside the dense blob. */
 double vvli_host_synthetic_normal(uint64_t seed, uint64_t tensor_id, uint64_t index);
 
+/* Llama-3 RoPE frequency table for vvli_gpu_set_rope_table (head_dim / 2
+ * values). No reference counterpart: the reference has no RoPE scaling (its
+ * applyRoPE, src/llm.zig:1337-1371, always uses 1/pow(theta, 2i/head_dim)).
+ * Starts from exactly that f32 table and applies the published Llama-3
+ * scaling in f32: wavelen = 2*pi/inv_freq; wavelen > original_max_pos /
+ * low_freq_factor -> inv_freq / factor; wavelen < original_max_pos /
+ * high_freq_factor -> unchanged; otherwise (1 - s) * inv_freq / factor +
+ * s * inv_freq with s = (original_max_pos / wavelen - low_freq_factor) /
+ * (high_freq_factor - low_freq_factor). Returns VVLI_INVALID_CONFIG for an
+ * odd or zero head_dim, factor <= 0 or high_freq_factor <= low_freq_factor. */
+int vvli_host_llama3_inv_freq(uint32_t head_dim, float theta, float factor, float low_freq_factor,
+                              float high_freq_factor, uint32_t original_max_pos, float* inv_freq_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
                                             c_int, c_int]),
             "orc_rmsnorm": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_size_t, c_float, c_int]),
             "orc_rope": (None, [c_void_p, c_size_t, c_size_t, c_size_t, c_float, c_uint32, c_void_p]),
+            "orc_llama3_inv_freq": (c_int, [c_uint32, c_float, c_float, c_float, c_float, c_uint32, c_void_p]),
             "orc_softmax": (None, [c_void_p, c_size_t]),
             "orc_attention": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t,
                                      c_void_p, c_int]),
@@ -149,6 +150,14 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, lanes: int = 16) -> np.nda
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.zeros_like(x)
     lib().orc_rmsnorm(_p(out), _p(x), _p(np.ascontiguousarray(w)), kind, x.size, eps, lanes)
+    return out
+
+
+def llama3_inv_freq(head_dim: int, theta: float, factor: float, low_freq_factor: float, high_freq_factor: float,
+                    original_max_pos: int) -> np.ndarray:
+    out = np.zeros(head_dim // 2, dtype=np.float32)
+    _check(lib().orc_llama3_inv_freq(head_dim, theta, factor, low_freq_factor, high_freq_factor, original_max_pos,
+                                     _p(out)))
     return out
 
 

@@ -347,6 +347,33 @@ static void rotate_pair(float* v, size_t first, size_t second, size_t dim_index,
     v[second] = x0 * s + x1 * c;
 }
 
+int orc_llama3_inv_freq(uint32_t head_dim, float theta, float factor, float low_freq_factor, float high_freq_factor,
+                        uint32_t original_max_pos, float* out) {
+    /* Llama-3 scaling (as in HF transformers' _compute_llama3_parameters, f32
+     * tensors): base table 1/powf(theta, 2i/hd) as rotatePair computes it
+     * (src/llm.zig:1360-1366); band edges old/low and old/high; linear blend
+     * in the middle band. */
+    if (head_dim == 0 || (head_dim & 1u) || !(factor > 0.0f) || !(low_freq_factor > 0.0f) ||
+        !(high_freq_factor > low_freq_factor) || original_max_pos == 0)
+        return ORC_INVALID_CONFIG;
+    const float old_ctx = (float)original_max_pos;
+    const float lo_edge = old_ctx / low_freq_factor, hi_edge = old_ctx / high_freq_factor;
+    const float twopi = (float)(2.0 * 3.14159265358979323846);
+    for (uint32_t i = 0; 2 * i < head_dim; ++i) {
+        float base = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+        float wl = twopi / base;
+        if (wl > lo_edge) {
+            out[i] = base / factor;
+        } else if (wl < hi_edge) {
+            out[i] = base;
+        } else {
+            float sm = (old_ctx / wl - low_freq_factor) / (high_freq_factor - low_freq_factor);
+            out[i] = (1.0f - sm) * base / factor + sm * base;
+        }
+    }
+    return ORC_OK;
+}
+
 void orc_rope(float* values, size_t heads, size_t hd, size_t pos, float theta, uint32_t layout,
               const float* inv_freq) {
     /* src/llm.zig:1337-1358 applyRoPE. interleaved pairs (i, i+1) with

@@ -93,6 +93,11 @@ void orc_rmsnorm(float* out, const float* x, const void* w, uint32_t weight_kind
 /* inv_freq may be NULL: then the reference formula 1/pow(theta, d/hd) is used. */
 void orc_rope(float* values, size_t heads, size_t head_dim, size_t pos, float theta, uint32_t layout,
               const float* inv_freq);
+/* Llama-3 scaled frequency table (head_dim/2 values; no reference counterpart,
+ * the published Llama-3 closed form applied to the reference's f32 table).
+ * Returns ORC_INVALID_CONFIG for bad parameters. */
+int orc_llama3_inv_freq(uint32_t head_dim, float theta, float factor, float low_freq_factor, float high_freq_factor,
+                        uint32_t original_max_pos, float* out);
 void orc_softmax(float* values, size_t n);
 /* q: heads*hd; keys/values: [T][kv_heads*hd] rows for t = 0..pos. */
 void orc_attention(float* out, const float* q, const float* keys, const float* values, size_t heads,

@@ -196,3 +196,34 @@ def test_runner_errors(built):
         assert e.value.name == "ContextFull"
         # The runner still works after the errors.
         assert np.isfinite(gpu.forward_token(3, 0)).all()
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
+def test_llama3_rope_table_matches_oracle(path, built, oracle_mod, host_threads):
+    """A Llama-3 scaled RoPE table (vvli_host_llama3_inv_freq, pinned against
+    Hugging Face in the CPU tests) set on both sides: token steps agree."""
+    cfg, kind, how, _ = CASES["llama_small"]
+    blob = make_blob(cfg, kind, how)
+    table = R.llama3_inv_freq(cfg.head_dim(), cfg.rope_theta, factor=32.0, low_freq_factor=1.0,
+                              high_freq_factor=4.0, original_max_pos=64)  # a short original context: every band used
+    orc = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+    orc.set_rope_table(table)
+    toks = np.random.default_rng(5).integers(0, cfg.vocab_size, size=24)
+    print(f"llama3 rope path={path}", flush=True)
+    with R.Runner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path(path)
+        gpu.set_rope_table(table)
+        for pos, tok in enumerate(toks):
+            ref = orc.forward_token(int(tok), pos)
+            got = gpu.forward_token(int(tok), pos)
+            e = rel_err(got, ref)
+            assert e <= TOL, f"pos {pos}: logits rel err {e:.3e}"
+        # Clearing the table restores the reference formula.
+        gpu.set_rope_table(None)
+        gpu.kv_clear()
+        for pos, tok in enumerate(toks[:8]):
+            plain = gpu.forward_token(int(tok), pos).copy()
+        orc2 = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+        for pos, tok in enumerate(toks[:8]):
+            ref_plain = orc2.forward_token(int(tok), pos)
+        assert rel_err(plain, ref_plain) <= TOL

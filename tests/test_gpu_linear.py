@@ -1,0 +1,67 @@
+"""GPU parity of the C2 op (vvli_gpu_linear: Y[m,n] = sum_k bf16 W[n,k] *
+X[m,k] (+ bias[n]), f32 accumulation) against the oracle's linearInto
+restatement (oracle/vvli_oracle.c, src/llm.zig:1228-1285), row by row.
+
+Bar: per output row, max |gpu - ref| / max |ref| <= 2e-3 (f32 accumulation
+on both sides; the order of the K sum differs)."""
+import numpy as np
+import pytest
+
+from vvli_amd import runtime as R
+from vvli_amd._lib import VvliError
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+# (M, N, K, bias): decode shapes of the benchmark model at M = 1, small and
+# ragged ones, and M > 1 (the reference runs M independent linearInto calls).
+SHAPES = [
+    (1, 2048, 2048, False),
+    (1, 512, 2048, False),
+    (3, 1000, 896, True),
+    (8, 2048, 8192, False),
+    (17, 333, 64, True),
+    (64, 1024, 2048, False),
+]
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    b = a.astype(np.float32).view(np.uint32)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)  # RNE (src/llm.zig:799-803)
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", SHAPES)
+def test_linear_matches_oracle(M, N, K, has_bias, oracle_mod):
+    import torch
+
+    rng = np.random.default_rng(M * 100003 + N * 7 + K)
+    w = bf16_bits(rng.normal(0, 0.02, size=(N, K)))
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    bias = bf16_bits(rng.normal(0, 0.02, size=N)) if has_bias else None
+    dev = torch.device("cuda", 0)
+    dw = torch.from_numpy(w.view(np.int16)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    db = torch.from_numpy(bias.view(np.int16)).to(dev) if has_bias else None
+    print(f"linear M={M} N={N} K={K} bias={has_bias}", flush=True)
+    R.linear(dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), M, N, K, None if db is None else db.data_ptr())
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy()
+    for m in range(M):
+        ref = oracle_mod.linear(w, x[m], bias)
+        e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+        assert e <= TOL, f"row {m}: rel err {e:.3e}"
+
+
+def test_linear_rejects_bad_shapes():
+    import torch
+
+    dev = torch.device("cuda", 0)
+    w = torch.zeros((16, 12), dtype=torch.int16, device=dev)
+    x = torch.zeros((1, 12), dtype=torch.float32, device=dev)
+    y = torch.zeros((1, 16), dtype=torch.float32, device=dev)
+    with pytest.raises(VvliError):  # K must be a multiple of 8
+        R.linear(w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 16, 12)
+    with pytest.raises(VvliError):  # NULL pointer
+        R.linear(0, x.data_ptr(), y.data_ptr(), 1, 16, 8)

@@ -359,3 +359,34 @@ def test_generator_loop_replays_forward_steps(oracle_mod):
     c = oracle_mod.OracleRunner(cfg, data["blob"], 40, threads=2)
     toks2, _ = c.generate_greedy(data["tokens"][:5], 20, eos=eos)
     assert list(toks2) == manual[: manual.index(eos) + 1]
+
+
+def test_llama3_rope_table_matches_hf_fixture(oracle_mod):
+    """Llama-3 RoPE scaling (no reference counterpart): the oracle's table and
+    the library's vvli_host_llama3_inv_freq against Hugging Face's
+    _compute_llama3_parameters (tests/golden/llama3_rope.npz, make_rope_golden.py)."""
+    from vvli_amd import runtime as R
+
+    data = np.load(GOLDEN / "llama3_rope.npz")
+    for name in ("llama32", "llama31"):
+        hd, theta, factor, lo, hi, orig = data[name + "_params"]
+        ref = data[name]
+        args = (int(hd), float(theta), float(factor), float(lo), float(hi), int(orig))
+        for got in (oracle_mod.llama3_inv_freq(*args), R.llama3_inv_freq(*args)):
+            np.testing.assert_allclose(got, ref, rtol=2e-7, atol=0)
+        # Band structure of the closed form: short wavelengths keep the
+        # reference frequency, long ones are divided by `factor`.
+        base = oracle_mod.llama3_inv_freq(int(hd), float(theta), 1.0, 1.0, 4.0, int(orig))
+        wl = 2 * np.pi / base
+        assert np.all(ref[wl < orig / hi] == base[wl < orig / hi])
+        np.testing.assert_allclose(ref[wl > orig / lo], base[wl > orig / lo] / factor, rtol=1e-6)
+
+
+def test_llama3_rope_table_rejects_bad_parameters(oracle_mod):
+    from vvli_amd import runtime as R
+    from vvli_amd._lib import VvliError
+
+    with pytest.raises(VvliError):
+        R.llama3_inv_freq(63, 5e5)
+    with pytest.raises(VvliError):
+        R.llama3_inv_freq(64, 5e5, factor=8.0, low_freq_factor=4.0, high_freq_factor=1.0)

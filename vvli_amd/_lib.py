@@ -109,6 +109,7 @@ PROTOTYPES = {
     "vvli_host_fill_deterministic": (None, [c_void_p, c_size_t, c_uint32]),
     "vvli_host_fill_synthetic": (c_int, [POINTER(CConfig), c_uint64, c_float, c_void_p, c_size_t, c_uint32]),
     "vvli_host_synthetic_normal": (c_double, [c_uint64, c_uint64, c_uint64]),
+    "vvli_host_llama3_inv_freq": (c_int, [c_uint32, c_float, c_float, c_float, c_float, c_uint32, c_void_p]),
 }
 
 _lib = None

@@ -139,15 +139,27 @@ struct MkTile {
 
 __device__ __forceinline__ uint32_t mk_tiles(const MkGemv& g, int mode) {
     const uint32_t total = g.r0 + g.r1 + g.r2;
-    return mode == kGemvGateUp ? total : (total + 1) / 2;
+    return (mode == kGemvGateUp || g.split) ? total : (total + 1) / 2;
 }
+
+// Units (8 weights) streamed per tile row: a split tile streams half rows.
+__device__ __forceinline__ uint32_t mk_units(const MkGemv& g) { return g.split ? g.K / 16 : g.K / 8; }
 
 // Tile `tile`: gate row t and up row t (SwiGLU), else rows 2t, 2t+1 of the
 // stacked segments (segments hold an even number of rows, so a tile never
 // straddles two; an odd last row re-reads its own row as the second).
 __device__ __forceinline__ void mk_make_tile(const MkGemv& g, int mode, uint32_t tile, MkTile& t) {
     const uint32_t K = g.K;
-    if (mode == kGemvGateUp) {
+    if (g.split) {  // row t: first half in p[0], second half in p[1]
+        const bool v = tile < g.r0;
+        const uint32_t r = v ? tile : 0;
+        t.p[0] = g.w0 + (size_t)r * K;
+        t.p[1] = t.p[0] + K / 2;
+        t.row[0] = t.row[1] = r;
+        t.seg = 0;
+        t.valid[0] = v;
+        t.valid[1] = false;
+    } else if (mode == kGemvGateUp) {
         const bool v = tile < g.r0;
         const uint32_t r = v ? tile : 0;
         t.p[0] = g.w0 + (size_t)r * K;
@@ -208,7 +220,7 @@ __device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkW
             for (int j = 0; j < kNJC; ++j) buf[r][j] = make_uint4(0, 0, 0, 0);
         return false;
     }
-    issue<uint16_t, 2>(buf, t.p, 0, g.K / 8, w.lane);
+    issue<uint16_t, 2>(buf, t.p, 0, mk_units(g), w.lane);
     return true;
 }
 
@@ -219,6 +231,33 @@ struct MkResid {
     uint32_t tag;
     const uint16_t* bf16;
 };
+
+// acc[r] += W_r . x_r over one item's units: row 0 against xs0, row 1
+// against xs1 (the same vector unless the tile holds a split row).
+__device__ __forceinline__ void consume_rows(const uint4 (&buf)[2][kNJC], const float* xs0, const float* xs1,
+                                             uint32_t ubase, uint32_t U, int lane, float (&acc)[2]) {
+    if (xs1 == xs0) {  // two rows against one x: load x once
+        consume<uint16_t, 2>(buf, xs0, ubase, U, lane, acc);
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < kNJC; ++j) {
+        const uint32_t u = ubase + j * kWave + lane;
+        if (u < U) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const float* xr = (r == 0 ? xs0 : xs1) + (size_t)u * 8;
+                const float4 x0 = *reinterpret_cast<const float4*>(xr);
+                const float4 x1 = *reinterpret_cast<const float4*>(xr + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                float wf[8];
+                WeightTraits<uint16_t>::expand(buf[r][j], wf);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[r] = fmaf(wf[e], xv[e], acc[r]);
+            }
+        }
+    }
+}
 
 // Run this wave's tiles of a GEMV phase (`mode` is uniform over the grid);
 // bufA/tA hold the prefetched first item when `have` is set. Outputs are
@@ -234,8 +273,9 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
                                         uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
                                         uint32_t tag, const MkResid& rs, uint32_t* err) {
     const int lane = w.lane;
-    const uint32_t U = g.K / 8;
+    const uint32_t U = mk_units(g);
     const uint32_t per_item = kNJC * kWave;
+    const float* xs1 = g.split ? xs + g.K / 2 : xs;  // x of the second streamed row
     const uint32_t nchunk = (U + per_item - 1) / per_item;
     const uint32_t ntiles = mk_tiles(g, mode);
     const uint32_t me = mk_owner(w, ntiles);
@@ -309,16 +349,21 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
         float acc[2] = {acc0, acc1};
         if (it & 1) {
             if (more) issue<uint16_t, 2>(bufA, tn.p, nbase, U, lane);
-            consume<uint16_t, 2>(bufB, xs, chunk * per_item, U, lane, acc);
+            consume_rows(bufB, xs, xs1, chunk * per_item, U, lane, acc);
         } else {
             if (more) issue<uint16_t, 2>(bufB, tn.p, nbase, U, lane);
-            consume<uint16_t, 2>(bufA, xs, chunk * per_item, U, lane, acc);
+            consume_rows(bufA, xs, xs1, chunk * per_item, U, lane, acc);
         }
         acc0 = acc[0];
         acc1 = acc[1];
         if (chunk == nchunk - 1) {
-            float v0 = wave_sum(acc0);
-            const float v1 = wave_sum(acc1);
+            float v0, v1 = 0.f;
+            if (g.split) {
+                v0 = wave_sum(acc0 + acc1);  // the row's two halves
+            } else {
+                v0 = wave_sum(acc0);
+                v1 = wave_sum(acc1);
+            }
             acc0 = acc1 = 0.f;
             if (mode == kGemvGateUp) {
                 v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387

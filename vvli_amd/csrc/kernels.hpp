@@ -135,6 +135,7 @@ struct DecodeGemv {
     uint32_t r0, r1, r2;
     const uint16_t* w_up;
     uint32_t K;
+    uint32_t split;  // one row per tile, its two halves streamed side by side (long rows, few of them)
 };
 
 // Activations of the persistent step are arrays of tagged 64-bit words: the

@@ -532,6 +532,9 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
             gg.w0 = L.gate, gg.w_up = L.up, gg.o0 = m->mk_tw + tl.tff, gg.r0 = cfg->inter, gg.K = H;
             DecodeGemv& gd = dg[l * 4 + 3];
             gd.w0 = L.down, gd.o0 = x_in, gd.r0 = H, gd.K = cfg->inter;
+            // Down rows are long (inter) and few (hidden): split each row in
+            // two halves so that every wave of the grid streams.
+            gd.split = (cfg->inter % 16 == 0 && cfg->inter >= 2 * H) ? 1u : 0u;
         }
         DecodeGemv& gl = dg[static_cast<size_t>(cfg->layers) * 4];
         gl.w0 = static_cast<const uint16_t*>(wslice(m, cfg->tie ? m->layout.embed : m->layout.lm_head));

@@ -44,6 +44,16 @@ def deterministic_blob(cfg: Config, weight_kind: int = WEIGHT_F32) -> np.ndarray
     return blob
 
 
+def llama3_inv_freq(head_dim: int, theta: float, factor: float = 32.0, low_freq_factor: float = 1.0,
+                    high_freq_factor: float = 4.0, original_max_pos: int = 8192) -> np.ndarray:
+    """Llama-3 RoPE frequencies for Runner.set_rope_table (vvli_host_llama3_inv_freq).
+    Defaults: Llama-3.2's rope_scaling."""
+    out = np.zeros(head_dim // 2, dtype=np.float32)
+    _lib.check(_lib.lib().vvli_host_llama3_inv_freq(head_dim, theta, factor, low_freq_factor, high_freq_factor,
+                                                     original_max_pos, _ptr(out)))
+    return out
+
+
 def argmax(logits: np.ndarray) -> int:
     """llm.argmax (src/llm.zig:778-789): first index of the strict maximum."""
     best, bv = 0, logits[0]
