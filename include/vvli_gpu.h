@@ -46,6 +46,7 @@ enum {
     VVLI_UNSUPPORTED_VERSION = 13,  /* gguf.Error.UnsupportedGgufVersion */
     VVLI_OUTPUT_TOO_SMALL = 14,     /* generator.Error.OutputTooSmall */
     VVLI_INVALID_SAMPLING = 15,     /* generator.Error.InvalidSamplingOptions */
+    VVLI_UNSUPPORTED_METADATA = 16, /* gguf.Error.UnsupportedMetadataType */
     VVLI_NULL_ARG = 100             /* NULL required argument (metal_smoke.m:24) */
 };
 

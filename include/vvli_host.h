@@ -50,6 +50,63 @@ double vvli_host_synthetic_normal(uint64_t seed, uint64_t tensor_id, uint64_t in
 int vvli_host_llama3_inv_freq(uint32_t head_dim, float theta, float factor, float low_freq_factor,
                               float high_freq_factor, uint32_t original_max_pos, float* inv_freq_out);
 
+/* ---------------------------------------------------------------------- */
+/* Checkpoint loaders (src/llm.zig:839-1226, src/gguf.zig:234-354)          */
+/* ---------------------------------------------------------------------- */
+/* Progress callback: LoadProgress.report (called with (0, total, "start"),
+ * then once per tensor with the tensor's name; src/llm.zig:68-75, 1067-1079). */
+typedef void (*vvli_host_progress_fn)(void* user, size_t completed, size_t total, const char* name);
+
+/* Config.fromJson, src/llm.zig:98-145 (HF config.json text, len bytes):
+ * model_type llama/mistral/olmoe/qwen2, required vocab_size, hidden_size,
+ * intermediate_size, num_hidden_layers, num_attention_heads,
+ * max_position_embeddings (absent -> VVLI_MISSING_FIELD, not a non-negative
+ * integer -> VVLI_INVALID_CONFIG); defaults kv_heads = heads, rope_theta
+ * 1e4, rms_norm_eps 1e-6, tie false, attention_bias = (qwen2), split-half
+ * RoPE; eos/pad ids take the first element of an array. weight_kind is stored
+ * in out. Malformed JSON -> VVLI_INVALID_FILE. Values above 2^32-1 ->
+ * VVLI_INVALID_CONFIG (the C config holds 32-bit fields). */
+int vvli_host_config_from_json(const char* json, size_t len, uint32_t weight_kind, vvli_gpu_config* out);
+
+/* gguf.parse + Config.fromGguf, src/gguf.zig:234-284 and src/llm.zig:153-193:
+ * magic "GGUF", version 2 or 3 (else VVLI_UNSUPPORTED_VERSION), metadata and
+ * tensor tables (unknown metadata or tensor type ids ->
+ * VVLI_UNSUPPORTED_METADATA, truncation or 0/ >8 dims -> VVLI_INVALID_FILE),
+ * data start aligned to general.alignment (default 32). Config: prefix =
+ * general.architecture, vocab = length of tokenizer.ggml.tokens, interleaved
+ * RoPE, tie iff the file has no output.weight, no q/k/v bias. */
+int vvli_host_config_from_gguf(const void* bytes, size_t len, uint32_t weight_kind, vvli_gpu_config* out);
+
+/* loadSafetensorsIntoOwnedModel, src/llm.zig:923-1006 and 1149-1218: fills the
+ * blob (cfg->weight_kind, OwnedModel.assignSlices layout, padding zeroed) from
+ * a whole model.safetensors image. Tensors are looked up by their HF names;
+ * F32 and BF16 only (else VVLI_UNSUPPORTED_DTYPE), converted to the blob's
+ * type (f32->bf16 round-to-nearest-even, bf16->f32 exact). A missing tensor ->
+ * VVLI_MISSING_TENSOR; a shape whose element count differs, offsets out of
+ * range or a byte length that does not match -> VVLI_INVALID_WEIGHT. MoE and
+ * olmoe configs -> VVLI_UNSUPPORTED_ARCH (OwnedModel.init, :424-446). */
+int vvli_host_load_safetensors(const vvli_gpu_config* cfg, const void* bytes, size_t len, void* blob,
+                               size_t blob_elems, vvli_host_progress_fn progress, void* user);
+
+/* loadGgufIntoOwnedModel, src/llm.zig:1008-1147: the same for a GGUF image and
+ * llama.cpp tensor names (token_embd, blk.N.attn_norm/attn_q/attn_k/attn_v/
+ * attn_output/ffn_norm/ffn_gate/ffn_up/ffn_down, output_norm, output); F32,
+ * F16 and BF16 tensors (f16 widened exactly, then RNE to bf16 for bf16 blobs);
+ * quantised types -> VVLI_UNSUPPORTED_DTYPE; cfg->qkv_bias ->
+ * VVLI_UNSUPPORTED_ARCH. cfg normally comes from vvli_host_config_from_gguf. */
+int vvli_host_load_gguf(const vvli_gpu_config* cfg, const void* bytes, size_t len, void* blob, size_t blob_elems,
+                        vvli_host_progress_fn progress, void* user);
+
+/* Read-only memory map of a whole file (the reference maps checkpoints the
+ * same way, src/llm.zig:870-880, 901-911). An empty or unreadable file ->
+ * VVLI_INVALID_FILE. Release with vvli_host_unmap_file(data, len). */
+int vvli_host_map_file(const char* path, const void** data, size_t* len);
+int vvli_host_unmap_file(const void* data, size_t len);
+
+/* f16ToF32, src/llm.zig:795-797: exact IEEE binary16 -> binary32 (NaN payloads
+ * kept), exposed for tests. */
+float vvli_host_f16_to_f32(uint16_t bits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,7 @@ ERROR_NAMES = {
     13: "UnsupportedGgufVersion",
     14: "OutputTooSmall",
     15: "InvalidSamplingOptions",
+    16: "UnsupportedMetadataType",
     100: "NullArgument",
 }
 
@@ -81,6 +82,9 @@ class CStats(ctypes.Structure):
     ]
 
 
+# void (*)(void* user, size_t completed, size_t total, const char* name)
+PROGRESS_FN = ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_char_p)
+
 # name -> (restype, argtypes): every symbol the two headers declare.
 PROTOTYPES = {
     "vvli_gpu_abi_version": (c_uint32, []),
@@ -110,6 +114,14 @@ PROTOTYPES = {
     "vvli_host_fill_synthetic": (c_int, [POINTER(CConfig), c_uint64, c_float, c_void_p, c_size_t, c_uint32]),
     "vvli_host_synthetic_normal": (c_double, [c_uint64, c_uint64, c_uint64]),
     "vvli_host_llama3_inv_freq": (c_int, [c_uint32, c_float, c_float, c_float, c_float, c_uint32, c_void_p]),
+    "vvli_host_config_from_json": (c_int, [c_char_p, c_size_t, c_uint32, POINTER(CConfig)]),
+    "vvli_host_config_from_gguf": (c_int, [c_void_p, c_size_t, c_uint32, POINTER(CConfig)]),
+    "vvli_host_load_safetensors": (
+        c_int, [POINTER(CConfig), c_void_p, c_size_t, c_void_p, c_size_t, PROGRESS_FN, c_void_p]),
+    "vvli_host_load_gguf": (c_int, [POINTER(CConfig), c_void_p, c_size_t, c_void_p, c_size_t, PROGRESS_FN, c_void_p]),
+    "vvli_host_map_file": (c_int, [c_char_p, POINTER(c_void_p), POINTER(c_size_t)]),
+    "vvli_host_unmap_file": (c_int, [c_void_p, c_size_t]),
+    "vvli_host_f16_to_f32": (c_float, [ctypes.c_uint16]),
 }
 
 _lib = None

@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
-import json
+
+import numpy as np
 
 from . import _lib
 
@@ -84,67 +85,48 @@ class Config:
         return int(_lib.lib().vvli_gpu_storage_element_count(ctypes.byref(self.to_c(weight_kind))))
 
     @classmethod
-    def from_json(cls, text: str) -> "Config":
-        """Config.fromJson (src/llm.zig:99-147): HF config.json keys."""
-        o = json.loads(text)
-        if not isinstance(o, dict):
-            raise _lib.VvliError(1, "config is not a JSON object")
-        mt = o.get("model_type")
-        if not isinstance(mt, str):
-            raise _lib.VvliError(9, "model_type")
-        if mt not in ARCH:
-            raise _lib.VvliError(6, f"model_type {mt}")
-
-        def req(key):
-            v = o.get(key)
-            if v is None:
-                raise _lib.VvliError(9, key)
-            if not isinstance(v, int) or isinstance(v, bool) or v < 0:
-                raise _lib.VvliError(1, key)
-            return v
-
-        def opt_int(key):
-            v = o.get(key)
-            return v if isinstance(v, int) and not isinstance(v, bool) and v >= 0 else None
-
-        def opt_float(key, default):
-            v = o.get(key)
-            return float(v) if isinstance(v, (int, float)) and not isinstance(v, bool) else default
-
-        def opt_bool(key, default):
-            v = o.get(key)
-            return v if isinstance(v, bool) else default
-
-        def token_id(key):
-            v = o.get(key)
-            if isinstance(v, list):
-                v = v[0] if v else None
-            return v if isinstance(v, int) and not isinstance(v, bool) and v >= 0 else 0
-
-        heads = req("num_attention_heads")
-        experts = opt_int("num_experts") or 0
-        cfg = cls(
-            architecture=mt,
-            vocab_size=req("vocab_size"),
-            hidden_size=req("hidden_size"),
-            intermediate_size=req("intermediate_size"),
-            num_hidden_layers=req("num_hidden_layers"),
-            num_attention_heads=heads,
-            num_key_value_heads=opt_int("num_key_value_heads") or heads,
-            num_experts=experts,
-            num_experts_per_token=opt_int("num_experts_per_tok") or 0,
-            qk_norm=mt == "olmoe",
-            rope_layout=ROPE_SPLIT_HALF,
-            max_position_embeddings=req("max_position_embeddings"),
-            rope_theta=opt_float("rope_theta", 10_000.0),
-            rms_norm_eps=opt_float("rms_norm_eps", 0.000001),
-            tie_word_embeddings=opt_bool("tie_word_embeddings", False),
-            qkv_bias=opt_bool("attention_bias", mt == "qwen2"),
-            eos_token_id=token_id("eos_token_id"),
-            pad_token_id=token_id("pad_token_id"),
+    def from_c(cls, c: _lib.CConfig) -> "Config":
+        """The inverse of to_c (weight_kind is not part of Config)."""
+        names = {v: k for k, v in ARCH.items()}
+        return cls(
+            architecture=names[c.arch],
+            vocab_size=c.vocab,
+            hidden_size=c.hidden,
+            intermediate_size=c.inter,
+            num_hidden_layers=c.layers,
+            num_attention_heads=c.heads,
+            num_key_value_heads=c.kv_heads,
+            max_position_embeddings=c.max_pos,
+            rope_layout=c.rope_layout,
+            num_experts=c.num_experts,
+            num_experts_per_token=c.experts_per_tok,
+            rope_theta=c.rope_theta,
+            rms_norm_eps=c.rms_eps,
+            tie_word_embeddings=bool(c.tie),
+            qkv_bias=bool(c.qkv_bias),
+            qk_norm=bool(c.qk_norm),
+            eos_token_id=c.eos_token_id,
+            pad_token_id=c.pad_token_id,
         )
-        cfg.validate()
-        return cfg
+
+    @classmethod
+    def from_json(cls, text: str | bytes) -> "Config":
+        """Config.fromJson (src/llm.zig:98-145): HF config.json keys, parsed by
+        vvli_host_config_from_json."""
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        c = _lib.CConfig()
+        _lib.check(_lib.lib().vvli_host_config_from_json(raw, len(raw), WEIGHT_BF16, ctypes.byref(c)))
+        return cls.from_c(c)
+
+    @classmethod
+    def from_gguf(cls, data) -> "Config":
+        """Config.fromGguf (src/llm.zig:153-193) over a whole GGUF image (bytes,
+        bytearray, numpy array or anything exposing the buffer protocol)."""
+        buf = np.frombuffer(data, dtype=np.uint8)
+        c = _lib.CConfig()
+        _lib.check(_lib.lib().vvli_host_config_from_gguf(ctypes.c_void_p(buf.ctypes.data), buf.size, WEIGHT_BF16,
+                                                         ctypes.byref(c)))
+        return cls.from_c(c)
 
 
 # ---------------------------------------------------------------------------

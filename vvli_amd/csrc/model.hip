@@ -442,7 +442,6 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
         }
         (void)hipGetLastError();
     }
-    const uint32_t G = cfg->heads / cfg->kv_heads;
     const size_t part_floats = attn_part_floats(cfg->heads, cfg->kv_heads, hd, m->nsplit);
     const uint32_t nkeys_alloc = std::max<uint32_t>(m->nkeys, m->mk_blocks * 8);
     m->out_cap = max_seq_len + 1;
