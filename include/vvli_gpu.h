@@ -130,10 +130,13 @@ int vvli_gpu_forward_token_debug(vvli_gpu_model* model, uint32_t token, uint32_t
  * may be NULL): KVCache.keySlice / valueSlice, src/llm.zig:581-589. */
 int vvli_gpu_kv_read(vvli_gpu_model* model, uint32_t layer, uint32_t pos, float* k_out, float* v_out);
 
-/* Batched prompt processing: the prompt loop of src/generator.zig:243-251 run
- * as MFMA GEMMs plus causal attention. Writes K/V for positions
- * start_pos..start_pos+n-1 and returns the logits / argmax of the last one,
- * the same state the token loop leaves. */
+/* Prompt processing: the prompt loop of src/generator.zig:243-251. Writes K/V
+ * for positions start_pos..start_pos+n-1 and returns the logits / argmax of
+ * the last one, leaving the state the token loop leaves (the next forward is
+ * at start_pos+n). Batched (every row of a chunk of up to 2048 tokens through
+ * each layer at once: MFMA GEMMs with f32 activations split into two bf16
+ * halves, causal GQA attention) for bf16 weights with head_dim 32/64/128,
+ * else one token step per prompt token; see vvli_gpu_set_prefill_path. */
 int vvli_gpu_prefill(vvli_gpu_model* model, const uint32_t* tokens, uint32_t n, uint32_t start_pos,
                      float* last_logits, uint32_t* argmax_out);
 
@@ -164,6 +167,10 @@ int vvli_gpu_profile_step(vvli_gpu_model* model, uint32_t token, uint32_t pos, f
  * only; VVLI_INVALID_CONFIG if unavailable). For A/B measurement and for
  * checking both against the same reference. */
 int vvli_gpu_set_decode_path(vvli_gpu_model* model, uint32_t path);
+/* How vvli_gpu_prefill (and generate with VVLI_GEN_BATCHED_PREFILL) runs the
+ * prompt: 0 = auto (batched where supported), 1 = token loop, 2 = batched
+ * (VVLI_INVALID_CONFIG if the model does not support it). */
+int vvli_gpu_set_prefill_path(vvli_gpu_model* model, uint32_t path);
 /* One persistent step with phase timestamps (100 MHz ticks): ticks_out holds
  * (n_blocks + 1) * stride values. With stride >= 16 * (5 * layers + 2), phase
  * k of the step (per layer q/k/v, attention, o, gate/up, down; then logits)
@@ -187,7 +194,9 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
  * Y[m,n] = sum_k bf16 W[n,k] * X[m,k] (+ bias[n]) with f32 accumulation.
  * dW: N*K bf16, dX: M*K f32, dBias: N bf16 or NULL, dY: M*N f32, all device
  * pointers; K must be a multiple of 8. stream: hipStream_t or NULL for the
- * null stream. Asynchronous: returns after the launch. */
+ * null stream. Asynchronous: returns after the launch. M < 4 runs one GEMV per
+ * row; M >= 4 one MFMA GEMM (X split into two bf16 halves, so the products
+ * keep about 16 bits of each f32 activation). */
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream);
 

@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 # (M, N, K, bias): decode shapes of the benchmark model at M = 1, small and
-# ragged ones, and M > 1 (the reference runs M independent linearInto calls).
+# ragged ones, and M > 1 (the reference runs M independent linearInto calls;
+# from M = 4 the library runs one MFMA GEMM).
 SHAPES = [
     (1, 2048, 2048, False),
     (1, 512, 2048, False),
@@ -23,6 +24,13 @@ SHAPES = [
     (8, 2048, 8192, False),
     (17, 333, 64, True),
     (64, 1024, 2048, False),
+    # GEMM path (M >= 4): prefill-sized rows, ragged tiles, stacked-output widths.
+    (4, 130, 24, True),
+    (128, 3072, 2048, False),
+    (130, 1000, 896, True),
+    (512, 2048, 2048, True),
+    (300, 8192, 128, False),
+    (33, 257, 4864, True),
 ]
 
 

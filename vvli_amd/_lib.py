@@ -107,6 +107,7 @@ PROTOTYPES = {
     ),
     "vvli_gpu_profile_step": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, POINTER(c_uint32)]),
     "vvli_gpu_set_decode_path": (c_int, [c_void_p, c_uint32]),
+    "vvli_gpu_set_prefill_path": (c_int, [c_void_p, c_uint32]),
     "vvli_gpu_profile_persistent": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, POINTER(c_uint32)]),
     "vvli_gpu_last_launch_time": (c_int, [c_void_p, POINTER(ctypes.c_float)]),
     "vvli_gpu_linear": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_void_p]),

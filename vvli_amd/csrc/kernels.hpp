@@ -186,4 +186,56 @@ uint32_t decode_step_phases_per_step(uint32_t layers);
 hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu);
 hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// Batched prefill (prefill.hip): bf16-weight GEMM on MFMA with f32 activations
+// split hi/lo, and the per-row kernels around it.
+// ---------------------------------------------------------------------------
+enum GemmMode {
+    kGemmPlain = 0,   // out[m][n] = A_m . W_n (+ bias[n]); W stacked from up to 3 segments
+    kGemmResid = 1,   // out[m][n] += A_m . W_n
+    kGemmGateUp = 2,  // out[m][n] = silu(A_m . Wg_n) * (A_m . Wu_n)
+};
+
+struct GemmArgs {
+    const float* a = nullptr;          // [M][lda] f32
+    uint32_t lda = 0;
+    const float* row_scale = nullptr;  // with norm_w: A_m = (a_m * norm_w) * row_scale[m]
+    const uint16_t* norm_w = nullptr;  // [K] bf16
+    const uint16_t* w[3] = {nullptr, nullptr, nullptr};  // bf16 [rows][K] segments (GateUp: w[0] = gate)
+    const uint16_t* bias[3] = {nullptr, nullptr, nullptr};
+    uint32_t seg_end[3] = {0, 0, 0};   // cumulative rows of the segments (seg_end[2] = N for Plain)
+    const uint16_t* w_up = nullptr;    // GateUp: up rows
+    float* out = nullptr;
+    uint32_t ldo = 0;
+    uint32_t M = 0, N = 0, K = 0;      // K % 8 == 0
+};
+hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s);
+
+hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s);
+hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
+                                float* x, hipStream_t s);
+
+struct PrefillRopeArgs {
+    float* qkv;              // [rows][ld]: q | k | v of each row
+    uint32_t ld, rows, start;
+    uint32_t heads, kv_heads, hd, kvdim, rope_layout;
+    const float* rope_cs;    // [max_seq][hd/2][2]
+    float* kcache;           // this layer's [max_seq][kvdim]
+    float* vcache;
+};
+hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s);
+
+struct PrefillAttnArgs {
+    const float* q;          // [rows][ldq], rotated
+    uint32_t ldq;
+    const float* kcache;     // this layer's [max_seq][kvdim]
+    const float* vcache;
+    float* out;              // [rows][ldo]
+    uint32_t ldo;
+    uint32_t rows, start;    // row t sits at position start + t
+    uint32_t heads, kv_heads, kvdim;
+    float scale;
+};
+hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s);
+
 }  // namespace vvli

@@ -69,6 +69,15 @@ struct vvli_gpu_model {
     bool mk_pending = false;      // a persistent launch ran since the last error check
     hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last persistent launch
     bool mk_timed = false;
+    // Batched prefill (bf16 only): chunk buffers, allocated on first use.
+    bool pf_ok = false;
+    uint32_t prefill_path = 0;  // 0 auto, 1 token loop, 2 batched
+    uint32_t pf_rows = 0;       // rows per chunk the buffers hold
+    float* pf_x = nullptr;      // [rows][H] residual stream
+    float* pf_qkv = nullptr;    // [rows][H + 2 kv]
+    float* pf_attn = nullptr;   // [rows][H]
+    float* pf_ff = nullptr;     // [rows][I]
+    float* pf_scale = nullptr;  // [rows] RMS scales
 };
 
 namespace {
@@ -128,6 +137,8 @@ int check_kernel_shapes(const vvli_gpu_config& c) {
         return set_error(VVLI_INVALID_CONFIG, "hidden/intermediate must be multiples of %u", e);
     return VVLI_OK;
 }
+
+int enqueue_logits(vvli_gpu_model* m, hipStream_t s);
 
 // The layers, final norm and logits of one step (embedding already in x).
 int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
@@ -224,7 +235,15 @@ int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
             HIP_TRY(hipMemcpyAsync(hidden_dbg + static_cast<size_t>(l) * H, m->x, H * sizeof(float),
                                    hipMemcpyDeviceToDevice, s));
     }
-    // Final RMSNorm + logits (lm_head, or the embedding when tied: logitsMatrix, src/llm.zig:410-412).
+    return enqueue_logits(m, s);
+}
+
+// Final RMSNorm + logits + argmax of the hidden state in x.
+int enqueue_logits(vvli_gpu_model* m, hipStream_t s) {
+    const vvli_gpu_config& c = m->cfg;
+    const int kind = static_cast<int>(c.weight_kind);
+    const uint32_t H = c.hidden;
+    // logitsMatrix: lm_head, or the embedding when tied (src/llm.zig:410-412).
     GemvArgs gl;
     gl.w[0] = wslice(m, c.tie ? m->layout.embed : m->layout.lm_head);
     gl.out[0] = m->logits;
@@ -381,13 +400,116 @@ int read_outputs(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
     return VVLI_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Batched prefill: every prompt row of a chunk through each layer at once
+// (prefill.hip). Same KV rows and last logits as the token loop, within the
+// f32 tolerance; bf16 weights and head_dim 32 / 64 / 128.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPrefillChunk = 2048;  // rows per pass; bounds the chunk buffers
+
+bool prefill_supported(const vvli_gpu_config& c) {
+    const uint32_t hd = head_dim(c);
+    return c.weight_kind == VVLI_WEIGHT_BF16 && (hd == 32 || hd == 64 || hd == 128);
+}
+
+bool use_batched_prefill(const vvli_gpu_model* m) { return m->prefill_path != 1 && prefill_supported(m->cfg); }
+
+int ensure_prefill_buffers(vvli_gpu_model* m) {
+    if (m->pf_scale) return VVLI_OK;
+    const vvli_gpu_config& c = m->cfg;
+    const size_t rows = std::min(m->max_seq, kPrefillChunk);
+    const size_t H = c.hidden, kv = kv_dim(c), I = c.inter;
+    float** bufs[] = {&m->pf_x, &m->pf_qkv, &m->pf_attn, &m->pf_ff, &m->pf_scale};
+    const size_t sizes[] = {rows * H, rows * (H + 2 * kv), rows * H, rows * I, rows};
+    for (int i = 0; i < 5; ++i) {
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(bufs[i]), sizes[i] * sizeof(float));
+        if (e != hipSuccess) {
+            for (float** b : bufs) {
+                if (*b) (void)hipFree(*b);
+                *b = nullptr;
+            }
+            return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR,
+                             "prefill buffers (%zu rows): %s", rows, hipGetErrorString(e));
+        }
+    }
+    m->pf_rows = static_cast<uint32_t>(rows);
+    return VVLI_OK;
+}
+
+// Prompt tokens are already in m->prompt[start .. start + n). Leaves the KV
+// rows of those positions, the last row's logits and argmax, and the step
+// state as the token loop leaves it (next position start + n, next token the
+// argmax; with `counting` the argmax is out_tokens[0]).
+int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint32_t last_token, uint32_t counting) {
+    int rc = ensure_prefill_buffers(m);
+    if (rc) return rc;
+    const vvli_gpu_config& c = m->cfg;
+    hipStream_t s = m->stream;
+    const uint32_t H = c.hidden, kv = kv_dim(c), I = c.inter, hd = head_dim(c), ldqkv = H + 2 * kv;
+    const uint16_t* embed = static_cast<const uint16_t*>(wslice(m, m->layout.embed));
+    auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+    for (uint32_t c0 = 0; c0 < n; c0 += m->pf_rows) {
+        const uint32_t P = std::min(m->pf_rows, n - c0);
+        const uint32_t pos0 = start + c0;
+        LAUNCH(launch_prefill_embed(embed, m->prompt + pos0, P, H, m->pf_x, s));
+        for (uint32_t l = 0; l < c.layers; ++l) {
+            const LayerSlices& L = m->layout.layers[l];
+            float* kc = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
+            float* vc = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
+            // input RMSNorm fused into the q|k|v GEMM (+ bias)
+            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+            GemmArgs gq;
+            gq.a = m->pf_x, gq.lda = H, gq.row_scale = m->pf_scale, gq.norm_w = w16(L.input_norm);
+            gq.w[0] = w16(L.q), gq.w[1] = w16(L.k), gq.w[2] = w16(L.v);
+            gq.bias[0] = w16(L.q_bias), gq.bias[1] = w16(L.k_bias), gq.bias[2] = w16(L.v_bias);
+            gq.seg_end[0] = H, gq.seg_end[1] = H + kv, gq.seg_end[2] = H + 2 * kv;
+            gq.out = m->pf_qkv, gq.ldo = ldqkv, gq.M = P, gq.N = ldqkv, gq.K = H;
+            LAUNCH(launch_gemm_bf16(kGemmPlain, gq, s));
+            // RoPE on q and k, k/v appended at positions pos0 ..
+            PrefillRopeArgs ra{m->pf_qkv, ldqkv, P, pos0, c.heads, c.kv_heads, hd, kv, c.rope_layout,
+                               m->rope_cs, kc, vc};
+            LAUNCH(launch_prefill_rope_kv(ra, s));
+            PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
+                               1.0f / sqrtf(static_cast<float>(hd))};
+            LAUNCH(launch_prefill_attn(aa, hd, s));
+            // x += attn . Wo^T
+            GemmArgs go;
+            go.a = m->pf_attn, go.lda = H, go.w[0] = w16(L.o);
+            go.seg_end[0] = go.seg_end[1] = go.seg_end[2] = H;
+            go.out = m->pf_x, go.ldo = H, go.M = P, go.N = H, go.K = H;
+            LAUNCH(launch_gemm_bf16(kGemmResid, go, s));
+            // post-attention RMSNorm fused into gate/up + SwiGLU
+            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+            GemmArgs gu;
+            gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(L.post_norm);
+            gu.w[0] = w16(L.gate), gu.w_up = w16(L.up);
+            gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
+            gu.out = m->pf_ff, gu.ldo = I, gu.M = P, gu.N = I, gu.K = H;
+            LAUNCH(launch_gemm_bf16(kGemmGateUp, gu, s));
+            // x += ff . Wd^T
+            GemmArgs gd;
+            gd.a = m->pf_ff, gd.lda = I, gd.w[0] = w16(L.down);
+            gd.seg_end[0] = gd.seg_end[1] = gd.seg_end[2] = H;
+            gd.out = m->pf_x, gd.ldo = H, gd.M = P, gd.N = H, gd.K = I;
+            LAUNCH(launch_gemm_bf16(kGemmResid, gd, s));
+        }
+        if (c0 + P == n)
+            HIP_TRY(hipMemcpyAsync(m->x, m->pf_x + static_cast<size_t>(P - 1) * H, H * sizeof(float),
+                                   hipMemcpyDeviceToDevice, s));
+    }
+    // State of the token loop after its last prompt step, then that step's logits.
+    LAUNCH(launch_set_state(m->state, last_token, start + n - 1, start + n, counting, s));
+    return enqueue_logits(m, s);
+}
+
 void free_model(vvli_gpu_model* m) {
     if (!m) return;
     (void)hipSetDevice(m->device);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
-                    m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err};
+                    m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
+                    m->pf_scale};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -553,14 +675,19 @@ int64_t now_ns();
 // (token-at-a-time, as the reference), one for the decode steps; the device
 // feeds each argmax back as the next token and stops on EOS.
 int generate_persistent(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
-                        uint32_t* out_tokens, uint32_t* n_out, vvli_gpu_stats* stats) {
+                        bool batched, uint32_t* out_tokens, uint32_t* n_out, vvli_gpu_stats* stats) {
     const uint32_t avail = m->max_seq - n_prompt;  // positions left for decode forwards
     if (eos < 0 && static_cast<uint64_t>(n_prompt) + max_new > m->max_seq)
         return set_error(VVLI_CONTEXT_FULL, "prompt %u + %u new tokens > max_seq_len %u", n_prompt, max_new, m->max_seq);
     const int64_t t0 = now_ns();
     HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
-    int rc = run_persistent(m, n_prompt, eos);
+    int rc;
+    if (batched) {
+        rc = enqueue_prefill_batched(m, 0, n_prompt, prompt[n_prompt - 1], 1);
+    } else {
+        HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
+        rc = run_persistent(m, n_prompt, eos);
+    }
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
@@ -666,6 +793,15 @@ int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
     if (path == 2 && !m->mk_ok)
         return set_error(VVLI_INVALID_CONFIG, "persistent decode step unavailable (bf16 weights, fits one CU)");
     m->path = path;
+    return VVLI_OK;
+}
+
+int vvli_gpu_set_prefill_path(vvli_gpu_model* m, uint32_t path) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (path > 2) return set_error(VVLI_INVALID_CONFIG, "prefill path %u not in 0..2", path);
+    if (path == 2 && !prefill_supported(m->cfg))
+        return set_error(VVLI_INVALID_CONFIG, "batched prefill needs bf16 weights and head_dim 32, 64 or 128");
+    m->prefill_path = path;
     return VVLI_OK;
 }
 
@@ -789,6 +925,11 @@ int vvli_gpu_prefill(vvli_gpu_model* m, const uint32_t* tokens, uint32_t n, uint
     HIP_TRY(hipSetDevice(m->device));
     // Prompt tokens live at their absolute positions in `prompt`.
     HIP_TRY(hipMemcpyAsync(m->prompt + start_pos, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
+    if (use_batched_prefill(m)) {
+        int rc = enqueue_prefill_batched(m, start_pos, n, tokens[n - 1], 0);
+        if (rc) return rc;
+        return read_outputs(m, last_logits, argmax_out);
+    }
     HIP_TRY(launch_set_state(m->state, tokens[0], start_pos, start_pos + n, 0, m->stream));
     if (use_persistent(m)) {
         int rc = run_persistent(m, n, -1);
@@ -810,16 +951,21 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
         if (prompt[i] >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "prompt token %u >= vocab", prompt[i]);
     if (n_prompt > m->max_seq)
         return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
-    (void)flags;
+    const bool batched = (flags & VVLI_GEN_BATCHED_PREFILL) && use_batched_prefill(m);
     HIP_TRY(hipSetDevice(m->device));
-    if (use_persistent(m)) return generate_persistent(m, prompt, n_prompt, max_new, eos, out_tokens, n_out, stats);
+    if (use_persistent(m))
+        return generate_persistent(m, prompt, n_prompt, max_new, eos, batched, out_tokens, n_out, stats);
     int rc = ensure_graph(m);
     if (rc) return rc;
     const int64_t t0 = now_ns();
-    // Prefill: one step per prompt token, chained on the device.
+    // Prefill: batched, or one step per prompt token chained on the device.
     HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
-    for (uint32_t i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    if (batched) {
+        if ((rc = enqueue_prefill_batched(m, 0, n_prompt, prompt[n_prompt - 1], 1))) return rc;
+    } else {
+        HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 1, m->stream));
+        for (uint32_t i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    }
     HIP_TRY(hipStreamSynchronize(m->stream));
     const int64_t t1 = now_ns();
     // Decode: out[0] is the argmax of the last prompt step. Each step
@@ -861,6 +1007,9 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
     return VVLI_OK;
 }
 
+// Rows from which vvli_gpu_linear runs one GEMM instead of a GEMV per row.
+constexpr uint32_t kLinearGemmMinRows = 4;
+
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream) {
     if (!dW || !dX || !dY) return set_error(VVLI_NULL_ARG, "NULL device pointer to vvli_gpu_linear");
@@ -869,6 +1018,15 @@ int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, 
     int rc = init_once();
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M >= kLinearGemmMinRows) {
+        // One MFMA GEMM reads W once for all rows (activations split hi/lo).
+        GemmArgs g;
+        g.a = dX, g.lda = K, g.w[0] = dW, g.bias[0] = dBias;
+        g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+        g.out = dY, g.ldo = N, g.M = M, g.N = N, g.K = K;
+        HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
+        return VVLI_OK;
+    }
     for (uint32_t mi = 0; mi < M; ++mi) {
         GemvArgs g;
         g.w[0] = dW;

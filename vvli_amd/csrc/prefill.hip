@@ -1,0 +1,446 @@
+// prefill.hip -- batched prompt processing: the P prompt tokens of a chunk go
+// through each layer together instead of one token step at a time.
+//
+// Reference semantics: the prefill loop of generator.zig (src/generator.zig:
+// 243-251) forwards the prompt token by token (Runner.forwardToken,
+// src/llm.zig:702-766); what it leaves behind is the KV cache rows of every
+// prompt position and the logits of the last one. This file computes the same
+// rows and logits with matrix products over all P tokens:
+//
+//   X = embed(tokens)                                    [P][H] f32
+//   per layer:
+//     s_r   = 1 / sqrt(mean(X_r^2) + eps)                row_rms_kernel
+//     QKV   = ((X * w_in) * s) . [Wq|Wk|Wv]^T + bias     gemm (A-prologue norm)
+//     rotate q, k (RoPE at each row's position); append k, v to the cache
+//     A     = causal GQA attention over cache rows 0..pos  prefill_attn_kernel
+//     X    += A . Wo^T                                   gemm (residual epilogue)
+//     s_r   = RMS of X rows
+//     F     = silu((X*w_post*s) . Wg^T) * ((X*w_post*s) . Wu^T)   gemm (gate/up)
+//     X    += F . Wd^T                                   gemm (residual epilogue)
+//   last row of X -> final norm, logits, argmax (the decode step's kernels)
+//
+// GEMM on MFMA (v_mfma_f32_16x16x32_bf16). Weights are bf16; activations are
+// f32 and are split into hi = bf16(a) and lo = bf16(a - hi), so that
+// a . w = hi . w + lo . w holds to about 2^-16 relative per product (bf16
+// weights are exact in both): two MFMAs per product keep the f32 activation
+// precision the reference computes with, where one bf16 rounding of the
+// activations would cost about 2^-9.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace vvli {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// GEMM tile: 128 (rows of A) x 128 (rows of W) x 32 (K) per step, 256 threads
+// as 2 x 2 waves of 64 x 64, each wave 4 x 4 MFMA tiles of 16 x 16.
+// v_mfma_f32_16x16x32_bf16 lane layout (lane l): A row l%16, k 8*(l/16)..+7;
+// B column l%16, same k; D rows 4*(l/16)+j (j = 0..3), column l%16.
+// LDS rows are padded to 40 bf16 (80 bytes): the 16 rows one 16-lane group
+// reads then start in 16 distinct 16-byte bank groups.
+// ---------------------------------------------------------------------------
+constexpr int kGemmThreads = 256;
+constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kLdsRow = 40;  // bf16 per LDS row
+constexpr int kTileElems = kBM * kLdsRow;
+
+__device__ inline uint16_t to_bf16_rne(float v) {
+    uint32_t b = __float_as_uint(v);
+    return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ inline float from_bf16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+struct GemmTileRegs {
+    float a[16];     // 16 consecutive K of one A row
+    uint16_t b[16];  // 16 consecutive K of one W row
+};
+
+// Row of W feeding B-tile row r of block column n0 (GateUp interleaves gate and
+// up rows in groups of 16 so one lane holds both halves of an output).
+template <int MODE>
+__device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int r, bool& valid) {
+    if (MODE == kGemmGateUp) {
+        const uint32_t n = n0 / 2 + (r / 32) * 16 + (r % 16);
+        valid = n < g.N;
+        return ((r / 16) & 1 ? g.w_up : g.w[0]) + static_cast<size_t>(valid ? n : 0) * g.K;
+    }
+    const uint32_t n = n0 + r;
+    valid = n < g.N;
+    const uint32_t nn = valid ? n : 0;
+    if (nn < g.seg_end[0]) return g.w[0] + static_cast<size_t>(nn) * g.K;
+    if (nn < g.seg_end[1]) return g.w[1] + static_cast<size_t>(nn - g.seg_end[0]) * g.K;
+    return g.w[2] + static_cast<size_t>(nn - g.seg_end[1]) * g.K;
+}
+
+template <int MODE>
+__device__ inline void gemm_load(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t k0, GemmTileRegs& t) {
+    const int tid = threadIdx.x;
+    const int r = tid >> 1;
+    const uint32_t kc = k0 + (tid & 1) * 16;
+    // A: K is a multiple of 8, so each half of the 16-wide chunk is all in or all out.
+    const uint32_t row = m0 + r;
+    const float* ap = g.a + static_cast<size_t>(row < g.M ? row : 0) * g.lda + kc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const bool in = row < g.M && kc + 8 * h < g.K;
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        if (in) {
+            v0 = *reinterpret_cast<const float4*>(ap + 8 * h);
+            v1 = *reinterpret_cast<const float4*>(ap + 8 * h + 4);
+        }
+        t.a[8 * h + 0] = v0.x, t.a[8 * h + 1] = v0.y, t.a[8 * h + 2] = v0.z, t.a[8 * h + 3] = v0.w;
+        t.a[8 * h + 4] = v1.x, t.a[8 * h + 5] = v1.y, t.a[8 * h + 6] = v1.z, t.a[8 * h + 7] = v1.w;
+    }
+    bool valid;
+    const uint16_t* wp = gemm_w_row<MODE>(g, n0, r, valid) + kc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (valid && kc + 8 * h < g.K) v = *reinterpret_cast<const u16x8*>(wp + 8 * h);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t.b[8 * h + j] = v[j];
+    }
+}
+
+// Normalise (optional), split into hi/lo, and store one thread's chunk.
+__device__ inline void gemm_store(const GemmArgs& g, uint32_t m0, uint32_t k0, const GemmTileRegs& t,
+                                  uint16_t* ahi, uint16_t* alo, uint16_t* bs) {
+    const int tid = threadIdx.x;
+    const int r = tid >> 1, c = (tid & 1) * 16;
+    const uint32_t kc = k0 + c;
+    float scale = 1.0f;
+    if (g.row_scale) {
+        const uint32_t row = m0 + r;
+        scale = row < g.M ? g.row_scale[row] : 0.0f;
+    }
+    u16x8 nw[2] = {{0, 0, 0, 0, 0, 0, 0, 0}, {0, 0, 0, 0, 0, 0, 0, 0}};
+    if (g.norm_w) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            if (kc + 8 * h < g.K) nw[h] = *reinterpret_cast<const u16x8*>(g.norm_w + kc + 8 * h);
+    }
+    u16x8 hi[2], lo[2], bb[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        float v = t.a[j];
+        // rmsNormInto order: (x * w) * scale (src/llm.zig:1297)
+        if (g.norm_w) v = __fmul_rn(__fmul_rn(v, from_bf16(nw[j / 8][j % 8])), scale);
+        const uint16_t h = to_bf16_rne(v);
+        hi[j / 8][j % 8] = h;
+        lo[j / 8][j % 8] = to_bf16_rne(v - from_bf16(h));
+        bb[j / 8][j % 8] = t.b[j];
+    }
+    *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c) = hi[0];
+    *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c + 8) = hi[1];
+    *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c) = lo[0];
+    *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c + 8) = lo[1];
+    *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c) = bb[0];
+    *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c + 8) = bb[1];
+}
+
+__device__ inline float silu_mul(float gv, float uv) {
+    return __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), uv);  // siluMulInto, src/llm.zig:1382-1387
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][3][kTileElems];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = blockIdx.y * kBM;
+    const uint32_t n0 = blockIdx.x * kBN;
+    const uint32_t nk = (g.K + kBK - 1) / kBK;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    GemmTileRegs t;
+    gemm_load<MODE>(g, m0, n0, 0, t);
+    gemm_store(g, m0, 0, t, lds[0][0], lds[0][1], lds[0][2]);
+    __syncthreads();
+
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) gemm_load<MODE>(g, m0, n0, (kt + 1) * kBK, t);
+        const uint16_t* ahi = lds[cur][0];
+        const uint16_t* alo = lds[cur][1];
+        const uint16_t* bs = lds[cur][2];
+        bf16x8 bf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bf[j] = *reinterpret_cast<const bf16x8*>(bs + (wn * 64 + j * 16 + fr) * kLdsRow + fk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = (wm * 64 + i * 16 + fr) * kLdsRow + fk;
+            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(ahi + row);
+            const bf16x8 al = *reinterpret_cast<const bf16x8*>(alo + row);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bf[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more) {
+            const int nxt = cur ^ 1;
+            gemm_store(g, m0, (kt + 1) * kBK, t, lds[nxt][0], lds[nxt][1], lds[nxt][2]);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue.
+    const int rq = 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jr = 0; jr < 4; ++jr) {
+            const uint32_t row = m0 + wm * 64 + i * 16 + rq + jr;
+            if (row >= g.M) continue;
+            float* orow = g.out + static_cast<size_t>(row) * g.ldo;
+            if (MODE == kGemmGateUp) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 2) {
+                    const uint32_t n = n0 / 2 + (wn * 2 + j / 2) * 16 + fr;
+                    if (n < g.N) orow[n] = silu_mul(acc[i][j][jr], acc[i][j + 1][jr]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t n = n0 + wn * 64 + j * 16 + fr;
+                    if (n >= g.N) continue;
+                    float v = acc[i][j][jr];
+                    if (MODE == kGemmResid) {
+                        orow[n] = __fadd_rn(orow[n], v);  // addInto (src/llm.zig:1389-1396)
+                    } else {
+                        const uint16_t* b = n < g.seg_end[0] ? g.bias[0] : n < g.seg_end[1] ? g.bias[1] : g.bias[2];
+                        if (b) {
+                            const uint32_t bi = n < g.seg_end[0] ? n : n < g.seg_end[1] ? n - g.seg_end[0]
+                                                                                        : n - g.seg_end[1];
+                            v = __fadd_rn(v, from_bf16(b[bi]));
+                        }
+                        orow[n] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row statistics, embedding, RoPE + cache append.
+// ---------------------------------------------------------------------------
+constexpr int kRowThreads = 256;
+
+// s_r = 1 / sqrt(sum(x^2) / n + eps) for each row (rmsNormInto's scale, src/llm.zig:1292-1293).
+__global__ __launch_bounds__(kRowThreads) void row_rms_kernel(const float* __restrict__ x, uint32_t n, uint32_t rows,
+                                                             float eps, float* __restrict__ scale) {
+    const uint32_t wave = (blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= rows) return;
+    const float* r = x + static_cast<size_t>(wave) * n;
+    float acc = 0.f;
+    for (uint32_t i = lane * 4; i < n; i += 256) {
+        const float4 v = *reinterpret_cast<const float4*>(r + i);
+        acc = fmaf(v.x, v.x, acc);
+        acc = fmaf(v.y, v.y, acc);
+        acc = fmaf(v.z, v.z, acc);
+        acc = fmaf(v.w, v.w, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) scale[wave] = 1.0f / sqrtf(acc / static_cast<float>(n) + eps);
+}
+
+// X[t] = embed[tokens[t]] (copyEmbeddingToken, src/llm.zig:1373-1380).
+__global__ __launch_bounds__(kRowThreads) void prefill_embed_kernel(const uint16_t* __restrict__ embed,
+                                                                   const uint32_t* __restrict__ tokens, uint32_t n,
+                                                                   float* __restrict__ x) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t i = blockIdx.x * kRowThreads + threadIdx.x;
+    if (i >= n) return;
+    x[static_cast<size_t>(t) * n + i] = from_bf16(embed[static_cast<size_t>(tokens[t]) * n + i]);
+}
+
+__device__ inline void rot(float* v, int a, int b, float c, float s) {
+    // rotatePair, src/llm.zig:1360-1371: x0*c - x1*s, x0*s + x1*c (unfused)
+    const float x0 = v[a], x1 = v[b];
+    v[a] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    v[b] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
+// One block per token row t (position start + t): rotate its q heads in place
+// and its k head vectors, then write k and v to the cache rows of that position.
+__global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRopeArgs a) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t pos = a.start + t;
+    float* row = a.qkv + static_cast<size_t>(t) * a.ld;
+    const float* cs = a.rope_cs + static_cast<size_t>(pos) * a.hd;
+    const uint32_t half = a.hd / 2;
+    const uint32_t qpairs = a.heads * half, kpairs = a.kv_heads * half;
+    float* kc = a.kcache + static_cast<size_t>(pos) * a.kvdim;
+    float* vc = a.vcache + static_cast<size_t>(pos) * a.kvdim;
+    for (uint32_t p = threadIdx.x; p < qpairs + kpairs; p += kRowThreads) {
+        const bool is_q = p < qpairs;
+        const uint32_t pp = is_q ? p : p - qpairs;
+        const uint32_t h = pp / half, i = pp % half;
+        float* v = row + (is_q ? 0 : a.heads * a.hd) + h * a.hd;
+        const int f = a.rope_layout == 0 ? 2 * i : i;
+        const int s = a.rope_layout == 0 ? 2 * i + 1 : i + half;
+        rot(v, f, s, cs[2 * i], cs[2 * i + 1]);
+        if (!is_q) {
+            kc[h * a.hd + f] = v[f];
+            kc[h * a.hd + s] = v[s];
+        }
+    }
+    const float* vsrc = row + (a.heads + a.kv_heads) * a.hd;
+    for (uint32_t i = threadIdx.x; i < a.kvdim; i += kRowThreads) vc[i] = vsrc[i];
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA attention for a chunk of prompt rows (computeAttentionInto,
+// src/llm.zig:1302-1335, for every row at once). One wave per (kv head,
+// group of consecutive rows): lane = (row, q head of the group); each lane
+// keeps its q and its output accumulator in registers and walks the cache
+// rows 0..max position of the wave in chunks of 16 keys with an online
+// softmax (chunk max, one rescale per chunk). Key and value rows are the same
+// for every lane, so their loads are wave-uniform. Keys past a lane's own
+// position are masked out.
+// ---------------------------------------------------------------------------
+constexpr int kAttnThreads = 256;
+constexpr int kKeyChunk = 16;
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t item = blockIdx.x * (kAttnThreads / 64) + (threadIdx.x >> 6);
+    const uint32_t G = a.heads / a.kv_heads;
+    const uint32_t rows_per_wave = 64 / G;
+    const uint32_t row_groups = (a.rows + rows_per_wave - 1) / rows_per_wave;
+    if (item >= row_groups * a.kv_heads) return;
+    const uint32_t kvh = item / row_groups;
+    const uint32_t r0 = (item % row_groups) * rows_per_wave;
+    const uint32_t lr = lane / G, gq = lane % G;
+    const bool active = lr < rows_per_wave && r0 + lr < a.rows;
+    const uint32_t row = active ? r0 + lr : r0;
+    const uint32_t my_pos = a.start + row;
+    const uint32_t last_row = min(r0 + rows_per_wave, a.rows) - 1;
+    const uint32_t n_keys = a.start + last_row + 1;  // wave-uniform
+    const uint32_t qh = kvh * G + gq;
+
+    float q[HD], acc[HD];
+    const float* qp = a.q + static_cast<size_t>(row) * a.ldq + qh * HD;
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(qp + d);
+        q[d] = v.x, q[d + 1] = v.y, q[d + 2] = v.z, q[d + 3] = v.w;
+        acc[d] = acc[d + 1] = acc[d + 2] = acc[d + 3] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    const float* kb = a.kcache + kvh * HD;
+    const float* vb = a.vcache + kvh * HD;
+    for (uint32_t j0 = 0; j0 < n_keys; j0 += kKeyChunk) {
+        float s[kKeyChunk];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kKeyChunk; ++c) {
+            const uint32_t j = j0 + c;
+            float dot = 0.f;
+            if (j < n_keys) {
+                const float* kr = kb + static_cast<size_t>(j) * a.kvdim;
+#pragma unroll
+                for (int d = 0; d < HD; d += 4) {
+                    const float4 kv4 = *reinterpret_cast<const float4*>(kr + d);
+                    dot = fmaf(q[d], kv4.x, dot);
+                    dot = fmaf(q[d + 1], kv4.y, dot);
+                    dot = fmaf(q[d + 2], kv4.z, dot);
+                    dot = fmaf(q[d + 3], kv4.w, dot);
+                }
+            }
+            s[c] = j <= my_pos ? __fmul_rn(dot, a.scale) : -INFINITY;
+            cmax = fmaxf(cmax, s[c]);
+        }
+        const float m_new = fmaxf(m, cmax);
+        const float corr = expf(m - m_new);
+        l *= corr;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) acc[d] *= corr;
+#pragma unroll
+        for (int c = 0; c < kKeyChunk; ++c) {
+            const uint32_t j = j0 + c;
+            if (j < n_keys) {
+                const float e = expf(s[c] - m_new);
+                l += e;
+                const float* vr = vb + static_cast<size_t>(j) * a.kvdim;
+#pragma unroll
+                for (int d = 0; d < HD; d += 4) {
+                    const float4 vv = *reinterpret_cast<const float4*>(vr + d);
+                    acc[d] = fmaf(e, vv.x, acc[d]);
+                    acc[d + 1] = fmaf(e, vv.y, acc[d + 1]);
+                    acc[d + 2] = fmaf(e, vv.z, acc[d + 2]);
+                    acc[d + 3] = fmaf(e, vv.w, acc[d + 3]);
+                }
+            }
+        }
+        m = m_new;
+    }
+    if (!active) return;
+    const float inv = 1.0f / l;
+    float* op = a.out + static_cast<size_t>(row) * a.ldo + qh * HD;
+#pragma unroll
+    for (int d = 0; d < HD; d += 4)
+        *reinterpret_cast<float4*>(op + d) =
+            make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
+}
+
+}  // namespace
+
+hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
+    if (g.M == 0 || g.N == 0) return hipSuccess;
+    const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
+    const dim3 grid((cols + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+    switch (mode) {
+        case kGemmPlain: return vlaunch(gemm_bf16_kernel<kGemmPlain>, grid, dim3(kGemmThreads), 0, s, g);
+        case kGemmResid: return vlaunch(gemm_bf16_kernel<kGemmResid>, grid, dim3(kGemmThreads), 0, s, g);
+        case kGemmGateUp: return vlaunch(gemm_bf16_kernel<kGemmGateUp>, grid, dim3(kGemmThreads), 0, s, g);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s) {
+    const uint32_t waves_per_block = kRowThreads / 64;
+    return vlaunch(row_rms_kernel, dim3((rows + waves_per_block - 1) / waves_per_block), dim3(kRowThreads), 0, s, x,
+                   n, rows, eps, scale);
+}
+
+hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
+                                float* x, hipStream_t s) {
+    return vlaunch(prefill_embed_kernel, dim3((hidden + kRowThreads - 1) / kRowThreads, rows), dim3(kRowThreads), 0,
+                   s, embed, tokens, hidden, x);
+}
+
+hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
+    return vlaunch(prefill_rope_kv_kernel, dim3(a.rows), dim3(kRowThreads), 0, s, a);
+}
+
+hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s) {
+    const uint32_t G = a.heads / a.kv_heads;
+    const uint32_t rows_per_wave = 64 / G;
+    const uint32_t items = (a.rows + rows_per_wave - 1) / rows_per_wave * a.kv_heads;
+    const dim3 grid((items + kAttnThreads / 64 - 1) / (kAttnThreads / 64));
+    switch (hd) {
+        case 32: return vlaunch(prefill_attn_kernel<32>, grid, dim3(kAttnThreads), 0, s, a);
+        case 64: return vlaunch(prefill_attn_kernel<64>, grid, dim3(kAttnThreads), 0, s, a);
+        case 128: return vlaunch(prefill_attn_kernel<128>, grid, dim3(kAttnThreads), 0, s, a);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace vvli

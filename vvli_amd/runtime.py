@@ -198,6 +198,10 @@ class Runner:
         _lib.check(_lib.lib().vvli_gpu_set_decode_path(self._h, {"auto": 0, "graph": 1, "persistent": 2}[path]))
         self._path = path
 
+    def set_prefill_path(self, path: str) -> None:
+        """'auto', 'loop' (one token step per prompt token) or 'batched' (GEMM prefill)."""
+        _lib.check(_lib.lib().vvli_gpu_set_prefill_path(self._h, {"auto": 0, "loop": 1, "batched": 2}[path]))
+
     def prefill(self, tokens, start_pos: int = 0) -> tuple[np.ndarray, int]:
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
         am = c_uint32()
