@@ -124,6 +124,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],
+                    help="prompt processing: batched GEMM prefill, or one token step per prompt token (the reference's loop)")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
@@ -147,15 +149,17 @@ def main() -> int:
           flush=True)
     runner = R.Runner(cfg, blob, args.ctx)
     runner.set_decode_path(args.path)
+    runner.set_prefill_path("auto" if args.prefill == "batched" else "loop")
+    batched = args.prefill == "batched"
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
 
     # Warmup: graph capture, clocks, caches.
-    runner.generate_greedy_measured(prompt[:16], max(1, args.warmup))
+    runner.generate_greedy_measured(prompt[:16], max(1, args.warmup), batched_prefill=batched)
     runner.kv_clear()
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    tokens, stats = runner.generate_greedy_measured(prompt, args.steps)
+    tokens, stats = runner.generate_greedy_measured(prompt, args.steps, batched_prefill=batched)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     persistent = args.path != "graph" and runner.persistent_available()
@@ -251,7 +255,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "llama-3.2-1b bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
-                   "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32",
+                   "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32", "prefill": args.prefill,
                    "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(prefill_tok_s, 2),
         "step_roofline": {"bytes_per_token_avg": step_bytes // args.steps, "achieved": round(step_gbs, 1),

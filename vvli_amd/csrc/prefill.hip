@@ -307,45 +307,51 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
 // ---------------------------------------------------------------------------
 // Causal GQA attention for a chunk of prompt rows (computeAttentionInto,
 // src/llm.zig:1302-1335, for every row at once). One wave per (kv head,
-// group of consecutive rows): lane = (row, q head of the group); each lane
-// keeps its q and its output accumulator in registers and walks the cache
-// rows 0..max position of the wave in chunks of 16 keys with an online
-// softmax (chunk max, one rescale per chunk). Key and value rows are the same
-// for every lane, so their loads are wave-uniform. Keys past a lane's own
-// position are masked out.
+// group of consecutive rows); four lanes per (row, q head) pair, each holding
+// a quarter of head_dim of q and of the output accumulator, so one wave
+// covers 16 pairs (16 / G rows of the G heads sharing the kv head). The wave
+// walks cache rows 0 .. its last row's position in chunks of 16 keys: a dot
+// product is a quarter per lane plus two xor shuffles, then an online softmax
+// (chunk max, one rescale per chunk). Keys past a pair's own position are
+// masked. Waves take the row groups from the last (longest) to the first.
 // ---------------------------------------------------------------------------
 constexpr int kAttnThreads = 256;
 constexpr int kKeyChunk = 16;
+constexpr int kLanesPerPair = 4;
+constexpr int kPairsPerWave = 64 / kLanesPerPair;
 
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnArgs a) {
+    constexpr int DS = HD / kLanesPerPair;  // dims per lane
     const int lane = threadIdx.x & 63;
     const uint32_t item = blockIdx.x * (kAttnThreads / 64) + (threadIdx.x >> 6);
     const uint32_t G = a.heads / a.kv_heads;
-    const uint32_t rows_per_wave = 64 / G;
+    const uint32_t rows_per_wave = kPairsPerWave / G;
     const uint32_t row_groups = (a.rows + rows_per_wave - 1) / rows_per_wave;
     if (item >= row_groups * a.kv_heads) return;
-    const uint32_t kvh = item / row_groups;
-    const uint32_t r0 = (item % row_groups) * rows_per_wave;
-    const uint32_t lr = lane / G, gq = lane % G;
+    const uint32_t kvh = item % a.kv_heads;
+    const uint32_t r0 = (row_groups - 1 - item / a.kv_heads) * rows_per_wave;
+    const uint32_t pair = lane / kLanesPerPair, part = lane % kLanesPerPair;
+    const uint32_t lr = pair / G, gq = pair % G;
     const bool active = lr < rows_per_wave && r0 + lr < a.rows;
     const uint32_t row = active ? r0 + lr : r0;
     const uint32_t my_pos = a.start + row;
     const uint32_t last_row = min(r0 + rows_per_wave, a.rows) - 1;
     const uint32_t n_keys = a.start + last_row + 1;  // wave-uniform
-    const uint32_t qh = kvh * G + gq;
+    const uint32_t qh = kvh * G + (active ? gq : 0);
+    const uint32_t d0 = part * DS;
 
-    float q[HD], acc[HD];
-    const float* qp = a.q + static_cast<size_t>(row) * a.ldq + qh * HD;
+    float q[DS], acc[DS];
+    const float* qp = a.q + static_cast<size_t>(row) * a.ldq + qh * HD + d0;
 #pragma unroll
-    for (int d = 0; d < HD; d += 4) {
+    for (int d = 0; d < DS; d += 4) {
         const float4 v = *reinterpret_cast<const float4*>(qp + d);
         q[d] = v.x, q[d + 1] = v.y, q[d + 2] = v.z, q[d + 3] = v.w;
         acc[d] = acc[d + 1] = acc[d + 2] = acc[d + 3] = 0.f;
     }
     float m = -INFINITY, l = 0.f;
-    const float* kb = a.kcache + kvh * HD;
-    const float* vb = a.vcache + kvh * HD;
+    const float* kb = a.kcache + kvh * HD + d0;
+    const float* vb = a.vcache + kvh * HD + d0;
     for (uint32_t j0 = 0; j0 < n_keys; j0 += kKeyChunk) {
         float s[kKeyChunk];
         float cmax = -INFINITY;
@@ -356,7 +362,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
             if (j < n_keys) {
                 const float* kr = kb + static_cast<size_t>(j) * a.kvdim;
 #pragma unroll
-                for (int d = 0; d < HD; d += 4) {
+                for (int d = 0; d < DS; d += 4) {
                     const float4 kv4 = *reinterpret_cast<const float4*>(kr + d);
                     dot = fmaf(q[d], kv4.x, dot);
                     dot = fmaf(q[d + 1], kv4.y, dot);
@@ -364,6 +370,8 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
                     dot = fmaf(q[d + 3], kv4.w, dot);
                 }
             }
+            dot += __shfl_xor(dot, 1, 64);
+            dot += __shfl_xor(dot, 2, 64);
             s[c] = j <= my_pos ? __fmul_rn(dot, a.scale) : -INFINITY;
             cmax = fmaxf(cmax, s[c]);
         }
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
         const float corr = expf(m - m_new);
         l *= corr;
 #pragma unroll
-        for (int d = 0; d < HD; ++d) acc[d] *= corr;
+        for (int d = 0; d < DS; ++d) acc[d] *= corr;
 #pragma unroll
         for (int c = 0; c < kKeyChunk; ++c) {
             const uint32_t j = j0 + c;
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
                 l += e;
                 const float* vr = vb + static_cast<size_t>(j) * a.kvdim;
 #pragma unroll
-                for (int d = 0; d < HD; d += 4) {
+                for (int d = 0; d < DS; d += 4) {
                     const float4 vv = *reinterpret_cast<const float4*>(vr + d);
                     acc[d] = fmaf(e, vv.x, acc[d]);
                     acc[d + 1] = fmaf(e, vv.y, acc[d + 1]);
@@ -393,9 +401,9 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
     }
     if (!active) return;
     const float inv = 1.0f / l;
-    float* op = a.out + static_cast<size_t>(row) * a.ldo + qh * HD;
+    float* op = a.out + static_cast<size_t>(row) * a.ldo + qh * HD + d0;
 #pragma unroll
-    for (int d = 0; d < HD; d += 4)
+    for (int d = 0; d < DS; d += 4)
         *reinterpret_cast<float4*>(op + d) =
             make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
 }
@@ -432,7 +440,8 @@ hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
 
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s) {
     const uint32_t G = a.heads / a.kv_heads;
-    const uint32_t rows_per_wave = 64 / G;
+    if (G == 0 || G > static_cast<uint32_t>(kPairsPerWave)) return hipErrorInvalidValue;
+    const uint32_t rows_per_wave = kPairsPerWave / G;
     const uint32_t items = (a.rows + rows_per_wave - 1) / rows_per_wave * a.kv_heads;
     const dim3 grid((items + kAttnThreads / 64 - 1) / (kAttnThreads / 64));
     switch (hd) {
