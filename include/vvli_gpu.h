@@ -107,6 +107,24 @@ uint64_t vvli_gpu_storage_element_count(const vvli_gpu_config* cfg);
 int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,
                           size_t blob_elems, vvli_gpu_model** out);
 int vvli_gpu_model_destroy(vvli_gpu_model* model);
+
+/* Mixture-of-experts decoder (OLMoE form). No reference counterpart: the
+ * reference's Config carries num_experts / num_experts_per_tok / qk_norm
+ * (src/llm.zig:86-88) but its runner rejects them (src/llm.zig:218-223,426).
+ * Semantics follow HF transformers' OLMoE: q and k RMS-normalised over their
+ * full width after the projections (cfg->qk_norm), router softmax in f32,
+ * top-k (ties to the lower expert id) without renormalisation, experts
+ * silu(gate) * up then down, summed in ascending expert id with their
+ * probabilities. Blob (dtype bf16 only): embed; per layer input_norm, q,
+ * (q_bias), k, (k_bias), v, (v_bias), (q_norm [hidden], k_norm [kv]), o,
+ * post_norm, router [E][hidden], gate_up [E][2*inter][hidden] (gate rows then
+ * up rows, HF's fused layout), down [E][hidden][inter]; final_norm; lm_head
+ * unless tied; every slice 64-byte aligned. The handle works with every token
+ * entry point below (the per-kernel graph path; prefill runs the token loop).
+ * Limits: <= 256 experts, experts_per_tok <= 16. */
+uint64_t vvli_gpu_moe_storage_element_count(const vvli_gpu_config* cfg);
+int vvli_gpu_moe_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,
+                              size_t blob_elems, vvli_gpu_model** out);
 /* KVCache.clear, src/llm.zig:576-579. */
 int vvli_gpu_kv_clear(vvli_gpu_model* model);
 /* Replace the RoPE inverse-frequency table (n = head_dim/2). NULL restores

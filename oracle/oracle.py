@@ -45,6 +45,18 @@ class OrcLayerOffsets(ctypes.Structure):
                 ("input_norm", "q", "q_bias", "k", "k_bias", "v", "v_bias", "o", "post_norm", "gate", "up", "down")]
 
 
+class OrcMoeConfig(ctypes.Structure):
+    _fields_ = [("base", OrcConfig), ("experts", c_uint32), ("top_k", c_uint32), ("qk_norm", c_uint32)]
+
+
+MOE_SLOTS = ("input_norm", "q", "q_bias", "k", "k_bias", "v", "v_bias", "q_norm", "k_norm", "o", "post_norm", "router",
+             "gate_up", "down")
+
+
+class OrcMoeLayerOffsets(ctypes.Structure):
+    _fields_ = [(n, c_size_t) for n in MOE_SLOTS]
+
+
 class OrcStats(ctypes.Structure):
     _fields_ = [("prompt_tokens", c_uint64), ("generated_tokens", c_uint64), ("prefill_ns", c_int64),
                 ("decode_ns", c_int64), ("total_ns", c_int64)]
@@ -92,6 +104,14 @@ def lib() -> ctypes.CDLL:
             "orc_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
             "orc_generate_greedy": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_int64, c_void_p, P(c_uint32),
                                             P(OrcStats)]),
+            "orc_moe_layout": (c_size_t, [P(OrcMoeConfig), c_void_p, P(c_size_t), P(c_size_t), P(c_size_t)]),
+            "orc_moe_rmsnorm": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_size_t, c_float]),
+            "orc_moe_route": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+            "orc_moe_runner_create": (c_int, [P(OrcMoeConfig), c_void_p, c_size_t, c_uint32, c_int, c_int,
+                                              P(c_void_p)]),
+            "orc_moe_runner_destroy": (None, [c_void_p]),
+            "orc_moe_forward_token": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]),
+            "orc_moe_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
             "orc_adjusted_logit": (c_float, [c_float, c_uint16, c_float]),
             "orc_greedy_with_penalties": (c_uint32, [c_void_p, c_void_p, c_size_t, c_float]),
         }
@@ -296,6 +316,84 @@ class OracleRunner:
         _check(lib().orc_generate_greedy(self._h, _p(p), p.size, max_new, -1 if eos is None else eos, _p(out),
                                          byref(n), byref(st)))
         return out[: n.value].copy(), st
+
+
+def orc_moe_config(cfg, weight_kind: int) -> OrcMoeConfig:
+    return OrcMoeConfig(orc_config(cfg, weight_kind), cfg.num_experts, cfg.num_experts_per_token, int(cfg.qk_norm))
+
+
+def moe_layout(cfg, weight_kind: int) -> dict:
+    c = orc_moe_config(cfg, weight_kind)
+    arr = (OrcMoeLayerOffsets * cfg.num_hidden_layers)()
+    e, fn, lm = c_size_t(), c_size_t(), c_size_t()
+    total = lib().orc_moe_layout(byref(c), arr, byref(e), byref(fn), byref(lm))
+    none = (1 << 64) - 1
+    layers = [{k: (None if getattr(a, k) == none else getattr(a, k)) for k in MOE_SLOTS} for a in arr]
+    return {"embed": e.value, "final_norm": fn.value, "lm_head": None if lm.value == none else lm.value,
+            "layers": layers, "total": int(total)}
+
+
+def moe_route(logits: np.ndarray, top_k: int):
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    idx = np.zeros(top_k, dtype=np.uint32)
+    w = np.zeros(top_k, dtype=np.float32)
+    lib().orc_moe_route(_p(lg), lg.size, top_k, _p(idx), _p(w))
+    return idx, w
+
+
+class OracleMoeRunner:
+    """CPU restatement of the MoE (OLMoE-form) token step; borrows ``blob``."""
+
+    def __init__(self, cfg, blob: np.ndarray, max_seq_len: int, threads: int = 0, lanes: int = 16):
+        self.cfg = cfg
+        self.blob = np.ascontiguousarray(blob)
+        kind = 1 if self.blob.dtype == np.uint16 else 0
+        self._c = orc_moe_config(cfg, kind)
+        h = c_void_p()
+        _check(lib().orc_moe_runner_create(byref(self._c), _p(self.blob), self.blob.size, max_seq_len, threads, lanes,
+                                           byref(h)))
+        self._h = h
+        self.logits = np.zeros(cfg.vocab_size, dtype=np.float32)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().orc_moe_runner_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward_token(self, token: int, pos: int, want_hidden: bool = False):
+        L = self.cfg.num_hidden_layers
+        hidden = np.zeros((L, self.cfg.hidden_size), dtype=np.float32) if want_hidden else None
+        experts = np.zeros((L, self.cfg.num_experts_per_token), dtype=np.uint32) if want_hidden else None
+        _check(lib().orc_moe_forward_token(self._h, token, pos, _p(self.logits), _p(hidden), _p(experts)))
+        return (self.logits.copy(), hidden, experts) if want_hidden else self.logits.copy()
+
+    def kv_read(self, layer: int, pos: int):
+        kv = self.cfg.kv_dim()
+        k = np.zeros(kv, dtype=np.float32)
+        v = np.zeros(kv, dtype=np.float32)
+        _check(lib().orc_moe_kv_read(self._h, layer, pos, _p(k), _p(v)))
+        return k, v
+
+    def generate_greedy(self, prompt, max_new: int):
+        """The generator loop (src/generator.zig:243-293) over this step: prompt
+        token by token, then the argmax of each step is emitted and forwarded."""
+        pos, logits = 0, None
+        for t in prompt:
+            logits = self.forward_token(int(t), pos)
+            pos += 1
+        out = []
+        for i in range(max_new):
+            tok = int(lib().orc_argmax(_p(logits), logits.size))
+            out.append(tok)
+            logits = self.forward_token(tok, pos)
+            pos += 1
+        return np.array(out, dtype=np.uint32)
 
 
 def cpu_count() -> int:

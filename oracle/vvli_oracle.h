@@ -134,6 +134,32 @@ typedef struct orc_stats {
 int orc_generate_greedy(orc_runner* r, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
                         uint32_t* out_tokens, uint32_t* n_out, orc_stats* stats);
 
+/* ---- mixture-of-experts step (vvli_oracle_moe.c; no reference counterpart:
+ * HF OLMoE semantics, see that file's header) ---- */
+typedef struct orc_moe_config {
+    orc_config base;  /* inter = per-expert intermediate size */
+    uint32_t experts, top_k, qk_norm;
+} orc_moe_config;
+typedef struct orc_moe_layer_offsets {
+    size_t input_norm, q, q_bias, k, k_bias, v, v_bias, q_norm, k_norm, o, post_norm, router, gate_up, down;
+} orc_moe_layer_offsets;
+/* Blob: embed; per layer input_norm, q, (q_bias), k, (k_bias), v, (v_bias),
+ * (q_norm [hidden], k_norm [kv]), o, post_norm, router [E][H], gate_up
+ * [E][2I][H] (gate rows then up rows), down [E][H][I]; final_norm; lm_head
+ * unless tied. Each slice 64-byte aligned. Returns the element count. */
+size_t orc_moe_layout(const orc_moe_config* c, orc_moe_layer_offsets* layers, size_t* embed, size_t* final_norm,
+                      size_t* lm_head);
+void orc_moe_rmsnorm(float* out, const float* x, const void* w, uint32_t kind, size_t n, float eps);
+void orc_moe_route(const float* logits, size_t n, size_t top_k, uint32_t* idx, float* weights);
+typedef struct orc_moe_runner orc_moe_runner;
+int orc_moe_runner_create(const orc_moe_config* c, const void* blob, size_t blob_elems, uint32_t max_seq_len,
+                          int threads, int lanes, orc_moe_runner** out);
+void orc_moe_runner_destroy(orc_moe_runner* r);
+/* experts_out: layers*top_k selected expert ids (nullable). */
+int orc_moe_forward_token(orc_moe_runner* r, uint32_t token, uint32_t pos, float* logits_out, float* hidden_out,
+                          uint32_t* experts_out);
+int orc_moe_kv_read(const orc_moe_runner* r, uint32_t layer, uint32_t pos, float* k_out, float* v_out);
+
 /* ---- sampler pieces: src/generator.zig:338-463 ---- */
 float orc_adjusted_logit(float logit, uint16_t repeat_count, float repeat_penalty);
 uint32_t orc_greedy_with_penalties(const float* logits, const uint16_t* counts, size_t n, float repeat_penalty);

@@ -94,6 +94,8 @@ PROTOTYPES = {
     "vvli_gpu_storage_element_count": (c_uint64, [POINTER(CConfig)]),
     "vvli_gpu_model_create": (c_int, [POINTER(CConfig), c_uint32, c_void_p, c_size_t, POINTER(c_void_p)]),
     "vvli_gpu_model_destroy": (c_int, [c_void_p]),
+    "vvli_gpu_moe_storage_element_count": (c_uint64, [POINTER(CConfig)]),
+    "vvli_gpu_moe_model_create": (c_int, [POINTER(CConfig), c_uint32, c_void_p, c_size_t, POINTER(c_void_p)]),
     "vvli_gpu_kv_clear": (c_int, [c_void_p]),
     "vvli_gpu_set_rope_table": (c_int, [c_void_p, c_void_p, c_uint32]),
     "vvli_gpu_forward_token": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, POINTER(c_uint32)]),

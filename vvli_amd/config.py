@@ -82,7 +82,11 @@ class Config:
         return int(_lib.lib().vvli_gpu_parameter_count(ctypes.byref(self.to_c())))
 
     def storage_element_count(self, weight_kind: int = WEIGHT_BF16) -> int:
-        return int(_lib.lib().vvli_gpu_storage_element_count(ctypes.byref(self.to_c(weight_kind))))
+        """Blob elements: the dense layout (storageElementCount, src/llm.zig:814-837),
+        or the MoE layout of vvli_gpu_moe_storage_element_count for MoE configs."""
+        fn = (_lib.lib().vvli_gpu_moe_storage_element_count if self.num_experts
+              else _lib.lib().vvli_gpu_storage_element_count)
+        return int(fn(ctypes.byref(self.to_c(weight_kind))))
 
     @classmethod
     def from_c(cls, c: _lib.CConfig) -> "Config":
@@ -214,9 +218,35 @@ def qwen25_7b() -> Config:
     )
 
 
+def olmoe_1b_7b() -> Config:
+    """OLMoE-1B-7B shape: 16 layers, hidden 2048, 16/16 heads (hd 128), 64
+    experts x inter 1024, top-8, QK-norm, vocab 50304, untied."""
+    return Config(
+        architecture="olmoe",
+        vocab_size=50304,
+        hidden_size=2048,
+        intermediate_size=1024,
+        num_hidden_layers=16,
+        num_attention_heads=16,
+        num_key_value_heads=16,
+        max_position_embeddings=4096,
+        rope_theta=10_000.0,
+        rms_norm_eps=1e-5,
+        tie_word_embeddings=False,
+        qkv_bias=False,
+        rope_layout=ROPE_SPLIT_HALF,
+        num_experts=64,
+        num_experts_per_token=8,
+        qk_norm=True,
+        eos_token_id=50279,
+        pad_token_id=1,
+    )
+
+
 NAMED = {
     "tiny": tiny_test,
     "qwen2.5-0.5b": qwen25_05b,
     "llama-3.2-1b": llama32_1b,
     "qwen2.5-7b": qwen25_7b,
+    "olmoe-1b-7b": olmoe_1b_7b,
 }

@@ -92,6 +92,41 @@ BlobLayout compute_layout(const vvli_gpu_config& c) {
     return L;
 }
 
+MoeLayout compute_moe_layout(const vvli_gpu_config& c) {
+    const size_t ea = kAlignBytes / elem_bytes(c);
+    const size_t h = c.hidden, kv = kv_dim(c), inter = c.inter, e = c.num_experts;
+    size_t cur = 0;
+    auto take = [&](size_t len) {
+        cur = (cur + ea - 1) / ea * ea;
+        size_t s = cur;
+        cur += len;
+        return s;
+    };
+    MoeLayout L;
+    L.embed = take(static_cast<size_t>(c.vocab) * h);
+    L.layers.resize(c.layers);
+    for (auto& s : L.layers) {
+        s.input_norm = take(h);
+        s.q = take(h * h);
+        s.q_bias = c.qkv_bias ? take(h) : kNone;
+        s.k = take(kv * h);
+        s.k_bias = c.qkv_bias ? take(kv) : kNone;
+        s.v = take(kv * h);
+        s.v_bias = c.qkv_bias ? take(kv) : kNone;
+        s.q_norm = c.qk_norm ? take(h) : kNone;
+        s.k_norm = c.qk_norm ? take(kv) : kNone;
+        s.o = take(h * h);
+        s.post_norm = take(h);
+        s.router = take(e * h);
+        s.gate_up = take(e * 2 * inter * h);
+        s.down = take(e * h * inter);
+    }
+    L.final_norm = take(h);
+    L.lm_head = c.tie ? kNone : take(static_cast<size_t>(c.vocab) * h);
+    L.total = cur;
+    return L;
+}
+
 }  // namespace vvli
 
 extern "C" {
@@ -110,6 +145,11 @@ uint64_t vvli_gpu_parameter_count(const vvli_gpu_config* cfg) { return cfg ? vvl
 uint64_t vvli_gpu_storage_element_count(const vvli_gpu_config* cfg) {
     if (!cfg || cfg->num_experts != 0) return 0;
     return vvli::compute_layout(*cfg).total;
+}
+
+uint64_t vvli_gpu_moe_storage_element_count(const vvli_gpu_config* cfg) {
+    if (!cfg || cfg->num_experts == 0) return 0;
+    return vvli::compute_moe_layout(*cfg).total;
 }
 
 }  // extern "C"

@@ -64,14 +64,47 @@ double vvli_host_synthetic_normal(uint64_t seed, uint64_t tensor_id, uint64_t in
 int vvli_host_fill_synthetic(const vvli_gpu_config* cfg, uint64_t seed, float stddev, void* blob, size_t blob_elems,
                              uint32_t threads) {
     if (!cfg || !blob) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_host_fill_synthetic");
-    int rc = validate_config(*cfg, true);
+    const bool moe = cfg->num_experts != 0;
+    int rc = validate_config(*cfg, !moe);
     if (rc) return rc;
-    const BlobLayout L = compute_layout(*cfg);
-    if (blob_elems < L.total) return set_error(VVLI_INVALID_WEIGHT, "blob too small for the layout");
     const size_t h = cfg->hidden, kv = kv_dim(*cfg), inter = cfg->inter;
     std::vector<Slice> slices;
-    slices.push_back({L.embed, static_cast<size_t>(cfg->vocab) * h, 0, false});
-    for (uint32_t l = 0; l < cfg->layers; ++l) {
+    size_t total = 0;
+    if (moe) {
+        const MoeLayout M = compute_moe_layout(*cfg);
+        if (blob_elems < M.total) return set_error(VVLI_INVALID_WEIGHT, "blob too small for the layout");
+        total = M.total;
+        const size_t e = cfg->num_experts;
+        slices.push_back({M.embed, static_cast<size_t>(cfg->vocab) * h, 0, false});
+        for (uint32_t l = 0; l < cfg->layers; ++l) {
+            const MoeLayerSlices& s = M.layers[l];
+            const uint64_t b = 1 + 16ull * l;
+            slices.push_back({s.input_norm, h, b + 0, true});
+            slices.push_back({s.q, h * h, b + 1, false});
+            if (s.q_bias != kNone) slices.push_back({s.q_bias, h, b + 2, false});
+            slices.push_back({s.k, kv * h, b + 3, false});
+            if (s.k_bias != kNone) slices.push_back({s.k_bias, kv, b + 4, false});
+            slices.push_back({s.v, kv * h, b + 5, false});
+            if (s.v_bias != kNone) slices.push_back({s.v_bias, kv, b + 6, false});
+            if (s.q_norm != kNone) slices.push_back({s.q_norm, h, b + 7, true});
+            if (s.k_norm != kNone) slices.push_back({s.k_norm, kv, b + 8, true});
+            slices.push_back({s.o, h * h, b + 9, false});
+            slices.push_back({s.post_norm, h, b + 10, true});
+            slices.push_back({s.router, e * h, b + 11, false});
+            slices.push_back({s.gate_up, e * 2 * inter * h, b + 12, false});
+            slices.push_back({s.down, e * h * inter, b + 13, false});
+        }
+        slices.push_back({M.final_norm, h, 1 + 16ull * cfg->layers, true});
+        if (M.lm_head != kNone)
+            slices.push_back({M.lm_head, static_cast<size_t>(cfg->vocab) * h, 2 + 16ull * cfg->layers, false});
+    }
+    const BlobLayout L = moe ? BlobLayout{} : compute_layout(*cfg);
+    if (!moe && blob_elems < L.total) return set_error(VVLI_INVALID_WEIGHT, "blob too small for the layout");
+    if (!moe) {
+        total = L.total;
+        slices.push_back({L.embed, static_cast<size_t>(cfg->vocab) * h, 0, false});
+    }
+    for (uint32_t l = 0; !moe && l < cfg->layers; ++l) {
         const LayerSlices& s = L.layers[l];
         const uint64_t b = 1 + 12ull * l;
         slices.push_back({s.input_norm, h, b + 0, true});
@@ -87,12 +120,15 @@ int vvli_host_fill_synthetic(const vvli_gpu_config* cfg, uint64_t seed, float st
         slices.push_back({s.up, inter * h, b + 10, false});
         slices.push_back({s.down, h * inter, b + 11, false});
     }
-    slices.push_back({L.final_norm, h, 1 + 12ull * cfg->layers, true});
-    if (L.lm_head != kNone) slices.push_back({L.lm_head, static_cast<size_t>(cfg->vocab) * h, 2 + 12ull * cfg->layers, false});
+    if (!moe) {
+        slices.push_back({L.final_norm, h, 1 + 12ull * cfg->layers, true});
+        if (L.lm_head != kNone)
+            slices.push_back({L.lm_head, static_cast<size_t>(cfg->vocab) * h, 2 + 12ull * cfg->layers, false});
+    }
 
     const bool bf16 = cfg->weight_kind == VVLI_WEIGHT_BF16;
     const size_t eb = bf16 ? 2 : 4;
-    std::memset(blob, 0, L.total * eb);  // alignment padding
+    std::memset(blob, 0, total * eb);  // alignment padding
     unsigned nt = threads ? threads : std::thread::hardware_concurrency();
     if (nt == 0) nt = 1;
     // Work items: fixed-size chunks of every slice.

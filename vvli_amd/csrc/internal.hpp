@@ -32,9 +32,22 @@ struct BlobLayout {
     std::vector<LayerSlices> layers;
 };
 
+// Mixture-of-experts blob (no reference counterpart: the reference rejects
+// MoE configs). Per layer: input_norm, q, (q_bias), k, (k_bias), v, (v_bias),
+// (q_norm [H], k_norm [kv]), o, post_norm, router [E][H], gate_up [E][2I][H]
+// (gate rows, then up rows), down [E][H][I]; each slice 64-byte aligned.
+struct MoeLayerSlices {
+    size_t input_norm, q, q_bias, k, k_bias, v, v_bias, q_norm, k_norm, o, post_norm, router, gate_up, down;
+};
+struct MoeLayout {
+    size_t embed = 0, final_norm = 0, lm_head = kNone, total = 0;
+    std::vector<MoeLayerSlices> layers;
+};
+
 int validate_config(const vvli_gpu_config& c, bool require_dense);
 uint64_t parameter_count(const vvli_gpu_config& c);
 BlobLayout compute_layout(const vvli_gpu_config& c);
+MoeLayout compute_moe_layout(const vvli_gpu_config& c);
 
 // bf16 <-> f32 (src/llm.zig:791-803).
 inline float bf16_to_f32(uint16_t b) {

@@ -238,4 +238,28 @@ struct PrefillAttnArgs {
 };
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// Mixture-of-experts step pieces (moe.hip).
+// ---------------------------------------------------------------------------
+constexpr int kMaxTopK = 16;
+
+struct MoeGemvArgs {
+    const uint16_t* w = nullptr;         // GateUp: [E][2 rows_per_slot][K]; Down: [E][rows_per_slot][K]
+    const uint32_t* experts = nullptr;   // [top_k] expert ids (device)
+    uint32_t top_k = 0, rows_per_slot = 0, K = 0;
+    const float* x = nullptr;            // GateUp: residual stream (K); Down: activations (top_k * K)
+    uint32_t x_len = 0;
+    const uint16_t* norm_w = nullptr;    // GateUp: post-attention RMSNorm weight
+    float eps = 0.f;
+    float* out = nullptr;                // [top_k * rows_per_slot]
+};
+hipError_t launch_qk_norm(float* q, const uint16_t* wq, uint32_t nq, float* k, const uint16_t* wk, uint32_t nk,
+                          float eps, hipStream_t s);
+hipError_t launch_moe_route(const float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight,
+                            hipStream_t s);
+hipError_t moe_gemv_init_attributes();
+hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s);  // kGemvGateUp or kGemvPlain (down)
+hipError_t launch_moe_combine(float* x, const float* partial, const uint32_t* idx, const float* w, uint32_t top_k,
+                              uint32_t H, hipStream_t s);
+
 }  // namespace vvli

@@ -69,6 +69,13 @@ struct vvli_gpu_model {
     bool mk_pending = false;      // a persistent launch ran since the last error check
     hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last persistent launch
     bool mk_timed = false;
+    // Mixture-of-experts model (vvli_gpu_moe_model_create).
+    bool moe = false;
+    MoeLayout moe_layout;
+    float* moe_router = nullptr;   // [E] router logits
+    uint32_t* moe_idx = nullptr;   // [top_k] selected experts
+    float* moe_w = nullptr;        // [top_k] their probabilities
+    float* moe_part = nullptr;     // [top_k][H] expert outputs
     // Batched prefill (bf16 only): chunk buffers, allocated on first use.
     bool pf_ok = false;
     uint32_t prefill_path = 0;  // 0 auto, 1 token loop, 2 batched
@@ -99,7 +106,10 @@ const void* wslice(const vvli_gpu_model* m, size_t off) {
 int init_once() {
     static std::once_flag flag;
     static hipError_t err = hipSuccess;
-    std::call_once(flag, [] { err = gemv_init_attributes(); });
+    std::call_once(flag, [] {
+        err = gemv_init_attributes();
+        if (err == hipSuccess) err = moe_gemv_init_attributes();
+    });
     HIP_TRY(err);
     return VVLI_OK;
 }
@@ -140,97 +150,153 @@ int check_kernel_shapes(const vvli_gpu_config& c) {
 
 int enqueue_logits(vvli_gpu_model* m, hipStream_t s);
 
-// The layers, final norm and logits of one step (embedding already in x).
-int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+// Slices of the attention half of a layer (dense and MoE blobs share it).
+struct AttnSlices {
+    size_t input_norm, q, q_bias, k, k_bias, v, v_bias, q_norm, k_norm, o;
+};
+
+// input RMSNorm + q/k/v (+ bias) [+ q/k RMSNorm] + RoPE + KV append +
+// attention + o_proj with the residual add, for layer l.
+int enqueue_attention_half(vvli_gpu_model* m, hipStream_t s, uint32_t l, const AttnSlices& L) {
     const vvli_gpu_config& c = m->cfg;
     const int kind = static_cast<int>(c.weight_kind);
-    const uint32_t H = c.hidden, kv = kv_dim(c), I = c.inter, hd = head_dim(c);
+    const uint32_t H = c.hidden, kv = kv_dim(c), hd = head_dim(c);
     float* q = m->qkv;
     float* kn = m->qkv + H;
     float* vn = m->qkv + H + kv;
     const uint32_t rplain = gemv_rows_per_block(kGemvPlain);
     const bool stack = (H % rplain == 0) && (kv % rplain == 0);
-    for (uint32_t l = 0; l < c.layers; ++l) {
-        const LayerSlices& L = m->layout.layers[l];
-        // 1. input RMSNorm + q/k/v projections (+ bias).
-        GemvArgs g;
-        g.x = m->x;
-        g.norm_w = wslice(m, L.input_norm);
-        g.eps = c.rms_eps;
-        g.K = H;
-        if (stack) {
-            g.w[0] = wslice(m, L.q);
-            g.w[1] = wslice(m, L.k);
-            g.w[2] = wslice(m, L.v);
-            g.bias[0] = wslice(m, L.q_bias);
-            g.bias[1] = wslice(m, L.k_bias);
-            g.bias[2] = wslice(m, L.v_bias);
-            g.out[0] = q;
-            g.out[1] = kn;
-            g.out[2] = vn;
-            g.rows[0] = H;
-            g.rows[1] = kv;
-            g.rows[2] = kv;
-            LAUNCH(launch_gemv(kind, kGemvPlain, g, s));
-        } else {
-            const size_t wo[3] = {L.q, L.k, L.v}, bo[3] = {L.q_bias, L.k_bias, L.v_bias};
-            float* outs[3] = {q, kn, vn};
-            const uint32_t rows[3] = {H, kv, kv};
-            for (int i = 0; i < 3; ++i) {
-                GemvArgs gi = g;
-                gi.w[0] = wslice(m, wo[i]);
-                gi.bias[0] = wslice(m, bo[i]);
-                gi.out[0] = outs[i];
-                gi.rows[0] = rows[i];
-                LAUNCH(launch_gemv(kind, kGemvPlain, gi, s));
-            }
+    // 1. input RMSNorm + q/k/v projections (+ bias).
+    GemvArgs g;
+    g.x = m->x;
+    g.norm_w = wslice(m, L.input_norm);
+    g.eps = c.rms_eps;
+    g.K = H;
+    if (stack) {
+        g.w[0] = wslice(m, L.q);
+        g.w[1] = wslice(m, L.k);
+        g.w[2] = wslice(m, L.v);
+        g.bias[0] = wslice(m, L.q_bias);
+        g.bias[1] = wslice(m, L.k_bias);
+        g.bias[2] = wslice(m, L.v_bias);
+        g.out[0] = q;
+        g.out[1] = kn;
+        g.out[2] = vn;
+        g.rows[0] = H;
+        g.rows[1] = kv;
+        g.rows[2] = kv;
+        LAUNCH(launch_gemv(kind, kGemvPlain, g, s));
+    } else {
+        const size_t wo[3] = {L.q, L.k, L.v}, bo[3] = {L.q_bias, L.k_bias, L.v_bias};
+        float* outs[3] = {q, kn, vn};
+        const uint32_t rows[3] = {H, kv, kv};
+        for (int i = 0; i < 3; ++i) {
+            GemvArgs gi = g;
+            gi.w[0] = wslice(m, wo[i]);
+            gi.bias[0] = wslice(m, bo[i]);
+            gi.out[0] = outs[i];
+            gi.rows[0] = rows[i];
+            LAUNCH(launch_gemv(kind, kGemvPlain, gi, s));
         }
-        // 2. RoPE + KV append + attention.
-        AttnArgs a;
-        a.q = q;
-        a.k_new = kn;
-        a.v_new = vn;
-        a.kcache = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
-        a.vcache = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
-        a.pos = &m->state->pos;
-        a.rope_cs = m->rope_cs;
-        a.part = m->part;
-        a.counters = m->counters;
-        a.out = m->attn;
-        a.heads = c.heads;
-        a.kv_heads = c.kv_heads;
-        a.hd = hd;
-        a.nsplit = m->nsplit;
-        a.rope_layout = c.rope_layout;
-        a.scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/llm.zig:1313
-        LAUNCH(launch_attn_decode(a, s));
-        // 3. x += Wo . attn
-        GemvArgs go;
-        go.w[0] = wslice(m, L.o);
-        go.out[0] = m->x;
-        go.rows[0] = H;
-        go.x = m->attn;
-        go.K = H;
-        LAUNCH(launch_gemv(kind, kGemvResid, go, s));
-        // 4. post-attention RMSNorm + gate/up + SwiGLU.
-        GemvArgs gu;
-        gu.w[0] = wslice(m, L.gate);
-        gu.w_up = wslice(m, L.up);
-        gu.out[0] = m->ff;
-        gu.rows[0] = I;
-        gu.x = m->x;
-        gu.norm_w = wslice(m, L.post_norm);
-        gu.eps = c.rms_eps;
-        gu.K = H;
-        LAUNCH(launch_gemv(kind, kGemvGateUp, gu, s));
-        // 5. x += Wd . ff
-        GemvArgs gd;
-        gd.w[0] = wslice(m, L.down);
-        gd.out[0] = m->x;
-        gd.rows[0] = H;
-        gd.x = m->ff;
-        gd.K = I;
-        LAUNCH(launch_gemv(kind, kGemvResid, gd, s));
+    }
+    // QK-norm over the full q and k (MoE models that carry it).
+    if (L.q_norm != kNone)
+        LAUNCH(launch_qk_norm(q, static_cast<const uint16_t*>(wslice(m, L.q_norm)), H, kn,
+                              static_cast<const uint16_t*>(wslice(m, L.k_norm)), kv, c.rms_eps, s));
+    // 2. RoPE + KV append + attention.
+    AttnArgs a;
+    a.q = q;
+    a.k_new = kn;
+    a.v_new = vn;
+    a.kcache = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
+    a.vcache = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
+    a.pos = &m->state->pos;
+    a.rope_cs = m->rope_cs;
+    a.part = m->part;
+    a.counters = m->counters;
+    a.out = m->attn;
+    a.heads = c.heads;
+    a.kv_heads = c.kv_heads;
+    a.hd = hd;
+    a.nsplit = m->nsplit;
+    a.rope_layout = c.rope_layout;
+    a.scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/llm.zig:1313
+    LAUNCH(launch_attn_decode(a, s));
+    // 3. x += Wo . attn
+    GemvArgs go;
+    go.w[0] = wslice(m, L.o);
+    go.out[0] = m->x;
+    go.rows[0] = H;
+    go.x = m->attn;
+    go.K = H;
+    LAUNCH(launch_gemv(kind, kGemvResid, go, s));
+    return VVLI_OK;
+}
+
+// Router + top-k + selected experts + weighted combine into x (MoE layer l).
+int enqueue_moe_ffn(vvli_gpu_model* m, hipStream_t s, uint32_t l) {
+    const vvli_gpu_config& c = m->cfg;
+    const MoeLayerSlices& L = m->moe_layout.layers[l];
+    const uint32_t H = c.hidden, I = c.inter, E = c.num_experts, K = c.experts_per_tok;
+    auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+    GemvArgs gr;
+    gr.w[0] = wslice(m, L.router);
+    gr.out[0] = m->moe_router;
+    gr.rows[0] = E;
+    gr.x = m->x;
+    gr.norm_w = wslice(m, L.post_norm);
+    gr.eps = c.rms_eps;
+    gr.K = H;
+    LAUNCH(launch_gemv(static_cast<int>(c.weight_kind), kGemvPlain, gr, s));
+    LAUNCH(launch_moe_route(m->moe_router, E, K, m->moe_idx, m->moe_w, s));
+    MoeGemvArgs gu;
+    gu.w = w16(L.gate_up), gu.experts = m->moe_idx, gu.top_k = K, gu.rows_per_slot = I, gu.K = H;
+    gu.x = m->x, gu.x_len = H, gu.norm_w = w16(L.post_norm), gu.eps = c.rms_eps, gu.out = m->ff;
+    LAUNCH(launch_moe_gemv(kGemvGateUp, gu, s));
+    MoeGemvArgs gd;
+    gd.w = w16(L.down), gd.experts = m->moe_idx, gd.top_k = K, gd.rows_per_slot = H, gd.K = I;
+    gd.x = m->ff, gd.x_len = K * I, gd.out = m->moe_part;
+    LAUNCH(launch_moe_gemv(kGemvPlain, gd, s));
+    LAUNCH(launch_moe_combine(m->x, m->moe_part, m->moe_idx, m->moe_w, K, H, s));
+    return VVLI_OK;
+}
+
+// The layers, final norm and logits of one step (embedding already in x).
+int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+    const vvli_gpu_config& c = m->cfg;
+    const int kind = static_cast<int>(c.weight_kind);
+    const uint32_t H = c.hidden, I = c.inter;
+    int rc;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        if (m->moe) {
+            const MoeLayerSlices& L = m->moe_layout.layers[l];
+            const AttnSlices as{L.input_norm, L.q, L.q_bias, L.k, L.k_bias, L.v, L.v_bias, L.q_norm, L.k_norm, L.o};
+            if ((rc = enqueue_attention_half(m, s, l, as))) return rc;
+            if ((rc = enqueue_moe_ffn(m, s, l))) return rc;
+        } else {
+            const LayerSlices& L = m->layout.layers[l];
+            const AttnSlices as{L.input_norm, L.q, L.q_bias, L.k, L.k_bias, L.v, L.v_bias, kNone, kNone, L.o};
+            if ((rc = enqueue_attention_half(m, s, l, as))) return rc;
+            // 4. post-attention RMSNorm + gate/up + SwiGLU.
+            GemvArgs gu;
+            gu.w[0] = wslice(m, L.gate);
+            gu.w_up = wslice(m, L.up);
+            gu.out[0] = m->ff;
+            gu.rows[0] = I;
+            gu.x = m->x;
+            gu.norm_w = wslice(m, L.post_norm);
+            gu.eps = c.rms_eps;
+            gu.K = H;
+            LAUNCH(launch_gemv(kind, kGemvGateUp, gu, s));
+            // 5. x += Wd . ff
+            GemvArgs gd;
+            gd.w[0] = wslice(m, L.down);
+            gd.out[0] = m->x;
+            gd.rows[0] = H;
+            gd.x = m->ff;
+            gd.K = I;
+            LAUNCH(launch_gemv(kind, kGemvResid, gd, s));
+        }
         if (hidden_dbg)
             HIP_TRY(hipMemcpyAsync(hidden_dbg + static_cast<size_t>(l) * H, m->x, H * sizeof(float),
                                    hipMemcpyDeviceToDevice, s));
@@ -412,7 +478,9 @@ bool prefill_supported(const vvli_gpu_config& c) {
     return c.weight_kind == VVLI_WEIGHT_BF16 && (hd == 32 || hd == 64 || hd == 128);
 }
 
-bool use_batched_prefill(const vvli_gpu_model* m) { return m->prefill_path != 1 && prefill_supported(m->cfg); }
+bool use_batched_prefill(const vvli_gpu_model* m) {
+    return m->prefill_path != 1 && !m->moe && prefill_supported(m->cfg);
+}
 
 int ensure_prefill_buffers(vvli_gpu_model* m) {
     if (m->pf_scale) return VVLI_OK;
@@ -509,7 +577,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale};
+                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_part};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -527,12 +595,21 @@ int dmalloc(T** p, size_t count) {
 }
 
 int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob, size_t blob_elems,
-                vvli_gpu_model** out) {
+                vvli_gpu_model** out, bool moe) {
     if (!cfg || !host_blob || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create");
     *out = nullptr;
-    int rc = validate_config(*cfg, true);
+    int rc = validate_config(*cfg, !moe);
     if (rc) return rc;
     if ((rc = check_kernel_shapes(*cfg))) return rc;
+    if (moe) {
+        if (cfg->num_experts == 0) return set_error(VVLI_INVALID_CONFIG, "MoE model with num_experts = 0");
+        if (cfg->weight_kind != VVLI_WEIGHT_BF16) return set_error(VVLI_UNSUPPORTED_DTYPE, "MoE models need bf16 weights");
+        if (cfg->num_experts > 256 || cfg->experts_per_tok > static_cast<uint32_t>(kMaxTopK))
+            return set_error(VVLI_INVALID_CONFIG, "MoE kernels take up to 256 experts and top-%d", kMaxTopK);
+        if (static_cast<size_t>(cfg->experts_per_tok) * cfg->inter * sizeof(float) > 150 * 1024)
+            return set_error(VVLI_INVALID_CONFIG, "experts_per_tok * intermediate must fit LDS (%u * %u)",
+                             cfg->experts_per_tok, cfg->inter);
+    }
     if (max_seq_len == 0 || max_seq_len > cfg->max_pos)  // KVCache.init, src/llm.zig:548
         return set_error(VVLI_INVALID_CONFIG, "max_seq_len %u not in 1..%u", max_seq_len, cfg->max_pos);
     if ((rc = init_once())) return rc;
@@ -540,7 +617,16 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     auto* m = new vvli_gpu_model();
     m->cfg = *cfg;
     m->max_seq = max_seq_len;
-    m->layout = compute_layout(*cfg);
+    m->moe = moe;
+    if (moe) {
+        m->moe_layout = compute_moe_layout(*cfg);
+        m->layout.embed = m->moe_layout.embed;
+        m->layout.final_norm = m->moe_layout.final_norm;
+        m->layout.lm_head = m->moe_layout.lm_head;
+        m->layout.total = m->moe_layout.total;
+    } else {
+        m->layout = compute_layout(*cfg);
+    }
     m->ebytes = elem_bytes(*cfg);
     if (blob_elems < m->layout.total) {
         free_model(m);
@@ -552,7 +638,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     m->nsplit = attn_nsplit(max_seq_len);
     m->nkeys = gemv_num_keys(cfg->vocab);
     // Persistent step: bf16 only, one 512-thread block per CU if it fits.
-    if (cfg->weight_kind == VVLI_WEIGHT_BF16) {
+    if (cfg->weight_kind == VVLI_WEIGHT_BF16 && !moe) {
         int cus = 0, bpc = 0;
         m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->layers, hd);
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
@@ -582,7 +668,13 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(dmalloc(&m->x, H));
     TRY_ALLOC(dmalloc(&m->qkv, H + 2 * kv));
     TRY_ALLOC(dmalloc(&m->attn, H));
-    TRY_ALLOC(dmalloc(&m->ff, cfg->inter));
+    TRY_ALLOC(dmalloc(&m->ff, static_cast<size_t>(cfg->inter) * (moe ? cfg->experts_per_tok : 1)));
+    if (moe) {
+        TRY_ALLOC(dmalloc(&m->moe_router, cfg->num_experts));
+        TRY_ALLOC(dmalloc(&m->moe_idx, cfg->experts_per_tok));
+        TRY_ALLOC(dmalloc(&m->moe_w, cfg->experts_per_tok));
+        TRY_ALLOC(dmalloc(&m->moe_part, static_cast<size_t>(cfg->experts_per_tok) * H));
+    }
     TRY_ALLOC(dmalloc(&m->logits, cfg->vocab));
     TRY_ALLOC(dmalloc(&m->hidden, static_cast<size_t>(cfg->layers) * H));
     TRY_ALLOC(dmalloc(&m->part, part_floats));
@@ -618,6 +710,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
     TRY_ALLOC(fail_hip(hipMemset(m->state, 0, sizeof(StepState)), "state"));
+    if (moe) TRY_ALLOC(fail_hip(hipMemset(m->moe_idx, 0, cfg->experts_per_tok * sizeof(uint32_t)), "expert ids"));
     if (m->mk_tw) {
         TRY_ALLOC(fail_hip(hipMemset(m->mk_tw, 0, m->mk_tw_words * sizeof(unsigned long long)), "tag clear"));
         TRY_ALLOC(fail_hip(hipMemset(m->mk_err, 0, 32 * sizeof(uint32_t)), "error clear"));
@@ -735,7 +828,13 @@ extern "C" {
 int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob, size_t blob_elems,
                           vvli_gpu_model** out) {
     clear_error();
-    return create_impl(cfg, max_seq_len, host_blob, blob_elems, out);
+    return create_impl(cfg, max_seq_len, host_blob, blob_elems, out, false);
+}
+
+int vvli_gpu_moe_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,
+                              size_t blob_elems, vvli_gpu_model** out) {
+    clear_error();
+    return create_impl(cfg, max_seq_len, host_blob, blob_elems, out, true);
 }
 
 int vvli_gpu_model_destroy(vvli_gpu_model* model) {
@@ -799,7 +898,7 @@ int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
 int vvli_gpu_set_prefill_path(vvli_gpu_model* m, uint32_t path) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     if (path > 2) return set_error(VVLI_INVALID_CONFIG, "prefill path %u not in 0..2", path);
-    if (path == 2 && !prefill_supported(m->cfg))
+    if (path == 2 && (m->moe || !prefill_supported(m->cfg)))
         return set_error(VVLI_INVALID_CONFIG, "batched prefill needs bf16 weights and head_dim 32, 64 or 128");
     m->prefill_path = path;
     return VVLI_OK;

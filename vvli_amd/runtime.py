@@ -107,10 +107,15 @@ class Runner:
         self._c = cfg.to_c(weight_kind)
         handle = c_void_p()
         blob = np.ascontiguousarray(blob)
-        _lib.check(_lib.lib().vvli_gpu_model_create(byref(self._c), max_seq_len, _ptr(blob), blob.size, byref(handle)))
+        _lib.check(self._create(byref(self._c), max_seq_len, _ptr(blob), blob.size, byref(handle)))
         self._h = handle
         self._path = "auto"
         self.logits = np.zeros(cfg.vocab_size, dtype=np.float32)
+
+    @staticmethod
+    def _create(*args):
+        # llm.Runner: dense decoders only; MoE configs are rejected like OwnedModel.init.
+        return _lib.lib().vvli_gpu_model_create(*args)
 
     def close(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:
@@ -222,6 +227,16 @@ class Runner:
                                                        byref(n), byref(st)))
         stats = Stats(st.prompt_tokens, st.generated_tokens, st.prefill_ns, st.decode_ns, st.total_ns)
         return out[: n.value].copy(), stats
+
+
+class MoeRunner(Runner):
+    """Token step of a mixture-of-experts decoder (OLMoE form) through
+    vvli_gpu_moe_model_create; same methods as Runner. No reference
+    counterpart: the reference runner rejects MoE configs (src/llm.zig:426)."""
+
+    @staticmethod
+    def _create(*args):
+        return _lib.lib().vvli_gpu_moe_model_create(*args)
 
 
 def linear(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None = None, stream: int | None = None) -> None:
