@@ -237,6 +237,8 @@ struct PrefillAttnArgs {
     float scale;
 };
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s);
+// false (default): the MFMA flash-attention kernel; true: the f32 vector kernel.
+extern bool prefill_attn_vector;
 
 // ---------------------------------------------------------------------------
 // Mixture-of-experts step pieces (moe.hip).

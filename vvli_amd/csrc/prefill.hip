@@ -25,6 +25,10 @@
 // weights are exact in both): two MFMAs per product keep the f32 activation
 // precision the reference computes with, where one bf16 rounding of the
 // activations would cost about 2^-9.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -35,6 +39,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // GEMM tile: 128 (rows of A) x 128 (rows of W) x 32 (K) per step, 256 threads
@@ -154,7 +159,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
     const int wm = wave >> 1, wn = wave & 1;
     const uint32_t m0 = blockIdx.y * kBM;
     const uint32_t n0 = blockIdx.x * kBN;
-    const uint32_t nk = (g.K + kBK - 1) / kBK;
+    // Split K across gridDim.z blocks (partial sums added atomically).
+    const uint32_t nk_all = (g.K + kBK - 1) / kBK;
+    const uint32_t per_split = (nk_all + gridDim.z - 1) / gridDim.z;
+    const uint32_t kt0 = blockIdx.z * per_split;
+    const uint32_t nk = kt0 < nk_all ? min(per_split, nk_all - kt0) : 0;
+    const bool split = gridDim.z > 1;
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -162,16 +172,17 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    if (nk == 0) return;  // empty split (uniform per block)
     GemmTileRegs t;
-    gemm_load<MODE>(g, m0, n0, 0, t);
-    gemm_store(g, m0, 0, t, lds[0][0], lds[0][1], lds[0][2]);
+    gemm_load<MODE>(g, m0, n0, kt0 * kBK, t);
+    gemm_store(g, m0, kt0 * kBK, t, lds[0][0], lds[0][1], lds[0][2]);
     __syncthreads();
 
     const int fr = lane & 15, fk = 8 * (lane >> 4);
     for (uint32_t kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) gemm_load<MODE>(g, m0, n0, (kt + 1) * kBK, t);
+        if (more) gemm_load<MODE>(g, m0, n0, (kt0 + kt + 1) * kBK, t);
         const uint16_t* ahi = lds[cur][0];
         const uint16_t* alo = lds[cur][1];
         const uint16_t* bs = lds[cur][2];
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
         }
         if (more) {
             const int nxt = cur ^ 1;
-            gemm_store(g, m0, (kt + 1) * kBK, t, lds[nxt][0], lds[nxt][1], lds[nxt][2]);
+            gemm_store(g, m0, (kt0 + kt + 1) * kBK, t, lds[nxt][0], lds[nxt][1], lds[nxt][2]);
         }
         __syncthreads();
     }
@@ -219,15 +230,17 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
                     if (n >= g.N) continue;
                     float v = acc[i][j][jr];
                     if (MODE == kGemmResid) {
-                        orow[n] = __fadd_rn(orow[n], v);  // addInto (src/llm.zig:1389-1396)
+                        if (split) unsafeAtomicAdd(&orow[n], v);
+                        else orow[n] = __fadd_rn(orow[n], v);  // addInto (src/llm.zig:1389-1396)
                     } else {
                         const uint16_t* b = n < g.seg_end[0] ? g.bias[0] : n < g.seg_end[1] ? g.bias[1] : g.bias[2];
-                        if (b) {
+                        if (b && blockIdx.z == 0) {
                             const uint32_t bi = n < g.seg_end[0] ? n : n < g.seg_end[1] ? n - g.seg_end[0]
                                                                                         : n - g.seg_end[1];
                             v = __fadd_rn(v, from_bf16(b[bi]));
                         }
-                        orow[n] = v;
+                        if (split) unsafeAtomicAdd(&orow[n], v);  // output zeroed before the launch
+                        else orow[n] = v;
                     }
                 }
             }
@@ -408,12 +421,269 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
             make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
 }
 
+// ---------------------------------------------------------------------------
+// Causal GQA attention on MFMA (flash-attention form) for a chunk of prompt
+// rows. Block = (kv head, 64 query vectors); a query vector is one (row, q
+// head) pair of the G heads sharing the kv head, rows_per_block = 64 / G rows
+// (vectors past rows_per_block * G are idle). Wave w owns vectors 16w..16w+15.
+// Per 64-key tile of the cache: K and V rows are staged once in LDS as bf16
+// hi/lo halves (V transposed to [dim][key]), S = Q . K^T on MFMA as
+// qh.kh + qh.kl + ql.kh (f32 accumulate), scaled and masked causally, an
+// online softmax in f32 (row max and sum over 16-lane groups), P split hi/lo
+// through LDS into the A-operand layout, and O += P . V as ph.vh + ph.vl +
+// pl.vh. Each product keeps ~16 bits of both operands, like the f32 path it
+// replaces. v_mfma_f32_16x16x32_bf16 layout as the GEMM's.
+// ---------------------------------------------------------------------------
+constexpr int kFaThreads = 256;
+constexpr int kFaKeys = 64;            // keys per tile
+constexpr int kFaVecs = 64;            // query vectors per block
+constexpr int kFaVtRow = kFaKeys + 8;  // bf16 per transposed-V / P row (144 bytes)
+
+template <int HD>
+struct FaLds {
+    static constexpr int KRow = HD + 8;  // bf16 per K row
+    uint16_t k_hi[kFaKeys * KRow], k_lo[kFaKeys * KRow];
+    uint16_t vt_hi[HD * kFaVtRow], vt_lo[HD * kFaVtRow];
+    uint16_t p_hi[4][16 * kFaVtRow], p_lo[4][16 * kFaVtRow];
+};
+
+__device__ inline void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+    hi = to_bf16_rne(v);
+    lo = to_bf16_rne(v - from_bf16(hi));
+}
+
+template <int HD>
+__global__ __launch_bounds__(kFaThreads) void prefill_fa_kernel(PrefillAttnArgs a) {
+    constexpr int DS = HD / 32;         // 32-dim MFMA steps for S
+    constexpr int NT = HD / 16;         // 16-dim output tiles for O
+    constexpr int TD = HD / 8;          // dims per staging thread
+    static_assert(HD % 32 == 0 && TD % 4 == 0, "head_dim 32, 64 or 128");
+    __shared__ __attribute__((aligned(16))) FaLds<HD> lds;
+    constexpr int KRow = FaLds<HD>::KRow;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t G = a.heads / a.kv_heads;
+    const uint32_t rows_per_block = kFaVecs / G;
+    const uint32_t row_groups = (a.rows + rows_per_block - 1) / rows_per_block;
+    const uint32_t kvh = blockIdx.x % a.kv_heads;
+    const uint32_t r0 = (row_groups - 1 - blockIdx.x / a.kv_heads) * rows_per_block;  // longest first
+    const uint32_t last_row = min(r0 + rows_per_block, a.rows) - 1;
+    const uint32_t n_keys = a.start + last_row + 1;   // keys this block needs
+    const uint32_t key_limit = a.start + a.rows;      // cache rows written so far
+
+    // Q operand (A layout): vector v = 16 wave + lane%16, dims 8(lane/16)+32 s ..
+    const int fr = lane & 15, fq = lane >> 4;
+    bf16x8 qh[DS], ql[DS];
+    {
+        const uint32_t v = wave * 16 + fr;
+        const uint32_t t = v / G, g = v % G;
+        const bool valid = t < rows_per_block && r0 + t < a.rows;
+        const float* qp = a.q + static_cast<size_t>(valid ? r0 + t : 0) * a.ldq + (kvh * G + (valid ? g : 0)) * HD;
+#pragma unroll
+        for (int s = 0; s < DS; ++s) {
+            float x[8];
+            const float4 x0 = valid ? *reinterpret_cast<const float4*>(qp + 32 * s + 8 * fq) : make_float4(0, 0, 0, 0);
+            const float4 x1 = valid ? *reinterpret_cast<const float4*>(qp + 32 * s + 8 * fq + 4) : make_float4(0, 0, 0, 0);
+            x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint16_t h, l;
+                split_bf16(x[e], h, l);
+                qh[s][e] = __builtin_bit_cast(__bf16, h);
+                ql[s][e] = __builtin_bit_cast(__bf16, l);
+            }
+        }
+    }
+    // Positions of this lane's four S / O rows (C layout rows 4(lane/16)+j).
+    uint32_t pos_j[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t v = wave * 16 + 4 * fq + j;
+        const uint32_t t = min(v / G, rows_per_block - 1);
+        pos_j[j] = a.start + min(r0 + t, a.rows - 1);
+    }
+
+    f32x4 o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_j[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, l_j[4] = {0.f, 0.f, 0.f, 0.f};
+
+    // Staging: thread -> key pair (2 kp, 2 kp + 1), dims TD (tid%8) .. +TD.
+    const int kp = tid >> 3, dc = (tid & 7) * TD;
+    const float* kbase = a.kcache + kvh * HD + dc;
+    const float* vbase = a.vcache + kvh * HD + dc;
+    float kreg[2][TD], vreg[2][TD];
+    auto load_tile = [&](uint32_t j0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const uint32_t key = j0 + 2 * kp + r;
+            const bool in = key < key_limit;
+            const float* kr = kbase + static_cast<size_t>(in ? key : 0) * a.kvdim;
+            const float* vr = vbase + static_cast<size_t>(in ? key : 0) * a.kvdim;
+#pragma unroll
+            for (int d = 0; d < TD; d += 4) {
+                const float4 kv4 = in ? *reinterpret_cast<const float4*>(kr + d) : make_float4(0, 0, 0, 0);
+                const float4 vv4 = in ? *reinterpret_cast<const float4*>(vr + d) : make_float4(0, 0, 0, 0);
+                kreg[r][d] = kv4.x, kreg[r][d + 1] = kv4.y, kreg[r][d + 2] = kv4.z, kreg[r][d + 3] = kv4.w;
+                vreg[r][d] = vv4.x, vreg[r][d + 1] = vv4.y, vreg[r][d + 2] = vv4.z, vreg[r][d + 3] = vv4.w;
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int key = 2 * kp + r;
+#pragma unroll
+            for (int d = 0; d < TD; d += 4) {  // TD = HD / 8 is a multiple of 4
+                u16x4 h, l;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint16_t hh, ll;
+                    split_bf16(kreg[r][d + e], hh, ll);
+                    h[e] = hh, l[e] = ll;
+                }
+                *reinterpret_cast<u16x4*>(&lds.k_hi[key * KRow + dc + d]) = h;
+                *reinterpret_cast<u16x4*>(&lds.k_lo[key * KRow + dc + d]) = l;
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < TD; ++d) {
+            uint16_t h0, l0, h1, l1;
+            split_bf16(vreg[0][d], h0, l0);
+            split_bf16(vreg[1][d], h1, l1);
+            *reinterpret_cast<uint32_t*>(&lds.vt_hi[(dc + d) * kFaVtRow + 2 * kp]) = h0 | (uint32_t(h1) << 16);
+            *reinterpret_cast<uint32_t*>(&lds.vt_lo[(dc + d) * kFaVtRow + 2 * kp]) = l0 | (uint32_t(l1) << 16);
+        }
+    };
+
+    const uint32_t n_tiles = (n_keys + kFaKeys - 1) / kFaKeys;
+    load_tile(0);
+    uint16_t* ph = lds.p_hi[wave];
+    uint16_t* pl = lds.p_lo[wave];
+    for (uint32_t it = 0; it < n_tiles; ++it) {
+        const uint32_t j0 = it * kFaKeys;
+        store_tile();
+        __syncthreads();
+        if (it + 1 < n_tiles) load_tile(j0 + kFaKeys);
+        // S = Q . K^T for 4 tiles of 16 keys.
+        f32x4 sacc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int krow = (kt * 16 + fr) * KRow;
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&lds.k_hi[krow + 32 * s + 8 * fq]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&lds.k_lo[krow + 32 * s + 8 * fq]);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[s], kh, sacc[kt], 0, 0, 0);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[s], kl, sacc[kt], 0, 0, 0);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[s], kh, sacc[kt], 0, 0, 0);
+            }
+        }
+        // Scale, mask, online softmax per row (row j of this lane's group: 16 lanes).
+        float corr[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const uint32_t key = j0 + kt * 16 + fr;
+                const float sv = key <= pos_j[j] ? __fmul_rn(sacc[kt][j], a.scale) : -INFINITY;
+                sacc[kt][j] = sv;
+                mx = fmaxf(mx, sv);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            const float m_new = fmaxf(m_j[j], mx);
+            corr[j] = expf(m_j[j] - m_new);
+            float sum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const float p = expf(sacc[kt][j] - m_new);
+                sum += p;
+                uint16_t h, l;
+                split_bf16(p, h, l);
+                const int idx = (4 * fq + j) * kFaVtRow + kt * 16 + fr;
+                ph[idx] = h;
+                pl[idx] = l;
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+            l_j[j] = l_j[j] * corr[j] + sum;
+            m_j[j] = m_new;
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[n][j] *= corr[j];
+        __syncthreads();  // P visible in the A layout
+        // O += P . V over two 32-key steps.
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 pah = *reinterpret_cast<const bf16x8*>(&ph[fr * kFaVtRow + 32 * ks + 8 * fq]);
+            const bf16x8 pal = *reinterpret_cast<const bf16x8*>(&pl[fr * kFaVtRow + 32 * ks + 8 * fq]);
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const int vrow = (n * 16 + fr) * kFaVtRow + 32 * ks + 8 * fq;
+                const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&lds.vt_hi[vrow]);
+                const bf16x8 vl = *reinterpret_cast<const bf16x8*>(&lds.vt_lo[vrow]);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pah, vh, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pah, vl, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pal, vh, o[n], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // K/V/P tiles free for the next iteration
+    }
+    // out[row][qh * HD + d] = O / l for valid vectors (C layout: rows 4(lane/16)+j, column lane%16).
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t v = wave * 16 + 4 * fq + j;
+        const uint32_t t = v / G, g = v % G;
+        if (t >= rows_per_block || r0 + t >= a.rows) continue;
+        float* op = a.out + static_cast<size_t>(r0 + t) * a.ldo + (kvh * G + g) * HD;
+        const float inv = 1.0f / l_j[j];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) op[n * 16 + fr] = o[n][j] * inv;
+    }
+}
+
 }  // namespace
+
+// VVLI_PREFILL_ATTN=vector selects the f32 vector kernel (A/B measurement).
+bool prefill_attn_vector = [] {
+    const char* e = getenv("VVLI_PREFILL_ATTN");
+    return e != nullptr && strcmp(e, "vector") == 0;
+}();
+
+__global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) out[i] = 0.f;
+}
+
+// K splits for a launch: enough blocks for about two per CU, each split at
+// least 8 K steps; SwiGLU tiles are never split (the epilogue is nonlinear),
+// plain tiles only when the output rows are dense (they are zeroed first).
+uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
+    if (mode == kGemmGateUp || (mode == kGemmPlain && g.ldo != g.N)) return 1;
+    const uint32_t nk = (g.K + kBK - 1) / kBK;
+    const uint32_t max_splits = nk / 8 > 0 ? nk / 8 : 1;
+    uint32_t want = (512 + tiles - 1) / tiles;
+    if (want > max_splits) want = max_splits;
+    if (want > 32) want = 32;
+    return want > 0 ? want : 1;
+}
 
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
-    const dim3 grid((cols + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+    const uint32_t gx = (cols + kBN - 1) / kBN, gy = (g.M + kBM - 1) / kBM;
+    const uint32_t splits = gemm_k_splits(mode, g, gx * gy);
+    if (splits > 1 && mode == kGemmPlain) {
+        const size_t n = static_cast<size_t>(g.M) * g.ldo;
+        const uint32_t blocks = static_cast<uint32_t>(std::min<size_t>((n + 255) / 256, 4096));
+        hipError_t e = vlaunch(zero_rows_kernel, dim3(blocks), dim3(256), 0, s, g.out, n);
+        if (e != hipSuccess) return e;
+    }
+    const dim3 grid(gx, gy, splits);
     switch (mode) {
         case kGemmPlain: return vlaunch(gemm_bf16_kernel<kGemmPlain>, grid, dim3(kGemmThreads), 0, s, g);
         case kGemmResid: return vlaunch(gemm_bf16_kernel<kGemmResid>, grid, dim3(kGemmThreads), 0, s, g);
@@ -439,6 +709,19 @@ hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s) {
+    if (a.rows == 0) return hipSuccess;
+    if (!prefill_attn_vector) {
+        const uint32_t G = a.heads / a.kv_heads;
+        if (G == 0 || G > static_cast<uint32_t>(kFaVecs)) return hipErrorInvalidValue;
+        const uint32_t rows_per_block = kFaVecs / G;
+        const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block * a.kv_heads);
+        switch (hd) {
+            case 32: return vlaunch(prefill_fa_kernel<32>, grid, dim3(kFaThreads), 0, s, a);
+            case 64: return vlaunch(prefill_fa_kernel<64>, grid, dim3(kFaThreads), 0, s, a);
+            case 128: return vlaunch(prefill_fa_kernel<128>, grid, dim3(kFaThreads), 0, s, a);
+            default: return hipErrorInvalidValue;
+        }
+    }
     const uint32_t G = a.heads / a.kv_heads;
     if (G == 0 || G > static_cast<uint32_t>(kPairsPerWave)) return hipErrorInvalidValue;
     const uint32_t rows_per_wave = kPairsPerWave / G;
