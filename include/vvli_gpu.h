@@ -169,6 +169,40 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint
                              int64_t eos, uint32_t flags, uint32_t* out_tokens, uint32_t* n_out,
                              vvli_gpu_stats* stats);
 
+/* Sampling options: generator.Options (src/generator.zig:14-23). */
+typedef struct vvli_gpu_sampling {
+    float temperature;       /* <= 0: greedy with the repeat penalty */
+    float top_p;             /* (0, 1] */
+    uint32_t top_k;          /* 0 = no limit; on the device at most 1024 candidates */
+    float repeat_penalty;    /* >= 1; 1 disables it */
+    uint32_t repeat_last_n;  /* window of prompt + generated tokens, <= 65535 */
+    uint64_t seed;           /* DefaultPrng seed; 0 -> 0x9e3779b97f4a7c15 as Sampler.init */
+} vvli_gpu_sampling;
+
+/* generateGreedyMeasured* with Options (src/generator.zig:221-293) and
+ * Sampler.next (:93-120) on the device: repeat penalty over the last
+ * repeat_last_n tokens, greedy when temperature <= 0, else the top_k finite
+ * adjusted logits (ties to the lower id), p = exp((l - l_max) / T) summed in
+ * candidate order, the top_p cut, one Random.float(f32) draw from Zig's
+ * DefaultPrng (xoshiro256++, SplitMix64-seeded) and the cumulative pick. The
+ * first token is sampled from the prompt's last logits; every sampled token is
+ * forwarded (the last one too), so max_new tokens take max_new forwards, as
+ * in the reference. Greedy without a penalty runs vvli_gpu_generate_greedy.
+ * Candidate lists over 1024 (top_k 0 or > 1024 with a larger vocab) return
+ * VVLI_INVALID_SAMPLING. */
+int vvli_gpu_generate(vvli_gpu_model* model, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                      int64_t eos, uint32_t flags, const vvli_gpu_sampling* opts, uint32_t* out_tokens,
+                      uint32_t* n_out, vvli_gpu_stats* stats);
+/* Sampler.next (src/generator.zig:93-120) on host logits with the device
+ * kernel: the repeat counts come from prompt + generated (buildRepeatCounts),
+ * prng_state is the DefaultPrng state (s[0..3]) advanced in place when a
+ * random unit is drawn. For hosts that keep their own generation loop. */
+int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* prompt, uint32_t n_prompt,
+                          const uint32_t* generated, uint32_t n_generated, const vvli_gpu_sampling* opts,
+                          uint64_t prng_state[4], uint32_t* token_out);
+/* DefaultPrng.init(seed) as Sampler.init calls it (seed 0 mapped first). */
+void vvli_gpu_prng_seed(uint64_t seed, uint64_t state_out[4]);
+
 /* ---------------------------------------------------------------------- */
 /* Measurement (no reference counterpart: the reference has no profiler)   */
 /* ---------------------------------------------------------------------- */

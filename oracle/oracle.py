@@ -57,6 +57,11 @@ class OrcMoeLayerOffsets(ctypes.Structure):
     _fields_ = [(n, c_size_t) for n in MOE_SLOTS]
 
 
+class OrcSampling(ctypes.Structure):
+    _fields_ = [("temperature", c_float), ("top_p", c_float), ("top_k", c_uint32), ("repeat_penalty", c_float),
+                ("repeat_last_n", c_uint32), ("seed", c_uint64)]
+
+
 class OrcStats(ctypes.Structure):
     _fields_ = [("prompt_tokens", c_uint64), ("generated_tokens", c_uint64), ("prefill_ns", c_int64),
                 ("decode_ns", c_int64), ("total_ns", c_int64)]
@@ -112,6 +117,17 @@ def lib() -> ctypes.CDLL:
             "orc_moe_runner_destroy": (None, [c_void_p]),
             "orc_moe_forward_token": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]),
             "orc_moe_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+            "orc_splitmix64_next": (c_uint64, [P(c_uint64)]),
+            "orc_prng_seed": (None, [c_void_p, c_uint64]),
+            "orc_prng_next": (c_uint64, [c_void_p]),
+            "orc_prng_float": (c_float, [c_void_p]),
+            "orc_build_candidates": (c_size_t, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, P(OrcSampling)]),
+            "orc_prepare_probabilities": (c_size_t, [c_void_p, c_void_p, c_size_t, P(OrcSampling)]),
+            "orc_sample_candidate": (c_uint32, [c_void_p, c_void_p, c_size_t, c_float]),
+            "orc_sampler_next": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, P(OrcSampling),
+                                         c_void_p, P(c_uint32)]),
+            "orc_generate_sampled": (c_int, [c_void_p, c_size_t, c_void_p, c_uint32, c_uint32, c_int64,
+                                             P(OrcSampling), c_void_p, P(c_uint32)]),
             "orc_adjusted_logit": (c_float, [c_float, c_uint16, c_float]),
             "orc_greedy_with_penalties": (c_uint32, [c_void_p, c_void_p, c_size_t, c_float]),
         }
@@ -308,6 +324,15 @@ class OracleRunner:
         t = None if inv_freq is None else np.ascontiguousarray(inv_freq, dtype=np.float32)
         _check(lib().orc_set_rope_table(self._h, _p(t), 0 if t is None else t.size))
 
+    def generate_sampled(self, prompt, max_new: int, opts, eos: int | None = None):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(1, max_new), dtype=np.uint32)
+        n = c_uint32()
+        c = orc_sampling(opts)
+        _check(lib().orc_generate_sampled(self._h, self.cfg.vocab_size, _p(p), p.size, max_new,
+                                          -1 if eos is None else eos, byref(c), _p(out), byref(n)))
+        return out[: n.value].copy()
+
     def generate_greedy(self, prompt, max_new: int, eos: int | None = None):
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(max(1, max_new), dtype=np.uint32)
@@ -316,6 +341,27 @@ class OracleRunner:
         _check(lib().orc_generate_greedy(self._h, _p(p), p.size, max_new, -1 if eos is None else eos, _p(out),
                                          byref(n), byref(st)))
         return out[: n.value].copy(), st
+
+
+def orc_sampling(opts) -> OrcSampling:
+    return OrcSampling(opts.temperature, opts.top_p, opts.top_k, opts.repeat_penalty, opts.repeat_last_n, opts.seed)
+
+
+def prng_seed(seed: int) -> np.ndarray:
+    st = np.zeros(4, dtype=np.uint64)
+    lib().orc_prng_seed(_p(st), seed)
+    return st
+
+
+def sampler_next(logits, prompt, generated, opts, prng_state: np.ndarray) -> int:
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    p = np.ascontiguousarray(prompt, dtype=np.uint32)
+    g = np.ascontiguousarray(generated, dtype=np.uint32)
+    tok = c_uint32()
+    c = orc_sampling(opts)
+    _check(lib().orc_sampler_next(_p(lg), lg.size, _p(p), p.size, _p(g), g.size, byref(c), _p(prng_state),
+                                  byref(tok)))
+    return tok.value
 
 
 def orc_moe_config(cfg, weight_kind: int) -> OrcMoeConfig:

@@ -47,6 +47,7 @@ enum {
     ORC_OUT_OF_MEMORY = 7,
     ORC_THREAD_SPAWN_FAILED = 9,
     ORC_EMPTY_PROMPT = 10,
+    ORC_INVALID_SAMPLING = 15,
     ORC_NULL_ARG = 100,
 };
 
@@ -163,6 +164,32 @@ int orc_moe_kv_read(const orc_moe_runner* r, uint32_t layer, uint32_t pos, float
 /* ---- sampler pieces: src/generator.zig:338-463 ---- */
 float orc_adjusted_logit(float logit, uint16_t repeat_count, float repeat_penalty);
 uint32_t orc_greedy_with_penalties(const float* logits, const uint16_t* counts, size_t n, float repeat_penalty);
+
+/* ---- token sampler (vvli_oracle_sample.c): src/generator.zig:14-23, 65-127,
+ * 329-463; PRNG = Zig's DefaultPrng (xoshiro256++ / SplitMix64) ---- */
+typedef struct orc_sampling {
+    float temperature, top_p;
+    uint32_t top_k;
+    float repeat_penalty;
+    uint32_t repeat_last_n;
+    uint64_t seed;
+} orc_sampling;
+uint64_t orc_splitmix64_next(uint64_t* state);
+void orc_prng_seed(uint64_t state[4], uint64_t seed);
+uint64_t orc_prng_next(uint64_t state[4]);
+float orc_prng_float(uint64_t state[4]);
+int orc_sampling_validate(const orc_sampling* o);
+void orc_build_repeat_counts(uint16_t* counts, size_t n, const uint32_t* prompt, size_t n_prompt,
+                             const uint32_t* generated, size_t n_generated, const orc_sampling* o);
+size_t orc_build_candidates(uint32_t* ids, float* scores, const float* logits, const uint16_t* counts, size_t n,
+                            const orc_sampling* o);
+size_t orc_prepare_probabilities(float* probs, const float* scores, size_t count, const orc_sampling* o);
+uint32_t orc_sample_candidate(const uint32_t* ids, const float* probs, size_t count, float random_unit);
+int orc_sampler_next(const float* logits, size_t n, const uint32_t* prompt, size_t n_prompt,
+                     const uint32_t* generated, size_t n_generated, const orc_sampling* o, uint64_t prng[4],
+                     uint32_t* token_out);
+int orc_generate_sampled(orc_runner* r, size_t vocab, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                         int64_t eos, const orc_sampling* o, uint32_t* out_tokens, uint32_t* n_out);
 
 #ifdef __cplusplus
 }

@@ -82,6 +82,17 @@ class CStats(ctypes.Structure):
     ]
 
 
+class CSampling(ctypes.Structure):
+    _fields_ = [
+        ("temperature", c_float),
+        ("top_p", c_float),
+        ("top_k", c_uint32),
+        ("repeat_penalty", c_float),
+        ("repeat_last_n", c_uint32),
+        ("seed", c_uint64),
+    ]
+
+
 # void (*)(void* user, size_t completed, size_t total, const char* name)
 PROGRESS_FN = ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_char_p)
 
@@ -107,6 +118,15 @@ PROTOTYPES = {
         c_int,
         [c_void_p, c_void_p, c_uint32, c_uint32, c_int64, c_uint32, c_void_p, POINTER(c_uint32), POINTER(CStats)],
     ),
+    "vvli_gpu_generate": (
+        c_int,
+        [c_void_p, c_void_p, c_uint32, c_uint32, c_int64, c_uint32, POINTER(CSampling), c_void_p, POINTER(c_uint32),
+         POINTER(CStats)],
+    ),
+    "vvli_gpu_sampler_next": (
+        c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, POINTER(CSampling), c_void_p,
+                POINTER(c_uint32)]),
+    "vvli_gpu_prng_seed": (None, [c_uint64, c_void_p]),
     "vvli_gpu_profile_step": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, POINTER(c_uint32)]),
     "vvli_gpu_set_decode_path": (c_int, [c_void_p, c_uint32]),
     "vvli_gpu_set_prefill_path": (c_int, [c_void_p, c_uint32]),

@@ -264,4 +264,27 @@ hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s);  // k
 hipError_t launch_moe_combine(float* x, const float* partial, const uint32_t* idx, const float* w, uint32_t top_k,
                               uint32_t H, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// Token sampling (sample.hip): Sampler.next on device logits.
+// ---------------------------------------------------------------------------
+constexpr int kMaxSampleTopK = 1024;
+struct SampleArgs {
+    const float* logits = nullptr;
+    uint32_t vocab = 0;
+    uint32_t* counts = nullptr;       // [vocab] repeat counts of the window (nullable: no penalty)
+    float temperature = 0.f, top_p = 1.f, repeat_penalty = 1.f;
+    uint32_t top_k = 0, repeat_last_n = 0;
+    unsigned long long* prng = nullptr;  // device xoshiro256++ state [4]
+    uint32_t* result = nullptr;       // nullable: the token
+    StepState* state = nullptr;       // nullable: advanced like the greedy finish
+    uint32_t advance_pos = 1;         // 0 for a sample taken before any forward
+    const uint32_t* prompt = nullptr;
+    uint32_t n_prompt = 0;
+    uint32_t* out_tokens = nullptr;
+    uint32_t out_cap = 0;
+};
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
+hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
+                                uint32_t last_n, hipStream_t s);
+
 }  // namespace vvli

@@ -76,6 +76,10 @@ struct vvli_gpu_model {
     uint32_t* moe_idx = nullptr;   // [top_k] selected experts
     float* moe_w = nullptr;        // [top_k] their probabilities
     float* moe_part = nullptr;     // [top_k][H] expert outputs
+    // On-device sampling (vvli_gpu_generate with temperature > 0 or a repeat penalty).
+    uint32_t* sample_counts = nullptr;        // [vocab] repeat counts of the window
+    unsigned long long* sample_prng = nullptr;  // xoshiro256++ state [4]
+    hipGraphExec_t graph_sample = nullptr;    // token step ending in the sampler
     // Batched prefill (bf16 only): chunk buffers, allocated on first use.
     bool pf_ok = false;
     uint32_t prefill_path = 0;  // 0 auto, 1 token loop, 2 batched
@@ -148,7 +152,7 @@ int check_kernel_shapes(const vvli_gpu_config& c) {
     return VVLI_OK;
 }
 
-int enqueue_logits(vvli_gpu_model* m, hipStream_t s);
+int enqueue_logits(vvli_gpu_model* m, hipStream_t s, const SampleArgs* smp = nullptr);
 
 // Slices of the attention half of a layer (dense and MoE blobs share it).
 struct AttnSlices {
@@ -261,8 +265,9 @@ int enqueue_moe_ffn(vvli_gpu_model* m, hipStream_t s, uint32_t l) {
     return VVLI_OK;
 }
 
-// The layers, final norm and logits of one step (embedding already in x).
-int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+// The layers, final norm and logits of one step (embedding already in x);
+// the step ends in the greedy finish, or in the sampler when smp is given.
+int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg, const SampleArgs* smp = nullptr) {
     const vvli_gpu_config& c = m->cfg;
     const int kind = static_cast<int>(c.weight_kind);
     const uint32_t H = c.hidden, I = c.inter;
@@ -301,11 +306,11 @@ int enqueue_body(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
             HIP_TRY(hipMemcpyAsync(hidden_dbg + static_cast<size_t>(l) * H, m->x, H * sizeof(float),
                                    hipMemcpyDeviceToDevice, s));
     }
-    return enqueue_logits(m, s);
+    return enqueue_logits(m, s, smp);
 }
 
-// Final RMSNorm + logits + argmax of the hidden state in x.
-int enqueue_logits(vvli_gpu_model* m, hipStream_t s) {
+// Final RMSNorm + logits + argmax (or sampler) of the hidden state in x.
+int enqueue_logits(vvli_gpu_model* m, hipStream_t s, const SampleArgs* smp) {
     const vvli_gpu_config& c = m->cfg;
     const int kind = static_cast<int>(c.weight_kind);
     const uint32_t H = c.hidden;
@@ -320,14 +325,15 @@ int enqueue_logits(vvli_gpu_model* m, hipStream_t s) {
     gl.K = H;
     gl.block_keys = m->keys;
     LAUNCH(launch_gemv(kind, kGemvLogits, gl, s));
-    LAUNCH(launch_argmax_finish(m->keys, m->nkeys, m->logits, m->state, m->prompt, m->out_tokens, m->out_cap, s));
+    if (smp) LAUNCH(launch_sample(*smp, s));
+    else LAUNCH(launch_argmax_finish(m->keys, m->nkeys, m->logits, m->state, m->prompt, m->out_tokens, m->out_cap, s));
     return VVLI_OK;
 }
 
-int enqueue_step(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg) {
+int enqueue_step(vvli_gpu_model* m, hipStream_t s, float* hidden_dbg, const SampleArgs* smp = nullptr) {
     LAUNCH(launch_embed(static_cast<int>(m->cfg.weight_kind), wslice(m, m->layout.embed), m->state, m->x,
                         m->cfg.hidden, s));
-    return enqueue_body(m, s, hidden_dbg);
+    return enqueue_body(m, s, hidden_dbg, smp);
 }
 
 int ensure_graph(vvli_gpu_model* m) {
@@ -345,6 +351,58 @@ int ensure_graph(vvli_gpu_model* m) {
     (void)hipGraphDestroy(g);
     HIP_TRY(e);
     return VVLI_OK;
+}
+
+// The token step ending in the sampler; options are kernel arguments, so the
+// graph is captured again for every generate call.
+int capture_sample_graph(vvli_gpu_model* m, const SampleArgs& sa) {
+    if (m->graph_sample) {
+        (void)hipGraphExecDestroy(m->graph_sample);
+        m->graph_sample = nullptr;
+    }
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, m->stream, nullptr, &sa);
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc != VVLI_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    HIP_TRY(e);
+    e = hipGraphInstantiate(&m->graph_sample, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_TRY(e);
+    return VVLI_OK;
+}
+
+// validateSamplingOptions (src/generator.zig:329-333) plus the device limits:
+// at most 1024 candidates, a repeat window that fits 16-bit counts.
+int validate_sampling(const vvli_gpu_sampling& o, uint32_t vocab) {
+    if (o.temperature < 0.0f || std::isnan(o.temperature))
+        return set_error(VVLI_INVALID_SAMPLING, "temperature %g", o.temperature);
+    if (o.top_p <= 0.0f || o.top_p > 1.0f || std::isnan(o.top_p))
+        return set_error(VVLI_INVALID_SAMPLING, "top_p %g not in (0, 1]", o.top_p);
+    if (o.repeat_penalty < 1.0f || std::isnan(o.repeat_penalty))
+        return set_error(VVLI_INVALID_SAMPLING, "repeat_penalty %g < 1", o.repeat_penalty);
+    const uint32_t limit = (o.top_k == 0 || o.top_k > vocab) ? vocab : o.top_k;
+    if (o.temperature > 0.0f && limit > static_cast<uint32_t>(kMaxSampleTopK))
+        return set_error(VVLI_INVALID_SAMPLING, "device sampling takes at most %d candidates (top_k %u, vocab %u)",
+                         kMaxSampleTopK, o.top_k, vocab);
+    if (o.repeat_last_n > 65535) return set_error(VVLI_INVALID_SAMPLING, "repeat_last_n %u > 65535", o.repeat_last_n);
+    return VVLI_OK;
+}
+
+void prng_seed(uint64_t seed, uint64_t out[4]) {
+    // DefaultPrng.init: four SplitMix64 outputs; Sampler.init maps seed 0 to
+    // 0x9e3779b97f4a7c15 (src/generator.zig:70-75).
+    uint64_t x = seed ? seed : 0x9e3779b97f4a7c15ull;
+    for (int i = 0; i < 4; ++i) {
+        x += 0x9e3779b97f4a7c15ull;
+        uint64_t z = x;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        out[i] = z ^ (z >> 31);
+    }
 }
 
 // Auto picks the persistent step where it is available (bf16 weights): on the
@@ -574,10 +632,12 @@ void free_model(vvli_gpu_model* m) {
     if (!m) return;
     (void)hipSetDevice(m->device);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    if (m->graph_sample) (void)hipGraphExecDestroy(m->graph_sample);
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_part};
+                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_part, m->sample_counts,
+                    m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -804,6 +864,88 @@ int generate_persistent(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_pr
         if (produced < max_new && !hit_eos)
             return set_error(VVLI_CONTEXT_FULL, "decode reached max_seq_len %u after %u tokens", m->max_seq, produced);
     }
+    const int64_t t2 = now_ns();
+    *n_out = produced;
+    if (stats) {
+        stats->prompt_tokens = n_prompt;
+        stats->generated_tokens = produced;
+        stats->prefill_ns = t1 - t0;
+        stats->decode_ns = t2 - t1;
+        stats->total_ns = t2 - t0;
+    }
+    return VVLI_OK;
+}
+
+// generateGreedyMeasured with Options (src/generator.zig:221-293): the prompt
+// token by token (or batched), then Sampler.next on the device after every
+// forward; the sampled token is forwarded, the last one too.
+int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
+                     bool batched, const vvli_gpu_sampling& o, uint32_t* out_tokens, uint32_t* n_out,
+                     vvli_gpu_stats* stats) {
+    const vvli_gpu_config& c = m->cfg;
+    if (eos < 0 && static_cast<uint64_t>(n_prompt) + max_new > m->max_seq)
+        return set_error(VVLI_CONTEXT_FULL, "prompt %u + %u new tokens > max_seq_len %u", n_prompt, max_new, m->max_seq);
+    int rc;
+    if (!m->sample_counts && (rc = dmalloc(&m->sample_counts, c.vocab))) return rc;
+    if (!m->sample_prng && (rc = dmalloc(&m->sample_prng, 4))) return rc;
+    const bool penalty = o.repeat_penalty > 1.0f && o.repeat_last_n > 0;
+    SampleArgs sa;
+    sa.logits = m->logits;
+    sa.vocab = c.vocab;
+    sa.counts = penalty ? m->sample_counts : nullptr;
+    sa.temperature = o.temperature;
+    sa.top_p = o.top_p;
+    sa.repeat_penalty = o.repeat_penalty;
+    sa.top_k = (o.top_k == 0 || o.top_k > c.vocab) ? c.vocab : o.top_k;
+    sa.repeat_last_n = o.repeat_last_n;
+    sa.prng = m->sample_prng;
+    sa.state = m->state;
+    sa.prompt = m->prompt;
+    sa.n_prompt = n_prompt;
+    sa.out_tokens = m->out_tokens;
+    sa.out_cap = m->out_cap;
+    if ((rc = capture_sample_graph(m, sa))) return rc;
+    const int64_t t0 = now_ns();
+    HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
+    if (batched) {
+        if ((rc = enqueue_prefill_batched(m, 0, n_prompt, prompt[n_prompt - 1], 0))) return rc;
+    } else {
+        if ((rc = ensure_graph(m))) return rc;
+        HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 0, m->stream));
+        for (uint32_t i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    const int64_t t1 = now_ns();
+    // Sampler.init: PRNG state, repeat counts of the prompt's window.
+    uint64_t st4[4];
+    prng_seed(o.seed, st4);
+    HIP_TRY(hipMemcpy(m->sample_prng, st4, sizeof(st4), hipMemcpyHostToDevice));
+    if (penalty) HIP_TRY(launch_sample_counts(m->sample_counts, c.vocab, m->prompt, n_prompt, o.repeat_last_n, m->stream));
+    uint32_t produced = 0;
+    if (max_new > 0) {
+        SampleArgs first = sa;  // the first token comes from the prompt's last logits
+        first.advance_pos = 0;
+        HIP_TRY(launch_sample(first, m->stream));
+        if (eos < 0) {
+            for (uint32_t i = 0; i < max_new; ++i) HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
+            produced = max_new;
+        } else {
+            uint32_t pos = n_prompt;
+            while (produced < max_new) {
+                HIP_TRY(hipMemcpyAsync(m->h_state, m->state, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+                HIP_TRY(hipStreamSynchronize(m->stream));
+                const uint32_t next = m->h_state->argmax;
+                ++produced;
+                if (static_cast<int64_t>(next) == eos) break;
+                if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len", pos);
+                HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
+                ++pos;
+            }
+        }
+        HIP_TRY(hipMemcpyAsync(out_tokens, m->out_tokens, produced * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                               m->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
     const int64_t t2 = now_ns();
     *n_out = produced;
     if (stats) {
@@ -1108,6 +1250,88 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
 
 // Rows from which vvli_gpu_linear runs one GEMM instead of a GEMV per row.
 constexpr uint32_t kLinearGemmMinRows = 4;
+
+int vvli_gpu_generate(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
+                      uint32_t flags, const vvli_gpu_sampling* opts, uint32_t* out_tokens, uint32_t* n_out,
+                      vvli_gpu_stats* stats) {
+    if (!m || !out_tokens || !n_out || !opts) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_generate");
+    if (n_prompt == 0 || !prompt) return set_error(VVLI_EMPTY_PROMPT, "empty prompt");
+    int rc = validate_sampling(*opts, m->cfg.vocab);
+    if (rc) return rc;
+    // Greedy without a penalty is llm.argmax: the greedy path (persistent step where available).
+    if (opts->temperature <= 0.0f && !(opts->repeat_penalty > 1.0f && opts->repeat_last_n > 0))
+        return vvli_gpu_generate_greedy(m, prompt, n_prompt, max_new, eos, flags, out_tokens, n_out, stats);
+    for (uint32_t i = 0; i < n_prompt; ++i)
+        if (prompt[i] >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "prompt token %u >= vocab", prompt[i]);
+    if (n_prompt > m->max_seq)
+        return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    const bool batched = (flags & VVLI_GEN_BATCHED_PREFILL) && use_batched_prefill(m);
+    return generate_sampled(m, prompt, n_prompt, max_new, eos, batched, *opts, out_tokens, n_out, stats);
+}
+
+void vvli_gpu_prng_seed(uint64_t seed, uint64_t state_out[4]) {
+    if (state_out) prng_seed(seed, state_out);
+}
+
+int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* prompt, uint32_t n_prompt,
+                          const uint32_t* generated, uint32_t n_generated, const vvli_gpu_sampling* opts,
+                          uint64_t prng_state[4], uint32_t* token_out) {
+    if (!logits || !opts || !prng_state || !token_out || (n_prompt && !prompt) || (n_generated && !generated))
+        return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_sampler_next");
+    if (n == 0) return set_error(VVLI_INVALID_CONFIG, "empty logits");
+    clear_error();
+    int rc = validate_sampling(*opts, n);
+    if (rc) return rc;
+    // buildRepeatCounts (src/generator.zig:335-351) on the host.
+    std::vector<uint32_t> counts(n, 0);
+    const bool penalty = opts->repeat_penalty > 1.0f && opts->repeat_last_n > 0;
+    if (penalty) {
+        const uint64_t total = static_cast<uint64_t>(n_prompt) + n_generated;
+        const uint64_t start = total > opts->repeat_last_n ? total - opts->repeat_last_n : 0;
+        for (uint64_t i = start; i < total; ++i) {
+            const uint32_t t = i < n_prompt ? prompt[i] : generated[i - n_prompt];
+            if (t < n && counts[t] < 0xffff) ++counts[t];
+        }
+    }
+    float* d_logits = nullptr;
+    uint32_t *d_counts = nullptr, *d_result = nullptr;
+    unsigned long long* d_prng = nullptr;
+    auto release = [&] {
+        if (d_logits) (void)hipFree(d_logits);
+        if (d_counts) (void)hipFree(d_counts);
+        if (d_result) (void)hipFree(d_result);
+        if (d_prng) (void)hipFree(d_prng);
+    };
+    hipError_t e = hipMalloc(&d_logits, n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d_counts, n * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d_result, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d_prng, 4 * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemcpy(d_logits, logits, n * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d_counts, counts.data(), n * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d_prng, prng_state, 4 * sizeof(uint64_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        SampleArgs sa;
+        sa.logits = d_logits;
+        sa.vocab = n;
+        sa.counts = penalty ? d_counts : nullptr;
+        sa.temperature = opts->temperature;
+        sa.top_p = opts->top_p;
+        sa.repeat_penalty = opts->repeat_penalty;
+        sa.top_k = (opts->top_k == 0 || opts->top_k > n) ? n : opts->top_k;
+        sa.repeat_last_n = opts->repeat_last_n;
+        sa.prng = d_prng;
+        sa.result = d_result;
+        e = launch_sample(sa, nullptr);
+    }
+    if (e == hipSuccess) e = hipMemcpy(token_out, d_result, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(prng_state, d_prng, 4 * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    release();
+    if (e != hipSuccess)
+        return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR, "sampler: %s",
+                         hipGetErrorString(e));
+    return VVLI_OK;
+}
 
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream) {

@@ -1,0 +1,316 @@
+// sample.hip -- on-device token sampling: VVLI's Sampler.next
+// (src/generator.zig:93-120) with its helpers (:335-463) and PRNG.
+//
+// One 1024-thread block per step, on the logits the step just wrote:
+//   scores   s_i = adjustedLogit(l_i, count_i) (repeat penalty, :391-394)
+//   T <= 0   greedyWithPenalties (:353-365): first index of the strict max
+//   T > 0    candidates = the top_k largest finite scores, descending, ties
+//            to the lower id (buildCandidates + insertTopCandidate), found by
+//            a 4-pass radix select on order-preserving score keys, gathered
+//            and bitonic-sorted in LDS (top_k <= 1024);
+//            p_i = exp((s_i - s_0) / T) in parallel, then one thread sums
+//            them in candidate order, applies the top_p cut (:428-449), draws
+//            u = Random.float(f32) from Zig's DefaultPrng (xoshiro256++,
+//            state in device memory) and walks the cumulative sum
+//            (sampleCandidate, :451-463).
+// Sequential f32 sums in candidate order keep the reference's rounding.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace vvli {
+
+namespace {
+
+constexpr int kT = 1024;  // threads of the sampling block
+constexpr int kMaxCand = kMaxSampleTopK;
+
+__device__ inline float adjusted(float logit, uint32_t count, float penalty) {
+    if (count == 0 || penalty <= 1.0f) return logit;
+    return logit < 0.0f ? __fmul_rn(logit, penalty) : __fdiv_rn(logit, penalty);
+}
+
+// Order-preserving key of a finite float (larger float -> larger key), >= 1;
+// -0 and +0 share a key, as they compare equal.
+__device__ inline uint32_t order_key(float v) {
+    const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ inline float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ inline uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+__device__ inline uint64_t xoshiro_next(uint64_t* s) {
+    const uint64_t result = rotl64(s[0] + s[3], 23) + s[0];
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl64(s[3], 45);
+    return result;
+}
+// Random.float(f32) of Zig's std.Random on DefaultPrng.
+__device__ inline float prng_float(uint64_t* s) {
+    const uint64_t r = xoshiro_next(s);
+    uint32_t lz = r ? static_cast<uint32_t>(__clzll(r)) : 64u;
+    if (lz >= 41) {
+        const uint64_t r2 = xoshiro_next(s);
+        lz = 41 + (r2 ? static_cast<uint32_t>(__clzll(r2)) : 64u);
+        if (lz == 41 + 64) lz += static_cast<uint32_t>(__clz(static_cast<uint32_t>(xoshiro_next(s)) | 0x7ffu));
+    }
+    return __uint_as_float(((126u - lz) << 23) | static_cast<uint32_t>(r & 0x7fffffull));
+}
+
+struct SampleShared {
+    uint32_t hist[256];
+    unsigned long long cand[kMaxCand];  // (score key << 32) | ~id, sorted descending
+    float prob[kMaxCand];
+    uint32_t scan_gt[kT], scan_eq[kT];
+    unsigned long long red[kT / 64];
+    uint32_t prefix, remaining, n_finite, token;
+};
+
+__device__ inline uint32_t block_sum_u32(uint32_t v, unsigned long long* red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t total = 0;
+    for (int w = 0; w < kT / 64; ++w) total += static_cast<uint32_t>(red[w]);
+    __syncthreads();
+    return total;
+}
+
+// Inclusive scan of one value per thread (thread order), via LDS.
+__device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* buf) {
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (int off = 1; off < kT; off <<= 1) {
+        const uint32_t add = threadIdx.x >= static_cast<uint32_t>(off) ? buf[threadIdx.x - off] : 0u;
+        __syncthreads();
+        buf[threadIdx.x] += add;
+        __syncthreads();
+    }
+    const uint32_t incl = buf[threadIdx.x];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
+    __shared__ SampleShared sh;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t V = a.vocab;
+    const uint32_t chunk = (V + kT - 1) / kT;
+    const uint32_t i0 = tid * chunk, i1 = min(V, i0 + chunk);
+    auto score = [&](uint32_t i) { return adjusted(a.logits[i], a.counts ? a.counts[i] : 0u, a.repeat_penalty); };
+
+    uint32_t tok = 0;
+    if (a.temperature <= 0.0f) {
+        // greedyWithPenalties: best starts at index 0; NaN never replaces it.
+        unsigned long long best = 0ull;
+        for (uint32_t i = i0; i < i1; ++i) {
+            const unsigned long long k = argmax_key(score(i), i);
+            best = k > best ? k : best;
+        }
+        best = wave_max_u64(best);
+        if ((tid & 63) == 0) sh.red[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 0; w < kT / 64; ++w) best = sh.red[w] > best ? sh.red[w] : best;
+            const float s0 = score(0);
+            sh.token = (s0 != s0) ? 0u : argmax_key_index(best);
+        }
+        __syncthreads();
+        tok = sh.token;
+    } else {
+        // Finite candidates and the limit (buildCandidates, :367-372).
+        uint32_t nf = 0;
+        for (uint32_t i = i0; i < i1; ++i) nf += isfinite(score(i)) ? 1u : 0u;
+        const uint32_t n_finite = block_sum_u32(nf, sh.red);
+        const uint32_t limit = min(a.top_k, V);
+        const uint32_t count = min(limit, n_finite);
+        if (count == 0) {
+            // llm.argmax of the raw logits (:111).
+            unsigned long long best = 0ull;
+            for (uint32_t i = i0; i < i1; ++i) {
+                const unsigned long long k = argmax_key(a.logits[i], i);
+                best = k > best ? k : best;
+            }
+            best = wave_max_u64(best);
+            if ((tid & 63) == 0) sh.red[tid >> 6] = best;
+            __syncthreads();
+            if (tid == 0) {
+                for (int w = 0; w < kT / 64; ++w) best = sh.red[w] > best ? sh.red[w] : best;
+                sh.token = (a.logits[0] != a.logits[0]) ? 0u : argmax_key_index(best);
+            }
+            __syncthreads();
+            tok = sh.token;
+        } else {
+            // Radix select: the key of the count-th largest finite score.
+            if (tid == 0) {
+                sh.prefix = 0;
+                sh.remaining = count;
+            }
+            for (int pass = 0; pass < 4; ++pass) {
+                const int shift = 24 - 8 * pass;
+                for (uint32_t b = tid; b < 256; b += kT) sh.hist[b] = 0;
+                __syncthreads();
+                const uint32_t prefix = sh.prefix;
+                for (uint32_t i = i0; i < i1; ++i) {
+                    const float s = score(i);
+                    if (!isfinite(s)) continue;
+                    const uint32_t k = order_key(s);
+                    if (pass > 0 && (k >> (shift + 8)) != prefix) continue;
+                    atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    uint32_t rem = sh.remaining, b = 255;
+                    for (;; --b) {
+                        if (sh.hist[b] >= rem || b == 0) break;
+                        rem -= sh.hist[b];
+                    }
+                    sh.prefix = (prefix << 8) | b;
+                    sh.remaining = rem;
+                }
+                __syncthreads();
+            }
+            const uint32_t thr = sh.prefix;        // key of the count-th largest
+            const uint32_t need_eq = sh.remaining;  // how many keys equal to thr are taken
+            // Gather: every key > thr, and the need_eq lowest-id keys == thr.
+            uint32_t ngt = 0, neq = 0;
+            for (uint32_t i = i0; i < i1; ++i) {
+                const float s = score(i);
+                if (!isfinite(s)) continue;
+                const uint32_t k = order_key(s);
+                ngt += k > thr ? 1u : 0u;
+                neq += k == thr ? 1u : 0u;
+            }
+            const uint32_t off_gt = block_exclusive_scan(ngt, sh.scan_gt);
+            const uint32_t off_eq = block_exclusive_scan(neq, sh.scan_eq);
+            const uint32_t n_gt = count - need_eq;
+            for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = 0ull;
+            __syncthreads();
+            uint32_t wg = off_gt, we = off_eq;
+            for (uint32_t i = i0; i < i1; ++i) {
+                const float s = score(i);
+                if (!isfinite(s)) continue;
+                const uint32_t k = order_key(s);
+                const unsigned long long key = (static_cast<unsigned long long>(k) << 32) | (0xffffffffu - i);
+                if (k > thr) sh.cand[wg++] = key;
+                else if (k == thr && we < need_eq) sh.cand[n_gt + we++] = key;
+                else if (k == thr) ++we;
+            }
+            __syncthreads();
+            // Bitonic sort of kMaxCand keys, descending.
+            for (uint32_t size = 2; size <= static_cast<uint32_t>(kMaxCand); size <<= 1) {
+                for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                    for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) {
+                        const uint32_t p = j ^ stride;
+                        if (p > j) {
+                            const bool desc = (j & size) == 0;
+                            const unsigned long long x = sh.cand[j], y = sh.cand[p];
+                            if (desc ? (x < y) : (x > y)) {
+                                sh.cand[j] = y;
+                                sh.cand[p] = x;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+            // Probabilities (prepareProbabilities): exp in parallel, sums in order.
+            const float temperature = fmaxf(a.temperature, 1e-6f);
+            const float s0 = key_value(static_cast<uint32_t>(sh.cand[0] >> 32));
+            for (uint32_t j = tid; j < count; j += kT) {
+                const float sj = key_value(static_cast<uint32_t>(sh.cand[j] >> 32));
+                const float p = expf(__fdiv_rn(__fsub_rn(sj, s0), temperature));
+                sh.prob[j] = isfinite(p) ? p : 0.0f;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float total = 0.0f;
+                for (uint32_t j = 0; j < count; ++j) total = __fadd_rn(total, sh.prob[j]);
+                uint32_t k = count;
+                if (total <= 0.0f || !isfinite(total)) {
+                    k = 1;
+                } else if (a.top_p < 1.0f) {
+                    float cum = 0.0f;
+                    for (uint32_t j = 0; j < count; ++j) {
+                        cum = __fadd_rn(cum, sh.prob[j]);
+                        if (__fdiv_rn(cum, total) >= a.top_p) {
+                            k = j + 1;
+                            break;
+                        }
+                    }
+                }
+                // sampleCandidate with one draw of Random.float(f32).
+                uint64_t s[4] = {a.prng[0], a.prng[1], a.prng[2], a.prng[3]};
+                const float u = prng_float(s);
+                for (int q = 0; q < 4; ++q) a.prng[q] = s[q];
+                float t2 = 0.0f;
+                for (uint32_t j = 0; j < k; ++j) t2 = __fadd_rn(t2, sh.prob[j]);
+                uint32_t pick = 0;
+                if (t2 > 0.0f && isfinite(t2)) {
+                    const float target = __fmul_rn(fminf(u, 0.99999994f), t2);
+                    float cum = 0.0f;
+                    pick = k - 1;
+                    for (uint32_t j = 0; j < k; ++j) {
+                        cum = __fadd_rn(cum, sh.prob[j]);
+                        if (target <= cum) {
+                            pick = j;
+                            break;
+                        }
+                    }
+                }
+                sh.token = 0xffffffffu - static_cast<uint32_t>(sh.cand[pick] & 0xffffffffull);
+            }
+            __syncthreads();
+            tok = sh.token;
+        }
+    }
+    if (tid != 0) return;
+    if (a.result) *a.result = tok;
+    StepState* st = a.state;
+    if (!st) return;
+    // Advance the step state as the greedy finish does, then the repeat window.
+    const uint32_t next_pos = st->pos + (a.advance_pos ? 1u : 0u);
+    st->argmax = tok;
+    st->pos = next_pos;
+    st->token = tok;
+    const uint32_t produced = st->n_out;
+    if (produced < a.out_cap) a.out_tokens[produced] = tok;
+    st->n_out = produced + 1;
+    if (a.counts && a.repeat_penalty > 1.0f && a.repeat_last_n > 0) {
+        a.counts[tok] += 1;
+        const uint32_t total = a.n_prompt + produced + 1;  // history length after this token
+        if (total > a.repeat_last_n) {
+            const uint32_t h = total - 1 - a.repeat_last_n;  // leaves the window
+            const uint32_t old = h < a.n_prompt ? a.prompt[h] : a.out_tokens[h - a.n_prompt];
+            a.counts[old] -= 1;
+        }
+    }
+}
+
+// counts = occurrences of each token in the last repeat_last_n prompt tokens.
+__global__ __launch_bounds__(kT) void sample_counts_kernel(uint32_t* counts, uint32_t V, const uint32_t* prompt,
+                                                          uint32_t n_prompt, uint32_t last_n) {
+    for (uint32_t i = threadIdx.x; i < V; i += kT) counts[i] = 0;
+    __syncthreads();
+    const uint32_t start = n_prompt > last_n ? n_prompt - last_n : 0;
+    for (uint32_t i = start + threadIdx.x; i < n_prompt; i += kT) atomicAdd(&counts[prompt[i]], 1u);
+}
+
+}  // namespace
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
+    return vlaunch(sample_kernel, dim3(1), dim3(kT), 0, s, a);
+}
+
+hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
+                                uint32_t last_n, hipStream_t s) {
+    return vlaunch(sample_counts_kernel, dim3(1), dim3(kT), 0, s, counts, vocab, prompt, n_prompt, last_n);
+}
+
+}  // namespace vvli

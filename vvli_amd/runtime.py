@@ -214,6 +214,21 @@ class Runner:
         return self.logits, am.value
 
     # ---- generator ----
+    def generate(self, prompt, max_new_tokens: int, sampling: "Sampling", eos_token_id: int | None = None,
+                 batched_prefill: bool = False) -> tuple[np.ndarray, Stats]:
+        """generateGreedyMeasured with Options (src/generator.zig:221-293): sampling on the device."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(1, max_new_tokens), dtype=np.uint32)
+        n = c_uint32()
+        st = _lib.CStats()
+        c = sampling.to_c()
+        eos = -1 if eos_token_id is None else int(eos_token_id)
+        _lib.check(_lib.lib().vvli_gpu_generate(self._h, _ptr(p), p.size, max_new_tokens, eos,
+                                                1 if batched_prefill else 0, byref(c), _ptr(out), byref(n),
+                                                byref(st)))
+        stats = Stats(st.prompt_tokens, st.generated_tokens, st.prefill_ns, st.decode_ns, st.total_ns)
+        return out[: n.value].copy(), stats
+
     def generate_greedy_measured(self, prompt, max_new_tokens: int, eos_token_id: int | None = None,
                                  batched_prefill: bool = False) -> tuple[np.ndarray, Stats]:
         """generateGreedyMeasured (src/generator.zig:177-293), greedy sampler."""
@@ -237,6 +252,43 @@ class MoeRunner(Runner):
     @staticmethod
     def _create(*args):
         return _lib.lib().vvli_gpu_moe_model_create(*args)
+
+
+@dataclasses.dataclass
+class Sampling:
+    """generator.Options (src/generator.zig:14-23): the sampler's settings."""
+
+    temperature: float = 0.8
+    top_p: float = 0.95
+    top_k: int = 40
+    repeat_penalty: float = 1.10
+    repeat_last_n: int = 64
+    seed: int = 0
+
+    def to_c(self) -> _lib.CSampling:
+        return _lib.CSampling(self.temperature, self.top_p, self.top_k, self.repeat_penalty, self.repeat_last_n,
+                              self.seed)
+
+
+def prng_seed(seed: int) -> np.ndarray:
+    """DefaultPrng.init(seed) as Sampler.init calls it (seed 0 mapped first)."""
+    st = np.zeros(4, dtype=np.uint64)
+    _lib.lib().vvli_gpu_prng_seed(seed, _ptr(st))
+    return st
+
+
+def sampler_next(logits: np.ndarray, prompt, generated, opts: Sampling, prng_state: np.ndarray) -> int:
+    """Sampler.next (src/generator.zig:93-120) on the device; advances prng_state in place."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    p = np.ascontiguousarray(prompt, dtype=np.uint32)
+    g = np.ascontiguousarray(generated, dtype=np.uint32)
+    assert prng_state.dtype == np.uint64 and prng_state.size == 4 and prng_state.flags.c_contiguous
+    tok = c_uint32()
+    c = opts.to_c()
+    _lib.check(_lib.lib().vvli_gpu_sampler_next(_ptr(lg), lg.size, _ptr(p) if p.size else None, p.size,
+                                                _ptr(g) if g.size else None, g.size, byref(c), _ptr(prng_state),
+                                                byref(tok)))
+    return tok.value
 
 
 def linear(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None = None, stream: int | None = None) -> None:
