@@ -21,7 +21,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxGroup = 16;
-constexpr uint32_t kMinChunk = 64;  // positions per block before another split is used
 constexpr int kMaxSplit = 64;
 
 __device__ inline void rope_pair(const float* src, float* dst, int first, int second, float c, float s) {
@@ -30,6 +29,8 @@ __device__ inline void rope_pair(const float* src, float* dst, int first, int se
     dst[first] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     dst[second] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
 }
+
+__device__ inline float bf16_to_f32_dev(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
 __device__ inline float ld_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -70,26 +71,55 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     const uint32_t pos = *a.pos;
     const uint32_t T = pos + 1;
     uint32_t chunk = (T + a.nsplit - 1) / a.nsplit;
-    if (chunk < kMinChunk) chunk = kMinChunk;
+    if (chunk < static_cast<uint32_t>(TILE)) chunk = TILE;  // one LDS tile per split at least
     const uint32_t t0 = s * chunk;
     const uint32_t t1 = min(t0 + chunk, T);
     const float* cs = a.rope_cs + (size_t)pos * hd;  // [hd/2][2]
 
     if (t0 < t1) {
+        const bool owns_pos = pos >= t0 && pos < t1;
+        const float* qsrc = a.q + (size_t)h * G * hd;
+        const float* ksrc = a.k_new + (size_t)h * hd;
+        if (a.q_norm) {
+            // QK-norm over the full q and the full k (HF OLMoE:
+            // w * (x * 1/sqrt(mean(x^2) + eps))), then RoPE from LDS.
+            float sq = 0.f, sk = 0.f;
+            for (uint32_t i = tid; i < a.heads * a.hd; i += kThreads) sq = fmaf(a.q[i], a.q[i], sq);
+            for (uint32_t i = tid; i < kvw; i += kThreads) sk = fmaf(a.k_new[i], a.k_new[i], sk);
+            sq = wave_sum(sq);
+            sk = wave_sum(sk);
+            if (lane == 0) {
+                wsplit[0][wave] = sq;
+                wsplit[1][wave] = sk;
+            }
+            __syncthreads();
+            float tq = 0.f, tk = 0.f;
+            for (int w = 0; w < kThreads / kWave; ++w) tq += wsplit[0][w], tk += wsplit[1][w];
+            const float scq = 1.0f / sqrtf(tq / (float)(a.heads * a.hd) + a.norm_eps);
+            const float sck = 1.0f / sqrtf(tk / (float)kvw + a.norm_eps);
+            for (int idx = tid; idx < G * hd; idx += kThreads) {
+                const int g = idx / hd, d = idx - g * hd;
+                const uint32_t qi = (h * G + g) * hd + d;
+                qs[g][d] = bf16_to_f32_dev(a.q_norm[qi]) * (a.q[qi] * scq);
+            }
+            if (owns_pos)
+                for (int d = tid; d < hd; d += kThreads)
+                    knew[d] = bf16_to_f32_dev(a.k_norm[h * hd + d]) * (ksrc[d] * sck);
+            __syncthreads();
+            qsrc = nullptr;
+        }
         // RoPE'd q for the group's heads.
         for (int idx = tid; idx < G * half; idx += kThreads) {
             const int g = idx / half, i = idx - g * half;
             int f, sc;
             pair_index(a.rope_layout, i, hd, f, sc);
-            rope_pair(a.q + (size_t)(h * G + g) * hd, qs[g], f, sc, cs[2 * i], cs[2 * i + 1]);
+            rope_pair(qsrc ? qsrc + (size_t)g * hd : qs[g], qs[g], f, sc, cs[2 * i], cs[2 * i + 1]);
         }
-        const bool owns_pos = pos >= t0 && pos < t1;
         if (owns_pos) {
-            const float* kn = a.k_new + (size_t)h * hd;
             for (int i = tid; i < half; i += kThreads) {
                 int f, sc;
                 pair_index(a.rope_layout, i, hd, f, sc);
-                rope_pair(kn, knew, f, sc, cs[2 * i], cs[2 * i + 1]);
+                rope_pair(a.q_norm ? knew : ksrc, knew, f, sc, cs[2 * i], cs[2 * i + 1]);
             }
             for (int d = tid; d < hd; d += kThreads) vnew[d] = a.v_new[(size_t)h * hd + d];
         }
@@ -134,17 +164,26 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
                 *reinterpret_cast<float4*>(&vs[j][c4]) = vv4;
             }
             __syncthreads();
-            // Scores s[g][j] = (q_g . K_j) * scale.
-            for (int idx = tid; idx < G * TILE; idx += kThreads) {
-                const int g = idx / TILE, j = idx - g * TILE;
-                float d0 = 0.f;
-                if (j < tlen) {
-                    for (int d = 0; d < hd; ++d) d0 = fmaf(qs[g][d], ks[j][d], d0);
-                    d0 *= a.scale;
-                } else {
-                    d0 = -INFINITY;
+            // Scores s[g][j] = (q_g . K_j) * scale; QP threads per (g, j) pair
+            // (adjacent lanes) each take hd / QP dimensions, summed by xor shuffles.
+            {
+                const int pairs = G * TILE;
+                int QP = kThreads / pairs;
+                QP = QP >= 16 ? 16 : QP >= 8 ? 8 : QP >= 4 ? 4 : QP >= 2 ? 2 : 1;
+                while (QP > 1 && hd % QP != 0) QP >>= 1;
+                const int dpart = hd / QP;
+                for (int base = 0; base < pairs * QP; base += kThreads) {
+                    const int idx = base + tid;
+                    const int pr = idx / QP, qp = idx - pr * QP;
+                    const int g = pr / TILE, j = pr - g * TILE;
+                    float d0 = 0.f;
+                    if (pr < pairs && j < tlen) {
+                        const int d0i = qp * dpart;
+                        for (int d = d0i; d < d0i + dpart; ++d) d0 = fmaf(qs[g][d], ks[j][d], d0);
+                    }
+                    for (int off = 1; off < QP; off <<= 1) d0 += __shfl_xor(d0, off, kWave);
+                    if (pr < pairs && qp == 0) ps[g][j] = j < tlen ? d0 * a.scale : -INFINITY;
                 }
-                ps[g][j] = d0;
             }
             __syncthreads();
             // Online softmax update, one wave per q head.
@@ -242,8 +281,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 
 }  // namespace
 
-uint32_t attn_nsplit(uint32_t max_seq) {
-    const uint32_t n = (max_seq + kMinChunk - 1) / kMinChunk;
+uint32_t attn_nsplit(uint32_t max_seq, uint32_t hd) {
+    const uint32_t tile = hd <= 64 ? 64u : 32u;  // TILE of the kernel instance
+    const uint32_t n = (max_seq + tile - 1) / tile;
     return n < 1 ? 1 : (n > (uint32_t)kMaxSplit ? (uint32_t)kMaxSplit : n);
 }
 

@@ -80,12 +80,17 @@ struct AttnArgs {
     float* out = nullptr;            // heads*hd
     uint32_t heads = 0, kv_heads = 0, hd = 0, nsplit = 0, rope_layout = 0;
     float scale = 0.f;               // 1/sqrt(hd)
+    // QK-norm (MoE models): RMSNorm weights of the full q / k, applied before RoPE.
+    const uint16_t* q_norm = nullptr;
+    const uint16_t* k_norm = nullptr;
+    float norm_eps = 0.f;
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s);
 size_t attn_part_floats(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t nsplit);
 // Split count for a cache of max_seq positions (grid = nsplit x kv_heads; a
-// step at position pos uses ceil((pos+1)/chunk) of them, chunk >= 64).
-uint32_t attn_nsplit(uint32_t max_seq);
+// step at position pos uses ceil((pos+1)/chunk) of them, chunk >= one LDS
+// tile: 64 positions at head_dim <= 64, 32 above).
+uint32_t attn_nsplit(uint32_t max_seq, uint32_t hd);
 
 // ---------------------------------------------------------------------------
 // Small kernels.
@@ -255,14 +260,23 @@ struct MoeGemvArgs {
     float eps = 0.f;
     float* out = nullptr;                // [top_k * rows_per_slot]
 };
-hipError_t launch_qk_norm(float* q, const uint16_t* wq, uint32_t nq, float* k, const uint16_t* wk, uint32_t nk,
-                          float eps, hipStream_t s);
-hipError_t launch_moe_route(const float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight,
-                            hipStream_t s);
 hipError_t moe_gemv_init_attributes();
-hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s);  // kGemvGateUp or kGemvPlain (down)
-hipError_t launch_moe_combine(float* x, const float* partial, const uint32_t* idx, const float* w, uint32_t top_k,
-                              uint32_t H, hipStream_t s);
+hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s);  // kGemvGateUp
+// Down projection of the selected experts added into x (float atomics).
+hipError_t launch_moe_down(const MoeGemvArgs& a, float* x, const float* slot_w, hipStream_t s);
+struct MoeRouterArgs {
+    const uint16_t* w = nullptr;       // [E][H] router
+    const float* x = nullptr;          // residual stream [H]
+    const uint16_t* norm_w = nullptr;  // post-attention RMSNorm weight
+    float eps = 0.f;
+    uint32_t H = 0, E = 0, top_k = 0;
+    float* logits = nullptr;           // [E] scratch
+    uint32_t* ticket = nullptr;        // zero between launches (the routing block resets it)
+    uint32_t* idx = nullptr;           // [top_k] selected experts
+    float* weight = nullptr;           // [top_k] their probabilities
+};
+// Router GEMV + softmax + top-k in one launch.
+hipError_t launch_moe_router(const MoeRouterArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Token sampling (sample.hip): Sampler.next on device logits.

@@ -75,7 +75,7 @@ struct vvli_gpu_model {
     float* moe_router = nullptr;   // [E] router logits
     uint32_t* moe_idx = nullptr;   // [top_k] selected experts
     float* moe_w = nullptr;        // [top_k] their probabilities
-    float* moe_part = nullptr;     // [top_k][H] expert outputs
+    uint32_t* moe_ticket = nullptr;  // router completion ticket (zero between launches)
     // On-device sampling (vvli_gpu_generate with temperature > 0 or a repeat penalty).
     uint32_t* sample_counts = nullptr;        // [vocab] repeat counts of the window
     unsigned long long* sample_prng = nullptr;  // xoshiro256++ state [4]
@@ -203,10 +203,6 @@ int enqueue_attention_half(vvli_gpu_model* m, hipStream_t s, uint32_t l, const A
             LAUNCH(launch_gemv(kind, kGemvPlain, gi, s));
         }
     }
-    // QK-norm over the full q and k (MoE models that carry it).
-    if (L.q_norm != kNone)
-        LAUNCH(launch_qk_norm(q, static_cast<const uint16_t*>(wslice(m, L.q_norm)), H, kn,
-                              static_cast<const uint16_t*>(wslice(m, L.k_norm)), kv, c.rms_eps, s));
     // 2. RoPE + KV append + attention.
     AttnArgs a;
     a.q = q;
@@ -225,6 +221,11 @@ int enqueue_attention_half(vvli_gpu_model* m, hipStream_t s, uint32_t l, const A
     a.nsplit = m->nsplit;
     a.rope_layout = c.rope_layout;
     a.scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/llm.zig:1313
+    if (L.q_norm != kNone) {  // QK-norm over the full q and k (MoE models that carry it)
+        a.q_norm = static_cast<const uint16_t*>(wslice(m, L.q_norm));
+        a.k_norm = static_cast<const uint16_t*>(wslice(m, L.k_norm));
+        a.norm_eps = c.rms_eps;
+    }
     LAUNCH(launch_attn_decode(a, s));
     // 3. x += Wo . attn
     GemvArgs go;
@@ -243,25 +244,19 @@ int enqueue_moe_ffn(vvli_gpu_model* m, hipStream_t s, uint32_t l) {
     const MoeLayerSlices& L = m->moe_layout.layers[l];
     const uint32_t H = c.hidden, I = c.inter, E = c.num_experts, K = c.experts_per_tok;
     auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
-    GemvArgs gr;
-    gr.w[0] = wslice(m, L.router);
-    gr.out[0] = m->moe_router;
-    gr.rows[0] = E;
-    gr.x = m->x;
-    gr.norm_w = wslice(m, L.post_norm);
-    gr.eps = c.rms_eps;
-    gr.K = H;
-    LAUNCH(launch_gemv(static_cast<int>(c.weight_kind), kGemvPlain, gr, s));
-    LAUNCH(launch_moe_route(m->moe_router, E, K, m->moe_idx, m->moe_w, s));
+    MoeRouterArgs ra;
+    ra.w = w16(L.router), ra.x = m->x, ra.norm_w = w16(L.post_norm), ra.eps = c.rms_eps;
+    ra.H = H, ra.E = E, ra.top_k = K, ra.logits = m->moe_router, ra.ticket = m->moe_ticket;
+    ra.idx = m->moe_idx, ra.weight = m->moe_w;
+    LAUNCH(launch_moe_router(ra, s));
     MoeGemvArgs gu;
     gu.w = w16(L.gate_up), gu.experts = m->moe_idx, gu.top_k = K, gu.rows_per_slot = I, gu.K = H;
     gu.x = m->x, gu.x_len = H, gu.norm_w = w16(L.post_norm), gu.eps = c.rms_eps, gu.out = m->ff;
     LAUNCH(launch_moe_gemv(kGemvGateUp, gu, s));
     MoeGemvArgs gd;
     gd.w = w16(L.down), gd.experts = m->moe_idx, gd.top_k = K, gd.rows_per_slot = H, gd.K = I;
-    gd.x = m->ff, gd.x_len = K * I, gd.out = m->moe_part;
-    LAUNCH(launch_moe_gemv(kGemvPlain, gd, s));
-    LAUNCH(launch_moe_combine(m->x, m->moe_part, m->moe_idx, m->moe_w, K, H, s));
+    gd.x = m->ff, gd.x_len = K * I;
+    LAUNCH(launch_moe_down(gd, m->x, m->moe_w, s));
     return VVLI_OK;
 }
 
@@ -636,7 +631,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_part, m->sample_counts,
+                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -695,7 +690,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     (void)hipGetDevice(&m->device);
     const uint32_t H = cfg->hidden, kv = kv_dim(*cfg), hd = head_dim(*cfg);
     const size_t kvlen = static_cast<size_t>(cfg->layers) * max_seq_len * kv;
-    m->nsplit = attn_nsplit(max_seq_len);
+    m->nsplit = attn_nsplit(max_seq_len, hd);
     m->nkeys = gemv_num_keys(cfg->vocab);
     // Persistent step: bf16 only, one 512-thread block per CU if it fits.
     if (cfg->weight_kind == VVLI_WEIGHT_BF16 && !moe) {
@@ -733,7 +728,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
         TRY_ALLOC(dmalloc(&m->moe_router, cfg->num_experts));
         TRY_ALLOC(dmalloc(&m->moe_idx, cfg->experts_per_tok));
         TRY_ALLOC(dmalloc(&m->moe_w, cfg->experts_per_tok));
-        TRY_ALLOC(dmalloc(&m->moe_part, static_cast<size_t>(cfg->experts_per_tok) * H));
+        TRY_ALLOC(dmalloc(&m->moe_ticket, 1));
     }
     TRY_ALLOC(dmalloc(&m->logits, cfg->vocab));
     TRY_ALLOC(dmalloc(&m->hidden, static_cast<size_t>(cfg->layers) * H));
@@ -770,7 +765,10 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
     TRY_ALLOC(fail_hip(hipMemset(m->state, 0, sizeof(StepState)), "state"));
-    if (moe) TRY_ALLOC(fail_hip(hipMemset(m->moe_idx, 0, cfg->experts_per_tok * sizeof(uint32_t)), "expert ids"));
+    if (moe) {
+        TRY_ALLOC(fail_hip(hipMemset(m->moe_idx, 0, cfg->experts_per_tok * sizeof(uint32_t)), "expert ids"));
+        TRY_ALLOC(fail_hip(hipMemset(m->moe_ticket, 0, sizeof(uint32_t)), "router ticket"));
+    }
     if (m->mk_tw) {
         TRY_ALLOC(fail_hip(hipMemset(m->mk_tw, 0, m->mk_tw_words * sizeof(unsigned long long)), "tag clear"));
         TRY_ALLOC(fail_hip(hipMemset(m->mk_err, 0, 32 * sizeof(uint32_t)), "error clear"));

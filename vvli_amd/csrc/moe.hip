@@ -3,13 +3,14 @@
 // The reference has no MoE forward pass (its runner rejects such configs,
 // src/llm.zig:218-223,426); the semantics follow HF transformers' OLMoE
 // (models/olmoe/modeling_olmoe.py, transformers 5.15):
-//   qk-norm   q = w_q * (q * 1/sqrt(mean(q^2) + eps)) over the full q, same for k
+//   qk-norm   q = w_q * (q * 1/sqrt(mean(q^2) + eps)) over the full q, same for
+//             k (folded into the decode attention kernel, attention.hip)
 //   router    p = softmax(W_r . norm(x)) in f32, the top-k by p (ties: lower
 //             expert id), weights p_k without renormalisation
 //   experts   act_k = silu(gate_k) * up_k (fused [2I][H] gate|up matrix),
 //             out_k = W_down,k . act_k
-//   combine   x += sum over the selected experts in ascending expert id of
-//             (out_k * p_k)
+//   combine   x += sum over the selected experts of (out_k * p_k) (float
+//             atomics: the order over experts varies at the ulp level)
 // Every step reads the selected experts from device memory, so the token
 // step stays one replayable graph with no host round trip.
 #include "device_common.hpp"
@@ -25,30 +26,12 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 
 __device__ inline float bf(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// One block per vector: block 0 normalises q (nq values), block 1 k (nk).
-__global__ __launch_bounds__(kThreads) void qk_norm_kernel(float* __restrict__ q, const uint16_t* __restrict__ wq,
-                                                          uint32_t nq, float* __restrict__ k,
-                                                          const uint16_t* __restrict__ wk, uint32_t nk, float eps) {
-    __shared__ float red[kWavesPerBlock];
-    float* v = blockIdx.x == 0 ? q : k;
-    const uint16_t* w = blockIdx.x == 0 ? wq : wk;
-    const uint32_t n = blockIdx.x == 0 ? nq : nk;
-    float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += kThreads) ss = fmaf(v[i], v[i], ss);
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float total = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWavesPerBlock; ++i) total += red[i];
-    const float s = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += kThreads) v[i] = bf(w[i]) * (v[i] * s);
-}
+// Router: logits = W_r . norm(x), one row per wave over ceil(E / 4) blocks;
+// the last block to finish (atomic ticket) runs the softmax and top-k on the
+// logits (route_wave) and resets the ticket.
 
-// One wave: softmax over E <= 256 router logits, then top-k.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, uint32_t E, uint32_t top_k,
-                                                      uint32_t* __restrict__ idx, float* __restrict__ weight) {
-    const int lane = threadIdx.x;
+__device__ inline void route_wave(const float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight) {
+    const int lane = threadIdx.x & 63;
     float p[4];
     float mx = -INFINITY;
 #pragma unroll
@@ -68,8 +51,6 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
     sum = wave_sum(sum);
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] = p[j] / sum;
-    // Key: probability bits + 1 (non-negative floats order as integers), then
-    // the inverted id, so the maximum key is the highest probability, lowest id.
     uint32_t taken = 0;
     for (uint32_t r = 0; r < top_k; ++r) {
         unsigned long long best = 0ull;
@@ -88,6 +69,76 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
             weight[r] = __uint_as_float(static_cast<uint32_t>(best >> 32) - 1u);
         }
         if (static_cast<uint32_t>(lane) == e % 64) taken |= 1u << (e / 64);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void moe_router_kernel(MoeRouterArgs a) {
+    extern __shared__ float smem[];
+    float* xs = smem;                // [H] normalised input
+    float* red = smem + a.H;         // [waves]
+    __shared__ int last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Stage (x * w) * s.
+    float ss = 0.f;
+    for (uint32_t i = tid * 4; i < a.H; i += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(a.x + i);
+        *reinterpret_cast<float4*>(xs + i) = v;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) total += red[w];
+    const float scale = 1.0f / sqrtf(total / static_cast<float>(a.H) + a.eps);
+    for (uint32_t i = tid; i < a.H; i += kThreads) xs[i] = xs[i] * bf(a.norm_w[i]) * scale;
+    __syncthreads();
+    // Rows e = global wave id, stride = all waves of all blocks; sums in LDS.
+    __shared__ float row_logit[256];
+    const uint32_t gw = blockIdx.x * kWavesPerBlock + wave, nw = gridDim.x * kWavesPerBlock;
+    const uint32_t U = a.H / 8;
+    for (uint32_t e = gw; e < a.E; e += nw) {
+        const uint16_t* row = a.w + static_cast<size_t>(e) * a.H;
+        float acc = 0.f;
+        for (uint32_t u = lane; u < U; u += 64) {
+            const uint4 q = load_unit(row + static_cast<size_t>(u) * 8);
+            float wf[8];
+            WeightTraits<uint16_t>::expand(q, wf);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = fmaf(wf[j], xs[u * 8 + j], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) row_logit[e] = acc;
+    }
+    __syncthreads();
+    // Wave 0 publishes this block's rows, then takes a ticket (its release
+    // orders the wave's own stores); the last block routes.
+    if (wave == 0) {
+        for (uint32_t e = lane; e < a.E; e += 64)
+            if ((e % nw) / kWavesPerBlock == blockIdx.x)
+                __hip_atomic_store(a.logits + e, row_logit[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+            const uint32_t t = __hip_atomic_fetch_add(a.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            last = t == gridDim.x - 1;
+        }
+    }
+    __syncthreads();
+    if (!last) return;
+    if (wave == 0) {
+        float lg[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = lane + 64 * j;
+            lg[j] = e < a.E ? __hip_atomic_load(a.logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+        }
+        // route_wave reads logits through LDS.
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = lane + 64 * j;
+            if (e < a.E) xs[e] = lg[j];
+        }
+        route_wave(xs, a.E, a.top_k, a.idx, a.weight);
+        if (lane == 0) __hip_atomic_store(a.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -204,49 +255,88 @@ __global__ __launch_bounds__(kThreads) void moe_gemv_kernel(MoeGemvArgs a) {
     }
 }
 
-// x[r] += sum over slots in ascending expert id of partial[slot][r] * w[slot].
-__global__ __launch_bounds__(kThreads) void moe_combine_kernel(float* __restrict__ x, const float* __restrict__ partial,
-                                                              const uint32_t* __restrict__ idx,
-                                                              const float* __restrict__ w, uint32_t top_k,
-                                                              uint32_t H) {
-    const uint32_t r = blockIdx.x * kThreads + threadIdx.x;
-    if (r >= H) return;
-    uint32_t order[kMaxTopK];
-    for (uint32_t i = 0; i < top_k; ++i) order[i] = i;
-    for (uint32_t i = 1; i < top_k; ++i)  // insertion sort by expert id (top_k <= 16)
-        for (uint32_t j = i; j > 0 && idx[order[j - 1]] > idx[order[j]]; --j) {
-            const uint32_t t = order[j];
-            order[j] = order[j - 1];
-            order[j - 1] = t;
+// Down projection of the selected experts, combined into x: wave tiles of
+// four rows r..r+3 of one slot's expert; K = I is short (1024 at OLMoE), so
+// an item is two 16-byte units per lane per row (the whole row at once);
+// lane 0 adds p_slot * (W_down,e . act_slot) for its rows into x with float
+// atomics (the order over slots then varies at the ulp level).
+constexpr int kDownRows = 4;
+constexpr int kDownNJ = 2;
+
+__global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeGemvArgs a, float* __restrict__ x,
+                                                           const float* __restrict__ slot_w) {
+    extern __shared__ float smem[];
+    float* xs = smem;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * kWavesPerBlock;
+    const uint32_t K = a.K, U = K / 8;
+    const uint32_t per_item = kDownNJ * kWave;
+    const uint32_t nchunk = (U + per_item - 1) / per_item;
+    const uint32_t ntiles = a.top_k * a.rows_per_slot / kDownRows;
+    // Stage every slot's activations.
+    for (uint32_t i = threadIdx.x * 4; i < a.x_len; i += kThreads * 4)
+        *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(a.x + i);
+    __syncthreads();
+    for (uint32_t tile = wid; tile < ntiles; tile += nwaves) {
+        const uint32_t g0 = tile * kDownRows;
+        const uint32_t slot = g0 / a.rows_per_slot, r0 = g0 % a.rows_per_slot;
+        const uint32_t e = a.experts[slot];
+        const uint16_t* base = a.w + (static_cast<size_t>(e) * a.rows_per_slot + r0) * K;
+        const float* xsl = xs + static_cast<size_t>(slot) * K;
+        float acc[kDownRows] = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t c = 0; c < nchunk; ++c) {
+            uint4 buf[kDownRows][kDownNJ];
+#pragma unroll
+            for (int j = 0; j < kDownNJ; ++j) {
+                const uint32_t u = c * per_item + j * kWave + lane;
+#pragma unroll
+                for (int r = 0; r < kDownRows; ++r)
+                    buf[r][j] = u < U ? load_unit(base + static_cast<size_t>(r) * K + static_cast<size_t>(u) * 8)
+                                      : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < kDownNJ; ++j) {
+                const uint32_t u = c * per_item + j * kWave + lane;
+                if (u >= U) continue;
+                float xv[8];
+#pragma unroll
+                for (int q = 0; q < 8; q += 4) {
+                    const float4 t = *reinterpret_cast<const float4*>(xsl + static_cast<size_t>(u) * 8 + q);
+                    xv[q] = t.x, xv[q + 1] = t.y, xv[q + 2] = t.z, xv[q + 3] = t.w;
+                }
+#pragma unroll
+                for (int r = 0; r < kDownRows; ++r) {
+                    float wf[8];
+                    WeightTraits<uint16_t>::expand(buf[r][j], wf);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) acc[r] = fmaf(wf[q], xv[q], acc[r]);
+                }
+            }
         }
-    float s = 0.f;
-    for (uint32_t i = 0; i < top_k; ++i) {
-        const uint32_t slot = order[i];
-        s = __fadd_rn(s, __fmul_rn(partial[static_cast<size_t>(slot) * H + r], w[slot]));
+        const float pw = slot_w[slot];
+#pragma unroll
+        for (int r = 0; r < kDownRows; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == 0) unsafeAtomicAdd(x + r0 + r, __fmul_rn(s, pw));
+        }
     }
-    x[r] = __fadd_rn(x[r], s);
 }
 
 }  // namespace
-
-hipError_t launch_qk_norm(float* q, const uint16_t* wq, uint32_t nq, float* k, const uint16_t* wk, uint32_t nk,
-                          float eps, hipStream_t s) {
-    return vlaunch(qk_norm_kernel, dim3(2), dim3(kThreads), 0, s, q, wq, nq, k, wk, nk, eps);
-}
-
-hipError_t launch_moe_route(const float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight,
-                            hipStream_t s) {
-    if (E == 0 || E > 256 || top_k == 0 || top_k > E || top_k > static_cast<uint32_t>(kMaxTopK))
-        return hipErrorInvalidValue;
-    return vlaunch(moe_route_kernel, dim3(1), dim3(64), 0, s, logits, E, top_k, idx, weight);
-}
 
 hipError_t moe_gemv_init_attributes() {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemv_kernel<kGemvGateUp>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemv_kernel<kGemvPlain>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_down_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    // The router kernel also has static LDS: its dynamic part (the hidden
+    // vector) is capped at 64 KiB, hidden <= 16384.
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_router_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+    return e;
 }
 
 hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s) {
@@ -257,15 +347,25 @@ hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s) {
     uint32_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks > 1024) blocks = 1024;
     const size_t lds = (static_cast<size_t>(a.x_len) + kWavesPerBlock) * sizeof(float);
-    if (mode == kGemvGateUp) return vlaunch(moe_gemv_kernel<kGemvGateUp>, dim3(blocks), dim3(kThreads), lds, s, a);
-    return vlaunch(moe_gemv_kernel<kGemvPlain>, dim3(blocks), dim3(kThreads), lds, s, a);
+    if (mode != kGemvGateUp) return hipErrorInvalidValue;
+    return vlaunch(moe_gemv_kernel<kGemvGateUp>, dim3(blocks), dim3(kThreads), lds, s, a);
 }
 
-hipError_t launch_moe_combine(float* x, const float* partial, const uint32_t* idx, const float* w, uint32_t top_k,
-                              uint32_t H, hipStream_t s) {
-    if (top_k > static_cast<uint32_t>(kMaxTopK)) return hipErrorInvalidValue;
-    return vlaunch(moe_combine_kernel, dim3((H + kThreads - 1) / kThreads), dim3(kThreads), 0, s, x, partial, idx, w,
-                   top_k, H);
+hipError_t launch_moe_router(const MoeRouterArgs& a, hipStream_t s) {
+    if (a.E == 0 || a.E > 256 || a.top_k == 0 || a.top_k > a.E || a.top_k > static_cast<uint32_t>(kMaxTopK) ||
+        a.H % 8 != 0 || a.H > 16384 - kWavesPerBlock)
+        return hipErrorInvalidValue;
+    const size_t lds = (static_cast<size_t>(a.H) + kWavesPerBlock) * sizeof(float);
+    return vlaunch(moe_router_kernel, dim3((a.E + kWavesPerBlock - 1) / kWavesPerBlock), dim3(kThreads), lds, s, a);
+}
+
+hipError_t launch_moe_down(const MoeGemvArgs& a, float* x, const float* slot_w, hipStream_t s) {
+    if (a.K % 8 != 0 || a.x_len % 4 != 0 || a.rows_per_slot % kDownRows != 0) return hipErrorInvalidValue;
+    const uint32_t tiles = a.top_k * a.rows_per_slot / kDownRows;
+    uint32_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (blocks > 1024) blocks = 1024;
+    const size_t lds = static_cast<size_t>(a.x_len) * sizeof(float);
+    return vlaunch(moe_down_kernel, dim3(blocks), dim3(kThreads), lds, s, a, x, slot_w);
 }
 
 }  // namespace vvli
