@@ -113,6 +113,120 @@ def cpu_baseline(cfg, blob, budget_s: float, max_tokens: int) -> dict:
     return {"tokens": tokens, "seconds": dt, "threads": threads, "prompt": prompt}
 
 
+def make_blob(cfg):
+    """Seeded synthetic bf16 weights: N(0, 0.02), RMSNorm weights 1; MoE
+    routers N(0, 1/sqrt(hidden)) so router logits are about N(0, 1)."""
+    from vvli_amd import config as C
+    from vvli_amd import runtime as R
+
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02)
+    if cfg.num_experts:
+        n = cfg.num_experts * cfg.hidden_size
+        rng = np.random.default_rng(100)
+        for l in range(cfg.num_hidden_layers):
+            off = R.moe_slice_offset(cfg, l, "router")
+            v = rng.normal(0, 1 / np.sqrt(cfg.hidden_size), n).astype(np.float32).view(np.uint32).astype(np.uint64)
+            blob[off:off + n] = ((v + 0x7FFF + ((v >> 16) & 1)) >> 16).astype(np.uint16)
+    return blob
+
+
+def moe_token_bytes(cfg, pos: int) -> int:
+    """Algorithmic HBM bytes of one MoE decode token: attention weights, the
+    router, the top-k experts' gate/up/down, norms, lm_head, the embedding row
+    and the f32 KV read (0..pos) and write."""
+    H, I, V, kv = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.kv_dim()
+    E, K, L = cfg.num_experts, cfg.num_experts_per_token, cfg.num_hidden_layers
+    layer = 2 * (H * H * 2 + 2 * kv * H) + 2 * (2 * H + (H + kv if cfg.qk_norm else 0))
+    layer += E * H * 2 + K * 3 * I * H * 2
+    kv_bytes = L * 2 * kv * 4 * (pos + 2)
+    return L * layer + V * H * 2 + H * 2 + H * 2 + kv_bytes
+
+
+def moe_decode_main(args, cfg, blob) -> int:
+    """MoE decode (per-kernel graph path): tok/s and the whole-step roofline."""
+    import torch
+
+    from vvli_amd import runtime as R
+
+    runner = R.MoeRunner(cfg, blob, args.ctx)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
+    runner.generate_greedy_measured(prompt[:8], max(1, args.warmup))
+    runner.kv_clear()
+    torch.cuda.synchronize()
+    _, stats = runner.generate_greedy_measured(prompt, args.steps)
+    torch.cuda.synchronize()
+    decode_s = stats.decode_nanoseconds / 1e9
+    tok_s = args.steps / decode_s
+    step_bytes = sum(moe_token_bytes(cfg, p) for p in range(args.prompt, args.prompt + args.steps))
+    gbs = step_bytes / decode_s / 1e9
+    line = {
+        "metric": "decode tok/s @bs1 + HBM GB/s (% of peak), MoE", "value": round(tok_s, 2), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(decode_s * 1e3 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.model} bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
+                   "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32", "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": round(stats.prefill_tokens_per_second(), 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "MoE token step (per-kernel HIP graph, one replay per token)",
+                     "bytes_per_launch": step_bytes // args.steps},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    runner.close()
+    return 0
+
+
+def prefill_main(args, cfg, blob) -> int:
+    """Batched-prefill sweep (vvli_gpu_prefill): best of three per length.
+    Flops = 2 * rows * (projection weights) + 4 * heads * hd * (causal key
+    count) per layer: the useful work, without the lo half of the hi/lo split."""
+    import torch
+
+    from vvli_amd import runtime as R
+
+    runner = R.Runner(cfg, blob, args.ctx)
+    runner.set_prefill_path("batched")
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.ctx).astype(np.uint32)
+    runner.prefill(prompt[:64])
+    H, I, kv, L = cfg.hidden_size, cfg.intermediate_size, cfg.kv_dim(), cfg.num_hidden_layers
+    proj = L * (H * H + 2 * kv * H + H * H + 3 * I * H)
+
+    def flops(n):
+        return 2 * n * proj + L * 4 * cfg.num_attention_heads * cfg.head_dim() * n * (n + 1) // 2
+
+    sweep = {}
+    for n in sorted({128, 512, 2048, min(4096, args.ctx), args.prompt}):
+        if n > args.ctx:
+            continue
+        best = 1e9
+        for _ in range(3):
+            runner.kv_clear()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            runner.prefill(prompt[:n])
+            best = min(best, time.perf_counter() - t)
+        sweep[n] = {"ms": round(best * 1e3, 3), "tok_s": round(n / best, 1),
+                    "tflops": round(flops(n) / best / 1e12, 1)}
+        print(f"[bench] prefill n={n}: {best * 1e3:.2f} ms, {n / best:.0f} tok/s", file=sys.stderr, flush=True)
+    main_n = args.prompt
+    res = sweep[main_n]
+    line = {
+        "metric": "prefill tok/s (batched), bf16", "value": res["tok_s"], "unit": "tok/s", "n_gpus": 1,
+        "steps": 3, "warmup": 1, "ms_per_step": res["ms"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.model} bf16 prefill of {main_n} tokens", "ctx": args.ctx},
+        "roofline": {"bound": "mfma", "achieved": res["tflops"], "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(res["tflops"] / 2500.0, 4), "traffic": None,
+                     "kernel": "whole prefill (GEMMs + attention), wall clock"},
+        "sweep": sweep,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    runner.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +240,11 @@ def main() -> int:
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],
                     help="prompt processing: batched GEMM prefill, or one token step per prompt token (the reference's loop)")
+    ap.add_argument("--mode", default="decode", choices=["decode", "prefill"],
+                    help="decode: the headline decode benchmark; prefill: batched-prefill throughput sweep")
+    ap.add_argument("--model", default="llama-3.2-1b",
+                    choices=["llama-3.2-1b", "qwen2.5-0.5b", "qwen2.5-7b", "olmoe-1b-7b"],
+                    help="decoder shape (synthetic bf16 weights); the default is the headline workload")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
@@ -142,11 +261,15 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
-    cfg = C.llama32_1b()
+    cfg = C.NAMED[args.model]()
     t = time.perf_counter()
-    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02)
+    blob = make_blob(cfg)
     print(f"[bench] synthetic blob {blob.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f}s", file=sys.stderr,
           flush=True)
+    if args.mode == "prefill":
+        return prefill_main(args, cfg, blob)
+    if cfg.num_experts:
+        return moe_decode_main(args, cfg, blob)
     runner = R.Runner(cfg, blob, args.ctx)
     runner.set_decode_path(args.path)
     runner.set_prefill_path("auto" if args.prefill == "batched" else "loop")
@@ -254,7 +377,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "llama-3.2-1b bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
+        "config": {"workload": f"{args.model} bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
                    "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32", "prefill": args.prefill,
                    "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(prefill_tok_s, 2),

@@ -150,3 +150,12 @@ def test_moe_runner_rejects_what_it_cannot_run():
     with pytest.raises(_lib.VvliError) as e:
         R.MoeRunner(dense, np.zeros(16, np.uint16), 16)
     assert e.value.name == "InvalidConfig"
+
+
+def test_moe_slice_offsets_match_oracle(oracle_mod):
+    for cfg in (C.olmoe_1b_7b(), fixture()[1]):
+        lay = oracle_mod.moe_layout(cfg, C.WEIGHT_BF16)
+        for l in range(cfg.num_hidden_layers):
+            for k, v in lay["layers"][l].items():
+                if v is not None:
+                    assert R.moe_slice_offset(cfg, l, k) == v, (l, k)

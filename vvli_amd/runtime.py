@@ -54,6 +54,36 @@ def llama3_inv_freq(head_dim: int, theta: float, factor: float = 32.0, low_freq_
     return out
 
 
+def moe_slice_offset(cfg: Config, layer: int, slot: str, weight_kind: int = WEIGHT_BF16) -> int:
+    """Element offset of one slice of the MoE blob (vvli_gpu_moe_storage_element_count's
+    layout: per layer input_norm, q, (q_bias), k, (k_bias), v, (v_bias), (q_norm,
+    k_norm), o, post_norm, router, gate_up, down; 64-byte aligned)."""
+    ea = 64 // (2 if weight_kind == WEIGHT_BF16 else 4)
+    H, kv, I, E = cfg.hidden_size, cfg.kv_dim(), cfg.intermediate_size, cfg.num_experts
+    cur = 0
+
+    def take(n):
+        nonlocal cur
+        cur = (cur + ea - 1) // ea * ea
+        at = cur
+        cur += n
+        return at
+
+    take(cfg.vocab_size * H)
+    for l in range(cfg.num_hidden_layers):
+        sizes = [("input_norm", H), ("q", H * H), ("q_bias", H if cfg.qkv_bias else None), ("k", kv * H),
+                 ("k_bias", kv if cfg.qkv_bias else None), ("v", kv * H), ("v_bias", kv if cfg.qkv_bias else None),
+                 ("q_norm", H if cfg.qk_norm else None), ("k_norm", kv if cfg.qk_norm else None), ("o", H * H),
+                 ("post_norm", H), ("router", E * H), ("gate_up", E * 2 * I * H), ("down", E * H * I)]
+        for name, n in sizes:
+            if n is None:
+                continue
+            at = take(n)
+            if l == layer and name == slot:
+                return at
+    raise KeyError(slot)
+
+
 def argmax(logits: np.ndarray) -> int:
     """llm.argmax (src/llm.zig:778-789): first index of the strict maximum."""
     best, bv = 0, logits[0]
