@@ -108,6 +108,28 @@ int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, cons
                           size_t blob_elems, vvli_gpu_model** out);
 int vvli_gpu_model_destroy(vvli_gpu_model* model);
 
+/* Progress callback: LoadProgress.report (called with (0, total, "start"),
+ * then once per tensor with the tensor's name; src/llm.zig:68-75, 1067-1079). */
+typedef void (*vvli_host_progress_fn)(void* user, size_t completed, size_t total, const char* name);
+
+/* loadOwnedFromSafetensorsFile / loadOwnedFromGgufFile (src/llm.zig:849-921)
+ * straight into HBM: the same parsing, names, checks and error codes as
+ * vvli_host_load_safetensors / vvli_host_load_gguf, but no host blob. Tensors
+ * whose dtype matches the blob are copied from `bytes` (e.g. a read-only file
+ * mapping) to the device; F32 / F16 / BF16 tensors of another dtype are
+ * converted by a device kernel with the same bit rules (f32 -> bf16 round to
+ * nearest even, f16 widened exactly). The GGUF form derives the config
+ * (Config.fromGguf) and returns it in cfg_out (nullable). */
+int vvli_gpu_model_create_from_safetensors(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* bytes,
+                                           size_t len, vvli_host_progress_fn progress, void* user,
+                                           vvli_gpu_model** out);
+int vvli_gpu_model_create_from_gguf(const void* bytes, size_t len, uint32_t weight_kind, uint32_t max_seq_len,
+                                    vvli_host_progress_fn progress, void* user, vvli_gpu_config* cfg_out,
+                                    vvli_gpu_model** out);
+/* Copy n blob elements starting at elem_offset back to the host (the blob's
+ * dtype; for checks of what a loader wrote). */
+int vvli_gpu_read_weights(vvli_gpu_model* model, uint64_t elem_offset, uint64_t n, void* out);
+
 /* Mixture-of-experts decoder (OLMoE form). No reference counterpart: the
  * reference's Config carries num_experts / num_experts_per_tok / qk_norm
  * (src/llm.zig:86-88) but its runner rejects them (src/llm.zig:218-223,426).

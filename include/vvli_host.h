@@ -53,9 +53,7 @@ int vvli_host_llama3_inv_freq(uint32_t head_dim, float theta, float factor, floa
 /* ---------------------------------------------------------------------- */
 /* Checkpoint loaders (src/llm.zig:839-1226, src/gguf.zig:234-354)          */
 /* ---------------------------------------------------------------------- */
-/* Progress callback: LoadProgress.report (called with (0, total, "start"),
- * then once per tensor with the tensor's name; src/llm.zig:68-75, 1067-1079). */
-typedef void (*vvli_host_progress_fn)(void* user, size_t completed, size_t total, const char* name);
+/* vvli_host_progress_fn (LoadProgress.report) is declared in vvli_gpu.h. */
 
 /* Config.fromJson, src/llm.zig:98-145 (HF config.json text, len bytes):
  * model_type llama/mistral/olmoe/qwen2, required vocab_size, hidden_size,

@@ -14,6 +14,7 @@ import torch
 from vvli_amd import config as C
 from vvli_amd import loaders as L
 from vvli_amd import runtime as R
+from vvli_amd._lib import VvliError as VvliErr
 
 pytestmark = pytest.mark.gpu
 
@@ -88,3 +89,85 @@ def test_gguf_file_runs_like_oracle(tmp_path, oracle_mod, host_threads):
         for pos, tok in enumerate(tokens):
             e = rel_err(gpu.forward_token(int(tok), pos), orc.forward_token(int(tok), pos))
             assert e <= TOL, f"gguf pos {pos}: {e:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# Device-side loading (vvli_gpu_model_create_from_*): the blob written in HBM
+# must equal, bit for bit, the blob the host loader builds from the same file.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("kind", [C.WEIGHT_F32, C.WEIGHT_BF16])
+def test_device_gguf_blob_equals_host(kind, tmp_path):
+    from test_loaders import GG_BF16, GG_F16, GG_F32, gguf_cfg, gguf_for
+
+    want = gguf_cfg(tie=False)
+    w, _ = gguf_for(want, dtype_of=lambda n: (GG_F32, GG_F16, GG_BF16)[sum(map(ord, n)) % 3])
+    # f16 special values (subnormals, infinities, quiet and signalling NaNs) in the embedding.
+    specials = np.array([0x0001, 0x03FF, 0x7C00, 0xFC00, 0x7C01, 0x7E00, 0x7FFF, 0xFFFF, 0x3C00], np.uint16)
+    n = want.vocab_size * want.hidden_size
+    w.tensors[0][2] = GG_F16
+    w.tensors[0][3] = np.resize(specials, n).tobytes()
+    path = tmp_path / "m.gguf"
+    path.write_bytes(w.build())
+    cfg, host = L.load_gguf(path, kind)
+    print(f"device gguf kind={kind}", flush=True)
+    cfg2, runner = L.device_load_gguf(path, 16, kind)
+    with runner:
+        assert cfg2 == cfg
+        dev = runner.read_weights(0, host.size)
+        assert np.array_equal(dev.view(np.uint16 if kind == C.WEIGHT_BF16 else np.uint32),
+                              host.view(np.uint16 if kind == C.WEIGHT_BF16 else np.uint32))
+
+
+@pytest.mark.parametrize("kind", [C.WEIGHT_F32, C.WEIGHT_BF16])
+def test_device_safetensors_equals_host(kind, tmp_path):
+    from safetensors.torch import save_file
+    from test_loaders import random_tensors, tiny
+
+    cfg = tiny("qwen2", False, True)
+    tensors = random_tensors(cfg, "hf", 5, lambda n: torch.bfloat16 if sum(map(ord, n)) % 2 else torch.float32)
+    path = tmp_path / "model.safetensors"
+    save_file(tensors, str(path))
+    host = L.load_safetensors(cfg, path, kind)
+    seen = []
+    print(f"device safetensors kind={kind}", flush=True)
+    with L.device_load_safetensors(cfg, path, 16, kind, progress=lambda d, t, n: seen.append(n)) as runner:
+        assert np.array_equal(runner.read_weights(0, host.size), host)
+        assert seen[0] == "start" and seen[-1] == "lm_head.weight"
+        with R.Runner(cfg, host, 16) as ref:
+            for pos, tok in enumerate([3, 7, 1]):
+                assert np.array_equal(runner.forward_token(tok, pos), ref.forward_token(tok, pos))
+
+
+def test_device_loader_errors(tmp_path):
+    from safetensors.torch import save_file
+    from test_loaders import random_tensors, tiny
+
+    cfg = tiny("llama", True, False)
+    t = random_tensors(cfg, "hf", 1)
+    del t["model.norm.weight"]
+    path = tmp_path / "model.safetensors"
+    save_file(t, str(path))
+    with pytest.raises(VvliErr) as e:
+        L.device_load_safetensors(cfg, path, 16)
+    assert e.value.name == "MissingSafetensorsTensor"
+    (tmp_path / "bad.gguf").write_bytes(b"GGUF" + bytes(60))
+    with pytest.raises(VvliErr) as e:
+        L.device_load_gguf(tmp_path / "bad.gguf", 16)
+    assert e.value.name == "UnsupportedGgufVersion"
+
+
+def test_device_convert_spans_staging_chunks(tmp_path):
+    """An f32 embedding of 9000 x 2048 (70 MiB) converted to bf16 on the device
+    crosses the 64 MiB staging buffer: every chunk must land at its offset."""
+    from safetensors.torch import save_file
+    from test_loaders import random_tensors
+
+    cfg = C.Config(vocab_size=9000, hidden_size=2048, intermediate_size=256, num_hidden_layers=1,
+                   num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=16, rope_theta=1e4,
+                   rms_norm_eps=1e-6, tie_word_embeddings=True, architecture="llama", qkv_bias=False)
+    path = tmp_path / "model.safetensors"
+    save_file(random_tensors(cfg, "hf", 9), str(path))
+    host = L.load_safetensors(cfg, path, C.WEIGHT_BF16)
+    print("device safetensors 70 MiB embedding", flush=True)
+    with L.device_load_safetensors(cfg, path, 16, C.WEIGHT_BF16) as runner:
+        assert np.array_equal(runner.read_weights(0, host.size), host)

@@ -106,6 +106,11 @@ PROTOTYPES = {
     "vvli_gpu_model_create": (c_int, [POINTER(CConfig), c_uint32, c_void_p, c_size_t, POINTER(c_void_p)]),
     "vvli_gpu_model_destroy": (c_int, [c_void_p]),
     "vvli_gpu_moe_storage_element_count": (c_uint64, [POINTER(CConfig)]),
+    "vvli_gpu_model_create_from_safetensors": (
+        c_int, [POINTER(CConfig), c_uint32, c_void_p, c_size_t, PROGRESS_FN, c_void_p, POINTER(c_void_p)]),
+    "vvli_gpu_model_create_from_gguf": (
+        c_int, [c_void_p, c_size_t, c_uint32, c_uint32, PROGRESS_FN, c_void_p, POINTER(CConfig), POINTER(c_void_p)]),
+    "vvli_gpu_read_weights": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p]),
     "vvli_gpu_moe_model_create": (c_int, [POINTER(CConfig), c_uint32, c_void_p, c_size_t, POINTER(c_void_p)]),
     "vvli_gpu_kv_clear": (c_int, [c_void_p]),
     "vvli_gpu_set_rope_table": (c_int, [c_void_p, c_void_p, c_uint32]),

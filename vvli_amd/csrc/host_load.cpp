@@ -641,7 +641,8 @@ float f16_to_f32(uint16_t h) {
     return f;
 }
 
-enum SrcType { S_F32, S_F16, S_BF16 };
+using SrcType = TensorSrc;
+constexpr TensorSrc S_F32 = kSrcF32, S_F16 = kSrcF16, S_BF16 = kSrcBF16;
 
 // Copies `n` elements of type `src` from `raw` into blob slice `dst`, converting
 // to the blob's element type. Same-type copies are byte copies.
@@ -734,8 +735,8 @@ void report(vvli_host_progress_fn fn, void* user, size_t done, size_t total, con
 
 // One safetensors entry (parseTensorInfo + copyTensorIntoWeight,
 // src/llm.zig:1149-1218), checks in the reference's order.
-int copy_safetensor(const JVal& tensors, const uint8_t* data, size_t data_len, const Slot& s, void* blob,
-                    uint32_t kind) {
+int copy_safetensor(const JVal& tensors, const uint8_t* data, size_t data_len, const Slot& s, TensorPut put,
+                    void* ctx) {
     const char* name = s.hf.c_str();
     const JVal* meta = tensors.get(name);
     if (!meta) return set_error(VVLI_MISSING_TENSOR, "safetensors lacks %s", name);
@@ -769,13 +770,12 @@ int copy_safetensor(const JVal& tensors, const uint8_t* data, size_t data_len, c
     if (end - start != s.elems * esz)
         return set_error(VVLI_INVALID_WEIGHT, "%s: %llu bytes for %zu %s elements", name,
                          static_cast<unsigned long long>(end - start), s.elems, dt->s.c_str());
-    convert_into(blob, kind, s.offset, data + start, src, s.elems);
-    return VVLI_OK;
+    return put(ctx, s.offset, data + start, src, s.elems);
 }
 
 // One GGUF entry (copyGgufTensorIntoWeight + ggufTensorByteLen,
 // src/llm.zig:1081-1147).
-int copy_gguf_tensor(const GFile& f, const uint8_t* bytes, size_t len, const Slot& s, void* blob, uint32_t kind) {
+int copy_gguf_tensor(const GFile& f, const uint8_t* bytes, size_t len, const Slot& s, TensorPut put, void* ctx) {
     const char* name = s.gguf.c_str();
     const GTensor* t = f.tensor(s.gguf);
     if (!t) return set_error(VVLI_MISSING_TENSOR, "GGUF lacks %s", name);
@@ -795,11 +795,78 @@ int copy_gguf_tensor(const GFile& f, const uint8_t* bytes, size_t len, const Slo
     if (__builtin_add_overflow(f.data_start, t->offset, &start) || __builtin_add_overflow(start, nbytes, &end) ||
         end > len)
         return set_error(VVLI_INVALID_WEIGHT, "%s: data lies beyond the end of the file", name);
-    convert_into(blob, kind, s.offset, bytes + start, src, s.elems);
+    return put(ctx, s.offset, bytes + start, src, s.elems);
+}
+
+struct HostSink {
+    void* blob;
+    uint32_t kind;
+};
+int host_put(void* ctx, size_t dst, const uint8_t* raw, TensorSrc src, size_t n) {
+    auto* h = static_cast<HostSink*>(ctx);
+    convert_into(h->blob, h->kind, dst, raw, src, n);
     return VVLI_OK;
 }
 
 }  // namespace
+
+int load_safetensors_into(const vvli_gpu_config& cfg, const void* bytes, size_t len, TensorPut put, void* ctx,
+                          vvli_host_progress_fn progress, void* user) {
+    // OwnedModel.init (src/llm.zig:424-446) rejects configs the dense runner
+    // cannot hold before any tensor is read.
+    int rc = validate_config(cfg, true);
+    if (rc) return rc;
+    if (!bytes) return set_error(VVLI_NULL_ARG, "bytes is NULL");
+    const BlobLayout L = compute_layout(cfg);
+    const uint8_t* b = static_cast<const uint8_t*>(bytes);
+    if (len < 8) return set_error(VVLI_INVALID_WEIGHT, "safetensors file shorter than its 8-byte header length");
+    uint64_t hlen;
+    memcpy(&hlen, b, 8);
+    if (hlen > len - 8) return set_error(VVLI_INVALID_WEIGHT, "safetensors header runs past the end of the file");
+    JVal root;
+    if (!JsonReader(reinterpret_cast<const char*>(b + 8), hlen).document(root))
+        return set_error(VVLI_INVALID_FILE, "safetensors header is not valid JSON");
+    if (root.kind != JVal::Obj) return set_error(VVLI_INVALID_WEIGHT, "safetensors header is not an object");
+    const uint8_t* data = b + 8 + hlen;
+    const size_t data_len = len - 8 - hlen;
+    std::vector<Slot> list = slots(cfg, L);
+    report(progress, user, 0, list.size(), "start");
+    for (size_t k = 0; k < list.size(); ++k) {
+        if ((rc = copy_safetensor(root, data, data_len, list[k], put, ctx))) return rc;
+        report(progress, user, k + 1, list.size(), list[k].hf.c_str());
+    }
+    return VVLI_OK;
+}
+
+int load_gguf_into(const vvli_gpu_config& cfg, const void* bytes, size_t len, TensorPut put, void* ctx,
+                   vvli_host_progress_fn progress, void* user) {
+    int rc = validate_config(cfg, true);
+    if (rc) return rc;
+    if (!bytes) return set_error(VVLI_NULL_ARG, "bytes is NULL");
+    // loadGgufIntoOwnedModel (src/llm.zig:1008-1011): GGUF files carry no
+    // q/k/v bias tensors.
+    if (cfg.qkv_bias) return set_error(VVLI_UNSUPPORTED_ARCH, "GGUF loading does not support q/k/v bias");
+    GFile f;
+    const uint8_t* b = static_cast<const uint8_t*>(bytes);
+    if ((rc = gguf_parse(b, len, f))) return rc;
+    const BlobLayout L = compute_layout(cfg);
+    std::vector<Slot> list = slots(cfg, L);
+    report(progress, user, 0, list.size(), "start");
+    for (size_t k = 0; k < list.size(); ++k) {
+        if ((rc = copy_gguf_tensor(f, b, len, list[k], put, ctx))) return rc;
+        report(progress, user, k + 1, list.size(), list[k].gguf.c_str());
+    }
+    return VVLI_OK;
+}
+
+int gguf_config(const void* bytes, size_t len, uint32_t weight_kind, vvli_gpu_config& out) {
+    if (!bytes) return set_error(VVLI_NULL_ARG, "bytes is NULL");
+    GFile f;
+    int rc = gguf_parse(static_cast<const uint8_t*>(bytes), len, f);
+    if (rc) return rc;
+    return config_from_gguf(f, weight_kind, out);
+}
+
 }  // namespace vvli
 
 using namespace vvli;
@@ -818,11 +885,8 @@ int vvli_host_config_from_json(const char* json, size_t len, uint32_t weight_kin
 int vvli_host_config_from_gguf(const void* bytes, size_t len, uint32_t weight_kind, vvli_gpu_config* out) {
     if (!bytes || !out) return set_error(VVLI_NULL_ARG, "bytes or out is NULL");
     clear_error();
-    GFile f;
-    int rc = gguf_parse(static_cast<const uint8_t*>(bytes), len, f);
-    if (rc) return rc;
     vvli_gpu_config c;
-    rc = config_from_gguf(f, weight_kind, c);
+    const int rc = gguf_config(bytes, len, weight_kind, c);
     if (rc == VVLI_OK) *out = c;
     return rc;
 }
@@ -832,29 +896,11 @@ int vvli_host_load_safetensors(const vvli_gpu_config* cfg, const void* bytes, si
     BlobLayout L;
     int rc = check_target(cfg, blob, blob_elems, L);
     if (rc) return rc;
-    if (!bytes) return set_error(VVLI_NULL_ARG, "bytes is NULL");
     clear_error();
-    const uint8_t* b = static_cast<const uint8_t*>(bytes);
-    if (len < 8) return set_error(VVLI_INVALID_WEIGHT, "safetensors file shorter than its 8-byte header length");
-    uint64_t hlen;
-    memcpy(&hlen, b, 8);
-    if (hlen > len - 8) return set_error(VVLI_INVALID_WEIGHT, "safetensors header runs past the end of the file");
-    JVal root;
-    if (!JsonReader(reinterpret_cast<const char*>(b + 8), hlen).document(root))
-        return set_error(VVLI_INVALID_FILE, "safetensors header is not valid JSON");
-    if (root.kind != JVal::Obj) return set_error(VVLI_INVALID_WEIGHT, "safetensors header is not an object");
-    const uint8_t* data = b + 8 + hlen;
-    const size_t data_len = len - 8 - hlen;
-    std::vector<Slot> list = slots(*cfg, L);
     // Alignment padding stays zero, like a freshly allocated OwnedModel.
     memset(blob, 0, L.total * elem_bytes(*cfg));
-    report(progress, user, 0, list.size(), "start");
-    for (size_t k = 0; k < list.size(); ++k) {
-        rc = copy_safetensor(root, data, data_len, list[k], blob, cfg->weight_kind);
-        if (rc) return rc;
-        report(progress, user, k + 1, list.size(), list[k].hf.c_str());
-    }
-    return VVLI_OK;
+    HostSink sink{blob, cfg->weight_kind};
+    return load_safetensors_into(*cfg, bytes, len, host_put, &sink, progress, user);
 }
 
 int vvli_host_load_gguf(const vvli_gpu_config* cfg, const void* bytes, size_t len, void* blob, size_t blob_elems,
@@ -862,23 +908,10 @@ int vvli_host_load_gguf(const vvli_gpu_config* cfg, const void* bytes, size_t le
     BlobLayout L;
     int rc = check_target(cfg, blob, blob_elems, L);
     if (rc) return rc;
-    if (!bytes) return set_error(VVLI_NULL_ARG, "bytes is NULL");
     clear_error();
-    // loadGgufIntoOwnedModel (src/llm.zig:1008-1011): GGUF files carry no
-    // q/k/v bias tensors.
-    if (cfg->qkv_bias) return set_error(VVLI_UNSUPPORTED_ARCH, "GGUF loading does not support q/k/v bias");
-    GFile f;
-    const uint8_t* b = static_cast<const uint8_t*>(bytes);
-    if ((rc = gguf_parse(b, len, f))) return rc;
-    std::vector<Slot> list = slots(*cfg, L);
     memset(blob, 0, L.total * elem_bytes(*cfg));
-    report(progress, user, 0, list.size(), "start");
-    for (size_t k = 0; k < list.size(); ++k) {
-        rc = copy_gguf_tensor(f, b, len, list[k], blob, cfg->weight_kind);
-        if (rc) return rc;
-        report(progress, user, k + 1, list.size(), list[k].gguf.c_str());
-    }
-    return VVLI_OK;
+    HostSink sink{blob, cfg->weight_kind};
+    return load_gguf_into(*cfg, bytes, len, host_put, &sink, progress, user);
 }
 
 int vvli_host_map_file(const char* path, const void** data, size_t* len) {

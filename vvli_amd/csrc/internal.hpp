@@ -3,6 +3,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -43,6 +44,16 @@ struct MoeLayout {
     size_t embed = 0, final_norm = 0, lm_head = kNone, total = 0;
     std::vector<MoeLayerSlices> layers;
 };
+
+// Checkpoint loading (host_load.cpp): the parsers hand every tensor's raw
+// bytes to a `put` callback that places them in the blob (host or device).
+enum TensorSrc { kSrcF32 = 0, kSrcF16 = 1, kSrcBF16 = 2 };
+using TensorPut = int (*)(void* ctx, size_t dst_elem, const uint8_t* raw, TensorSrc src, size_t n);
+int load_safetensors_into(const vvli_gpu_config& cfg, const void* bytes, size_t len, TensorPut put, void* ctx,
+                          void (*progress)(void*, size_t, size_t, const char*), void* user);
+int load_gguf_into(const vvli_gpu_config& cfg, const void* bytes, size_t len, TensorPut put, void* ctx,
+                   void (*progress)(void*, size_t, size_t, const char*), void* user);
+int gguf_config(const void* bytes, size_t len, uint32_t weight_kind, vvli_gpu_config& out);
 
 int validate_config(const vvli_gpu_config& c, bool require_dense);
 uint64_t parameter_count(const vvli_gpu_config& c);

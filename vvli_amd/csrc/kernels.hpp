@@ -301,4 +301,8 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
 hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
                                 uint32_t last_n, hipStream_t s);
 
+// Dtype conversion for device-side loading (convert.hip): n elements of type
+// src_type (0 f32, 1 f16, 2 bf16) into dst elements of type kind (0 f32, 1 bf16).
+hipError_t launch_convert(const void* src, uint32_t src_type, void* dst, uint32_t kind, size_t n, hipStream_t s);
+
 }  // namespace vvli

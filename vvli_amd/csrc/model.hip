@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "internal.hpp"
+#include "vvli_host.h"
 #include "kernels.hpp"
 
 using namespace vvli;
@@ -649,9 +650,11 @@ int dmalloc(T** p, size_t count) {
     return VVLI_OK;
 }
 
+// host_blob == nullptr: the device blob is zeroed and filled by the caller.
 int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob, size_t blob_elems,
-                vvli_gpu_model** out, bool moe) {
-    if (!cfg || !host_blob || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create");
+                vvli_gpu_model** out, bool moe, bool blob_from_device = false) {
+    if (!cfg || (!host_blob && !blob_from_device) || !out)
+        return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create");
     *out = nullptr;
     int rc = validate_config(*cfg, !moe);
     if (rc) return rc;
@@ -683,7 +686,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
         m->layout = compute_layout(*cfg);
     }
     m->ebytes = elem_bytes(*cfg);
-    if (blob_elems < m->layout.total) {
+    if (!blob_from_device && blob_elems < m->layout.total) {
         free_model(m);
         return set_error(VVLI_INVALID_WEIGHT, "blob has %zu elements, layout needs %zu", blob_elems, m->layout.total);
     }
@@ -759,8 +762,12 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     auto fail_hip = [&](hipError_t e, const char* what) {
         return e == hipSuccess ? 0 : set_error(VVLI_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
     };
-    TRY_ALLOC(fail_hip(hipMemcpy(m->blob, host_blob, m->layout.total * m->ebytes, hipMemcpyHostToDevice),
-                       "blob upload"));
+    if (host_blob) {
+        TRY_ALLOC(fail_hip(hipMemcpy(m->blob, host_blob, m->layout.total * m->ebytes, hipMemcpyHostToDevice),
+                           "blob upload"));
+    } else {
+        TRY_ALLOC(fail_hip(hipMemset(m->blob, 0, m->layout.total * m->ebytes), "blob clear"));
+    }
     TRY_ALLOC(fail_hip(hipMemset(m->kcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->vcache, 0, kvlen * sizeof(float)), "kv clear"));
     TRY_ALLOC(fail_hip(hipMemset(m->counters, 0, cfg->kv_heads * sizeof(uint32_t)), "counters"));
@@ -969,6 +976,100 @@ int vvli_gpu_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, cons
                           vvli_gpu_model** out) {
     clear_error();
     return create_impl(cfg, max_seq_len, host_blob, blob_elems, out, false);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Places one tensor of a mapped checkpoint into the device blob: same-dtype
+// tensors are copied straight from the file bytes, others go through a
+// staging buffer and the conversion kernel, in chunks.
+struct DeviceSink {
+    vvli_gpu_model* m;
+    void* staging = nullptr;
+    size_t staging_bytes = 0;
+};
+
+int device_put(void* ctx, size_t dst, const uint8_t* raw, TensorSrc src, size_t n) {
+    auto* d = static_cast<DeviceSink*>(ctx);
+    vvli_gpu_model* m = d->m;
+    const uint32_t kind = m->cfg.weight_kind;
+    char* out = m->blob + dst * m->ebytes;
+    const bool same = (kind == VVLI_WEIGHT_F32 && src == kSrcF32) || (kind == VVLI_WEIGHT_BF16 && src == kSrcBF16);
+    if (same) {
+        HIP_TRY(hipMemcpyAsync(out, raw, n * m->ebytes, hipMemcpyHostToDevice, m->stream));
+        return VVLI_OK;
+    }
+    const size_t sb = src == kSrcF32 ? 4 : 2;
+    if (!d->staging) {
+        d->staging_bytes = 64ull << 20;
+        HIP_TRY(hipMalloc(&d->staging, d->staging_bytes));
+    }
+    const size_t per = d->staging_bytes / sb;
+    for (size_t off = 0; off < n; off += per) {
+        const size_t cnt = std::min(per, n - off);
+        // Stream order keeps the next chunk's copy behind this chunk's kernel.
+        HIP_TRY(hipMemcpyAsync(d->staging, raw + off * sb, cnt * sb, hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(launch_convert(d->staging, static_cast<uint32_t>(src), out + off * m->ebytes, kind, cnt, m->stream));
+    }
+    return VVLI_OK;
+}
+
+int finish_device_load(vvli_gpu_model* m, DeviceSink& sink, int rc, vvli_gpu_model** out) {
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (sink.staging) (void)hipFree(sink.staging);
+    if (rc == VVLI_OK && e != hipSuccess) rc = set_error(VVLI_HIP_ERROR, "device load: %s", hipGetErrorString(e));
+    if (rc != VVLI_OK) {
+        free_model(m);
+        return rc;
+    }
+    *out = m;
+    return VVLI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vvli_gpu_model_create_from_safetensors(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* bytes,
+                                           size_t len, vvli_host_progress_fn progress, void* user,
+                                           vvli_gpu_model** out) {
+    clear_error();
+    if (!cfg || !bytes || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create_from_safetensors");
+    vvli_gpu_model* m = nullptr;
+    int rc = create_impl(cfg, max_seq_len, nullptr, 0, &m, false, true);
+    if (rc) return rc;
+    DeviceSink sink{m};
+    rc = load_safetensors_into(*cfg, bytes, len, device_put, &sink, progress, user);
+    return finish_device_load(m, sink, rc, out);
+}
+
+int vvli_gpu_model_create_from_gguf(const void* bytes, size_t len, uint32_t weight_kind, uint32_t max_seq_len,
+                                    vvli_host_progress_fn progress, void* user, vvli_gpu_config* cfg_out,
+                                    vvli_gpu_model** out) {
+    clear_error();
+    if (!bytes || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_model_create_from_gguf");
+    vvli_gpu_config cfg;
+    int rc = gguf_config(bytes, len, weight_kind, cfg);
+    if (rc) return rc;
+    vvli_gpu_model* m = nullptr;
+    if ((rc = create_impl(&cfg, max_seq_len, nullptr, 0, &m, false, true))) return rc;
+    DeviceSink sink{m};
+    rc = load_gguf_into(cfg, bytes, len, device_put, &sink, progress, user);
+    if (rc == VVLI_OK && cfg_out) *cfg_out = cfg;
+    return finish_device_load(m, sink, rc, out);
+}
+
+int vvli_gpu_read_weights(vvli_gpu_model* m, uint64_t elem_offset, uint64_t n, void* out) {
+    if (!m || !out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_read_weights");
+    if (elem_offset > m->layout.total || n > m->layout.total - elem_offset)
+        return set_error(VVLI_INVALID_CONFIG, "weights [%llu, +%llu) outside the blob of %zu elements",
+                         static_cast<unsigned long long>(elem_offset), static_cast<unsigned long long>(n),
+                         m->layout.total);
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipMemcpy(out, m->blob + elem_offset * m->ebytes, n * m->ebytes, hipMemcpyDeviceToHost));
+    return VVLI_OK;
 }
 
 int vvli_gpu_moe_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,

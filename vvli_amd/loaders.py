@@ -88,6 +88,43 @@ def load_gguf(path: str | os.PathLike, weight_kind: int = WEIGHT_BF16,
         return _load_gguf(f.ptr, f.size.value, weight_kind, progress)
 
 
+def device_load_safetensors(cfg: Config, path: str | os.PathLike, max_seq_len: int, weight_kind: int = WEIGHT_BF16,
+                            progress: Progress = None):
+    """A Runner whose weights went from the mapped file straight to HBM
+    (vvli_gpu_model_create_from_safetensors): no host blob."""
+    from .runtime import Runner
+
+    with MappedFile(path) as f:
+        c = cfg.to_c(weight_kind)
+        h = c_void_p()
+        _lib.check(_lib.lib().vvli_gpu_model_create_from_safetensors(byref(c), max_seq_len, f.ptr, f.size.value,
+                                                                     _callback(progress), None, byref(h)))
+    return Runner.from_handle(cfg, h, max_seq_len, weight_kind)
+
+
+def device_load_directory(model_dir: str | os.PathLike, max_seq_len: int, weight_kind: int = WEIGHT_BF16,
+                          progress: Progress = None):
+    """config.json + model.safetensors straight to HBM; returns (Config, Runner)."""
+    with open(os.path.join(model_dir, "config.json"), "rb") as fh:
+        cfg = Config.from_json(fh.read())
+    return cfg, device_load_safetensors(cfg, os.path.join(model_dir, "model.safetensors"), max_seq_len, weight_kind,
+                                        progress)
+
+
+def device_load_gguf(path: str | os.PathLike, max_seq_len: int, weight_kind: int = WEIGHT_BF16,
+                     progress: Progress = None):
+    """A GGUF file straight to HBM (vvli_gpu_model_create_from_gguf); returns (Config, Runner)."""
+    from .runtime import Runner
+
+    with MappedFile(path) as f:
+        c = _lib.CConfig()
+        h = c_void_p()
+        _lib.check(_lib.lib().vvli_gpu_model_create_from_gguf(f.ptr, f.size.value, weight_kind, max_seq_len,
+                                                              _callback(progress), None, byref(c), byref(h)))
+    cfg = Config.from_c(c)
+    return cfg, Runner.from_handle(cfg, h, max_seq_len, weight_kind)
+
+
 def _load_safetensors(cfg, ptr, n, weight_kind, progress):
     blob = empty_blob(cfg, weight_kind)
     c = cfg.to_c(weight_kind)

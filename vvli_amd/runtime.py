@@ -147,6 +147,23 @@ class Runner:
         # llm.Runner: dense decoders only; MoE configs are rejected like OwnedModel.init.
         return _lib.lib().vvli_gpu_model_create(*args)
 
+    @classmethod
+    def from_handle(cls, cfg: Config, handle: c_void_p, max_seq_len: int, weight_kind: int) -> "Runner":
+        """Wraps a model handle created by another entry point (the device loaders)."""
+        r = cls.__new__(cls)
+        r.cfg, r.weight_kind, r.max_seq_len = cfg, weight_kind, max_seq_len
+        r._c = cfg.to_c(weight_kind)
+        r._h = handle
+        r._path = "auto"
+        r.logits = np.zeros(cfg.vocab_size, dtype=np.float32)
+        return r
+
+    def read_weights(self, offset: int, n: int) -> np.ndarray:
+        """vvli_gpu_read_weights: n blob elements from offset (blob dtype)."""
+        out = np.empty(n, dtype=_DTYPE[self.weight_kind])
+        _lib.check(_lib.lib().vvli_gpu_read_weights(self._h, offset, n, _ptr(out)))
+        return out
+
     def close(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:
             _lib.check(_lib.lib().vvli_gpu_model_destroy(self._h))
