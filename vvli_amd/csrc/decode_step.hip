@@ -33,6 +33,7 @@
 // Deadlock safety: the launch is cooperative (all blocks co-resident or the
 // launch fails), every poll is bounded, and a timeout raises a device error
 // flag that makes every block leave at its next poll; the host reports it.
+#include <algorithm>
 #include <cstdlib>
 
 #include "device_common.hpp"
@@ -196,6 +197,7 @@ struct MkWave {
     uint32_t wid;    // wave (t mod blocks) ... : spreads a short phase over every CU
     uint32_t wid_c;  // block-contiguous wave index: long phases sweep memory together
     uint32_t nw;
+    uint32_t wave;   // wave of the block
     int lane;
 };
 
@@ -209,10 +211,10 @@ __device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
 // before the phase input exists). Defines buf and t on every path, so they are
 // dead between a phase's last item and the next prefetch.
 __device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkWave& w, uint4 (&buf)[2][kNJC],
-                                            MkTile& t) {
-    const uint32_t ntiles = mk_tiles(g, mode);
+                                            MkTile& t, uint32_t t0 = 0) {
+    const uint32_t ntiles = mk_tiles(g, mode) - t0;
     const uint32_t me = mk_owner(w, ntiles);
-    mk_make_tile(g, mode, me < ntiles ? me : 0, t);
+    mk_make_tile(g, mode, t0 + (me < ntiles ? me : 0), t);
     if (me >= ntiles) {
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -259,8 +261,113 @@ __device__ __forceinline__ void consume_rows(const uint4 (&buf)[2][kNJC], const 
     }
 }
 
-// Run this wave's tiles of a GEMV phase (`mode` is uniform over the grid);
-// bufA/tA hold the prefetched first item when `have` is set. Outputs are
+// ---------------------------------------------------------------------------
+// Gate/up tiles in LDS. The attention phase leaves most blocks idle (only
+// kv_heads * splits units run) and HBM nearly so; those blocks copy the first
+// gate/up tiles of the layer into LDS (global_load_lds, 1 KiB per wave load)
+// and the gate/up phase takes them from there, so it streams fewer bytes
+// after its input arrives. Tiles [0, n) of the phase are LDS tiles: block
+// first_block + i holds tiles i*per_block .. +per_block-1, tile i*per_block+j
+// belongs to wave j mod 8 of the block (it loads and consumes it, so only its
+// own completion counter orders the copy and the reads). The remaining tiles
+// are streamed by every wave as usual.
+// LDS tile layout: [row (gate, up)][chunk][j < kNJC][lane] 16-byte units,
+// i.e. exactly the registers an item would hold.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+struct GLds {
+    uint32_t first_block;  // blocks >= first_block hold LDS tiles
+    uint32_t per_block;
+    uint32_t n;            // LDS tiles of the phase
+    uint32_t nchunk;       // items per row
+    uint32_t tile_bytes;
+    uint32_t per1;         // tiles of the first LDS range
+    uint32_t off1, off2;   // byte offsets of the two ranges in the dynamic LDS
+};
+
+// Byte offset (dynamic LDS) of the block's j-th tile.
+__device__ __forceinline__ uint32_t mk_glds_tile(const GLds& q, uint32_t j) {
+    return j < q.per1 ? q.off1 + j * q.tile_bytes : q.off2 + (j - q.per1) * q.tile_bytes;
+}
+
+__device__ __forceinline__ GLds mk_glds(const DecodeStepParams& p, uint32_t units, const MkGemv& g, bool on = true) {
+    GLds q;
+    q.first_block = units < gridDim.x ? units : gridDim.x;
+    q.per_block = on ? p.g_lds_tiles : 0;
+    const uint32_t cap = (gridDim.x - q.first_block) * q.per_block;
+    q.n = cap < g.r0 ? cap : g.r0;
+    q.nchunk = (g.K / 8 + kNJC * kWave - 1) / (kNJC * kWave);
+    q.tile_bytes = 2 * q.nchunk * kNJC * kWave * 16;
+    q.per1 = p.g_lds_tiles1;
+    q.off1 = p.g_lds_offset1;
+    q.off2 = p.g_lds_offset2;
+    return q;
+}
+
+// LDS tiles of this wave: j = wave, wave + 8, ... while j < per_block and the
+// tile index is < n.
+__device__ __forceinline__ uint32_t mk_glds_count(const GLds& q, uint32_t wave) {
+    if (q.n == 0 || blockIdx.x < q.first_block) return 0;
+    const uint32_t t0 = (blockIdx.x - q.first_block) * q.per_block;
+    if (t0 >= q.n) return 0;
+    const uint32_t lim = q.n - t0 < q.per_block ? q.n - t0 : q.per_block;
+    if (wave >= lim) return 0;
+    return (lim - 1 - wave) / kMkWaves + 1;
+}
+
+__device__ __forceinline__ void mk_glds_issue(const GLds& q, const MkGemv& g, char* lds, uint32_t wave, int lane) {
+    const uint32_t cnt = mk_glds_count(q, wave);
+    const uint32_t U = g.K / 8;
+    for (uint32_t k = 0; k < cnt; ++k) {
+        const uint32_t j = wave + k * kMkWaves;
+        const uint32_t t = (blockIdx.x - q.first_block) * q.per_block + j;
+        char* dst = lds + mk_glds_tile(q, j);
+        const uint16_t* gate = g.w0 + (size_t)t * g.K;
+        const uint16_t* up = g.w_up + (size_t)t * g.K;
+        for (uint32_t rc = 0; rc < 2 * q.nchunk; ++rc) {
+            const uint16_t* row = rc < q.nchunk ? gate : up;
+            const uint32_t c = rc < q.nchunk ? rc : rc - q.nchunk;
+#pragma unroll
+            for (int jj = 0; jj < kNJC; ++jj) {
+                const uint32_t u = c * (kNJC * kWave) + jj * kWave + lane;
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(row + (size_t)(u < U ? u : 0) * 8),
+                                                 (lds_void_t*)(dst + (rc * kNJC + jj) * kWave * 16), 16, 0, 0);
+            }
+        }
+    }
+}
+
+// The wave's LDS gate/up tiles: silu(gate . x) * (up . x) of its k-th tile
+// parked at park[k] in LDS (written out by mk_gemv once the streamed tiles
+// are done, so no store sits in front of the streamed loads).
+__device__ __forceinline__ void mk_glds_compute(const GLds& gl, const MkGemv& g, const float* xs, char* lds,
+                                                uint32_t park_off, const MkWave& w) {
+    const uint32_t n = mk_glds_count(gl, w.wave);
+    const uint32_t U = g.K / 8;
+    for (uint32_t k = 0; k < n; ++k) {
+        const char* src = lds + mk_glds_tile(gl, w.wave + k * kMkWaves) + w.lane * 16;
+        float acc[2] = {0.f, 0.f};
+        for (uint32_t c = 0; c < gl.nchunk; ++c) {
+            uint4 lb[2][kNJC];
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int jj = 0; jj < kNJC; ++jj)
+                    lb[r][jj] = *reinterpret_cast<const uint4*>(src + (((size_t)r * gl.nchunk + c) * kNJC + jj) *
+                                                                          kWave * 16);
+            consume<uint16_t, 2>(lb, xs, c * kNJC * kWave, U, w.lane, acc);
+        }
+        const float v0 = wave_sum(acc[0]), v1 = wave_sum(acc[1]);
+        if (w.lane == 0)  // siluMulInto, src/llm.zig:1382-1387
+            reinterpret_cast<float*>(lds + park_off)[w.wave * kWave + k] = (v0 / (1.0f + expf(-v0))) * v1;
+    }
+}
+
+
+// Run this wave's tiles of a GEMV phase (`mode` is uniform over the grid),
+// among the phase's tiles t0 .. end (t0 > 0: the first ones were taken from
+// LDS); bufA/tA hold the prefetched first item when `have` is set. Outputs are
 // tagged with `tag` (logits: plain floats plus the argmax key in `best`).
 //
 // Tile results are parked in lanes -- lane k holds the k-th tile of the
@@ -271,128 +378,134 @@ __device__ __forceinline__ void consume_rows(const uint4 (&buf)[2][kNJC], const 
 // checks the residual's tag only when it writes.
 __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
                                         uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
-                                        uint32_t tag, const MkResid& rs, uint32_t* err) {
+                                        uint32_t tag, const MkResid& rs, uint32_t t0, const float* park,
+                                        uint32_t lds_first, uint32_t n_lds, uint32_t* err) {
     const int lane = w.lane;
     const uint32_t U = mk_units(g);
     const uint32_t per_item = kNJC * kWave;
     const float* xs1 = g.split ? xs + g.K / 2 : xs;  // x of the second streamed row
     const uint32_t nchunk = (U + per_item - 1) / per_item;
-    const uint32_t ntiles = mk_tiles(g, mode);
+    const uint32_t ntiles = mk_tiles(g, mode) - t0;
     const uint32_t me = mk_owner(w, ntiles);
     const uint32_t my_tiles = me < ntiles ? (ntiles - 1 - me) / w.nw + 1 : 0;
     const uint32_t n_items = my_tiles * nchunk;
-    if (n_items == 0) return true;
-    if (!have) {
-        mk_make_tile(g, mode, me, tA);
-        issue<uint16_t, 2>(bufA, tA.p, 0, U, lane);
-    }
-    // Lane state of the open batch: rows, segment, addends, parked results.
-    uint32_t ra = 0, rb = 0;
-    int sa = 0;
-    bool va = false, vb = false;
-    tword wa = 0, wb = 0;  // residual words (tag checked at write time)
-    float ea = 0.f, eb = 0.f, oa = 0.f, ob = 0.f;
-    uint32_t base = 0, pending = 0;
     bool ok = true;
-    auto open_batch = [&]() {
-        const uint32_t k = base + (uint32_t)lane;
-        const bool mine = k < my_tiles;
-        MkTile t;
-        mk_make_tile(g, mode, mine ? me + k * w.nw : me, t);
-        ra = t.row[0];
-        rb = t.row[1];
-        sa = t.seg;
-        va = mine && t.valid[0];
-        vb = mine && t.valid[1];
-        ea = eb = 0.f;
-        if (mode == kGemvResid) {  // x = residual + proj (addInto, src/llm.zig:1389-1396)
-            if (rs.bf16) {
-                if (va) ea = __uint_as_float((uint32_t)*as_global(rs.bf16 + ra) << 16);
-                if (vb) eb = __uint_as_float((uint32_t)*as_global(rs.bf16 + rb) << 16);
-            } else {
-                wa = va ? ld_a(rs.src + ra) : tw_make_u(0, rs.tag);
-                wb = vb ? ld_a(rs.src + rb) : tw_make_u(0, rs.tag);
-            }
-        } else if (mode == kGemvPlain) {  // linearRange: dot + bias (src/llm.zig:1273)
-            const uint16_t* bias = seg_bias(g, sa);
-            if (bias && va) ea = __uint_as_float((uint32_t)*as_global(bias + ra) << 16);
-            if (bias && vb) eb = __uint_as_float((uint32_t)*as_global(bias + rb) << 16);
+    if (n_items) {
+        if (!have) {
+            mk_make_tile(g, mode, t0 + me, tA);
+            issue<uint16_t, 2>(bufA, tA.p, 0, U, lane);
         }
-    };
-    auto flush = [&]() {
-        if ((uint32_t)lane < pending) {
-            if (mode == kGemvLogits) {
-                if (va) *as_global(g.plain + ra) = oa;
-                if (vb) *as_global(g.plain + rb) = ob;
-            } else {
-                if (mode == kGemvResid && !rs.bf16) {
-                    ok = ok && poll_tw(rs.src + ra, rs.tag, wa, err) && poll_tw(rs.src + rb, rs.tag, wb, err);
-                    ea = tw_val(wa);
-                    eb = tw_val(wb);
+        // Lane state of the open batch: rows, segment, addends, parked results.
+        uint32_t ra = 0, rb = 0;
+        int sa = 0;
+        bool va = false, vb = false;
+        tword wa = 0, wb = 0;  // residual words (tag checked at write time)
+        float ea = 0.f, eb = 0.f, oa = 0.f, ob = 0.f;
+        uint32_t base = 0, pending = 0;
+        auto open_batch = [&]() {
+            const uint32_t k = base + (uint32_t)lane;
+            const bool mine = k < my_tiles;
+            MkTile t;
+            mk_make_tile(g, mode, t0 + (mine ? me + k * w.nw : me), t);
+            ra = t.row[0];
+            rb = t.row[1];
+            sa = t.seg;
+            va = mine && t.valid[0];
+            vb = mine && t.valid[1];
+            ea = eb = 0.f;
+            if (mode == kGemvResid) {  // x = residual + proj (addInto, src/llm.zig:1389-1396)
+                if (rs.bf16) {
+                    if (va) ea = __uint_as_float((uint32_t)*as_global(rs.bf16 + ra) << 16);
+                    if (vb) eb = __uint_as_float((uint32_t)*as_global(rs.bf16 + rb) << 16);
+                } else {
+                    wa = va ? ld_a(rs.src + ra) : tw_make_u(0, rs.tag);
+                    wb = vb ? ld_a(rs.src + rb) : tw_make_u(0, rs.tag);
                 }
-                tword* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
-                if (va) st_a(o + ra, tw_make(oa + ea, tag));
-                if (vb) st_a(o + rb, tw_make(ob + eb, tag));
+            } else if (mode == kGemvPlain) {  // linearRange: dot + bias (src/llm.zig:1273)
+                const uint16_t* bias = seg_bias(g, sa);
+                if (bias && va) ea = __uint_as_float((uint32_t)*as_global(bias + ra) << 16);
+                if (bias && vb) eb = __uint_as_float((uint32_t)*as_global(bias + rb) << 16);
             }
-        }
-        pending = 0;
-    };
-    open_batch();
-    uint4 bufB[2][kNJC];
-    MkTile tc = tA, tn = tA;  // tiles of the item being consumed / in flight
-    float acc0 = 0.f, acc1 = 0.f;
-    for (uint32_t it = 0; it < n_items; ++it) {
-        const uint32_t chunk = it % nchunk;
-        const bool more = it + 1 < n_items;
-        if (more && chunk == nchunk - 1) mk_make_tile(g, mode, me + ((it + 1) / nchunk) * w.nw, tn);
-        const uint32_t nbase = (chunk == nchunk - 1 ? 0 : chunk + 1) * per_item;
-        float acc[2] = {acc0, acc1};
-        if (it & 1) {
-            if (more) issue<uint16_t, 2>(bufA, tn.p, nbase, U, lane);
-            consume_rows(bufB, xs, xs1, chunk * per_item, U, lane, acc);
-        } else {
-            if (more) issue<uint16_t, 2>(bufB, tn.p, nbase, U, lane);
-            consume_rows(bufA, xs, xs1, chunk * per_item, U, lane, acc);
-        }
-        acc0 = acc[0];
-        acc1 = acc[1];
-        if (chunk == nchunk - 1) {
-            float v0, v1 = 0.f;
-            if (g.split) {
-                v0 = wave_sum(acc0 + acc1);  // the row's two halves
-            } else {
-                v0 = wave_sum(acc0);
-                v1 = wave_sum(acc1);
-            }
-            acc0 = acc1 = 0.f;
-            if (mode == kGemvGateUp) {
-                v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
-            } else if (mode == kGemvLogits && lane == 0) {
-                // llm.argmax (src/llm.zig:778-789): a NaN logit 0 makes the
-                // result 0 (every comparison with it fails): top key, index 0.
-                if (tc.valid[0]) {
-                    const unsigned long long k0 =
-                        (tc.row[0] == 0 && v0 != v0) ? ~0ull : argmax_key(v0, tc.row[0]);
-                    best = k0 > best ? k0 : best;
-                }
-                if (tc.valid[1]) {
-                    const unsigned long long k1 = argmax_key(v1, tc.row[1]);
-                    best = k1 > best ? k1 : best;
+        };
+        auto flush = [&]() {
+            if ((uint32_t)lane < pending) {
+                if (mode == kGemvLogits) {
+                    if (va) *as_global(g.plain + ra) = oa;
+                    if (vb) *as_global(g.plain + rb) = ob;
+                } else {
+                    if (mode == kGemvResid && !rs.bf16) {
+                        ok = ok && poll_tw(rs.src + ra, rs.tag, wa, err) && poll_tw(rs.src + rb, rs.tag, wb, err);
+                        ea = tw_val(wa);
+                        eb = tw_val(wb);
+                    }
+                    tword* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
+                    if (va) st_a(o + ra, tw_make(oa + ea, tag));
+                    if (vb) st_a(o + rb, tw_make(ob + eb, tag));
                 }
             }
-            if ((uint32_t)lane == pending) {
-                oa = v0;
-                ob = v1;
+            pending = 0;
+        };
+        open_batch();
+        uint4 bufB[2][kNJC];
+        MkTile tc = tA, tn = tA;  // tiles of the item being consumed / in flight
+        float acc0 = 0.f, acc1 = 0.f;
+        for (uint32_t it = 0; it < n_items; ++it) {
+            const uint32_t chunk = it % nchunk;
+            const bool more = it + 1 < n_items;
+            if (more && chunk == nchunk - 1) mk_make_tile(g, mode, t0 + me + ((it + 1) / nchunk) * w.nw, tn);
+            const uint32_t nbase = (chunk == nchunk - 1 ? 0 : chunk + 1) * per_item;
+            float acc[2] = {acc0, acc1};
+            if (it & 1) {
+                if (more) issue<uint16_t, 2>(bufA, tn.p, nbase, U, lane);
+                consume_rows(bufB, xs, xs1, chunk * per_item, U, lane, acc);
+            } else {
+                if (more) issue<uint16_t, 2>(bufB, tn.p, nbase, U, lane);
+                consume_rows(bufA, xs, xs1, chunk * per_item, U, lane, acc);
             }
-            if (++pending == kWave) {
-                flush();
-                base += kWave;
-                open_batch();
+            acc0 = acc[0];
+            acc1 = acc[1];
+            if (chunk == nchunk - 1) {
+                float v0, v1 = 0.f;
+                if (g.split) {
+                    v0 = wave_sum(acc0 + acc1);  // the row's two halves
+                } else {
+                    v0 = wave_sum(acc0);
+                    v1 = wave_sum(acc1);
+                }
+                acc0 = acc1 = 0.f;
+                if (mode == kGemvGateUp) {
+                    v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
+                } else if (mode == kGemvLogits && lane == 0) {
+                    // llm.argmax (src/llm.zig:778-789): a NaN logit 0 makes the
+                    // result 0 (every comparison with it fails): top key, index 0.
+                    if (tc.valid[0]) {
+                        const unsigned long long k0 =
+                            (tc.row[0] == 0 && v0 != v0) ? ~0ull : argmax_key(v0, tc.row[0]);
+                        best = k0 > best ? k0 : best;
+                    }
+                    if (tc.valid[1]) {
+                        const unsigned long long k1 = argmax_key(v1, tc.row[1]);
+                        best = k1 > best ? k1 : best;
+                    }
+                }
+                if ((uint32_t)lane == pending) {
+                    oa = v0;
+                    ob = v1;
+                }
+                if (++pending == kWave) {
+                    flush();
+                    base += kWave;
+                    open_batch();
+                }
+                tc = tn;
             }
-            tc = tn;
         }
+        flush();
     }
-    flush();
+    // Results of the wave's LDS tiles (gate/up phase), parked in LDS: written
+    // after the streamed tiles, so no store sits in front of their loads.
+    if ((uint32_t)lane < n_lds)
+        st_a(g.o0 + lds_first + (uint32_t)lane * kMkWaves, tw_make(park[w.wave * kWave + lane], tag));
     return ok;
 }
 
@@ -777,7 +890,11 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2)
                     if (s2 < (int)ns - 1) o = fmaf(tw_val(wv[s2]), wsp[s2 * G + g], o);
                 o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
-                st_a(p.tattn + (size_t)h * G * hd + idx, tw_make(o, tag_out));
+                // (An opaque copy of idx: hoisted out of every loop, the
+                // 64-bit store addresses would hold registers all kernel long.)
+                int idx_o = idx;
+                asm volatile("" : "+v"(idx_o));
+                st_a(p.tattn + (size_t)h * G * hd + idx_o, tw_make(o, tag_out));
             }
         }
 #undef VVLI_POLL_PARTIALS
@@ -861,6 +978,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     w.wid = wave * gridDim.x + blockIdx.x;
     w.wid_c = blockIdx.x * kMkWaves + wave;
     w.nw = gridDim.x * kMkWaves;
+    w.wave = wave;
     uint4 buf[2][kNJC];
     MkTile tile;
     unsigned long long best = 0ull;
@@ -901,6 +1019,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
         if (chunk < p.min_chunk) chunk = p.min_chunk;
         const uint32_t ns = (T + chunk - 1) / chunk;
         const uint16_t* emb = p.embed + (size_t)token * H;
+        const uint32_t units = p.kv_heads * ns;  // attention units run by blocks [0, units)
 
         for (uint32_t ph = 0; ph <= logits_ph; ++ph) {
             const MkPhase f = mk_phase(ph, p.layers);
@@ -908,11 +1027,30 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             bool ok = true;
             if (f.kind == kPhA && !f.logits) {
                 ok = mk_attention<HDMAX, EXACT>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag);
+                if (p.g_lds_tiles) {  // blocks without a unit: this layer's first gate/up tiles into LDS
+                    const MkGemv& gg = tb.gemv[f.layer * 4 + 2];
+                    const GLds q = mk_glds(p, units, gg);
+                    if (mk_glds_count(q, w.wave)) {
+                        // Start the copy once the q/k/v words show up, so it
+                        // does not queue in front of them and of the units'
+                        // K/V loads.
+                        tword qw = ld_a(p.tqkv);
+                        ok = ok && poll_tw(p.tqkv, tag - 1, qw, p.error);
+                        if (ok) mk_glds_issue(q, gg, reinterpret_cast<char*>(smem), w.wave, w.lane);
+                    }
+                }
             } else {
                 const MkGemv& g = mk_gemv_of(p, tb, f);
                 const int mode = mk_mode(f);
                 if (f.logits) best = 0ull;
-                if (blockIdx.x < mk_tiles(g, mode)) {  // the block has tiles: stage the input
+                // LDS tiles: gate/up phases only (gl.n = 0 otherwise).
+                const GLds gl = mk_glds(p, units, g, f.kind == kPhG && !f.logits && p.g_lds_tiles);
+                // The block has tiles (streamed: block < their count; or LDS
+                // tiles): stage the input.
+                const uint32_t n_streamed = mk_tiles(g, mode) - gl.n;
+                const bool has_lds =
+                    gl.n && blockIdx.x >= gl.first_block && (blockIdx.x - gl.first_block) * gl.per_block < gl.n;
+                if (blockIdx.x < n_streamed || has_lds) {
                     const tword* src = f.kind == kPhO ? p.tattn
                                                       : (f.kind == kPhD ? p.tff : (f.kind == kPhG ? p.tx + H : p.tx));
                     ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
@@ -924,7 +1062,15 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     rs.src = f.kind == kPhO ? p.tx : p.tx + H;
                     rs.tag = f.kind == kPhO ? tag - 3 : tag - 2;
                     rs.bf16 = (f.kind == kPhO && f.layer == 0) ? emb : nullptr;
-                    ok = ok && mk_gemv(g, mode, smem, w, buf, tile, have, best, tag, rs, p.error);
+                    const uint32_t n_lds = mk_glds_count(gl, w.wave);
+                    if (gl.n) {  // grid-uniform: LDS tiles while the first streamed item loads
+                        have = mk_prefetch(g, mode, w, buf, tile, gl.n);
+                        mk_glds_compute(gl, g, smem, reinterpret_cast<char*>(smem), p.g_lds_park, w);
+                    }
+                    ok = ok && mk_gemv(g, mode, smem, w, buf, tile, have, best, tag, rs, gl.n,
+                                       reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) + p.g_lds_park),
+                                       n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0, n_lds,
+                                       p.error);
                 }
                 if (f.logits && w.lane == 0) {
                     st_a(p.tkeys + 2 * w.wid, tw_make_u((uint32_t)(best >> 32), tag));
@@ -935,9 +1081,17 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             if (__syncthreads_or(!ok)) return;
             // Issue the first weights of the next GEMV phase (the next step's
             // first phase after the logits) before waiting for its input.
+            // (Not when the next phase starts with LDS tiles: those cover the
+            // first streamed item's latency, and the input poll is not queued
+            // behind it.)
             if (ph < logits_ph) {
                 const MkPhase nf = mk_phase(ph + 1, p.layers);
-                if (nf.kind != kPhA || nf.logits) have = mk_prefetch(mk_gemv_of(p, tb, nf), mk_mode(nf), w, buf, tile);
+                const MkGemv& ng = mk_gemv_of(p, tb, nf);
+                if (nf.kind == kPhG && !nf.logits && p.g_lds_tiles &&
+                    mk_glds(p, units, ng).n > 0)
+                    have = false;
+                else if (nf.kind != kPhA || nf.logits)
+                    have = mk_prefetch(ng, mk_mode(nf), w, buf, tile);
             } else if (step + 1 < p.n_steps) {
                 have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
@@ -999,6 +1153,33 @@ size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, u
 }
 
 uint32_t decode_step_phases_per_step(uint32_t layers) { return kPhPerLayer * layers + 2; }
+
+uint32_t decode_step_glds_tile_bytes(uint32_t K) {
+    const uint32_t nchunk = (K / 8 + kNJC * kWave - 1) / (kNJC * kWave);
+    return 2 * nchunk * kNJC * kWave * 16;
+}
+
+// Range 1: from the end of the hidden-sized staging (x and norm weights of the
+// q/k/v, o and gate/up phases, live while tiles are held) to the tables.
+// Range 2: after the tables and the result parking area, up to the LDS of a
+// CU (160 KiB) minus the kernel's static LDS and a margin.
+uint32_t decode_step_glds_plan(uint32_t hidden, uint32_t inter, uint32_t hd, size_t* lds, uint32_t* off1,
+                               uint32_t* tiles1, uint32_t* off2, uint32_t* park) {
+    constexpr size_t kLdsPerCu = 160 * 1024, kReserve = 1024, kMaxTiles = 64;
+    const size_t tb = decode_step_glds_tile_bytes(hidden);
+    const size_t a1 = ((size_t)2 * hidden * sizeof(float) + 1023) / 1024 * 1024;
+    const size_t e1 = decode_step_table_offset(hidden, inter, hd);
+    const size_t n1 = e1 > a1 ? std::min((e1 - a1) / tb, kMaxTiles) : 0;
+    const size_t ap = (*lds + 1023) / 1024 * 1024;  // result parking, then range 2
+    const size_t a2 = ap + kMkWaves * kWave * sizeof(float);
+    const size_t n2 = a2 + kReserve < kLdsPerCu ? std::min((kLdsPerCu - kReserve - a2) / tb, kMaxTiles - n1) : 0;
+    *off1 = static_cast<uint32_t>(a1);
+    *tiles1 = static_cast<uint32_t>(n1);
+    *off2 = static_cast<uint32_t>(a2);
+    *park = static_cast<uint32_t>(ap);
+    if (n2 > 0) *lds = a2 + n2 * tb;
+    return static_cast<uint32_t>(n1 + n2);
+}
 
 static const void* decode_step_fn(uint32_t hd) {
     if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true>);

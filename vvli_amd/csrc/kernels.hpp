@@ -183,7 +183,24 @@ struct DecodeStepParams {
     uint32_t timing_stride;
     uint32_t timing_slots;
     uint32_t table_lds_offset;  // bytes: where the kernel copies gemv[] / norms into LDS
+    // Gate/up tiles prefetched into LDS during the attention phase by the
+    // blocks that run no attention unit: g_lds_tiles tiles per block (0: off),
+    // tiles [0, g_lds_tiles1) from byte g_lds_offset1 of the dynamic LDS (the
+    // attention / down-projection staging space, which those blocks do not use
+    // while the tiles are held), the rest from byte g_lds_offset2.
+    uint32_t g_lds_offset1, g_lds_tiles1;
+    uint32_t g_lds_offset2;
+    uint32_t g_lds_tiles;
+    uint32_t g_lds_park;  // byte offset of [8 waves][64] f32: LDS tile results until they are written
 };
+
+// LDS bytes of one gate/up tile (gate row + up row of K bf16 weights, in
+// 1 KiB wave loads).
+uint32_t decode_step_glds_tile_bytes(uint32_t K);
+// Where the gate/up tiles fit (fills the offsets and first-range count) and
+// the new dynamic LDS size in *lds; returns the tile count per block.
+uint32_t decode_step_glds_plan(uint32_t hidden, uint32_t inter, uint32_t hd, size_t* lds, uint32_t* off1,
+                               uint32_t* tiles1, uint32_t* off2, uint32_t* park);
 
 size_t decode_step_table_offset(uint32_t hidden, uint32_t inter, uint32_t hd);
 size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, uint32_t hd);

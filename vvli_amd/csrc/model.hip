@@ -59,6 +59,7 @@ struct vvli_gpu_model {
     uint32_t path = 0;  // 0 auto, 1 per-kernel graph, 2 persistent
     uint32_t mk_blocks = 0;
     size_t mk_lds = 0;
+    uint32_t mk_glds_off1 = 0, mk_glds_tiles1 = 0, mk_glds_off2 = 0, mk_glds_tiles = 0, mk_glds_park = 0;
     uint32_t mk_nsplit = 1;
     DecodeLayer* mk_layers = nullptr;
     DecodeGemv* mk_gemv = nullptr;  // [layers * 4 + 1] phase descriptors
@@ -486,6 +487,11 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.timing_stride = timing_stride;
     p.timing_slots = timing_stride >= 16u * decode_step_phases_per_step(c.layers) ? 16u : 1u;
     p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, c.inter, p.hd));
+    p.g_lds_offset1 = m->mk_glds_off1;
+    p.g_lds_tiles1 = m->mk_glds_tiles1;
+    p.g_lds_offset2 = m->mk_glds_off2;
+    p.g_lds_tiles = m->mk_glds_tiles;
+    p.g_lds_park = m->mk_glds_park;
     m->mk_epoch += static_cast<uint32_t>(need);
     HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
     HIP_TRY(hipEventRecord(m->mk_ev0, m->stream));
@@ -705,6 +711,22 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
             m->mk_ok = true;
             m->mk_blocks = static_cast<uint32_t>(cus);
             m->mk_nsplit = std::max<uint32_t>(1, std::min<uint32_t>(16, (max_seq_len + 63) / 64));  // <= kMaxSplitMk
+            // The rest of the CU's LDS holds gate/up tiles (VVLI_DECODE_GLDS=0: off).
+            const char* env = getenv("VVLI_DECODE_GLDS");
+            uint32_t off1 = 0, n1 = 0, off2 = 0, park = 0;
+            size_t lds2 = m->mk_lds;
+            const uint32_t tiles =
+                (env && env[0] == '0') ? 0 : decode_step_glds_plan(H, cfg->inter, hd, &lds2, &off1, &n1, &off2, &park);
+            if (tiles > 0 && decode_step_max_blocks(hd, lds2, &bpc) == hipSuccess && bpc >= 1) {
+                m->mk_glds_off1 = off1;
+                m->mk_glds_tiles1 = n1;
+                m->mk_glds_off2 = off2;
+                m->mk_glds_tiles = tiles;
+                m->mk_glds_park = park;
+                m->mk_lds = lds2;
+            } else {
+                (void)decode_step_max_blocks(hd, m->mk_lds, &bpc);  // restore the attribute for the smaller size
+            }
         }
         (void)hipGetLastError();
     }
