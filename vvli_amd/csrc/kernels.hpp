@@ -230,7 +230,12 @@ struct GemmArgs {
     float* out = nullptr;
     uint32_t ldo = 0;
     uint32_t M = 0, N = 0, K = 0;      // K % 8 == 0
+    // Device scratch of gemm_split_elems(M, K) bf16: the launcher splits A
+    // (normalised when norm_w is set) into hi | lo planes there before the
+    // GEMM reads it.
+    uint16_t* a_hl = nullptr;
 };
+size_t gemm_split_elems(uint32_t M, uint32_t K);
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s);
 
 hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s);

@@ -91,6 +91,7 @@ struct vvli_gpu_model {
     float* pf_attn = nullptr;   // [rows][H]
     float* pf_ff = nullptr;     // [rows][I]
     float* pf_scale = nullptr;  // [rows] RMS scales
+    float* pf_ahl = nullptr;    // GEMM activations split hi | lo (gemm_split_elems bf16)
 };
 
 namespace {
@@ -547,9 +548,10 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
     const vvli_gpu_config& c = m->cfg;
     const size_t rows = std::min(m->max_seq, kPrefillChunk);
     const size_t H = c.hidden, kv = kv_dim(c), I = c.inter;
-    float** bufs[] = {&m->pf_x, &m->pf_qkv, &m->pf_attn, &m->pf_ff, &m->pf_scale};
-    const size_t sizes[] = {rows * H, rows * (H + 2 * kv), rows * H, rows * I, rows};
-    for (int i = 0; i < 5; ++i) {
+    float** bufs[] = {&m->pf_x, &m->pf_qkv, &m->pf_attn, &m->pf_ff, &m->pf_scale, &m->pf_ahl};
+    const size_t sizes[] = {rows * H, rows * (H + 2 * kv), rows * H, rows * I, rows,
+                            (gemm_split_elems(static_cast<uint32_t>(rows), static_cast<uint32_t>(std::max(H, I))) + 1) / 2};
+    for (int i = 0; i < 6; ++i) {
         hipError_t e = hipMalloc(reinterpret_cast<void**>(bufs[i]), sizes[i] * sizeof(float));
         if (e != hipSuccess) {
             for (float** b : bufs) {
@@ -592,6 +594,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gq.bias[0] = w16(L.q_bias), gq.bias[1] = w16(L.k_bias), gq.bias[2] = w16(L.v_bias);
             gq.seg_end[0] = H, gq.seg_end[1] = H + kv, gq.seg_end[2] = H + 2 * kv;
             gq.out = m->pf_qkv, gq.ldo = ldqkv, gq.M = P, gq.N = ldqkv, gq.K = H;
+            gq.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
             LAUNCH(launch_gemm_bf16(kGemmPlain, gq, s));
             // RoPE on q and k, k/v appended at positions pos0 ..
             PrefillRopeArgs ra{m->pf_qkv, ldqkv, P, pos0, c.heads, c.kv_heads, hd, kv, c.rope_layout,
@@ -605,6 +608,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             go.a = m->pf_attn, go.lda = H, go.w[0] = w16(L.o);
             go.seg_end[0] = go.seg_end[1] = go.seg_end[2] = H;
             go.out = m->pf_x, go.ldo = H, go.M = P, go.N = H, go.K = H;
+            go.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
             LAUNCH(launch_gemm_bf16(kGemmResid, go, s));
             // post-attention RMSNorm fused into gate/up + SwiGLU
             LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
@@ -613,12 +617,14 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gu.w[0] = w16(L.gate), gu.w_up = w16(L.up);
             gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
             gu.out = m->pf_ff, gu.ldo = I, gu.M = P, gu.N = I, gu.K = H;
+            gu.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
             LAUNCH(launch_gemm_bf16(kGemmGateUp, gu, s));
             // x += ff . Wd^T
             GemmArgs gd;
             gd.a = m->pf_ff, gd.lda = I, gd.w[0] = w16(L.down);
             gd.seg_end[0] = gd.seg_end[1] = gd.seg_end[2] = H;
             gd.out = m->pf_x, gd.ldo = H, gd.M = P, gd.N = H, gd.K = I;
+            gd.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
             LAUNCH(launch_gemm_bf16(kGemmResid, gd, s));
         }
         if (c0 + P == n)
@@ -638,7 +644,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
+                    m->pf_scale, m->pf_ahl, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -1463,12 +1469,19 @@ int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, 
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (M >= kLinearGemmMinRows) {
-        // One MFMA GEMM reads W once for all rows (activations split hi/lo).
+        // One MFMA GEMM reads W once for all rows (activations split hi/lo
+        // into stream-ordered scratch).
         GemmArgs g;
         g.a = dX, g.lda = K, g.w[0] = dW, g.bias[0] = dBias;
         g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
         g.out = dY, g.ldo = N, g.M = M, g.N = N, g.K = K;
-        HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
+        void* hl = nullptr;
+        HIP_TRY(hipMallocAsync(&hl, gemm_split_elems(M, K) * sizeof(uint16_t), s));
+        g.a_hl = static_cast<uint16_t*>(hl);
+        const hipError_t e = launch_gemm_bf16(kGemmPlain, g, s);
+        const hipError_t f = hipFreeAsync(hl, s);
+        HIP_TRY(e);
+        HIP_TRY(f);
         return VVLI_OK;
     }
     for (uint32_t mi = 0; mi < M; ++mi) {

@@ -61,9 +61,13 @@ __device__ inline uint16_t to_bf16_rne(float v) {
 __device__ inline float from_bf16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
 struct GemmTileRegs {
-    float a[16];     // 16 consecutive K of one A row
-    uint16_t b[16];  // 16 consecutive K of one W row
+    u16x8 hi[2], lo[2];  // 16 consecutive K of one A row, split hi | lo
+    u16x8 b[2];          // 16 consecutive K of one W row
 };
+
+// Row stride of the split A planes: K rounded up to whole K steps, the tail
+// zero-filled by gemm_split_kernel.
+__host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + kBK - 1) / kBK * kBK; }
 
 // Row of W feeding B-tile row r of block column n0 (GateUp interleaves gate and
 // up rows in groups of 16 so one lane holds both halves of an output).
@@ -82,70 +86,75 @@ __device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int
     return g.w[2] + static_cast<size_t>(nn - g.seg_end[1]) * g.K;
 }
 
+// One thread's share of a K step: A row m0 + tid/2 (hi and lo planes) and W
+// row r, K columns k0 + (tid & 1) * 16 .. +15. The loads are unconditional, so
+// that no branch or select ties them to the next step's stores and two steps
+// stay in flight: A rows past M read row 0 and W rows past N read W row 0
+// (those outputs are never written); past K, A reads its zero tail and W
+// reads 8 zeros of that tail too (K % 32 != 0 only), so tail products are 0.
 template <int MODE>
 __device__ inline void gemm_load(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t k0, GemmTileRegs& t) {
     const int tid = threadIdx.x;
     const int r = tid >> 1;
     const uint32_t kc = k0 + (tid & 1) * 16;
-    // A: K is a multiple of 8, so each half of the 16-wide chunk is all in or all out.
     const uint32_t row = m0 + r;
-    const float* ap = g.a + static_cast<size_t>(row < g.M ? row : 0) * g.lda + kc;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const bool in = row < g.M && kc + 8 * h < g.K;
-        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-        if (in) {
-            v0 = *reinterpret_cast<const float4*>(ap + 8 * h);
-            v1 = *reinterpret_cast<const float4*>(ap + 8 * h + 4);
-        }
-        t.a[8 * h + 0] = v0.x, t.a[8 * h + 1] = v0.y, t.a[8 * h + 2] = v0.z, t.a[8 * h + 3] = v0.w;
-        t.a[8 * h + 4] = v1.x, t.a[8 * h + 5] = v1.y, t.a[8 * h + 6] = v1.z, t.a[8 * h + 7] = v1.w;
-    }
+    const uint32_t kp = gemm_kp(g.K);
+    const size_t plane = static_cast<size_t>(g.M) * kp;
+    const uint16_t* hp = g.a_hl + static_cast<size_t>(row < g.M ? row : 0) * kp + kc;
     bool valid;
-    const uint16_t* wp = gemm_w_row<MODE>(g, n0, r, valid) + kc;
+    const uint16_t* wp = gemm_w_row<MODE>(g, n0, r, valid);
+    const uint16_t* zeros = g.a_hl + (kp - 8);  // A row 0, last 8 columns: inside the zero tail when K < kp
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (valid && kc + 8 * h < g.K) v = *reinterpret_cast<const u16x8*>(wp + 8 * h);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t.b[8 * h + j] = v[j];
+        t.hi[h] = *reinterpret_cast<const u16x8*>(hp + 8 * h);
+        t.lo[h] = *reinterpret_cast<const u16x8*>(hp + plane + 8 * h);
+        t.b[h] = *reinterpret_cast<const u16x8*>(kc + 8 * h < g.K ? wp + kc + 8 * h : zeros);
     }
 }
 
-// Normalise (optional), split into hi/lo, and store one thread's chunk.
-__device__ inline void gemm_store(const GemmArgs& g, uint32_t m0, uint32_t k0, const GemmTileRegs& t,
-                                  uint16_t* ahi, uint16_t* alo, uint16_t* bs) {
+__device__ inline void gemm_store(const GemmTileRegs& t, uint16_t* ahi, uint16_t* alo, uint16_t* bs) {
     const int tid = threadIdx.x;
     const int r = tid >> 1, c = (tid & 1) * 16;
-    const uint32_t kc = k0 + c;
-    float scale = 1.0f;
-    if (g.row_scale) {
-        const uint32_t row = m0 + r;
-        scale = row < g.M ? g.row_scale[row] : 0.0f;
-    }
-    u16x8 nw[2] = {{0, 0, 0, 0, 0, 0, 0, 0}, {0, 0, 0, 0, 0, 0, 0, 0}};
-    if (g.norm_w) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            if (kc + 8 * h < g.K) nw[h] = *reinterpret_cast<const u16x8*>(g.norm_w + kc + 8 * h);
+    for (int h = 0; h < 2; ++h) {
+        *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c + 8 * h) = t.hi[h];
+        *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c + 8 * h) = t.lo[h];
+        *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c + 8 * h) = t.b[h];
     }
-    u16x8 hi[2], lo[2], bb[2];
+}
+
+// A into hi | lo bf16 planes (a_hl[0][m][kp], a_hl[1][m][kp]) with the
+// RMSNorm prologue when norm_w is set: v = (a * w) * scale in rmsNormInto's
+// order (src/llm.zig:1297), hi = bf16(v), lo = bf16(v - hi); columns K .. kp
+// are zeros. 8 columns per thread.
+__global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs g) {
+    const uint32_t kp = gemm_kp(g.K);
+    const uint32_t groups = kp / 8;
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<size_t>(g.M) * groups) return;
+    const uint32_t m = static_cast<uint32_t>(i / groups), k = static_cast<uint32_t>(i % groups) * 8;
+    u16x8 hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = hi;
+    if (k < g.K) {  // K % 8 == 0: the group is all in or all out
+        const float* ap = g.a + static_cast<size_t>(m) * g.lda + k;
+        const float4 v0 = *reinterpret_cast<const float4*>(ap);
+        const float4 v1 = *reinterpret_cast<const float4*>(ap + 4);
+        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        if (g.norm_w) {
+            const u16x8 w = *reinterpret_cast<const u16x8*>(g.norm_w + k);
+            const float scale = g.row_scale[m];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        float v = t.a[j];
-        // rmsNormInto order: (x * w) * scale (src/llm.zig:1297)
-        if (g.norm_w) v = __fmul_rn(__fmul_rn(v, from_bf16(nw[j / 8][j % 8])), scale);
-        const uint16_t h = to_bf16_rne(v);
-        hi[j / 8][j % 8] = h;
-        lo[j / 8][j % 8] = to_bf16_rne(v - from_bf16(h));
-        bb[j / 8][j % 8] = t.b[j];
+            for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(__fmul_rn(v[j], from_bf16(w[j])), scale);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint16_t h = to_bf16_rne(v[j]);
+            hi[j] = h;
+            lo[j] = to_bf16_rne(v[j] - from_bf16(h));
+        }
     }
-    *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c) = hi[0];
-    *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c + 8) = hi[1];
-    *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c) = lo[0];
-    *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c + 8) = lo[1];
-    *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c) = bb[0];
-    *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c + 8) = bb[1];
+    uint16_t* out = g.a_hl + static_cast<size_t>(m) * kp + k;
+    *reinterpret_cast<u16x8*>(out) = hi;
+    *reinterpret_cast<u16x8*>(out + static_cast<size_t>(g.M) * kp) = lo;
 }
 
 __device__ inline float silu_mul(float gv, float uv) {
@@ -157,8 +166,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][3][kTileElems];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = blockIdx.y * kBM;
-    const uint32_t n0 = blockIdx.x * kBN;
+    // Tile of this block. Consecutive blocks go to the 8 XCDs in turn and each
+    // XCD has its own L2, so block b is mapped to tile u = offset(xcd) + b / 8:
+    // every XCD walks a contiguous run of tiles in M-fast order, and the
+    // blocks it runs together share their W rows (and their A rows across
+    // the few W columns in flight) through its L2 as they step through K in
+    // near lockstep.
+    const uint32_t tm = (g.M + kBM - 1) / kBM;
+    const uint32_t ntile = gridDim.x;
+    const uint32_t xcd = blockIdx.x % 8, per = ntile / 8, rem = ntile % 8;
+    const uint32_t u = xcd * per + min(xcd, rem) + blockIdx.x / 8;
+    const uint32_t m0 = (u % tm) * kBM;
+    const uint32_t n0 = (u / tm) * kBN;
     // Split K across gridDim.z blocks (partial sums added atomically).
     const uint32_t nk_all = (g.K + kBK - 1) / kBK;
     const uint32_t per_split = (nk_all + gridDim.z - 1) / gridDim.z;
@@ -173,39 +192,52 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (nk == 0) return;  // empty split (uniform per block)
-    GemmTileRegs t;
-    gemm_load<MODE>(g, m0, n0, kt0 * kBK, t);
-    gemm_store(g, m0, kt0 * kBK, t, lds[0][0], lds[0][1], lds[0][2]);
+    // Two K steps in flight through registers: while step kt is multiplied
+    // from LDS, step kt + 1 waits in registers for its LDS buffer and step
+    // kt + 2 is being loaded (global memory latency is about two steps).
+    GemmTileRegs ta, tb;
+    gemm_load<MODE>(g, m0, n0, kt0 * kBK, ta);
+    if (nk > 1) gemm_load<MODE>(g, m0, n0, (kt0 + 1) * kBK, tb);
+    gemm_store(ta, lds[0][0], lds[0][1], lds[0][2]);
     __syncthreads();
 
     const int fr = lane & 15, fk = 8 * (lane >> 4);
-    for (uint32_t kt = 0; kt < nk; ++kt) {
+    auto step = [&](uint32_t kt, GemmTileRegs& load_into, const GemmTileRegs& store_from) {
         const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) gemm_load<MODE>(g, m0, n0, (kt0 + kt + 1) * kBK, t);
+        // (Unconditional: past the last step it re-reads that step, so no
+        // branch merges the two register sets.)
+        gemm_load<MODE>(g, m0, n0, (kt0 + min(kt + 2, nk - 1)) * kBK, load_into);
         const uint16_t* ahi = lds[cur][0];
         const uint16_t* alo = lds[cur][1];
         const uint16_t* bs = lds[cur][2];
-        bf16x8 bf[4];
+        bf16x8 bf[4], ah[4], al[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             bf[j] = *reinterpret_cast<const bf16x8*>(bs + (wn * 64 + j * 16 + fr) * kLdsRow + fk);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = (wm * 64 + i * 16 + fr) * kLdsRow + fk;
-            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(ahi + row);
-            const bf16x8 al = *reinterpret_cast<const bf16x8*>(alo + row);
+            ah[i] = *reinterpret_cast<const bf16x8*>(ahi + row);
+            al[i] = *reinterpret_cast<const bf16x8*>(alo + row);
+        }
+        // All hi products, then all lo products: 16 independent accumulators
+        // between the two MFMAs that update one of them.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bf[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bf[j], acc[i][j], 0, 0, 0);
-            }
-        }
-        if (more) {
-            const int nxt = cur ^ 1;
-            gemm_store(g, m0, (kt0 + kt + 1) * kBK, t, lds[nxt][0], lds[nxt][1], lds[nxt][2]);
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bf[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bf[j], acc[i][j], 0, 0, 0);
+        if (kt + 1 < nk) gemm_store(store_from, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2]);
         __syncthreads();
+    };
+    for (uint32_t kt = 0; kt < nk; kt += 2) {
+        step(kt, ta, tb);
+        if (kt + 1 < nk) step(kt + 1, tb, ta);
     }
 
     // Epilogue.
@@ -672,8 +704,16 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     return want > 0 ? want : 1;
 }
 
+size_t gemm_split_elems(uint32_t M, uint32_t K) { return static_cast<size_t>(2) * M * gemm_kp(K); }
+
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
+    if (!g.a_hl || g.K % 8 != 0 || (g.norm_w && !g.row_scale)) return hipErrorInvalidValue;
+    {
+        const size_t n = static_cast<size_t>(g.M) * (gemm_kp(g.K) / 8);
+        hipError_t e = vlaunch(gemm_split_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, g);
+        if (e != hipSuccess) return e;
+    }
     const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
     const uint32_t gx = (cols + kBN - 1) / kBN, gy = (g.M + kBM - 1) / kBM;
     const uint32_t splits = gemm_k_splits(mode, g, gx * gy);
@@ -683,7 +723,7 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
         hipError_t e = vlaunch(zero_rows_kernel, dim3(blocks), dim3(256), 0, s, g.out, n);
         if (e != hipSuccess) return e;
     }
-    const dim3 grid(gx, gy, splits);
+    const dim3 grid(gx * gy, 1, splits);  // tiles in the XCD-aware order of the kernel
     switch (mode) {
         case kGemmPlain: return vlaunch(gemm_bf16_kernel<kGemmPlain>, grid, dim3(kGemmThreads), 0, s, g);
         case kGemmResid: return vlaunch(gemm_bf16_kernel<kGemmResid>, grid, dim3(kGemmThreads), 0, s, g);
