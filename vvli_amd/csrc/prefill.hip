@@ -42,28 +42,31 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
-// GEMM tile: 128 (rows of A) x 128 (rows of W) x 32 (K) per step, 256 threads
-// as 2 x 2 waves of 64 x 64, each wave 4 x 4 MFMA tiles of 16 x 16.
+// GEMM tile: 128 (rows of A) x 256 (rows of W) x 32 (K) per step, 512
+// threads as 2 x 4 waves of 64 x 64, each wave 4 x 4 MFMA tiles of 16 x 16.
 // v_mfma_f32_16x16x32_bf16 lane layout (lane l): A row l%16, k 8*(l/16)..+7;
 // B column l%16, same k; D rows 4*(l/16)+j (j = 0..3), column l%16.
-// LDS rows are padded to 40 bf16 (80 bytes): the 16 rows one 16-lane group
-// reads then start in 16 distinct 16-byte bank groups.
+//
+// Operands reach LDS by global_load_lds_dwordx4 (no registers in between):
+// 4 stages of [A hi 8 KiB | A lo 8 KiB | W 16 KiB], three K steps in flight.
+// An LDS row is 32 bf16 (64 bytes, four 16-byte chunks); chunk c of row r is
+// stored at position c ^ swz(r), which puts the 16 rows a 16-lane group reads
+// (and the 8 rows of an 8-lane group) in distinct bank groups. MFMA fragments
+// are read with ds_read_b128 in inline asm and waited for explicitly, so the
+// compiler does not tie them to the copies in flight.
 // ---------------------------------------------------------------------------
-constexpr int kGemmThreads = 256;
-constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kLdsRow = 40;  // bf16 per LDS row
-constexpr int kTileElems = kBM * kLdsRow;
+constexpr int kGemmThreads = 512;
+constexpr int kBM = 128, kBN = 256, kBK = 32, kStages = 4;
+constexpr int kOpA = kBM * kBK * 2;                  // bytes of one A plane tile
+constexpr int kStageBytes = 2 * kOpA + kBN * kBK * 2;
+constexpr int kDmaPerWave = kStageBytes / 1024 / (kGemmThreads / 64);  // 1 KiB copies per wave per stage
+constexpr int kGemmLds = kStages * kStageBytes;
 
 __device__ inline uint16_t to_bf16_rne(float v) {
     uint32_t b = __float_as_uint(v);
     return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
 }
 __device__ inline float from_bf16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
-
-struct GemmTileRegs {
-    u16x8 hi[2], lo[2];  // 16 consecutive K of one A row, split hi | lo
-    u16x8 b[2];          // 16 consecutive K of one W row
-};
 
 // Row stride of the split A planes: K rounded up to whole K steps, the tail
 // zero-filled by gemm_split_kernel.
@@ -86,41 +89,37 @@ __device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int
     return g.w[2] + static_cast<size_t>(nn - g.seg_end[1]) * g.K;
 }
 
-// One thread's share of a K step: A row m0 + tid/2 (hi and lo planes) and W
-// row r, K columns k0 + (tid & 1) * 16 .. +15. The loads are unconditional, so
-// that no branch or select ties them to the next step's stores and two steps
-// stay in flight: A rows past M read row 0 and W rows past N read W row 0
-// (those outputs are never written); past K, A reads its zero tail and W
-// reads 8 zeros of that tail too (K % 32 != 0 only), so tail products are 0.
-template <int MODE>
-__device__ inline void gemm_load(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t k0, GemmTileRegs& t) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1;
-    const uint32_t kc = k0 + (tid & 1) * 16;
-    const uint32_t row = m0 + r;
-    const uint32_t kp = gemm_kp(g.K);
-    const size_t plane = static_cast<size_t>(g.M) * kp;
-    const uint16_t* hp = g.a_hl + static_cast<size_t>(row < g.M ? row : 0) * kp + kc;
-    bool valid;
-    const uint16_t* wp = gemm_w_row<MODE>(g, n0, r, valid);
-    const uint16_t* zeros = g.a_hl + (kp - 8);  // A row 0, last 8 columns: inside the zero tail when K < kp
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        t.hi[h] = *reinterpret_cast<const u16x8*>(hp + 8 * h);
-        t.lo[h] = *reinterpret_cast<const u16x8*>(hp + plane + 8 * h);
-        t.b[h] = *reinterpret_cast<const u16x8*>(kc + 8 * h < g.K ? wp + kc + 8 * h : zeros);
-    }
-}
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-__device__ inline void gemm_store(const GemmTileRegs& t, uint16_t* ahi, uint16_t* alo, uint16_t* bs) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1, c = (tid & 1) * 16;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        *reinterpret_cast<u16x8*>(ahi + r * kLdsRow + c + 8 * h) = t.hi[h];
-        *reinterpret_cast<u16x8*>(alo + r * kLdsRow + c + 8 * h) = t.lo[h];
-        *reinterpret_cast<u16x8*>(bs + r * kLdsRow + c + 8 * h) = t.b[h];
-    }
+__device__ __forceinline__ uint32_t gemm_swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
+
+__device__ __forceinline__ void gemm_dma16(const void* src, char* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ uint32_t gemm_lds_addr(char* p) { return (uint32_t)(uintptr_t)(lds_void_t*)p; }
+__device__ __forceinline__ void gemm_barrier() { __builtin_amdgcn_s_barrier(); }
+
+// Wait until at most n of this wave's memory loads are in flight (n = 0, 4
+// or 8: whole stages of kDmaPerWave copies).
+__device__ __forceinline__ void gemm_wait_vm(int n) {
+    constexpr int kKeep = (7 << 4) | (15 << 8);  // expcnt, lgkmcnt: no wait
+    if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | kKeep);
+    else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | kKeep);
+    else __builtin_amdgcn_s_waitcnt(0 | kKeep);
+}
+static_assert(kDmaPerWave == 4, "gemm_wait_vm counts in stages of 4 copies");
+
+__device__ __forceinline__ bf16x8 gemm_lds_read(uint32_t addr) {
+    bf16x8 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+// Waits for the fragment reads; the fragments are operands, so nothing that
+// uses them can be scheduled before the wait.
+__device__ __forceinline__ void gemm_lds_wait(bf16x8 (&a)[4], bf16x8 (&l)[4], bf16x8 (&b)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(l[0]), "+v"(l[1]), "+v"(l[2]), "+v"(l[3]),
+                   "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 }
 
 // A into hi | lo bf16 planes (a_hl[0][m][kp], a_hl[1][m][kp]) with the
@@ -163,26 +162,27 @@ __device__ inline float silu_mul(float gv, float uv) {
 
 template <int MODE>
 __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2][3][kTileElems];
+    extern __shared__ __attribute__((aligned(1024))) char gemm_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;
     // Tile of this block. Consecutive blocks go to the 8 XCDs in turn and each
-    // XCD has its own L2, so block b is mapped to tile u = offset(xcd) + b / 8:
-    // every XCD walks a contiguous run of tiles in M-fast order, and the
-    // blocks it runs together share their W rows (and their A rows across
-    // the few W columns in flight) through its L2 as they step through K in
-    // near lockstep.
-    const uint32_t tm = (g.M + kBM - 1) / kBM;
+    // XCD has its own L2: block b is mapped to tile u = offset(xcd) + b / 8, so
+    // every XCD walks a contiguous run of tiles, ordered in panels of 8 W
+    // columns (M fastest inside a panel): the blocks an XCD runs together
+    // cover about 8 x 8 tiles and share their A and W slabs through its L2.
+    const uint32_t cols = MODE == kGemmGateUp ? 2 * g.N : g.N;
+    const uint32_t tm = (g.M + kBM - 1) / kBM, tn = (cols + kBN - 1) / kBN;
     const uint32_t ntile = gridDim.x;
     const uint32_t xcd = blockIdx.x % 8, per = ntile / 8, rem = ntile % 8;
     const uint32_t u = xcd * per + min(xcd, rem) + blockIdx.x / 8;
-    const uint32_t m0 = (u % tm) * kBM;
-    const uint32_t n0 = (u / tm) * kBN;
+    const uint32_t panel = u / (tm * 8), pw = min(8u, tn - 8 * panel), within = u - panel * tm * 8;
+    const uint32_t m0 = (within / pw) * kBM;
+    const uint32_t n0 = (8 * panel + within % pw) * kBN;
     // Split K across gridDim.z blocks (partial sums added atomically).
     const uint32_t nk_all = (g.K + kBK - 1) / kBK;
     const uint32_t per_split = (nk_all + gridDim.z - 1) / gridDim.z;
     const uint32_t kt0 = blockIdx.z * per_split;
-    const uint32_t nk = kt0 < nk_all ? min(per_split, nk_all - kt0) : 0;
+    const int nk = kt0 < nk_all ? static_cast<int>(min(per_split, nk_all - kt0)) : 0;
     const bool split = gridDim.z > 1;
 
     f32x4 acc[4][4];
@@ -190,57 +190,100 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
     if (nk == 0) return;  // empty split (uniform per block)
-    // Two K steps in flight through registers: while step kt is multiplied
-    // from LDS, step kt + 1 waits in registers for its LDS buffer and step
-    // kt + 2 is being loaded (global memory latency is about two steps).
-    GemmTileRegs ta, tb;
-    gemm_load<MODE>(g, m0, n0, kt0 * kBK, ta);
-    if (nk > 1) gemm_load<MODE>(g, m0, n0, (kt0 + 1) * kBK, tb);
-    gemm_store(ta, lds[0][0], lds[0][1], lds[0][2]);
-    __syncthreads();
 
-    const int fr = lane & 15, fk = 8 * (lane >> 4);
-    auto step = [&](uint32_t kt, GemmTileRegs& load_into, const GemmTileRegs& store_from) {
-        const int cur = kt & 1;
-        // (Unconditional: past the last step it re-reads that step, so no
-        // branch merges the two register sets.)
-        gemm_load<MODE>(g, m0, n0, (kt0 + min(kt + 2, nk - 1)) * kBK, load_into);
-        const uint16_t* ahi = lds[cur][0];
-        const uint16_t* alo = lds[cur][1];
-        const uint16_t* bs = lds[cur][2];
-        bf16x8 bf[4], ah[4], al[4];
+    // Copies: wave w issues 1 KiB copies q = 4w .. 4w+3 of a stage: q < 8 A hi
+    // rows 16q.., q < 16 A lo rows 16(q-8).., else W rows 16(q-16)..; lane l
+    // fetches row 16 (q % 8 or q - 16) + l/4, chunk (l & 3) ^ swz(row), which
+    // lands at position l & 3 of that row. A rows past M read row 0 and W rows
+    // past N read row 0 (their outputs are never written); past K, A reads its
+    // zero tail and W reads 8 zeros of that tail (only when K % 32 != 0).
+    const uint32_t kp = gemm_kp(g.K);
+    const uint16_t* zeros = g.a_hl + (kp - 8);
+    const uint16_t* src[kDmaPerWave];
+    uint32_t chunk[kDmaPerWave];
+    bool is_w[kDmaPerWave];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            bf[j] = *reinterpret_cast<const bf16x8*>(bs + (wn * 64 + j * 16 + fr) * kLdsRow + fk);
+    for (int i = 0; i < kDmaPerWave; ++i) {
+        const int q = wave * kDmaPerWave + i;
+        const int grp = q < 16 ? q % 8 : q - 16;
+        const uint32_t row = grp * 16 + lane / 4;
+        chunk[i] = (static_cast<uint32_t>(lane & 3) ^ gemm_swz(row)) * 8;
+        is_w[i] = q >= 16;
+        if (q < 16) {
+            const uint32_t gm = m0 + row < g.M ? m0 + row : 0;
+            src[i] = g.a_hl + (q >= 8 ? static_cast<size_t>(g.M) * kp : 0) + static_cast<size_t>(gm) * kp;
+        } else {
+            bool valid;
+            src[i] = gemm_w_row<MODE>(g, n0, static_cast<int>(row), valid);
+        }
+    }
+    auto issue = [&](int kt, int stage) {
+        const uint32_t k0 = (kt0 + kt) * kBK;
+#pragma unroll
+        for (int i = 0; i < kDmaPerWave; ++i) {
+            const uint32_t k = k0 + chunk[i];
+            const uint16_t* p = (is_w[i] && k >= g.K) ? zeros : src[i] + k;
+            gemm_dma16(p, gemm_smem + stage * kStageBytes + (wave * kDmaPerWave + i) * 1024);
+        }
+    };
+    // Fragment addresses within a stage.
+    const uint32_t lds0 = gemm_lds_addr(gemm_smem);
+    uint32_t fa[4], fb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t ra = wm * 64 + i * 16 + (lane & 15), rb = wn * 64 + i * 16 + (lane & 15);
+        const uint32_t qk = static_cast<uint32_t>(lane) >> 4;
+        fa[i] = lds0 + ra * 64 + ((qk ^ gemm_swz(ra)) << 4);
+        fb[i] = lds0 + 2 * kOpA + rb * 64 + ((qk ^ gemm_swz(rb)) << 4);
+    }
+    bf16x8 fh[2][4], fl[2][4], fw[2][4];
+    auto read_frags = [&](int kt, bf16x8 (&a)[4], bf16x8 (&l)[4], bf16x8 (&w)[4]) {
+        const uint32_t so = static_cast<uint32_t>(kt % kStages) * kStageBytes;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = (wm * 64 + i * 16 + fr) * kLdsRow + fk;
-            ah[i] = *reinterpret_cast<const bf16x8*>(ahi + row);
-            al[i] = *reinterpret_cast<const bf16x8*>(alo + row);
+            a[i] = gemm_lds_read(fa[i] + so);
+            l[i] = gemm_lds_read(fa[i] + so + kOpA);
+            w[i] = gemm_lds_read(fb[i] + so);
         }
-        // All hi products, then all lo products: 16 independent accumulators
-        // between the two MFMAs that update one of them.
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bf[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bf[j], acc[i][j], 0, 0, 0);
-        if (kt + 1 < nk) gemm_store(store_from, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2]);
-        __syncthreads();
     };
-    for (uint32_t kt = 0; kt < nk; kt += 2) {
-        step(kt, ta, tb);
-        if (kt + 1 < nk) step(kt + 1, tb, ta);
+    // All hi products, then all lo products: 16 independent accumulators
+    // between the two MFMAs that update one of them.
+    auto mfmas = [&](const bf16x8 (&a)[4], const bf16x8 (&l)[4], const bf16x8 (&w)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], w[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l[i], w[j], acc[i][j], 0, 0, 0);
+    };
+    // Prologue: stages 0 .. kStages-2 in flight, step 0's fragments read.
+    for (int s0 = 0; s0 < kStages - 1; ++s0)
+        if (s0 < nk) issue(s0, s0);
+    gemm_wait_vm(min(kStages - 2, nk - 1) * kDmaPerWave);
+    gemm_barrier();
+    read_frags(0, fh[0], fl[0], fw[0]);
+    gemm_lds_wait(fh[0], fl[0], fw[0]);
+    // Step kt: once stage kt+1 is in LDS for every wave (and every wave has
+    // read stage kt-1's fragments), refill stage kt-1 with step kt+3, read
+    // step kt+1's fragments and multiply step kt's.
+    auto step = [&](int kt, int cur) {
+        if (kt + 1 < nk) gemm_wait_vm(min(kStages - 3, nk - 2 - kt) * kDmaPerWave);
+        gemm_barrier();
+        if (kt + kStages - 1 < nk) issue(kt + kStages - 1, (kt + kStages - 1) % kStages);
+        if (kt + 1 < nk) read_frags(kt + 1, fh[cur ^ 1], fl[cur ^ 1], fw[cur ^ 1]);
+        mfmas(fh[cur], fl[cur], fw[cur]);
+        if (kt + 1 < nk) gemm_lds_wait(fh[cur ^ 1], fl[cur ^ 1], fw[cur ^ 1]);
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, 0);
+        if (kt + 1 < nk) step(kt + 1, 1);
     }
 
     // Epilogue.
+    const int fr = lane & 15;
     const int rq = 4 * (lane >> 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -714,6 +757,18 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
         hipError_t e = vlaunch(gemm_split_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, g);
         if (e != hipSuccess) return e;
     }
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_kernel<kGemmPlain>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_kernel<kGemmResid>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_kernel<kGemmGateUp>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
     const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
     const uint32_t gx = (cols + kBN - 1) / kBN, gy = (g.M + kBM - 1) / kBM;
     const uint32_t splits = gemm_k_splits(mode, g, gx * gy);
@@ -725,9 +780,9 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     }
     const dim3 grid(gx * gy, 1, splits);  // tiles in the XCD-aware order of the kernel
     switch (mode) {
-        case kGemmPlain: return vlaunch(gemm_bf16_kernel<kGemmPlain>, grid, dim3(kGemmThreads), 0, s, g);
-        case kGemmResid: return vlaunch(gemm_bf16_kernel<kGemmResid>, grid, dim3(kGemmThreads), 0, s, g);
-        case kGemmGateUp: return vlaunch(gemm_bf16_kernel<kGemmGateUp>, grid, dim3(kGemmThreads), 0, s, g);
+        case kGemmPlain: return vlaunch(gemm_bf16_kernel<kGemmPlain>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+        case kGemmResid: return vlaunch(gemm_bf16_kernel<kGemmResid>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+        case kGemmGateUp: return vlaunch(gemm_bf16_kernel<kGemmGateUp>, grid, dim3(kGemmThreads), kGemmLds, s, g);
         default: return hipErrorInvalidValue;
     }
 }
