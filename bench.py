@@ -76,16 +76,17 @@ def profile_kernels(runner, cfg, token: int, pos: int, reps: int = 3) -> dict:
     return out
 
 
-def measured_traffic(symbol: str):
-    """HBM bytes per launch of `symbol` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 256 MiB copy)."""
+def measured_traffic(symbol: str, model: str):
+    """HBM bytes per launch of `symbol` on `model` from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 256 MiB copy);
+    None where no summary covers that kernel and workload."""
     path = ROOT / "profiles" / "pmc_traffic_llama1b_decode.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
         parts = line.strip().split("\t")
-        if len(parts) == 3 and parts[0] == "traffic" and parts[1] == symbol:
-            return int(parts[2])
+        if len(parts) == 4 and parts[0] == "traffic" and parts[1] == symbol and parts[2] == model:
+            return int(parts[3])
     return None
 
 
@@ -325,12 +326,14 @@ def main() -> int:
         # decode launch runs all --steps tokens. Algorithmic bytes per launch =
         # sum over the decode positions of B(pos); duration = HIP events around
         # that launch on the model's stream.
-        sym = "decode_step_kernel<64, true> (persistent decode step)"
+        hd = cfg.head_dim()
+        tmpl = f"{64 if hd <= 64 else 128}, {'true' if hd in (64, 128) else 'false'}"
+        sym = f"decode_step_kernel<{tmpl}> (persistent decode step)"
         kernels = {sym: {"launches": 1, "total_us": decode_launch_ms * 1e3, "avg_us": decode_launch_ms * 1e3,
                          "bytes_per_launch": step_bytes, "gbs": step_bytes / (decode_launch_ms * 1e-3) / 1e9}}
     dom = max(kernels, key=lambda k: kernels[k]["total_us"])
     d = kernels[dom]
-    traffic = measured_traffic(dom.split(" (")[0])
+    traffic = measured_traffic(dom.split(" (")[0], args.model)
     roofline = {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 2),
