@@ -734,11 +734,13 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) out[i] = 0.f;
 }
 
-// K splits for a launch. One block runs per CU, so the launch should fill
-// whole rounds of the CUs: the smallest split count (each split at least 8
-// K steps, at most 32) whose blocks use the rounds they need best. SwiGLU
-// tiles are never split (the epilogue is nonlinear), plain tiles only when
-// the output rows are dense (they are zeroed first).
+// K splits for a launch. One block runs per CU. Splitting costs atomics, a
+// zeroing pass and shorter K loops (the copy pipeline fills and drains per
+// split), so it is used only when the tiles leave more than half of the CUs
+// idle: then as many splits as keep the launch within one round (each split
+// at least 8 K steps, at most 32). SwiGLU tiles are never split (the epilogue
+// is nonlinear), plain tiles only when the output rows are dense (they are
+// zeroed first).
 uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     if (mode == kGemmGateUp || (mode == kGemmPlain && g.ldo != g.N)) return 1;
     static const uint32_t cus = [] {
@@ -750,17 +752,8 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     }();
     const uint32_t nk = (g.K + kBK - 1) / kBK;
     const uint32_t max_splits = std::min<uint32_t>(32, nk / 8 > 0 ? nk / 8 : 1);
-    uint32_t best = 1;
-    double best_use = 0.0;
-    for (uint32_t sp = 1; sp <= max_splits && tiles * (sp - 1) < 4 * cus; ++sp) {
-        const uint32_t blocks = tiles * sp;
-        const double use = static_cast<double>(blocks) / (static_cast<double>((blocks + cus - 1) / cus) * cus);
-        if (use > best_use + 0.05) {
-            best_use = use;
-            best = sp;
-        }
-    }
-    return best;
+    if (2 * tiles > cus) return 1;
+    return std::max<uint32_t>(1, std::min<uint32_t>(max_splits, cus / tiles));
 }
 
 size_t gemm_split_elems(uint32_t M, uint32_t K) { return static_cast<size_t>(2) * M * gemm_kp(K); }
