@@ -1,7 +1,8 @@
 """ctypes wrapper of liboracle (vvli_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's CPU-baseline leg, as the checker. The product path never uses it.
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and bench.py's
+CPU-baseline leg, as the source of reference results. The product path never
+uses it.
 """
 from __future__ import annotations
 

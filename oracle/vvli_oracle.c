@@ -1,8 +1,8 @@
 /*
  * vvli_oracle.c -- CPU restatement of VVLI's dense-decoder forward pass.
  *
- * TEST INFRASTRUCTURE ONLY: the checker and the timed CPU baseline. The
- * product library never links or calls this file. See vvli_oracle.h for the
+ * TEST INFRASTRUCTURE ONLY: reference results for the parity tests and the
+ * timed CPU baseline. The product library never links or calls this file. See vvli_oracle.h for the
  * pinning status of each function.
  *
  * Built with -ffp-contract=off so that `acc + a*b` stays an unfused multiply

@@ -1,9 +1,9 @@
 /*
  * vvli_oracle.h -- CPU restatement of VVLI's dense-decoder forward pass.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the MI355X
- * library (libvvli_gpu.so) and the timed CPU baseline in bench.py. Nothing in
- * the product path links, loads or calls it.
+ * TEST INFRASTRUCTURE ONLY. This library gives the reference results the
+ * MI355X library (libvvli_gpu.so) is tested against, and the timed CPU
+ * baseline in bench.py. Nothing in the product path links, loads or calls it.
  *
  * Every function restates a function of the reference (risingsunomi/vvli,
  * Zig) and cites the file:line it follows. Operation order is kept where it

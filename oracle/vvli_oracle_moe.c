@@ -1,6 +1,6 @@
 /*
  * vvli_oracle_moe.c -- CPU restatement of a mixture-of-experts decoder step
- * (OLMoE form). TEST INFRASTRUCTURE ONLY: the checker of the GPU library's
+ * (OLMoE form). TEST INFRASTRUCTURE ONLY: reference results for the GPU
  * MoE runner; nothing in the product path links or calls it.
  *
  * The reference has no MoE forward pass: Config carries num_experts /

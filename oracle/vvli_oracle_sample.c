@@ -2,7 +2,7 @@
  * vvli_oracle_sample.c -- CPU restatement of VVLI's token sampler
  * (src/generator.zig:14-23 Options, 65-127 Sampler, 338-463 helpers) and of the
  * sampled generation loop (generateGreedyMeasuredInternal, :221-293).
- * TEST INFRASTRUCTURE ONLY: the checker of the GPU library's sampling kernel.
+ * TEST INFRASTRUCTURE ONLY: reference results for the GPU sampling kernel.
  *
  * The random stream is Zig's std.Random.DefaultPrng (Xoshiro256, the
  * xoshiro256++ generator of Blackman and Vigna, seeded by four SplitMix64

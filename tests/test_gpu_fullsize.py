@@ -2,7 +2,7 @@
 Llama-3.2-1B, Qwen2.5-7B, OLMoE-1B-7B) with seeded synthetic bf16 weights,
 against the oracle on the same blob.
 
-Bar (the north star's): the residual stream after every layer and the logits
+Bar: the residual stream after every layer and the logits
 within 2e-3 max relative error for the first positions, and the greedy tokens
 identical. Sequence lengths are cut to what the CPU oracle finishes in
 seconds; the GPU runs the same code paths the benchmark runs (persistent

@@ -1,5 +1,5 @@
 """Pins the oracle (oracle/vvli_oracle.c, the CPU restatement of the
-reference forward pass) before it is trusted as the GPU checker.
+reference forward pass) before the GPU parity tests rely on it.
 
 Each check is something the oracle's own formula cannot satisfy by
 construction: the reference's inline-test known answers, f64 brute force,

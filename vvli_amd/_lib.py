@@ -1,7 +1,6 @@
 """ctypes binding of libvvli_gpu.so (include/vvli_gpu.h, include/vvli_host.h).
 
-The library is built in-tree by ``__graft_entry__.build()`` (make -C
-vvli_amd/csrc). There is no fallback: if the shared object is missing the
+The library is built in-tree (make -C vvli_amd/csrc). There is no fallback: if the shared object is missing the
 import of any runtime object raises.
 """
 from __future__ import annotations
@@ -160,7 +159,7 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
-            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (make -C vvli_amd/csrc)")
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with make -C vvli_amd/csrc")
         handle = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | getattr(os, "RTLD_GLOBAL", 0))
         for name, (res, args) in PROTOTYPES.items():
             fn = getattr(handle, name)
