@@ -262,7 +262,13 @@ struct PrefillAttnArgs {
     uint32_t rows, start;    // row t sits at position start + t
     uint32_t heads, kv_heads, kvdim;
     float scale;
+    void* kv_pack = nullptr;       // MFMA kernel: packed K/V tiles, prefill_kv_pack_bytes(start + rows, ..)
+    size_t kv_pack_bytes = 0;
+    uint32_t kv_tiles = 0;         // set by launch_prefill_attn
 };
+// Bytes of the packed K/V tiles the MFMA attention kernel reads for `keys`
+// cache rows (0 for an unsupported head_dim).
+size_t prefill_kv_pack_bytes(uint32_t keys, uint32_t kv_heads, uint32_t hd);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s);
 // false (default): the MFMA flash-attention kernel; true: the f32 vector kernel.
 extern bool prefill_attn_vector;

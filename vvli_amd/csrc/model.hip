@@ -92,6 +92,8 @@ struct vvli_gpu_model {
     float* pf_ff = nullptr;     // [rows][I]
     float* pf_scale = nullptr;  // [rows] RMS scales
     float* pf_ahl = nullptr;    // GEMM activations split hi | lo (gemm_split_elems bf16)
+    void* pf_kvp = nullptr;     // packed K/V tiles of one layer for the attention kernel
+    size_t pf_kvp_bytes = 0;
 };
 
 namespace {
@@ -562,6 +564,18 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
                              "prefill buffers (%zu rows): %s", rows, hipGetErrorString(e));
         }
     }
+    const size_t kvp = prefill_kv_pack_bytes(static_cast<uint32_t>(m->max_seq), c.kv_heads, head_dim(c));
+    hipError_t e = hipMalloc(&m->pf_kvp, kvp);
+    if (e != hipSuccess) {
+        for (float** b : bufs) {
+            (void)hipFree(*b);
+            *b = nullptr;
+        }
+        m->pf_kvp = nullptr;
+        return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR,
+                         "prefill K/V tiles (%zu bytes): %s", kvp, hipGetErrorString(e));
+    }
+    m->pf_kvp_bytes = kvp;
     m->pf_rows = static_cast<uint32_t>(rows);
     return VVLI_OK;
 }
@@ -602,6 +616,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             LAUNCH(launch_prefill_rope_kv(ra, s));
             PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
                                1.0f / sqrtf(static_cast<float>(hd))};
+            aa.kv_pack = m->pf_kvp, aa.kv_pack_bytes = m->pf_kvp_bytes;
             LAUNCH(launch_prefill_attn(aa, hd, s));
             // x += attn . Wo^T
             GemmArgs go;
@@ -644,7 +659,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale, m->pf_ahl, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
+                    m->pf_scale, m->pf_ahl, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);

@@ -498,61 +498,146 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
 
 // ---------------------------------------------------------------------------
 // Causal GQA attention on MFMA (flash-attention form) for a chunk of prompt
-// rows. Block = (kv head, 64 query vectors); a query vector is one (row, q
-// head) pair of the G heads sharing the kv head, rows_per_block = 64 / G rows
-// (vectors past rows_per_block * G are idle). Wave w owns vectors 16w..16w+15.
-// Per 64-key tile of the cache: K and V rows are staged once in LDS as bf16
-// hi/lo halves (V transposed to [dim][key]), S = Q . K^T on MFMA as
-// qh.kh + qh.kl + ql.kh (f32 accumulate), scaled and masked causally, an
-// online softmax in f32 (row max and sum over 16-lane groups), P split hi/lo
-// through LDS into the A-operand layout, and O += P . V as ph.vh + ph.vl +
-// pl.vh. Each product keeps ~16 bits of both operands, like the f32 path it
-// replaces. v_mfma_f32_16x16x32_bf16 layout as the GEMM's.
+// rows.
+//
+// Packing (prefill_kv_pack_kernel): first, cache rows 0 .. start + rows - 1
+// of each kv head are split once into bf16 hi/lo halves and written as
+// per-tile images of the attention kernel's LDS stage,
+//   [K hi: TK keys x HD] [K lo] [V^T hi: HD dims x TK positions] [V^T lo],
+// TK = 64 keys (32 for head_dim 128). In every plane the 16-byte chunk c of
+// row r sits at chunk fa_swz(r, c), which puts the 8 rows an 8-lane group
+// reads with ds_read_b128 in distinct banks. V^T positions are permuted within
+// each 32-key group: position 8q + 4u + j holds key 16u + 4q + j (below).
+// Keys past the last cache row are zeros.
+//
+// Attention (prefill_fa_kernel): block = (kv head, 128 query vectors); a
+// query vector is one (row, q head) pair of the G heads sharing the kv head,
+// rows_per_block = 128 / G rows (vectors past rows_per_block * G are idle).
+// Wave w owns vectors 32w .. 32w + 31 as two groups of 16. Tile images are
+// copied whole into LDS by global_load_lds_dwordx4, two stages, tile i + 1
+// landing while tile i is used. Products are taken transposed so that the
+// softmax state of a vector stays in the lanes of one column:
+//   S^T  = K . Q^T   A = K rows (LDS), B = Q (registers); lane l gets
+//                    keys 16u + 4(l/16) + j of vector l%16
+//   O^T += V^T . P^T A = V^T rows (LDS), B = P: a lane's 8 values of a
+//                    32-key step, in (u, j) order, are its B fragment under
+//                    the permuted V^T positions, so P never leaves registers
+// Each product is hi.hi + lo.hi + hi.lo with f32 accumulation (about 2^-16
+// relative, like the f32 path it replaces). Online softmax per 32-key step in
+// f32: the row max over the lane's 8 values and two xor shuffles; the row sum
+// stays per lane until the end. v_mfma_f32_16x16x32_bf16 layout as the GEMM's.
 // ---------------------------------------------------------------------------
 constexpr int kFaThreads = 256;
-constexpr int kFaKeys = 64;            // keys per tile
-constexpr int kFaVecs = 64;            // query vectors per block
-constexpr int kFaVtRow = kFaKeys + 8;  // bf16 per transposed-V / P row (144 bytes)
+constexpr int kFaVecs = 128;  // query vectors per block
 
 template <int HD>
-struct FaLds {
-    static constexpr int KRow = HD + 8;  // bf16 per K row
-    uint16_t k_hi[kFaKeys * KRow], k_lo[kFaKeys * KRow];
-    uint16_t vt_hi[HD * kFaVtRow], vt_lo[HD * kFaVtRow];
-    uint16_t p_hi[4][16 * kFaVtRow], p_lo[4][16 * kFaVtRow];
+struct FaShape {
+    static constexpr int TK = HD == 128 ? 32 : 64;  // keys per tile
+    static constexpr int Plane = TK * HD * 2;       // bytes of one bf16 plane
+    static constexpr int Stage = 4 * Plane;         // K hi | K lo | V^T hi | V^T lo
+    static constexpr int DmaPerWave = Stage / 1024 / (kFaThreads / 64);
+    static_assert(Stage % (1024 * (kFaThreads / 64)) == 0, "whole 1 KiB copies per wave");
 };
+
+// Chunk position of 16-byte chunk c of row r in a plane of `chunks` chunks per row.
+__device__ __forceinline__ uint32_t fa_swz(uint32_t r, uint32_t c, uint32_t chunks) {
+    return chunks >= 8 ? c ^ (r & 7u) : c ^ ((r >> 1) & (chunks - 1u));
+}
+// Key (within the tile) held at V^T position p.
+__device__ __forceinline__ uint32_t fa_pos_key(uint32_t p) {
+    return (p & ~31u) | (((p >> 2) & 1u) << 4) | (((p >> 3) & 3u) << 2) | (p & 3u);
+}
 
 __device__ inline void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
     hi = to_bf16_rne(v);
     lo = to_bf16_rne(v - from_bf16(hi));
 }
 
+// One block per (key tile, kv head): K chunks straight to the K planes, the V
+// tile through LDS to the transposed planes.
 template <int HD>
-__global__ __launch_bounds__(kFaThreads) void prefill_fa_kernel(PrefillAttnArgs a) {
-    constexpr int DS = HD / 32;         // 32-dim MFMA steps for S
-    constexpr int NT = HD / 16;         // 16-dim output tiles for O
-    constexpr int TD = HD / 8;          // dims per staging thread
-    static_assert(HD % 32 == 0 && TD % 4 == 0, "head_dim 32, 64 or 128");
-    __shared__ __attribute__((aligned(16))) FaLds<HD> lds;
-    constexpr int KRow = FaLds<HD>::KRow;
+__global__ __launch_bounds__(256) void prefill_kv_pack_kernel(PrefillAttnArgs a) {
+    using S = FaShape<HD>;
+    constexpr int TK = S::TK, KCH = HD / 8, VCH = TK / 8;
+    __shared__ float vs[TK][HD + 1];
+    const uint32_t tile = blockIdx.x, h = blockIdx.y;
+    const uint32_t n_keys = a.start + a.rows;
+    char* img = static_cast<char*>(a.kv_pack) + (static_cast<size_t>(h) * a.kv_tiles + tile) * S::Stage;
+    for (int i = threadIdx.x; i < TK * KCH; i += 256) {
+        const uint32_t r = i / KCH, c = i % KCH, key = tile * TK + r;
+        float k[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (key < n_keys) {
+            const size_t off = static_cast<size_t>(key) * a.kvdim + h * HD + 8 * c;
+            const float4 k0 = *reinterpret_cast<const float4*>(a.kcache + off);
+            const float4 k1 = *reinterpret_cast<const float4*>(a.kcache + off + 4);
+            const float4 v0 = *reinterpret_cast<const float4*>(a.vcache + off);
+            const float4 v1 = *reinterpret_cast<const float4*>(a.vcache + off + 4);
+            k[0] = k0.x, k[1] = k0.y, k[2] = k0.z, k[3] = k0.w, k[4] = k1.x, k[5] = k1.y, k[6] = k1.z, k[7] = k1.w;
+            v[0] = v0.x, v[1] = v0.y, v[2] = v0.z, v[3] = v0.w, v[4] = v1.x, v[5] = v1.y, v[6] = v1.z, v[7] = v1.w;
+        }
+        u16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint16_t hh, ll;
+            split_bf16(k[e], hh, ll);
+            hi[e] = hh, lo[e] = ll;
+            vs[r][8 * c + e] = v[e];
+        }
+        const uint32_t o = r * (2 * HD) + fa_swz(r, c, KCH) * 16;
+        *reinterpret_cast<u16x8*>(img + o) = hi;
+        *reinterpret_cast<u16x8*>(img + S::Plane + o) = lo;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < HD * VCH; i += 256) {
+        const uint32_t d = i / VCH, c = i % VCH;
+        u16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint16_t hh, ll;
+            split_bf16(vs[fa_pos_key(8 * c + e)][d], hh, ll);
+            hi[e] = hh, lo[e] = ll;
+        }
+        const uint32_t o = d * (2 * TK) + fa_swz(d, c, VCH) * 16;
+        *reinterpret_cast<u16x8*>(img + 2 * S::Plane + o) = hi;
+        *reinterpret_cast<u16x8*>(img + 3 * S::Plane + o) = lo;
+    }
+}
+
+// Waits for a group of fragment reads (the fragments are operands, so their
+// uses cannot move above the wait).
+__device__ __forceinline__ void fa_lds_wait(bf16x8 (&f)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+}
+
+template <int HD>
+__global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fa_kernel(
+    PrefillAttnArgs a) {
+    using S = FaShape<HD>;
+    constexpr int TK = S::TK, DS = HD / 32, NT = HD / 16, SUB = TK / 32;
+    constexpr int KCH = HD / 8, VCH = TK / 8;
+    static_assert(HD % 32 == 0 && (DS + NT / 2) % 2 == 0, "head_dim 32, 64 or 128");
+    __shared__ __attribute__((aligned(1024))) char lds[2 * S::Stage];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 15, fq = lane >> 4;
     const uint32_t G = a.heads / a.kv_heads;
     const uint32_t rows_per_block = kFaVecs / G;
     const uint32_t row_groups = (a.rows + rows_per_block - 1) / rows_per_block;
     const uint32_t kvh = blockIdx.x % a.kv_heads;
     const uint32_t r0 = (row_groups - 1 - blockIdx.x / a.kv_heads) * rows_per_block;  // longest first
     const uint32_t last_row = min(r0 + rows_per_block, a.rows) - 1;
-    const uint32_t n_keys = a.start + last_row + 1;   // keys this block needs
-    const uint32_t key_limit = a.start + a.rows;      // cache rows written so far
+    const uint32_t n_tiles = (a.start + last_row + TK) / TK;  // keys 0 .. start + last_row
 
-    // Q operand (A layout): vector v = 16 wave + lane%16, dims 8(lane/16)+32 s ..
-    const int fr = lane & 15, fq = lane >> 4;
-    bf16x8 qh[DS], ql[DS];
-    {
-        const uint32_t v = wave * 16 + fr;
+    // Q as the B operand: group gi, lane l holds vector 32 wave + 16 gi + l%16,
+    // dims 32 s + 8 (l/16) .. +7, split hi/lo.
+    bf16x8 qh[2][DS], ql[2][DS];
+    uint32_t pos[2];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const uint32_t v = wave * 32 + gi * 16 + fr;
         const uint32_t t = v / G, g = v % G;
         const bool valid = t < rows_per_block && r0 + t < a.rows;
+        pos[gi] = a.start + min(r0 + min(t, rows_per_block - 1), a.rows - 1);
         const float* qp = a.q + static_cast<size_t>(valid ? r0 + t : 0) * a.ldq + (kvh * G + (valid ? g : 0)) * HD;
 #pragma unroll
         for (int s = 0; s < DS; ++s) {
@@ -564,161 +649,176 @@ __global__ __launch_bounds__(kFaThreads) void prefill_fa_kernel(PrefillAttnArgs 
             for (int e = 0; e < 8; ++e) {
                 uint16_t h, l;
                 split_bf16(x[e], h, l);
-                qh[s][e] = __builtin_bit_cast(__bf16, h);
-                ql[s][e] = __builtin_bit_cast(__bf16, l);
+                qh[gi][s][e] = __builtin_bit_cast(__bf16, h);
+                ql[gi][s][e] = __builtin_bit_cast(__bf16, l);
             }
         }
     }
-    // Positions of this lane's four S / O rows (C layout rows 4(lane/16)+j).
-    uint32_t pos_j[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t v = wave * 16 + 4 * fq + j;
-        const uint32_t t = min(v / G, rows_per_block - 1);
-        pos_j[j] = a.start + min(r0 + t, a.rows - 1);
-    }
+    // Last position among the wave's vectors: tiles that start past it are skipped.
+    const uint32_t t_last = min((static_cast<uint32_t>(wave) * 32u + 31u) / G, rows_per_block - 1);
+    const uint32_t pos_last = a.start + min(r0 + t_last, a.rows - 1);
 
-    f32x4 o[NT];
+    f32x4 o[2][NT];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_j[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, l_j[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) o[gi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
 
-    // Staging: thread -> key pair (2 kp, 2 kp + 1), dims TD (tid%8) .. +TD.
-    const int kp = tid >> 3, dc = (tid & 7) * TD;
-    const float* kbase = a.kcache + kvh * HD + dc;
-    const float* vbase = a.vcache + kvh * HD + dc;
-    float kreg[2][TD], vreg[2][TD];
-    auto load_tile = [&](uint32_t j0) {
+    // Copies: wave w moves bytes [w, w + 1) * DmaPerWave KiB of each tile image.
+    const char* src0 = static_cast<const char*>(a.kv_pack) + static_cast<size_t>(kvh) * a.kv_tiles * S::Stage +
+                       wave * S::DmaPerWave * 1024 + lane * 16;
+    char* dst0 = lds + wave * S::DmaPerWave * 1024;
+    auto issue = [&](uint32_t t, int st) {
+        const char* src = src0 + static_cast<size_t>(t) * S::Stage;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint32_t key = j0 + 2 * kp + r;
-            const bool in = key < key_limit;
-            const float* kr = kbase + static_cast<size_t>(in ? key : 0) * a.kvdim;
-            const float* vr = vbase + static_cast<size_t>(in ? key : 0) * a.kvdim;
-#pragma unroll
-            for (int d = 0; d < TD; d += 4) {
-                const float4 kv4 = in ? *reinterpret_cast<const float4*>(kr + d) : make_float4(0, 0, 0, 0);
-                const float4 vv4 = in ? *reinterpret_cast<const float4*>(vr + d) : make_float4(0, 0, 0, 0);
-                kreg[r][d] = kv4.x, kreg[r][d + 1] = kv4.y, kreg[r][d + 2] = kv4.z, kreg[r][d + 3] = kv4.w;
-                vreg[r][d] = vv4.x, vreg[r][d + 1] = vv4.y, vreg[r][d + 2] = vv4.z, vreg[r][d + 3] = vv4.w;
-            }
-        }
+        for (int i = 0; i < S::DmaPerWave; ++i) gemm_dma16(src + i * 1024, dst0 + st * S::Stage + i * 1024);
     };
-    auto store_tile = [&]() {
+    // Fragment offsets: K row 16u + l%16 of a 32-key step, chunk 4s + l/16;
+    // V^T row 16n + l%16, chunk 4ks + l/16 (both swizzled by the row).
+    const uint32_t lds0 = gemm_lds_addr(lds);
+    const uint32_t fk = KCH >= 8 ? (fr & 7) : ((fr >> 1) & 3);
+    const uint32_t fv = VCH >= 8 ? (fr & 7) : ((fr >> 1) & 3);
+    uint32_t koff[DS], voff[SUB];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int key = 2 * kp + r;
+    for (int s = 0; s < DS; ++s) koff[s] = fr * (2 * HD) + (((4 * s + fq) ^ fk) << 4);
 #pragma unroll
-            for (int d = 0; d < TD; d += 4) {  // TD = HD / 8 is a multiple of 4
-                u16x4 h, l;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    uint16_t hh, ll;
-                    split_bf16(kreg[r][d + e], hh, ll);
-                    h[e] = hh, l[e] = ll;
-                }
-                *reinterpret_cast<u16x4*>(&lds.k_hi[key * KRow + dc + d]) = h;
-                *reinterpret_cast<u16x4*>(&lds.k_lo[key * KRow + dc + d]) = l;
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < TD; ++d) {
-            uint16_t h0, l0, h1, l1;
-            split_bf16(vreg[0][d], h0, l0);
-            split_bf16(vreg[1][d], h1, l1);
-            *reinterpret_cast<uint32_t*>(&lds.vt_hi[(dc + d) * kFaVtRow + 2 * kp]) = h0 | (uint32_t(h1) << 16);
-            *reinterpret_cast<uint32_t*>(&lds.vt_lo[(dc + d) * kFaVtRow + 2 * kp]) = l0 | (uint32_t(l1) << 16);
-        }
+    for (int ks = 0; ks < SUB; ++ks) voff[ks] = 2 * S::Plane + fr * (2 * TK) + (((4 * ks + fq) ^ fv) << 4);
+    // Fragment groups: K of step ks, dims 32s.. = {hi, lo} x keys {0..15, 16..31};
+    // V^T of step ks, dims 32vg.. = {hi, lo} x dims {16(2vg).., 16(2vg+1)..}.
+    auto read_k = [&](bf16x8 (&f)[4], uint32_t sb, int ks, int s) {
+        const uint32_t b = sb + ks * 32 * (2 * HD) + koff[s];
+        f[0] = gemm_lds_read(b);
+        f[1] = gemm_lds_read(b + S::Plane);
+        f[2] = gemm_lds_read(b + 16 * (2 * HD));
+        f[3] = gemm_lds_read(b + 16 * (2 * HD) + S::Plane);
+    };
+    auto read_v = [&](bf16x8 (&f)[4], uint32_t sb, int ks, int vg) {
+        const uint32_t b = sb + voff[ks] + 2 * vg * 16 * (2 * TK);
+        f[0] = gemm_lds_read(b);
+        f[1] = gemm_lds_read(b + S::Plane);
+        f[2] = gemm_lds_read(b + 16 * (2 * TK));
+        f[3] = gemm_lds_read(b + 16 * (2 * TK) + S::Plane);
     };
 
-    const uint32_t n_tiles = (n_keys + kFaKeys - 1) / kFaKeys;
-    load_tile(0);
-    uint16_t* ph = lds.p_hi[wave];
-    uint16_t* pl = lds.p_lo[wave];
+    issue(0, 0);
     for (uint32_t it = 0; it < n_tiles; ++it) {
-        const uint32_t j0 = it * kFaKeys;
-        store_tile();
-        __syncthreads();
-        if (it + 1 < n_tiles) load_tile(j0 + kFaKeys);
-        // S = Q . K^T for 4 tiles of 16 keys.
-        f32x4 sacc[4];
+        const int st = it & 1;
+        gemm_wait_vm(0);  // this wave's copies of tile it
+        gemm_barrier();   // every wave's copies landed; stage st ^ 1 is no longer read
+        if (it + 1 < n_tiles) issue(it + 1, st ^ 1);
+        const uint32_t j0 = it * TK;
+        if (j0 > pos_last) continue;  // every key of the tile is masked for this wave
+        const uint32_t sb = lds0 + st * S::Stage;
+        bf16x8 f[2][4];
+        read_k(f[0], sb, 0, 0);
+        fa_lds_wait(f[0]);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const int krow = (kt * 16 + fr) * KRow;
+        for (int ks = 0; ks < SUB; ++ks) {
+            // S^T for 32 keys: group s holds dims 32s .. 32s + 31.
+            f32x4 sacc[2][2];
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) sacc[gi][0] = sacc[gi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < DS; ++s) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&lds.k_hi[krow + 32 * s + 8 * fq]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&lds.k_lo[krow + 32 * s + 8 * fq]);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[s], kh, sacc[kt], 0, 0, 0);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[s], kl, sacc[kt], 0, 0, 0);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[s], kh, sacc[kt], 0, 0, 0);
+                bf16x8(&cur)[4] = f[s & 1];
+                bf16x8(&nx)[4] = f[(s + 1) & 1];
+                if (s + 1 < DS) read_k(nx, sb, ks, s + 1);
+                else read_v(nx, sb, ks, 0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        sacc[gi][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * u], qh[gi][s], sacc[gi][u], 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        sacc[gi][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * u + 1], qh[gi][s], sacc[gi][u], 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        sacc[gi][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * u], ql[gi][s], sacc[gi][u], 0, 0, 0);
+                fa_lds_wait(nx);
+            }
+            // Scale, mask, online softmax; P as hi/lo B fragments.
+            bf16x8 ph[2], pl[2];
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t key = j0 + 32 * ks + 16 * u + 4 * fq + j;
+                        const float sv = key <= pos[gi] ? __fmul_rn(sacc[gi][u][j], a.scale) : -INFINITY;
+                        sacc[gi][u][j] = sv;
+                        mx = fmaxf(mx, sv);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m_run[gi], mx);  // finite: key 0 is in the first step
+                const float corr = expf(m_run[gi] - m_new);
+                float sum = 0.f;
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float p = expf(sacc[gi][u][j] - m_new);
+                        sum += p;
+                        uint16_t h, l;
+                        split_bf16(p, h, l);
+                        ph[gi][4 * u + j] = __builtin_bit_cast(__bf16, h);
+                        pl[gi][4 * u + j] = __builtin_bit_cast(__bf16, l);
+                    }
+                l_run[gi] = l_run[gi] * corr + sum;
+                m_run[gi] = m_new;
+#pragma unroll
+                for (int n = 0; n < NT; ++n) o[gi][n] *= corr;
+            }
+            // O^T += V^T . P^T, two 16-dim tiles per group.
+#pragma unroll
+            for (int vg = 0; vg < NT / 2; ++vg) {
+                bf16x8(&cur)[4] = f[(DS + vg) & 1];
+                bf16x8(&nx)[4] = f[(DS + vg + 1) & 1];
+                const bool more = vg + 1 < NT / 2 || ks + 1 < SUB;
+                if (vg + 1 < NT / 2) read_v(nx, sb, ks, vg + 1);
+                else if (ks + 1 < SUB) read_k(nx, sb, ks + 1, 0);
+#pragma unroll
+                for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        o[gi][2 * vg + nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * nn], ph[gi], o[gi][2 * vg + nn], 0, 0, 0);
+#pragma unroll
+                for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        o[gi][2 * vg + nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * nn + 1], ph[gi], o[gi][2 * vg + nn], 0, 0, 0);
+#pragma unroll
+                for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+                        o[gi][2 * vg + nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * nn], pl[gi], o[gi][2 * vg + nn], 0, 0, 0);
+                if (more) fa_lds_wait(nx);
             }
         }
-        // Scale, mask, online softmax per row (row j of this lane's group: 16 lanes).
-        float corr[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const uint32_t key = j0 + kt * 16 + fr;
-                const float sv = key <= pos_j[j] ? __fmul_rn(sacc[kt][j], a.scale) : -INFINITY;
-                sacc[kt][j] = sv;
-                mx = fmaxf(mx, sv);
-            }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float m_new = fmaxf(m_j[j], mx);
-            corr[j] = expf(m_j[j] - m_new);
-            float sum = 0.f;
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const float p = expf(sacc[kt][j] - m_new);
-                sum += p;
-                uint16_t h, l;
-                split_bf16(p, h, l);
-                const int idx = (4 * fq + j) * kFaVtRow + kt * 16 + fr;
-                ph[idx] = h;
-                pl[idx] = l;
-            }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
-            l_j[j] = l_j[j] * corr[j] + sum;
-            m_j[j] = m_new;
-        }
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[n][j] *= corr[j];
-        __syncthreads();  // P visible in the A layout
-        // O += P . V over two 32-key steps.
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 pah = *reinterpret_cast<const bf16x8*>(&ph[fr * kFaVtRow + 32 * ks + 8 * fq]);
-            const bf16x8 pal = *reinterpret_cast<const bf16x8*>(&pl[fr * kFaVtRow + 32 * ks + 8 * fq]);
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const int vrow = (n * 16 + fr) * kFaVtRow + 32 * ks + 8 * fq;
-                const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&lds.vt_hi[vrow]);
-                const bf16x8 vl = *reinterpret_cast<const bf16x8*>(&lds.vt_lo[vrow]);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pah, vh, o[n], 0, 0, 0);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pah, vl, o[n], 0, 0, 0);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pal, vh, o[n], 0, 0, 0);
-            }
-        }
-        __syncthreads();  // K/V/P tiles free for the next iteration
     }
-    // out[row][qh * HD + d] = O / l for valid vectors (C layout: rows 4(lane/16)+j, column lane%16).
+    // out[row][(kvh G + g) HD + d] = O / l: lane l holds dims 16n + 4(l/16) .. +3 of vector l%16.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t v = wave * 16 + 4 * fq + j;
+    for (int gi = 0; gi < 2; ++gi) {
+        float l = l_run[gi];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const uint32_t v = wave * 32 + gi * 16 + fr;
         const uint32_t t = v / G, g = v % G;
         if (t >= rows_per_block || r0 + t >= a.rows) continue;
-        float* op = a.out + static_cast<size_t>(r0 + t) * a.ldo + (kvh * G + g) * HD;
-        const float inv = 1.0f / l_j[j];
+        float* op = a.out + static_cast<size_t>(r0 + t) * a.ldo + (kvh * G + g) * HD + 4 * fq;
+        const float inv = 1.0f / l;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) op[n * 16 + fr] = o[n][j] * inv;
+        for (int n = 0; n < NT; ++n)
+            *reinterpret_cast<float4*>(op + 16 * n) =
+                make_float4(o[gi][n][0] * inv, o[gi][n][1] * inv, o[gi][n][2] * inv, o[gi][n][3] * inv);
     }
 }
 
@@ -754,6 +854,17 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     const uint32_t max_splits = std::min<uint32_t>(32, nk / 8 > 0 ? nk / 8 : 1);
     if (2 * tiles > cus) return 1;
     return std::max<uint32_t>(1, std::min<uint32_t>(max_splits, cus / tiles));
+}
+
+static uint32_t fa_tile_keys(uint32_t hd) { return hd == 128 ? FaShape<128>::TK : FaShape<64>::TK; }
+static_assert(FaShape<32>::Stage == 8 * 64 * 32 && FaShape<64>::Stage == 8 * 64 * 64 &&
+                  FaShape<128>::Stage == 8 * 32 * 128,
+              "prefill_kv_pack_bytes sizes tiles as 8 * keys * head_dim bytes");
+
+size_t prefill_kv_pack_bytes(uint32_t keys, uint32_t kv_heads, uint32_t hd) {
+    if (hd != 32 && hd != 64 && hd != 128) return 0;
+    const size_t tk = fa_tile_keys(hd);
+    return static_cast<size_t>(kv_heads) * ((keys + tk - 1) / tk) * (8 * tk * hd);
 }
 
 size_t gemm_split_elems(uint32_t M, uint32_t K) { return static_cast<size_t>(2) * M * gemm_kp(K); }
@@ -817,12 +928,24 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_
     if (!prefill_attn_vector) {
         const uint32_t G = a.heads / a.kv_heads;
         if (G == 0 || G > static_cast<uint32_t>(kFaVecs)) return hipErrorInvalidValue;
+        const uint32_t keys = a.start + a.rows;
+        const size_t need = prefill_kv_pack_bytes(keys, a.kv_heads, hd);
+        if (need == 0 || !a.kv_pack || a.kv_pack_bytes < need) return hipErrorInvalidValue;
+        PrefillAttnArgs b = a;
+        b.kv_tiles = (keys + fa_tile_keys(hd) - 1) / fa_tile_keys(hd);
         const uint32_t rows_per_block = kFaVecs / G;
-        const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block * a.kv_heads);
+        const dim3 pack(b.kv_tiles, a.kv_heads), grid((a.rows + rows_per_block - 1) / rows_per_block * a.kv_heads);
+        hipError_t e;
         switch (hd) {
-            case 32: return vlaunch(prefill_fa_kernel<32>, grid, dim3(kFaThreads), 0, s, a);
-            case 64: return vlaunch(prefill_fa_kernel<64>, grid, dim3(kFaThreads), 0, s, a);
-            case 128: return vlaunch(prefill_fa_kernel<128>, grid, dim3(kFaThreads), 0, s, a);
+            case 32:
+                e = vlaunch(prefill_kv_pack_kernel<32>, pack, dim3(256), 0, s, b);
+                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<32>, grid, dim3(kFaThreads), 0, s, b);
+            case 64:
+                e = vlaunch(prefill_kv_pack_kernel<64>, pack, dim3(256), 0, s, b);
+                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<64>, grid, dim3(kFaThreads), 0, s, b);
+            case 128:
+                e = vlaunch(prefill_kv_pack_kernel<128>, pack, dim3(256), 0, s, b);
+                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<128>, grid, dim3(kFaThreads), 0, s, b);
             default: return hipErrorInvalidValue;
         }
     }
