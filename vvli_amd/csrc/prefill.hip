@@ -50,8 +50,11 @@ typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 // Operands reach LDS by global_load_lds_dwordx4 (no registers in between):
 // 4 stages of [A hi 8 KiB | A lo 8 KiB | W 16 KiB], three K steps in flight.
 // An LDS row is 32 bf16 (64 bytes, four 16-byte chunks); chunk c of row r is
-// stored at position c ^ swz(r), which puts the 16 rows a 16-lane group reads
-// (and the 8 rows of an 8-lane group) in distinct bank groups. MFMA fragments
+// stored at position c ^ swz(r). ds_read_b128 serves a wave in four passes of
+// 16 lanes (lanes 0-7 with 24-31, 8-15 with 16-23, the same in the upper
+// half) over 64 four-byte banks; with swz(r) = (r >> 1) & 3 the 16 fragment
+// rows of each pass fall on 16 distinct 16-byte bank groups (no conflict
+// cycles in SQ_LDS_BANK_CONFLICT). MFMA fragments
 // are read with ds_read_b128 in inline asm and waited for explicitly, so the
 // compiler does not tie them to the copies in flight.
 // ---------------------------------------------------------------------------
@@ -91,7 +94,7 @@ __device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-__device__ __forceinline__ uint32_t gemm_swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
+__device__ __forceinline__ uint32_t gemm_swz(uint32_t r) { return (r >> 1) & 3u; }
 
 __device__ __forceinline__ void gemm_dma16(const void* src, char* dst) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
@@ -103,7 +106,8 @@ __device__ __forceinline__ void gemm_barrier() { __builtin_amdgcn_s_barrier(); }
 // or 8: whole stages of kDmaPerWave copies).
 __device__ __forceinline__ void gemm_wait_vm(int n) {
     constexpr int kKeep = (7 << 4) | (15 << 8);  // expcnt, lgkmcnt: no wait
-    if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | kKeep);
+    if (n >= 12) __builtin_amdgcn_s_waitcnt(12 | kKeep);
+    else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | kKeep);
     else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | kKeep);
     else __builtin_amdgcn_s_waitcnt(0 | kKeep);
 }
@@ -218,14 +222,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
             src[i] = gemm_w_row<MODE>(g, n0, static_cast<int>(row), valid);
         }
     }
+    auto issue_one = [&](int kt, int stage, int i) {
+        const uint32_t k = (kt0 + kt) * kBK + chunk[i];
+        const uint16_t* p = (is_w[i] && k >= g.K) ? zeros : src[i] + k;
+        gemm_dma16(p, gemm_smem + stage * kStageBytes + (wave * kDmaPerWave + i) * 1024);
+    };
     auto issue = [&](int kt, int stage) {
-        const uint32_t k0 = (kt0 + kt) * kBK;
 #pragma unroll
-        for (int i = 0; i < kDmaPerWave; ++i) {
-            const uint32_t k = k0 + chunk[i];
-            const uint16_t* p = (is_w[i] && k >= g.K) ? zeros : src[i] + k;
-            gemm_dma16(p, gemm_smem + stage * kStageBytes + (wave * kDmaPerWave + i) * 1024);
-        }
+        for (int i = 0; i < kDmaPerWave; ++i) issue_one(kt, stage, i);
     };
     // Fragment addresses within a stage.
     const uint32_t lds0 = gemm_lds_addr(gemm_smem);
@@ -247,18 +251,6 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
             w[i] = gemm_lds_read(fb[i] + so);
         }
     };
-    // All hi products, then all lo products: 16 independent accumulators
-    // between the two MFMAs that update one of them.
-    auto mfmas = [&](const bf16x8 (&a)[4], const bf16x8 (&l)[4], const bf16x8 (&w)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], w[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l[i], w[j], acc[i][j], 0, 0, 0);
-    };
     // Prologue: stages 0 .. kStages-2 in flight, step 0's fragments read.
     for (int s0 = 0; s0 < kStages - 1; ++s0)
         if (s0 < nk) issue(s0, s0);
@@ -269,13 +261,34 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
     // Step kt: once stage kt+1 is in LDS for every wave (and every wave has
     // read stage kt-1's fragments), refill stage kt-1 with step kt+3, read
     // step kt+1's fragments and multiply step kt's.
+    // The copies and fragment reads are spread between four groups of 8 MFMAs
+    // (hi products of A rows 0-31, 32-63, then the lo products) so that every
+    // wave keeps the MFMA pipe fed while it issues them; sched_barrier keeps
+    // the compiler from regrouping them.
     auto step = [&](int kt, int cur) {
         if (kt + 1 < nk) gemm_wait_vm(min(kStages - 3, nk - 2 - kt) * kDmaPerWave);
         gemm_barrier();
-        if (kt + kStages - 1 < nk) issue(kt + kStages - 1, (kt + kStages - 1) % kStages);
-        if (kt + 1 < nk) read_frags(kt + 1, fh[cur ^ 1], fl[cur ^ 1], fw[cur ^ 1]);
-        mfmas(fh[cur], fl[cur], fw[cur]);
-        if (kt + 1 < nk) gemm_lds_wait(fh[cur ^ 1], fl[cur ^ 1], fw[cur ^ 1]);
+        const bool more = kt + kStages - 1 < nk, next = kt + 1 < nk;
+        const int kn = kt + kStages - 1;
+        const uint32_t so = static_cast<uint32_t>((kt + 1) % kStages) * kStageBytes;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int i = (q & 1) * 2; i < (q & 1) * 2 + 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q < 2 ? fh[cur][i] : fl[cur][i], fw[cur][j],
+                                                                        acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) issue_one(kn, kn % kStages, q);
+            if (next) {
+                fh[cur ^ 1][q] = gemm_lds_read(fa[q] + so);
+                fl[cur ^ 1][q] = gemm_lds_read(fa[q] + so + kOpA);
+                fw[cur ^ 1][q] = gemm_lds_read(fb[q] + so);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (next) gemm_lds_wait(fh[cur ^ 1], fl[cur ^ 1], fw[cur ^ 1]);
     };
     for (int kt = 0; kt < nk; kt += 2) {
         step(kt, 0);
@@ -505,8 +518,10 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
 // per-tile images of the attention kernel's LDS stage,
 //   [K hi: TK keys x HD] [K lo] [V^T hi: HD dims x TK positions] [V^T lo],
 // TK = 64 keys (32 for head_dim 128). In every plane the 16-byte chunk c of
-// row r sits at chunk fa_swz(r, c), which puts the 8 rows an 8-lane group
-// reads with ds_read_b128 in distinct banks. V^T positions are permuted within
+// row r sits at chunk fa_swz(r, c), which keeps the fragment reads free of
+// bank conflicts under ds_read_b128's passes (see the GEMM tile notes): the
+// 16 lanes of a pass read 16 rows, two chunk columns, and land on 16 distinct
+// 16-byte bank groups for rows of 64, 128 and 256 bytes. V^T positions are permuted within
 // each 32-key group: position 8q + 4u + j holds key 16u + 4q + j (below).
 // Keys past the last cache row are zeros.
 //
@@ -541,7 +556,7 @@ struct FaShape {
 
 // Chunk position of 16-byte chunk c of row r in a plane of `chunks` chunks per row.
 __device__ __forceinline__ uint32_t fa_swz(uint32_t r, uint32_t c, uint32_t chunks) {
-    return chunks >= 8 ? c ^ (r & 7u) : c ^ ((r >> 1) & (chunks - 1u));
+    return chunks >= 16 ? c ^ (r & 15u) : chunks == 8 ? c ^ (r & 7u) : c ^ ((r >> 1) & (chunks - 1u));
 }
 // Key (within the tile) held at V^T position p.
 __device__ __forceinline__ uint32_t fa_pos_key(uint32_t p) {
@@ -677,8 +692,9 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
     // Fragment offsets: K row 16u + l%16 of a 32-key step, chunk 4s + l/16;
     // V^T row 16n + l%16, chunk 4ks + l/16 (both swizzled by the row).
     const uint32_t lds0 = gemm_lds_addr(lds);
-    const uint32_t fk = KCH >= 8 ? (fr & 7) : ((fr >> 1) & 3);
-    const uint32_t fv = VCH >= 8 ? (fr & 7) : ((fr >> 1) & 3);
+    static_assert(KCH <= 16 && VCH <= 16, "rows of at most 256 bytes");
+    const uint32_t fk = KCH == 16 ? fr : KCH == 8 ? (fr & 7) : ((fr >> 1) & 3);  // fa_swz of rows 16u + fr
+    const uint32_t fv = VCH == 16 ? fr : VCH == 8 ? (fr & 7) : ((fr >> 1) & 3);
     uint32_t koff[DS], voff[SUB];
 #pragma unroll
     for (int s = 0; s < DS; ++s) koff[s] = fr * (2 * HD) + (((4 * s + fq) ^ fk) << 4);
