@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -644,7 +645,9 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
     const uint32_t n_tiles = (a.start + last_row + TK) / TK;  // keys 0 .. start + last_row
 
     // Q as the B operand: group gi, lane l holds vector 32 wave + 16 gi + l%16,
-    // dims 32 s + 8 (l/16) .. +7, split hi/lo.
+    // dims 32 s + 8 (l/16) .. +7, scaled by scale * log2(e) (scores come out in
+    // base-2 units for v_exp_f32) and split hi/lo.
+    const float qscale = a.scale * 1.44269504088896341f;
     bf16x8 qh[2][DS], ql[2][DS];
     uint32_t pos[2];
 #pragma unroll
@@ -662,15 +665,18 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
             x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                uint16_t h, l;
-                split_bf16(x[e], h, l);
-                qh[gi][s][e] = __builtin_bit_cast(__bf16, h);
-                ql[gi][s][e] = __builtin_bit_cast(__bf16, l);
+                const float xs = __fmul_rn(x[e], qscale);
+                const __bf16 hb = static_cast<__bf16>(xs);  // v_cvt_pk_bf16_f32: round to nearest even
+                qh[gi][s][e] = hb;
+                ql[gi][s][e] = static_cast<__bf16>(xs - static_cast<float>(hb));
             }
         }
     }
-    // Last position among the wave's vectors: tiles that start past it are skipped.
+    // First and last positions among the wave's vectors: tiles that start past
+    // the last are skipped, tiles that end at or before the first need no mask.
+    const uint32_t t_first = min((static_cast<uint32_t>(wave) * 32u) / G, rows_per_block - 1);
     const uint32_t t_last = min((static_cast<uint32_t>(wave) * 32u + 31u) / G, rows_per_block - 1);
+    const uint32_t pos_first = a.start + min(r0 + t_first, a.rows - 1);
     const uint32_t pos_last = a.start + min(r0 + t_last, a.rows - 1);
 
     f32x4 o[2][NT];
@@ -717,15 +723,10 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
         f[3] = gemm_lds_read(b + 16 * (2 * TK) + S::Plane);
     };
 
-    issue(0, 0);
-    for (uint32_t it = 0; it < n_tiles; ++it) {
-        const int st = it & 1;
-        gemm_wait_vm(0);  // this wave's copies of tile it
-        gemm_barrier();   // every wave's copies landed; stage st ^ 1 is no longer read
-        if (it + 1 < n_tiles) issue(it + 1, st ^ 1);
-        const uint32_t j0 = it * TK;
-        if (j0 > pos_last) continue;  // every key of the tile is masked for this wave
-        const uint32_t sb = lds0 + st * S::Stage;
+    // One tile from LDS stage sb (keys j0 ..): MASKED compares every key with
+    // its vector's position, else the whole tile is visible to the wave.
+    auto tile = [&](uint32_t sb, uint32_t j0, auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
         bf16x8 f[2][4];
         read_k(f[0], sb, 0, 0);
         fa_lds_wait(f[0]);
@@ -758,8 +759,10 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
                         sacc[gi][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * u], ql[gi][s], sacc[gi][u], 0, 0, 0);
                 fa_lds_wait(nx);
             }
-            // Scale, mask, online softmax; P as hi/lo B fragments.
+            // Mask, online softmax in base 2 (v_exp_f32); P as hi/lo B fragments.
             bf16x8 ph[2], pl[2];
+            float corr[2];
+            bool grew = false;
 #pragma unroll
             for (int gi = 0; gi < 2; ++gi) {
                 float mx = -INFINITY;
@@ -767,31 +770,33 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t key = j0 + 32 * ks + 16 * u + 4 * fq + j;
-                        const float sv = key <= pos[gi] ? __fmul_rn(sacc[gi][u][j], a.scale) : -INFINITY;
-                        sacc[gi][u][j] = sv;
-                        mx = fmaxf(mx, sv);
+                        if (MASKED && j0 + 32 * ks + 16 * u + 4 * fq + j > pos[gi]) sacc[gi][u][j] = -INFINITY;
+                        mx = fmaxf(mx, sacc[gi][u][j]);
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                 const float m_new = fmaxf(m_run[gi], mx);  // finite: key 0 is in the first step
-                const float corr = expf(m_run[gi] - m_new);
+                grew |= m_new != m_run[gi];
+                corr[gi] = __builtin_amdgcn_exp2f(m_run[gi] - m_new);
                 float sum = 0.f;
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const float p = expf(sacc[gi][u][j] - m_new);
+                        const float p = __builtin_amdgcn_exp2f(sacc[gi][u][j] - m_new);
                         sum += p;
-                        uint16_t h, l;
-                        split_bf16(p, h, l);
-                        ph[gi][4 * u + j] = __builtin_bit_cast(__bf16, h);
-                        pl[gi][4 * u + j] = __builtin_bit_cast(__bf16, l);
+                        const __bf16 hb = static_cast<__bf16>(p);
+                        ph[gi][4 * u + j] = hb;
+                        pl[gi][4 * u + j] = static_cast<__bf16>(p - static_cast<float>(hb));
                     }
-                l_run[gi] = l_run[gi] * corr + sum;
+                l_run[gi] = l_run[gi] * corr[gi] + sum;
                 m_run[gi] = m_new;
+            }
+            if (__any(grew)) {  // corr is 1 wherever no row max grew
 #pragma unroll
-                for (int n = 0; n < NT; ++n) o[gi][n] *= corr;
+                for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+                    for (int n = 0; n < NT; ++n) o[gi][n] *= corr[gi];
             }
             // O^T += V^T . P^T, two 16-dim tiles per group.
 #pragma unroll
@@ -819,6 +824,19 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
                 if (more) fa_lds_wait(nx);
             }
         }
+    };
+
+    issue(0, 0);
+    for (uint32_t it = 0; it < n_tiles; ++it) {
+        const int st = it & 1;
+        gemm_wait_vm(0);  // this wave's copies of tile it
+        gemm_barrier();   // every wave's copies landed; stage st ^ 1 is no longer read
+        if (it + 1 < n_tiles) issue(it + 1, st ^ 1);
+        const uint32_t j0 = it * TK;
+        if (j0 > pos_last) continue;  // every key of the tile is masked for this wave
+        const uint32_t sb = lds0 + st * S::Stage;
+        if (j0 + TK - 1 <= pos_first) tile(sb, j0, std::false_type{});
+        else tile(sb, j0, std::true_type{});
     }
     // out[row][(kvh G + g) HD + d] = O / l: lane l holds dims 16n + 4(l/16) .. +3 of vector l%16.
 #pragma unroll
