@@ -110,6 +110,25 @@ __device__ __forceinline__ bool poll_tw(const tword* p, uint32_t tag, tword& w, 
     return true;
 }
 
+// Wait until both words carry `tag`: a retry reloads both (a word that is
+// there stays there until its reader is done), so the pair costs one memory
+// round trip after its later word lands.
+__device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint32_t tag, tword& w0, tword& w1,
+                                         uint32_t* err) {
+    uint32_t spins = 0;
+    while (tw_tag(w0) != tag || tw_tag(w1) != tag) {
+        if (++spins > kSpinLimit) {
+            st_a(err, 1u);
+            return false;
+        }
+        if ((spins & 63u) == 0 && ld_a(err) != 0) return false;
+        __builtin_amdgcn_s_sleep(1);
+        w0 = ld_a(p0);
+        w1 = ld_a(p1);
+    }
+    return true;
+}
+
 // Detail timing mark (16-slot timing only): slot 0 the block's staged input,
 // 1 + w wave w's end of the phase.
 __device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
@@ -544,11 +563,34 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
                 ld_coh_tw2(r, i * 16, a[k], b[k]);
                 nv[k] = (norm_w && i < n2) ? *as_global(reinterpret_cast<const uint32_t*>(norm_w + 2 * i)) : 0u;
             }
+            // The batch is polled as a whole: a retry reloads every pair that
+            // is not complete, so it ends one round trip after its last word
+            // lands (word-by-word polls would add a round trip per late word).
+            for (uint32_t spins = 0;; ) {
+                bool done = true;
+#pragma unroll
+                for (int k = 0; k < B; ++k)
+                    if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
+                if (done) break;
+                if (++spins > kSpinLimit) {
+                    st_a(err, 1u);
+                    ok = false;
+                    break;
+                }
+                if ((spins & 63u) == 0 && ld_a(err) != 0) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                // Every pair is reloaded (a complete word stays as it is until
+                // its reader is done; pairs past n read as zeros).
+#pragma unroll
+                for (int k = 0; k < B; ++k) ld_coh_tw2(r, (i0 + k * kMkThreads) * 16, a[k], b[k]);
+            }
 #pragma unroll
             for (int k = 0; k < B; ++k) {
                 const uint32_t i = i0 + k * kMkThreads;
                 if (i < n2) {
-                    ok = ok && poll_tw(src + 2 * i, tag, a[k], err) && poll_tw(src + 2 * i + 1, tag, b[k], err);
                     const float v0 = tw_val(a[k]), v1 = tw_val(b[k]);
                     *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(v0, v1);
                     if (norm_w)
@@ -685,29 +727,33 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const int f = inter ? 2 * i : i, sc = inter ? 2 * i + 1 : i + half;
             const tword* src = q + (size_t)(h * G + g) * hd;
             tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
-            ok = ok && poll_tw(src + f, tag_in, w0, p.error) && poll_tw(src + sc, tag_in, w1, p.error);
+            ok = ok && poll_tw2(src + f, src + sc, tag_in, w0, w1, p.error);
             const float x0 = tw_val(w0), x1 = tw_val(w1);
             const float c = cs[2 * i], sn = cs[2 * i + 1];
             qs[g * HDMAX + f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
             qs[g * HDMAX + sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
         }
-        if (owns) {
-            for (int i = tid; i < half; i += kMkThreads) {
-                const int f = inter ? 2 * i : i, sc = inter ? 2 * i + 1 : i + half;
-                const tword* src = kn_all + (size_t)h * hd;
-                tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
-                ok = ok && poll_tw(src + f, tag_in, w0, p.error) && poll_tw(src + sc, tag_in, w1, p.error);
+        if (owns) {  // the new k pair and v word of thread tid (hd <= kMkThreads), loaded together
+            static_assert(HDMAX <= kMkThreads, "one k pair and one v word per thread");
+            const tword* ksrc = kn_all + (size_t)h * hd;
+            const tword* vsrc = vn_all + (size_t)h * hd + tid;
+            const bool hk = tid < half, hv = tid < hd;
+            const int f = inter ? 2 * tid : tid, sc = inter ? 2 * tid + 1 : tid + half;
+            tword w0 = 0, w1 = 0, wv = 0;
+            if (hk) {
+                w0 = ld_a(ksrc + f);
+                w1 = ld_a(ksrc + sc);
+            }
+            if (hv) wv = ld_a(vsrc);
+            if (hk) ok = ok && poll_tw2(ksrc + f, ksrc + sc, tag_in, w0, w1, p.error);
+            if (hv) ok = ok && poll_tw(vsrc, tag_in, wv, p.error);
+            if (hk) {
                 const float x0 = tw_val(w0), x1 = tw_val(w1);
-                const float c = cs[2 * i], sn = cs[2 * i + 1];
+                const float c = cs[2 * tid], sn = cs[2 * tid + 1];
                 knew[f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
                 knew[sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
             }
-            for (int d = tid; d < hd; d += kMkThreads) {
-                const tword* src = vn_all + (size_t)h * hd + d;
-                tword wv = ld_a(src);
-                ok = ok && poll_tw(src, tag_in, wv, p.error);
-                vnew[d] = tw_val(wv);
-            }
+            if (hv) vnew[tid] = tw_val(wv);
         }
         if (tid < kMaxGroupMk) {
             m_s[tid] = -INFINITY;
@@ -1104,8 +1150,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             bool ok = true;
             for (uint32_t i = tid; i < w.nw; i += kMkThreads) {
                 tword hi = ld_a(p.tkeys + 2 * i), lo = ld_a(p.tkeys + 2 * i + 1);
-                ok = ok && poll_tw(p.tkeys + 2 * i, ktag, hi, p.error) &&
-                     poll_tw(p.tkeys + 2 * i + 1, ktag, lo, p.error);
+                ok = ok && poll_tw2(p.tkeys + 2 * i, p.tkeys + 2 * i + 1, ktag, hi, lo, p.error);
                 const unsigned long long k = ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
                 b = k > b ? k : b;
             }
