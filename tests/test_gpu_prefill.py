@@ -46,6 +46,10 @@ CASES = {
     "qwen05_heads": (cfg_small(vocab_size=2000, hidden_size=896, intermediate_size=4864, num_attention_heads=14,
                                num_key_value_heads=2), "synth", [150]),
     "hd32_g1": (cfg_small(hidden_size=128, num_attention_heads=4, num_key_value_heads=4), "synth", [65]),
+    # 1100 rows: ragged GEMM tiles in rows, gate/up columns (2 x 704) and K (704 for down), split K on
+    # o_proj / down, 18 row groups of the attention.
+    "big_tiles": (cfg_small(hidden_size=512, intermediate_size=704, num_attention_heads=8, num_key_value_heads=2,
+                            vocab_size=500), "synth", [1100]),
     # More rows than one chunk (2048): two passes, the second attending to the first's cache rows.
     "two_chunks": (cfg_small(hidden_size=128, intermediate_size=256, num_attention_heads=2, num_key_value_heads=1,
                              vocab_size=300), "synth", [2100]),
