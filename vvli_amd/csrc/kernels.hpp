@@ -232,9 +232,19 @@ struct GemmArgs {
     uint32_t M = 0, N = 0, K = 0;      // K % 8 == 0
     // Device scratch of gemm_split_elems(M, K) bf16: the launcher splits A
     // (normalised when norm_w is set) into hi | lo planes there before the
-    // GEMM reads it.
+    // GEMM reads it -- unless a_ready: a producer already wrote the planes.
+    // Rows are gemm_kp(K) elements with a zero tail; a_plane elements lie
+    // between the hi and the lo plane (0: M * gemm_kp(K)).
     uint16_t* a_hl = nullptr;
+    bool a_ready = false;
+    size_t a_plane = 0;
+    // GateUp only: write silu(gate) * up as split planes for the next GEMM
+    // (rows of gemm_kp(N) with a zero tail, out_plane elements apart) instead
+    // of f32 rows in out.
+    uint16_t* out_hl = nullptr;
+    size_t out_plane = 0;
 };
+__host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + 31) / 32 * 32; }
 size_t gemm_split_elems(uint32_t M, uint32_t K);
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s);
 
@@ -265,6 +275,10 @@ struct PrefillAttnArgs {
     void* kv_pack = nullptr;       // MFMA kernel: packed K/V tiles, prefill_kv_pack_bytes(start + rows, ..)
     size_t kv_pack_bytes = 0;
     uint32_t kv_tiles = 0;         // set by launch_prefill_attn
+    // MFMA kernel: write the output as GEMM split planes (rows of
+    // gemm_kp(heads * head_dim), out_plane elements apart) instead of out.
+    uint16_t* out_hl = nullptr;
+    size_t out_plane = 0;
 };
 // Bytes of the packed K/V tiles the MFMA attention kernel reads for `keys`
 // cache rows (0 for an unsupported head_dim).

@@ -89,9 +89,9 @@ struct vvli_gpu_model {
     float* pf_x = nullptr;      // [rows][H] residual stream
     float* pf_qkv = nullptr;    // [rows][H + 2 kv]
     float* pf_attn = nullptr;   // [rows][H]
-    float* pf_ff = nullptr;     // [rows][I]
     float* pf_scale = nullptr;  // [rows] RMS scales
     float* pf_ahl = nullptr;    // GEMM activations split hi | lo (gemm_split_elems bf16)
+    float* pf_ahl2 = nullptr;   // split planes written by attention (o_proj's A) and SwiGLU (down's A)
     void* pf_kvp = nullptr;     // packed K/V tiles of one layer for the attention kernel
     size_t pf_kvp_bytes = 0;
 };
@@ -550,9 +550,9 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
     const vvli_gpu_config& c = m->cfg;
     const size_t rows = std::min(m->max_seq, kPrefillChunk);
     const size_t H = c.hidden, kv = kv_dim(c), I = c.inter;
-    float** bufs[] = {&m->pf_x, &m->pf_qkv, &m->pf_attn, &m->pf_ff, &m->pf_scale, &m->pf_ahl};
-    const size_t sizes[] = {rows * H, rows * (H + 2 * kv), rows * H, rows * I, rows,
-                            (gemm_split_elems(static_cast<uint32_t>(rows), static_cast<uint32_t>(std::max(H, I))) + 1) / 2};
+    float** bufs[] = {&m->pf_x, &m->pf_qkv, &m->pf_attn, &m->pf_scale, &m->pf_ahl, &m->pf_ahl2};
+    const size_t split = (gemm_split_elems(static_cast<uint32_t>(rows), static_cast<uint32_t>(std::max(H, I))) + 1) / 2;
+    const size_t sizes[] = {rows * H, rows * (H + 2 * kv), rows * H, rows, split, split};
     for (int i = 0; i < 6; ++i) {
         hipError_t e = hipMalloc(reinterpret_cast<void**>(bufs[i]), sizes[i] * sizeof(float));
         if (e != hipSuccess) {
@@ -617,13 +617,17 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
                                1.0f / sqrtf(static_cast<float>(hd))};
             aa.kv_pack = m->pf_kvp, aa.kv_pack_bytes = m->pf_kvp_bytes;
+            // The MFMA attention writes o_proj's split planes itself (heads * hd = H, a multiple of 32).
+            const bool fused_o = !prefill_attn_vector;
+            if (fused_o) aa.out_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2), aa.out_plane = m->pf_rows * gemm_kp(H);
             LAUNCH(launch_prefill_attn(aa, hd, s));
             // x += attn . Wo^T
             GemmArgs go;
             go.a = m->pf_attn, go.lda = H, go.w[0] = w16(L.o);
             go.seg_end[0] = go.seg_end[1] = go.seg_end[2] = H;
             go.out = m->pf_x, go.ldo = H, go.M = P, go.N = H, go.K = H;
-            go.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
+            go.a_hl = reinterpret_cast<uint16_t*>(fused_o ? m->pf_ahl2 : m->pf_ahl);
+            if (fused_o) go.a_ready = true, go.a_plane = m->pf_rows * gemm_kp(H);
             LAUNCH(launch_gemm_bf16(kGemmResid, go, s));
             // post-attention RMSNorm fused into gate/up + SwiGLU
             LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
@@ -631,15 +635,18 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(L.post_norm);
             gu.w[0] = w16(L.gate), gu.w_up = w16(L.up);
             gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
-            gu.out = m->pf_ff, gu.ldo = I, gu.M = P, gu.N = I, gu.K = H;
+            gu.M = P, gu.N = I, gu.K = H;
             gu.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
+            // SwiGLU written as the down GEMM's split planes.
+            gu.out_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2), gu.out_plane = m->pf_rows * gemm_kp(I);
             LAUNCH(launch_gemm_bf16(kGemmGateUp, gu, s));
             // x += ff . Wd^T
             GemmArgs gd;
-            gd.a = m->pf_ff, gd.lda = I, gd.w[0] = w16(L.down);
+            gd.w[0] = w16(L.down);
             gd.seg_end[0] = gd.seg_end[1] = gd.seg_end[2] = H;
             gd.out = m->pf_x, gd.ldo = H, gd.M = P, gd.N = H, gd.K = I;
-            gd.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
+            gd.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2);
+            gd.a_ready = true, gd.a_plane = m->pf_rows * gemm_kp(I);
             LAUNCH(launch_gemm_bf16(kGemmResid, gd, s));
         }
         if (c0 + P == n)
@@ -658,8 +665,8 @@ void free_model(vvli_gpu_model* m) {
     if (m->graph_sample) (void)hipGraphExecDestroy(m->graph_sample);
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
-                    m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn, m->pf_ff,
-                    m->pf_scale, m->pf_ahl, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
+                    m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
+                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);

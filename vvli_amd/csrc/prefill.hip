@@ -72,9 +72,9 @@ __device__ inline uint16_t to_bf16_rne(float v) {
 }
 __device__ inline float from_bf16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// Row stride of the split A planes: K rounded up to whole K steps, the tail
-// zero-filled by gemm_split_kernel.
-__host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + kBK - 1) / kBK * kBK; }
+// Row stride of the split A planes (gemm_kp, kernels.hpp): K rounded up to
+// whole K steps, the tail zero-filled by gemm_split_kernel.
+static_assert(kBK == 32, "gemm_kp rounds to 32");
 
 // Row of W feeding B-tile row r of block column n0 (GateUp interleaves gate and
 // up rows in groups of 16 so one lane holds both halves of an output).
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs g) {
     }
     uint16_t* out = g.a_hl + static_cast<size_t>(m) * kp + k;
     *reinterpret_cast<u16x8*>(out) = hi;
-    *reinterpret_cast<u16x8*>(out + static_cast<size_t>(g.M) * kp) = lo;
+    *reinterpret_cast<u16x8*>(out + (g.a_plane ? g.a_plane : static_cast<size_t>(g.M) * kp)) = lo;
 }
 
 __device__ inline float silu_mul(float gv, float uv) {
@@ -217,7 +217,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
         is_w[i] = q >= 16;
         if (q < 16) {
             const uint32_t gm = m0 + row < g.M ? m0 + row : 0;
-            src[i] = g.a_hl + (q >= 8 ? static_cast<size_t>(g.M) * kp : 0) + static_cast<size_t>(gm) * kp;
+            const size_t plane = g.a_plane ? g.a_plane : static_cast<size_t>(g.M) * kp;
+            src[i] = g.a_hl + (q >= 8 ? plane : 0) + static_cast<size_t>(gm) * kp;
         } else {
             bool valid;
             src[i] = gemm_w_row<MODE>(g, n0, static_cast<int>(row), valid);
@@ -310,7 +311,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
                 for (int j = 0; j < 4; j += 2) {
                     const uint32_t n = n0 / 2 + (wn * 2 + j / 2) * 16 + fr;
-                    if (n < g.N) orow[n] = silu_mul(acc[i][j][jr], acc[i][j + 1][jr]);
+                    if (g.out_hl) {  // split planes of the next GEMM's A, zeros in the tail
+                        const uint32_t kpo = gemm_kp(g.N);
+                        if (n < kpo) {
+                            const float v = n < g.N ? silu_mul(acc[i][j][jr], acc[i][j + 1][jr]) : 0.f;
+                            const uint16_t h = to_bf16_rne(v);
+                            uint16_t* o = g.out_hl + static_cast<size_t>(row) * kpo + n;
+                            o[0] = h;
+                            o[g.out_plane] = to_bf16_rne(v - from_bf16(h));
+                        }
+                    } else if (n < g.N) {
+                        orow[n] = silu_mul(acc[i][j][jr], acc[i][j + 1][jr]);
+                    }
                 }
             } else {
 #pragma unroll
@@ -847,8 +859,24 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
         const uint32_t v = wave * 32 + gi * 16 + fr;
         const uint32_t t = v / G, g = v % G;
         if (t >= rows_per_block || r0 + t >= a.rows) continue;
-        float* op = a.out + static_cast<size_t>(r0 + t) * a.ldo + (kvh * G + g) * HD + 4 * fq;
         const float inv = 1.0f / l;
+        if (a.out_hl) {  // split planes of the o_proj GEMM's A (heads * HD is a multiple of 32: no tail)
+            uint16_t* hp = a.out_hl + static_cast<size_t>(r0 + t) * (a.heads * HD) + (kvh * G + g) * HD + 4 * fq;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                u16x4 h, lo;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint16_t hh, ll;
+                    split_bf16(o[gi][n][e] * inv, hh, ll);
+                    h[e] = hh, lo[e] = ll;
+                }
+                *reinterpret_cast<u16x4*>(hp + 16 * n) = h;
+                *reinterpret_cast<u16x4*>(hp + a.out_plane + 16 * n) = lo;
+            }
+            continue;
+        }
+        float* op = a.out + static_cast<size_t>(r0 + t) * a.ldo + (kvh * G + g) * HD + 4 * fq;
 #pragma unroll
         for (int n = 0; n < NT; ++n)
             *reinterpret_cast<float4*>(op + 16 * n) =
@@ -906,7 +934,11 @@ size_t gemm_split_elems(uint32_t M, uint32_t K) { return static_cast<size_t>(2) 
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     if (!g.a_hl || g.K % 8 != 0 || (g.norm_w && !g.row_scale)) return hipErrorInvalidValue;
-    {
+    if ((g.out_hl && mode != kGemmGateUp) || (!g.out_hl && !g.out) ||
+        (g.a_plane && g.a_plane < static_cast<size_t>(g.M) * gemm_kp(g.K)) ||
+        (g.out_hl && g.out_plane < static_cast<size_t>(g.M) * gemm_kp(g.N)))
+        return hipErrorInvalidValue;
+    if (!g.a_ready) {
         const size_t n = static_cast<size_t>(g.M) * (gemm_kp(g.K) / 8);
         hipError_t e = vlaunch(gemm_split_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, g);
         if (e != hipSuccess) return e;
@@ -965,6 +997,7 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_
         const uint32_t keys = a.start + a.rows;
         const size_t need = prefill_kv_pack_bytes(keys, a.kv_heads, hd);
         if (need == 0 || !a.kv_pack || a.kv_pack_bytes < need) return hipErrorInvalidValue;
+        if (a.out_hl && a.out_plane < static_cast<size_t>(a.rows) * a.heads * hd) return hipErrorInvalidValue;
         PrefillAttnArgs b = a;
         b.kv_tiles = (keys + fa_tile_keys(hd) - 1) / fa_tile_keys(hd);
         const uint32_t rows_per_block = kFaVecs / G;
@@ -984,7 +1017,7 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_
         }
     }
     const uint32_t G = a.heads / a.kv_heads;
-    if (G == 0 || G > static_cast<uint32_t>(kPairsPerWave)) return hipErrorInvalidValue;
+    if (G == 0 || G > static_cast<uint32_t>(kPairsPerWave) || a.out_hl) return hipErrorInvalidValue;  // f32 out only
     const uint32_t rows_per_wave = kPairsPerWave / G;
     const uint32_t items = (a.rows + rows_per_wave - 1) / rows_per_wave * a.kv_heads;
     const dim3 grid((items + kAttnThreads / 64 - 1) / (kAttnThreads / 64));
