@@ -243,9 +243,16 @@ struct GemmArgs {
     // of f32 rows in out.
     uint16_t* out_hl = nullptr;
     size_t out_plane = 0;
+    // GateUp: f32 scratch of M * 2N. When set, few row tiles may split K: the
+    // gate and up sums are added there atomically (the launcher zeroes it) and
+    // a SwiGLU pass writes out / out_hl.
+    float* gu_acc = nullptr;
 };
 __host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + 31) / 32 * 32; }
 size_t gemm_split_elems(uint32_t M, uint32_t K);
+// Most rows for which a GateUp GEMM of N outputs may split K (gu_acc of
+// rows * 2N floats is then needed).
+uint32_t gemm_gateup_split_rows(uint32_t N);
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s);
 
 hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s);

@@ -92,6 +92,8 @@ struct vvli_gpu_model {
     float* pf_scale = nullptr;  // [rows] RMS scales
     float* pf_ahl = nullptr;    // GEMM activations split hi | lo (gemm_split_elems bf16)
     float* pf_ahl2 = nullptr;   // split planes written by attention (o_proj's A) and SwiGLU (down's A)
+    float* pf_gu = nullptr;     // gate/up split-K sums for short chunks ([pf_gu_rows][2I])
+    uint32_t pf_gu_rows = 0;
     void* pf_kvp = nullptr;     // packed K/V tiles of one layer for the attention kernel
     size_t pf_kvp_bytes = 0;
 };
@@ -577,6 +579,12 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
     }
     m->pf_kvp_bytes = kvp;
     m->pf_rows = static_cast<uint32_t>(rows);
+    const uint32_t gu_rows = std::min<uint32_t>(m->pf_rows, gemm_gateup_split_rows(c.inter));
+    if (gu_rows > 0 && hipMalloc(reinterpret_cast<void**>(&m->pf_gu), static_cast<size_t>(gu_rows) * 2 * I *
+                                                                          sizeof(float)) == hipSuccess)
+        m->pf_gu_rows = gu_rows;
+    else
+        m->pf_gu = nullptr;  // short chunks then run gate/up unsplit
     return VVLI_OK;
 }
 
@@ -639,6 +647,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gu.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
             // SwiGLU written as the down GEMM's split planes.
             gu.out_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2), gu.out_plane = m->pf_rows * gemm_kp(I);
+            if (P <= m->pf_gu_rows) gu.gu_acc = m->pf_gu;
             LAUNCH(launch_gemm_bf16(kGemmGateUp, gu, s));
             // x += ff . Wd^T
             GemmArgs gd;
@@ -666,7 +675,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
-                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
+                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng};
     for (void* b : bufs)
         if (b) (void)hipFree(b);

@@ -311,7 +311,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
                 for (int j = 0; j < 4; j += 2) {
                     const uint32_t n = n0 / 2 + (wn * 2 + j / 2) * 16 + fr;
-                    if (g.out_hl) {  // split planes of the next GEMM's A, zeros in the tail
+                    if (split) {  // partial gate and up sums; gemm_swiglu_kernel finishes
+                        if (n < g.N) {
+                            float* gu = g.gu_acc + static_cast<size_t>(row) * (2 * g.N) + n;
+                            unsafeAtomicAdd(gu, acc[i][j][jr]);
+                            unsafeAtomicAdd(gu + g.N, acc[i][j + 1][jr]);
+                        }
+                    } else if (g.out_hl) {  // split planes of the next GEMM's A, zeros in the tail
                         const uint32_t kpo = gemm_kp(g.N);
                         if (n < kpo) {
                             const float v = n < g.N ? silu_mul(acc[i][j][jr], acc[i][j + 1][jr]) : 0.f;
@@ -892,6 +898,24 @@ bool prefill_attn_vector = [] {
     return e != nullptr && strcmp(e, "vector") == 0;
 }();
 
+// silu(gate) * up from the split-K sums of a GateUp GEMM, written as out's
+// f32 rows or as out_hl's split planes (zero tail), like the unsplit epilogue.
+__global__ __launch_bounds__(256) void gemm_swiglu_kernel(GemmArgs g) {
+    const uint32_t kpo = gemm_kp(g.N);
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
+    if (n >= kpo) return;
+    const float* gu = g.gu_acc + static_cast<size_t>(row) * (2 * g.N);
+    const float v = n < g.N ? silu_mul(gu[n], gu[g.N + n]) : 0.f;
+    if (g.out_hl) {
+        const uint16_t h = to_bf16_rne(v);
+        uint16_t* o = g.out_hl + static_cast<size_t>(row) * kpo + n;
+        o[0] = h;
+        o[g.out_plane] = to_bf16_rne(v - from_bf16(h));
+    } else if (n < g.N) {
+        g.out[static_cast<size_t>(row) * g.ldo + n] = v;
+    }
+}
+
 __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) out[i] = 0.f;
 }
@@ -902,9 +926,9 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
 // idle: then as many splits as keep the launch within one round (each split
 // at least 8 K steps, at most 32). SwiGLU tiles are never split (the epilogue
 // is nonlinear), plain tiles only when the output rows are dense (they are
-// zeroed first).
-uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
-    if (mode == kGemmGateUp || (mode == kGemmPlain && g.ldo != g.N)) return 1;
+// zeroed first; SwiGLU tiles only with a gate/up scratch, finished by a
+// separate pass).
+static uint32_t gemm_cus() {
     static const uint32_t cus = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -912,6 +936,12 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
             n = 256;
         return static_cast<uint32_t>(n);
     }();
+    return cus;
+}
+
+uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
+    if ((mode == kGemmGateUp && !g.gu_acc) || (mode == kGemmPlain && g.ldo != g.N)) return 1;
+    const uint32_t cus = gemm_cus();
     const uint32_t nk = (g.K + kBK - 1) / kBK;
     const uint32_t max_splits = std::min<uint32_t>(32, nk / 8 > 0 ? nk / 8 : 1);
     if (2 * tiles > cus) return 1;
@@ -927,6 +957,11 @@ size_t prefill_kv_pack_bytes(uint32_t keys, uint32_t kv_heads, uint32_t hd) {
     if (hd != 32 && hd != 64 && hd != 128) return 0;
     const size_t tk = fa_tile_keys(hd);
     return static_cast<size_t>(kv_heads) * ((keys + tk - 1) / tk) * (8 * tk * hd);
+}
+
+uint32_t gemm_gateup_split_rows(uint32_t N) {
+    const uint32_t tn = (2 * N + kBN - 1) / kBN;
+    return gemm_cus() / (2 * tn) * kBM;  // row count whose tiles leave half of the CUs idle
 }
 
 size_t gemm_split_elems(uint32_t M, uint32_t K) { return static_cast<size_t>(2) * M * gemm_kp(K); }
@@ -958,11 +993,18 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
     const uint32_t gx = (cols + kBN - 1) / kBN, gy = (g.M + kBM - 1) / kBM;
     const uint32_t splits = gemm_k_splits(mode, g, gx * gy);
-    if (splits > 1 && mode == kGemmPlain) {
-        const size_t n = static_cast<size_t>(g.M) * g.ldo;
+    if (splits > 1 && mode != kGemmResid) {
+        const bool gu = mode == kGemmGateUp;
+        const size_t n = static_cast<size_t>(g.M) * (gu ? 2 * g.N : g.ldo);
         const uint32_t blocks = static_cast<uint32_t>(std::min<size_t>((n + 255) / 256, 4096));
-        hipError_t e = vlaunch(zero_rows_kernel, dim3(blocks), dim3(256), 0, s, g.out, n);
+        hipError_t e = vlaunch(zero_rows_kernel, dim3(blocks), dim3(256), 0, s, gu ? g.gu_acc : g.out, n);
         if (e != hipSuccess) return e;
+    }
+    if (splits > 1 && mode == kGemmGateUp) {
+        const dim3 grid(gx * gy, 1, splits);
+        hipError_t e = vlaunch(gemm_bf16_kernel<kGemmGateUp>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+        if (e != hipSuccess) return e;
+        return vlaunch(gemm_swiglu_kernel, dim3((gemm_kp(g.N) + 255) / 256, g.M), dim3(256), 0, s, g);
     }
     const dim3 grid(gx * gy, 1, splits);  // tiles in the XCD-aware order of the kernel
     switch (mode) {
