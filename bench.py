@@ -228,6 +228,60 @@ def prefill_main(args, cfg, blob) -> int:
     return 0
 
 
+def linear_main(args) -> int:
+    """Isolated op sweep (vvli_gpu_linear) on the Llama-3.2-1B projection shapes:
+    bf16 W [N, K] ~ N(0, 0.02), f32 X [M, K] ~ N(0, 1), f32 Y [M, N]. Each
+    shape rotates over enough weight copies (>= 1 GiB) that W is read from HBM,
+    not from the 256 MB memory-side cache. Algorithmic bytes 2NK + 4MK + 4MN,
+    flops 2MNK; time per call = HIP events around `reps` calls on one stream."""
+    import torch
+
+    from vvli_amd import runtime as R
+
+    shapes = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (128256, 2048)]
+    ms = [1, 4, 16, 128, 512]
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    stream = torch.cuda.current_stream()
+    rows = []
+    for n, k in shapes:
+        wbytes = 2 * n * k
+        copies = max(2, -(-(1 << 30) // wbytes))
+        ws = [(torch.randn(n, k, device="cuda", generator=gen) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+        for m in ms:
+            x = torch.randn(m, k, device="cuda", generator=gen)
+            y = torch.empty(m, n, device="cuda")
+            reps = max(copies, 20)
+            for i in range(3):
+                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            nbytes = 2 * n * k + 4 * m * k + 4 * m * n
+            rows.append({"N": n, "K": k, "M": m, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                         "tflops": round(2 * m * n * k / us / 1e6, 1)})
+            print(f"[bench] linear N={n} K={k} M={m}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s, "
+                  f"{2 * m * n * k / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    gemv = [r for r in rows if r["M"] == 1]
+    agg = sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv) / sum(r["us"] for r in gemv) / 1e3
+    line = {
+        "metric": "linear op sweep: GEMV HBM GB/s (M=1, all five shapes)", "value": round(agg, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": len(rows), "warmup": 3, "ms_per_step": None, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 weights, f32 activations", "data": "synthetic",
+        "config": {"workload": "Llama-3.2-1B projection shapes x M in {1, 4, 16, 128, 512}, cold weights"},
+        "roofline": {"bound": "hbm", "achieved": round(agg, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(agg / 8000.0, 4), "traffic": None, "kernel": "vvli_gpu_linear, M = 1"},
+        "sweep": rows, "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,8 +295,9 @@ def main() -> int:
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],
                     help="prompt processing: batched GEMM prefill, or one token step per prompt token (the reference's loop)")
-    ap.add_argument("--mode", default="decode", choices=["decode", "prefill"],
-                    help="decode: the headline decode benchmark; prefill: batched-prefill throughput sweep")
+    ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "linear"],
+                    help="decode: the headline decode benchmark; prefill: batched-prefill throughput sweep; "
+                         "linear: the isolated op sweep (vvli_gpu_linear)")
     ap.add_argument("--model", default="llama-3.2-1b",
                     choices=["llama-3.2-1b", "qwen2.5-0.5b", "qwen2.5-7b", "olmoe-1b-7b"],
                     help="decoder shape (synthetic bf16 weights); the default is the headline workload")
@@ -262,6 +317,8 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
+    if args.mode == "linear":
+        return linear_main(args)
     cfg = C.NAMED[args.model]()
     t = time.perf_counter()
     blob = make_blob(cfg)

@@ -270,7 +270,9 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
  * pointers; K must be a multiple of 8. stream: hipStream_t or NULL for the
  * null stream. Asynchronous: returns after the launch. M < 4 runs one GEMV per
  * row; M >= 4 one MFMA GEMM (X split into two bf16 halves, so the products
- * keep about 16 bits of each f32 activation). */
+ * keep about 16 bits of each f32 activation) through a per-stream scratch of
+ * about 4*M*K bytes, allocated stream-ordered, grown when needed and kept
+ * until the process ends (calls on one stream use it in turn). */
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream);
 

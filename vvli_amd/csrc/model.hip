@@ -1506,13 +1506,32 @@ int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, 
         g.a = dX, g.lda = K, g.w[0] = dW, g.bias[0] = dBias;
         g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
         g.out = dY, g.ldo = N, g.M = M, g.N = N, g.K = K;
-        void* hl = nullptr;
-        HIP_TRY(hipMallocAsync(&hl, gemm_split_elems(M, K) * sizeof(uint16_t), s));
-        g.a_hl = static_cast<uint16_t*>(hl);
-        const hipError_t e = launch_gemm_bf16(kGemmPlain, g, s);
-        const hipError_t f = hipFreeAsync(hl, s);
-        HIP_TRY(e);
-        HIP_TRY(f);
+        // The split scratch is kept per stream and grows stream-ordered; the
+        // lock covers the enqueue, so calls on one stream use it in turn.
+        struct Scratch {
+            hipStream_t stream;
+            void* p;
+            size_t bytes;
+        };
+        static std::mutex mu;
+        static std::vector<Scratch> cache;
+        const size_t need = gemm_split_elems(M, K) * sizeof(uint16_t);
+        std::lock_guard<std::mutex> lock(mu);
+        Scratch* sc = nullptr;
+        for (Scratch& c : cache)
+            if (c.stream == s) sc = &c;
+        if (!sc) {
+            cache.push_back(Scratch{s, nullptr, 0});
+            sc = &cache.back();
+        }
+        if (sc->bytes < need) {
+            if (sc->p) HIP_TRY(hipFreeAsync(sc->p, s));
+            sc->p = nullptr, sc->bytes = 0;
+            HIP_TRY(hipMallocAsync(&sc->p, need, s));
+            sc->bytes = need;
+        }
+        g.a_hl = static_cast<uint16_t*>(sc->p);
+        HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
         return VVLI_OK;
     }
     for (uint32_t mi = 0; mi < M; ++mi) {
