@@ -73,3 +73,34 @@ def test_linear_rejects_bad_shapes():
         R.linear(w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 16, 12)
     with pytest.raises(VvliError):  # NULL pointer
         R.linear(0, x.data_ptr(), y.data_ptr(), 1, 16, 8)
+
+
+def test_linear_two_streams_growing_scratch(oracle_mod):
+    """Calls on two streams, interleaved, with M growing (the per-stream split
+    scratch is reallocated stream-ordered) and shrinking: every result matches
+    the oracle; a call queued behind a larger one on the same stream reuses
+    its scratch."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(7)
+    N, K = 384, 512
+    w = bf16_bits(rng.normal(0, 0.02, size=(N, K)))
+    dw = torch.from_numpy(w.view(np.int16)).to(dev)
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    jobs = []
+    for i, M in enumerate([4, 8, 64, 200, 16, 130]):
+        x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+        dx = torch.from_numpy(x).to(dev)
+        dy = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        s = streams[i % 2]
+        R.linear(dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), M, N, K, stream=s.cuda_stream)
+        jobs.append((x, dx, dy))
+    torch.cuda.synchronize()
+    for x, _, dy in jobs:
+        y = dy.cpu().numpy()
+        for m in range(x.shape[0]):
+            ref = oracle_mod.linear(w, x[m], None)
+            e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+            assert e <= TOL, f"M={x.shape[0]} row {m}: rel err {e:.3e}"
