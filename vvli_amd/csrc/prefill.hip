@@ -924,7 +924,7 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
 // zeroing pass and shorter K loops (the copy pipeline fills and drains per
 // split), so it is used only when the tiles leave more than half of the CUs
 // idle: then as many splits as keep the launch within one round (each split
-// at least 8 K steps, at most 32). SwiGLU tiles are never split (the epilogue
+// at least 8 or 16 K steps, at most 32). SwiGLU tiles are never split (the epilogue
 // is nonlinear), plain tiles only when the output rows are dense (they are
 // zeroed first; SwiGLU tiles only with a gate/up scratch, finished by a
 // separate pass).
@@ -943,7 +943,11 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     if ((mode == kGemmGateUp && !g.gu_acc) || (mode == kGemmPlain && g.ldo != g.N)) return 1;
     const uint32_t cus = gemm_cus();
     const uint32_t nk = (g.K + kBK - 1) / kBK;
-    const uint32_t max_splits = std::min<uint32_t>(32, nk / 8 > 0 ? nk / 8 : 1);
+    // Each split keeps at least 8 K steps (16 once there are 32 tiles: then
+    // half the CUs with twice the steps beat a full round of short loops,
+    // whose copy pipeline fills and drains per split).
+    const uint32_t min_steps = tiles >= 32 ? 16 : 8;
+    const uint32_t max_splits = std::min<uint32_t>(32, nk / min_steps > 0 ? nk / min_steps : 1);
     if (2 * tiles > cus) return 1;
     return std::max<uint32_t>(1, std::min<uint32_t>(max_splits, cus / tiles));
 }
