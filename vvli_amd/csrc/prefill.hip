@@ -924,10 +924,10 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
 // zeroing pass and shorter K loops (the copy pipeline fills and drains per
 // split), so it is used only when the tiles leave more than half of the CUs
 // idle: then as many splits as keep the launch within one round (each split
-// at least 8 or 16 K steps, at most 32). SwiGLU tiles are never split (the epilogue
-// is nonlinear), plain tiles only when the output rows are dense (they are
-// zeroed first; SwiGLU tiles only with a gate/up scratch, finished by a
-// separate pass).
+// at least 8 or 16 K steps, at most 32). Plain tiles split only when the
+// output rows are dense (they are zeroed first); SwiGLU tiles only with a
+// gate/up scratch (the epilogue is nonlinear: the sums go there and a
+// separate pass applies it).
 static uint32_t gemm_cus() {
     static const uint32_t cus = [] {
         int dev = 0, n = 0;
