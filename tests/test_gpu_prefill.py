@@ -43,6 +43,9 @@ CASES = {
                               rms_norm_eps=1e-5), "synth", [200]),
     "hd128_g7": (cfg_small(vocab_size=640, hidden_size=896, intermediate_size=1024, num_attention_heads=7,
                            num_key_value_heads=1, tie_word_embeddings=False), "synth", [70]),
+    # head_dim 128 (32-key tiles) with start_pos > 0: earlier cache rows packed again, ragged last tile.
+    "hd128_split": (cfg_small(vocab_size=640, hidden_size=896, intermediate_size=1024, num_attention_heads=7,
+                              num_key_value_heads=1, tie_word_embeddings=False), "synth", [45, 3, 97]),
     "qwen05_heads": (cfg_small(vocab_size=2000, hidden_size=896, intermediate_size=4864, num_attention_heads=14,
                                num_key_value_heads=2), "synth", [150]),
     "hd32_g1": (cfg_small(hidden_size=128, num_attention_heads=4, num_key_value_heads=4), "synth", [65]),
