@@ -228,6 +228,45 @@ def prefill_main(args, cfg, blob) -> int:
     return 0
 
 
+def sampled_main(args, cfg, blob) -> int:
+    """Sampled decode (vvli_gpu_generate with generator.Options defaults:
+    temperature 0.8, top-k 40, top-p 0.95, repeat penalty 1.1 over 64 tokens):
+    the whole-token roofline of the greedy benchmark over the same prompt and
+    steps; --path picks the decode implementation."""
+    from vvli_amd import runtime as R
+
+    runner = R.Runner(cfg, blob, args.ctx)
+    runner.set_decode_path(args.path)
+    runner.set_prefill_path("auto")
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
+    opts = R.Sampling(seed=7)
+    runner.generate(prompt[:16], max(1, args.warmup), opts, batched_prefill=True)
+    runner.kv_clear()
+    tokens, stats = runner.generate(prompt, args.steps, opts, batched_prefill=True)
+    assert stats.generated_tokens == args.steps
+    decode_s = stats.decode_nanoseconds / 1e9
+    tok_s = args.steps / decode_s
+    step_bytes = sum(token_bytes(cfg, p) for p in range(args.prompt, args.prompt + args.steps))
+    gbs = step_bytes / decode_s / 1e9
+    path = "persistent" if args.path != "graph" and runner.persistent_available() else "graph"
+    print(f"[bench] sampled decode {tok_s:.1f} tok/s ({path})", file=sys.stderr, flush=True)
+    line = {
+        "metric": "decode tok/s @bs1, sampled (T 0.8, top-k 40, top-p 0.95, repeat penalty 1.1)", "value": round(tok_s, 2),
+        "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(decode_s * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.model} bf16 sampled decode, bs1", "prompt_tokens": args.prompt,
+                   "decode_tokens": args.steps, "ctx": args.ctx, "path": path},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbs / 8000.0, 4), "traffic": None,
+                     "kernel": "whole token (step + sampler), wall clock"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    runner.close()
+    return 0
+
+
 def linear_main(args) -> int:
     """Isolated op sweep (vvli_gpu_linear) on the Llama-3.2-1B projection shapes:
     bf16 W [N, K] ~ N(0, 0.02), f32 X [M, K] ~ N(0, 1), f32 Y [M, N]. Each
@@ -301,6 +340,8 @@ def main() -> int:
     ap.add_argument("--model", default="llama-3.2-1b",
                     choices=["llama-3.2-1b", "qwen2.5-0.5b", "qwen2.5-7b", "olmoe-1b-7b"],
                     help="decoder shape (synthetic bf16 weights); the default is the headline workload")
+    ap.add_argument("--sampling", action="store_true",
+                    help="decode mode: sample with the generator's default options instead of greedy")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
@@ -328,6 +369,8 @@ def main() -> int:
         return prefill_main(args, cfg, blob)
     if cfg.num_experts:
         return moe_decode_main(args, cfg, blob)
+    if args.sampling:
+        return sampled_main(args, cfg, blob)
     runner = R.Runner(cfg, blob, args.ctx)
     runner.set_decode_path(args.path)
     runner.set_prefill_path("auto" if args.prefill == "batched" else "loop")

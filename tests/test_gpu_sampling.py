@@ -92,9 +92,10 @@ def cfg_small(**kw) -> C.Config:
     return C.Config(**base)
 
 
+@pytest.mark.parametrize("path", ["persistent", "graph"])
 @pytest.mark.parametrize("batched", [False, True])
 @pytest.mark.parametrize("k", [0, 2, 4])
-def test_generate_matches_oracle(k, batched, oracle_mod, host_threads):
+def test_generate_matches_oracle(k, batched, path, oracle_mod, host_threads):
     cfg = cfg_small()
     # N(0, 0.05) weights: logits spread enough that top-k and top-p cuts sit in clear gaps.
     blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=2, stddev=0.05)
@@ -102,8 +103,10 @@ def test_generate_matches_oracle(k, batched, oracle_mod, host_threads):
     prompt = np.random.default_rng(4).integers(0, cfg.vocab_size, 24).astype(np.uint32)
     orc = oracle_mod.OracleRunner(cfg, blob, 128, threads=host_threads)
     ref = orc.generate_sampled(prompt, 48, o)
-    print(f"generate k={k} batched={batched}", flush=True)
+    print(f"generate k={k} batched={batched} path={path}", flush=True)
     with R.Runner(cfg, blob, 128) as gpu:
+        gpu.set_decode_path(path)
+        assert path == "graph" or gpu.persistent_available()
         got, stats = gpu.generate(prompt, 48, o, batched_prefill=batched)
         assert stats.generated_tokens == 48
         np.testing.assert_array_equal(got, ref)

@@ -345,7 +345,13 @@ struct SampleArgs {
     uint32_t n_prompt = 0;
     uint32_t* out_tokens = nullptr;
     uint32_t out_cap = 0;
+    // Scratch of the two-stage top-k (nullable: one block scans the vocab):
+    // sample_cand_elems(vocab) keys and sample_nf_elems(vocab) counts.
+    unsigned long long* cand_buf = nullptr;
+    uint32_t* cand_nf = nullptr;
 };
+size_t sample_cand_elems(uint32_t vocab);
+size_t sample_nf_elems(uint32_t vocab);
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
 hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
                                 uint32_t last_n, hipStream_t s);

@@ -81,6 +81,8 @@ struct vvli_gpu_model {
     // On-device sampling (vvli_gpu_generate with temperature > 0 or a repeat penalty).
     uint32_t* sample_counts = nullptr;        // [vocab] repeat counts of the window
     unsigned long long* sample_prng = nullptr;  // xoshiro256++ state [4]
+    unsigned long long* sample_cand = nullptr;  // two-stage top-k survivors
+    uint32_t* sample_nf = nullptr;              // finite counts of the vocab slices
     hipGraphExec_t graph_sample = nullptr;    // token step ending in the sampler
     // Batched prefill (bf16 only): chunk buffers, allocated on first use.
     bool pf_ok = false;
@@ -676,7 +678,7 @@ void free_model(vvli_gpu_model* m) {
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
                     m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
-                    m->sample_prng};
+                    m->sample_prng, m->sample_cand, m->sample_nf};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -952,6 +954,8 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     int rc;
     if (!m->sample_counts && (rc = dmalloc(&m->sample_counts, c.vocab))) return rc;
     if (!m->sample_prng && (rc = dmalloc(&m->sample_prng, 4))) return rc;
+    if (!m->sample_cand && (rc = dmalloc(&m->sample_cand, sample_cand_elems(c.vocab)))) return rc;
+    if (!m->sample_nf && (rc = dmalloc(&m->sample_nf, sample_nf_elems(c.vocab)))) return rc;
     const bool penalty = o.repeat_penalty > 1.0f && o.repeat_last_n > 0;
     SampleArgs sa;
     sa.logits = m->logits;
@@ -963,23 +967,46 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     sa.top_k = (o.top_k == 0 || o.top_k > c.vocab) ? c.vocab : o.top_k;
     sa.repeat_last_n = o.repeat_last_n;
     sa.prng = m->sample_prng;
+    sa.cand_buf = m->sample_cand;
+    sa.cand_nf = m->sample_nf;
     sa.state = m->state;
     sa.prompt = m->prompt;
     sa.n_prompt = n_prompt;
     sa.out_tokens = m->out_tokens;
     sa.out_cap = m->out_cap;
-    if ((rc = capture_sample_graph(m, sa))) return rc;
+    // Persistent step where available: each token is one single-step launch
+    // (the step leaves the logits, token = argmax and pos + 1 in the state;
+    // counting is off, so it appends nothing) and the sampler then replaces the
+    // token without advancing pos. Else the captured step + sampler graph.
+    const bool persistent = use_persistent(m);
+    SampleArgs after_step = sa;
+    after_step.advance_pos = 0;
+    if (!persistent && (rc = capture_sample_graph(m, sa))) return rc;
     const int64_t t0 = now_ns();
     HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
     if (batched) {
         if ((rc = enqueue_prefill_batched(m, 0, n_prompt, prompt[n_prompt - 1], 0))) return rc;
+    } else if (persistent) {
+        HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 0, m->stream));
+        if ((rc = run_persistent(m, n_prompt, -1))) return rc;
     } else {
         if ((rc = ensure_graph(m))) return rc;
         HIP_TRY(launch_set_state(m->state, prompt[0], 0, n_prompt, 0, m->stream));
         for (uint32_t i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
     }
     HIP_TRY(hipStreamSynchronize(m->stream));
+    if (persistent && (rc = check_persistent_error(m))) return rc;
     const int64_t t1 = now_ns();
+    auto forward_and_sample = [&]() -> int {
+        if (!persistent) {
+            HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
+            return VVLI_OK;
+        }
+        int r = run_persistent(m, 1, -1);
+        if (r) return r;
+        HIP_TRY(launch_sample(after_step, m->stream));
+        return VVLI_OK;
+    };
     // Sampler.init: PRNG state, repeat counts of the prompt's window.
     uint64_t st4[4];
     prng_seed(o.seed, st4);
@@ -991,7 +1018,8 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
         first.advance_pos = 0;
         HIP_TRY(launch_sample(first, m->stream));
         if (eos < 0) {
-            for (uint32_t i = 0; i < max_new; ++i) HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
+            for (uint32_t i = 0; i < max_new; ++i)
+                if ((rc = forward_and_sample())) return rc;
             produced = max_new;
         } else {
             uint32_t pos = n_prompt;
@@ -1002,7 +1030,7 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
                 ++produced;
                 if (static_cast<int64_t>(next) == eos) break;
                 if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len", pos);
-                HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
+                if ((rc = forward_and_sample())) return rc;
                 ++pos;
             }
         }
@@ -1010,6 +1038,7 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
                                m->stream));
     }
     HIP_TRY(hipStreamSynchronize(m->stream));
+    if (persistent && (rc = check_persistent_error(m))) return rc;
     const int64_t t2 = now_ns();
     *n_out = produced;
     if (stats) {
@@ -1453,15 +1482,19 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
         }
     }
     float* d_logits = nullptr;
-    uint32_t *d_counts = nullptr, *d_result = nullptr;
-    unsigned long long* d_prng = nullptr;
+    uint32_t *d_counts = nullptr, *d_result = nullptr, *d_nf = nullptr;
+    unsigned long long *d_prng = nullptr, *d_cand = nullptr;
     auto release = [&] {
         if (d_logits) (void)hipFree(d_logits);
         if (d_counts) (void)hipFree(d_counts);
         if (d_result) (void)hipFree(d_result);
         if (d_prng) (void)hipFree(d_prng);
+        if (d_cand) (void)hipFree(d_cand);
+        if (d_nf) (void)hipFree(d_nf);
     };
     hipError_t e = hipMalloc(&d_logits, n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d_cand, sample_cand_elems(n) * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMalloc(&d_nf, sample_nf_elems(n) * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d_counts, n * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d_result, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d_prng, 4 * sizeof(unsigned long long));
@@ -1480,6 +1513,8 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
         sa.repeat_last_n = opts->repeat_last_n;
         sa.prng = d_prng;
         sa.result = d_result;
+        sa.cand_buf = d_cand;
+        sa.cand_nf = d_nf;
         e = launch_sample(sa, nullptr);
     }
     if (e == hipSuccess) e = hipMemcpy(token_out, d_result, sizeof(uint32_t), hipMemcpyDeviceToHost);

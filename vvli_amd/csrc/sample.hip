@@ -14,6 +14,14 @@
 //            state in device memory) and walks the cumulative sum
 //            (sampleCandidate, :451-463).
 // Sequential f32 sums in candidate order keep the reference's rounding.
+//
+// Two-stage top-k (top_k <= 128, scratch given): sample_local_kernel cuts
+// the vocab into slices of 4096 ids, one block each; a slice's keys
+// (score key << 32 | ~id; 0 for a non-finite score) are bitonic-sorted in LDS
+// and its top_k largest written out, with its finite count. The keys are
+// distinct, so every member of the global top_k is in its slice's top_k; the
+// sampling block then sorts the slices' survivors instead of scanning the
+// vocab (one block's scan is ~1 ms at a 128K vocab).
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -63,6 +71,30 @@ __device__ inline float prng_float(uint64_t* s) {
     return __uint_as_float(((126u - lz) << 23) | static_cast<uint32_t>(r & 0x7fffffull));
 }
 
+constexpr int kLocalIds = 4096;  // vocab slice of a local top-k block
+constexpr int kFastTopK = 128;   // largest top_k of the two-stage path
+constexpr int kSurvivors = 4096; // slices * top_k the sampling block sorts
+
+// Descending bitonic sort of n (a power of two) keys in LDS by the block.
+__device__ inline void bitonic_desc(unsigned long long* k, uint32_t n) {
+    for (uint32_t size = 2; size <= n; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+                const uint32_t p = j ^ stride;
+                if (p > j) {
+                    const bool desc = (j & size) == 0;
+                    const unsigned long long x = k[j], y = k[p];
+                    if (desc ? (x < y) : (x > y)) {
+                        k[j] = y;
+                        k[p] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 struct SampleShared {
     uint32_t hist[256];
     unsigned long long cand[kMaxCand];  // (score key << 32) | ~id, sorted descending
@@ -97,8 +129,40 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* buf) {
     return incl - v;
 }
 
+// One slice of kLocalIds ids per block: its top_k keys and its finite count.
+__global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
+    __shared__ unsigned long long keys[kLocalIds];
+    __shared__ uint32_t red[kT / 64];
+    const uint32_t tid = threadIdx.x, base = blockIdx.x * kLocalIds;
+    uint32_t nf = 0;
+    for (uint32_t j = tid; j < static_cast<uint32_t>(kLocalIds); j += kT) {
+        const uint32_t id = base + j;
+        unsigned long long key = 0ull;
+        if (id < a.vocab) {
+            const float s = adjusted(a.logits[id], a.counts ? a.counts[id] : 0u, a.repeat_penalty);
+            if (isfinite(s)) {
+                key = (static_cast<unsigned long long>(order_key(s)) << 32) | (0xffffffffu - id);
+                ++nf;
+            }
+        }
+        keys[j] = key;
+    }
+    for (int off = 32; off > 0; off >>= 1) nf += __shfl_xor(nf, off, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = nf;
+    __syncthreads();
+    bitonic_desc(keys, kLocalIds);
+    const uint32_t m = a.top_k;
+    for (uint32_t j = tid; j < m; j += kT) a.cand_buf[static_cast<size_t>(blockIdx.x) * m + j] = keys[j];
+    if (tid == 0) {
+        uint32_t total = 0;
+        for (int w = 0; w < kT / 64; ++w) total += red[w];
+        a.cand_nf[blockIdx.x] = total;
+    }
+}
+
 __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
     __shared__ SampleShared sh;
+    __shared__ unsigned long long surv[kSurvivors];  // two-stage path: the slices' top_k keys
     const uint32_t tid = threadIdx.x;
     const uint32_t V = a.vocab;
     const uint32_t chunk = (V + kT - 1) / kT;
@@ -125,8 +189,13 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
         tok = sh.token;
     } else {
         // Finite candidates and the limit (buildCandidates, :367-372).
+        const bool two_stage = a.cand_buf != nullptr;
+        const uint32_t slices = (V + kLocalIds - 1) / kLocalIds;
         uint32_t nf = 0;
-        for (uint32_t i = i0; i < i1; ++i) nf += isfinite(score(i)) ? 1u : 0u;
+        if (two_stage)
+            for (uint32_t b = tid; b < slices; b += kT) nf += a.cand_nf[b];
+        else
+            for (uint32_t i = i0; i < i1; ++i) nf += isfinite(score(i)) ? 1u : 0u;
         const uint32_t n_finite = block_sum_u32(nf, sh.red);
         const uint32_t limit = min(a.top_k, V);
         const uint32_t count = min(limit, n_finite);
@@ -147,6 +216,17 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             __syncthreads();
             tok = sh.token;
         } else {
+          if (two_stage) {
+            // The slices' survivors, sorted: the first count are the candidates.
+            const uint32_t total = slices * a.top_k;
+            uint32_t n = 1;
+            while (n < total) n <<= 1;
+            for (uint32_t j = tid; j < n; j += kT) surv[j] = j < total ? a.cand_buf[j] : 0ull;
+            __syncthreads();
+            bitonic_desc(surv, n);
+            for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = j < count ? surv[j] : 0ull;
+            __syncthreads();
+          } else {
             // Radix select: the key of the count-th largest finite score.
             if (tid == 0) {
                 sh.prefix = 0;
@@ -204,22 +284,8 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             }
             __syncthreads();
             // Bitonic sort of kMaxCand keys, descending.
-            for (uint32_t size = 2; size <= static_cast<uint32_t>(kMaxCand); size <<= 1) {
-                for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                    for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) {
-                        const uint32_t p = j ^ stride;
-                        if (p > j) {
-                            const bool desc = (j & size) == 0;
-                            const unsigned long long x = sh.cand[j], y = sh.cand[p];
-                            if (desc ? (x < y) : (x > y)) {
-                                sh.cand[j] = y;
-                                sh.cand[p] = x;
-                            }
-                        }
-                    }
-                    __syncthreads();
-                }
-            }
+            bitonic_desc(sh.cand, kMaxCand);
+          }
             // Probabilities (prepareProbabilities): exp in parallel, sums in order.
             const float temperature = fmaxf(a.temperature, 1e-6f);
             const float s0 = key_value(static_cast<uint32_t>(sh.cand[0] >> 32));
@@ -304,8 +370,21 @@ __global__ __launch_bounds__(kT) void sample_counts_kernel(uint32_t* counts, uin
 
 }  // namespace
 
+size_t sample_cand_elems(uint32_t vocab) { return static_cast<size_t>(kSurvivors); }
+size_t sample_nf_elems(uint32_t vocab) { return (vocab + kLocalIds - 1) / kLocalIds; }
+
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
-    return vlaunch(sample_kernel, dim3(1), dim3(kT), 0, s, a);
+    SampleArgs b = a;
+    const uint32_t slices = (a.vocab + kLocalIds - 1) / kLocalIds;
+    const bool two_stage = a.cand_buf && a.cand_nf && a.temperature > 0.0f && a.top_k <= kFastTopK &&
+                           slices * a.top_k <= static_cast<uint32_t>(kSurvivors);
+    if (!two_stage) {
+        b.cand_buf = nullptr;
+        b.cand_nf = nullptr;
+        return vlaunch(sample_kernel, dim3(1), dim3(kT), 0, s, b);
+    }
+    hipError_t e = vlaunch(sample_local_kernel, dim3(slices), dim3(kT), 0, s, b);
+    return e != hipSuccess ? e : vlaunch(sample_kernel, dim3(1), dim3(kT), 0, s, b);
 }
 
 hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
