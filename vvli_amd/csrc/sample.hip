@@ -15,12 +15,13 @@
 //            (sampleCandidate, :451-463).
 // Sequential f32 sums in candidate order keep the reference's rounding.
 //
-// Two-stage top-k (top_k <= 128, scratch given): sample_local_kernel cuts
-// the vocab into slices of 4096 ids, one block each; a slice's keys
-// (score key << 32 | ~id; 0 for a non-finite score) are bitonic-sorted in LDS
-// and its top_k largest written out, with its finite count. The keys are
-// distinct, so every member of the global top_k is in its slice's top_k; the
-// sampling block then sorts the slices' survivors instead of scanning the
+// Two-stage top-k (top_k <= 128, at most 64 slices, scratch given):
+// sample_local_kernel cuts the vocab into slices of 4096 ids, one block each,
+// and writes a slice's top_k keys (score key << 32 | ~id; 0 for a non-finite
+// score), descending, with its finite count: top_k rounds of a block max over
+// keys held in registers. The keys are distinct, so every member of the global
+// top_k is in its slice's top_k; the sampling block's first wave then merges
+// the slices' sorted lists (one list head per lane) instead of scanning the
 // vocab (one block's scan is ~1 ms at a 128K vocab).
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -73,7 +74,7 @@ __device__ inline float prng_float(uint64_t* s) {
 
 constexpr int kLocalIds = 4096;  // vocab slice of a local top-k block
 constexpr int kFastTopK = 128;   // largest top_k of the two-stage path
-constexpr int kSurvivors = 4096; // slices * top_k the sampling block sorts
+constexpr int kSurvivors = 4096; // slices * top_k the sampling block merges (slices <= 64)
 
 // Descending bitonic sort of n (a power of two) keys in LDS by the block.
 __device__ inline void bitonic_desc(unsigned long long* k, uint32_t n) {
@@ -95,12 +96,69 @@ __device__ inline void bitonic_desc(unsigned long long* k, uint32_t n) {
     }
 }
 
+// Max over a fully active wave: DPP within each 16-lane row (quad swaps, then
+// half-row and row mirrors), then the four row maxima read out of lanes 0, 16,
+// 32, 48. No LDS round trips, unlike a shuffle butterfly.
+template <int CTRL>
+__device__ inline unsigned long long dpp_max_step(unsigned long long v) {
+    const int lo = static_cast<int>(static_cast<uint32_t>(v)), hi = static_cast<int>(static_cast<uint32_t>(v >> 32));
+    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false));
+    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false));
+    const unsigned long long o = (static_cast<unsigned long long>(ohi) << 32) | olo;
+    return o > v ? o : v;
+}
+
+__device__ inline unsigned long long readlane_u64(unsigned long long v, int lane) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+__device__ inline unsigned long long wave_max_dpp(unsigned long long v) {
+    v = dpp_max_step<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141>(v);  // row_half_mirror
+    v = dpp_max_step<0x140>(v);  // row_mirror: every lane holds its row's max
+    unsigned long long m = readlane_u64(v, 0);
+    const unsigned long long m1 = readlane_u64(v, 16), m2 = readlane_u64(v, 32), m3 = readlane_u64(v, 48);
+    m = m1 > m ? m1 : m;
+    m = m2 > m ? m2 : m;
+    return m3 > m ? m3 : m;
+}
+
+// The k largest of the block's keys (R per thread, distinct, 0 = none),
+// descending, into out[0 .. k) (written by thread 0): k rounds of a block max
+// -- registers, then wave shuffles, then 16 wave maxima in LDS (red holds two
+// rounds, so one barrier per round) -- the winner's owner zeroing its copy.
+template <int R>
+__device__ inline void block_topk(unsigned long long (&v)[R], uint32_t k, unsigned long long* out,
+                                  unsigned long long (*red)[kT / 64]) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (uint32_t i = 0; i < k; ++i) {
+        unsigned long long mx = 0ull;
+#pragma unroll
+        for (int r = 0; r < R; ++r) mx = v[r] > mx ? v[r] : mx;
+        mx = wave_max_dpp(mx);
+        if (lane == 0) red[i & 1][wave] = mx;
+        __syncthreads();
+        unsigned long long b = 0ull;
+#pragma unroll
+        for (int w = 0; w < kT / 64; ++w) b = red[i & 1][w] > b ? red[i & 1][w] : b;
+        if (threadIdx.x == 0) out[i] = b;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (v[r] == b) v[r] = 0ull;
+    }
+    __syncthreads();
+}
+
 struct SampleShared {
     uint32_t hist[256];
     unsigned long long cand[kMaxCand];  // (score key << 32) | ~id, sorted descending
     float prob[kMaxCand];
     uint32_t scan_gt[kT], scan_eq[kT];
     unsigned long long red[kT / 64];
+    unsigned long long surv[kSurvivors];  // two-stage path: the slices' lists
     uint32_t prefix, remaining, n_finite, token;
 };
 
@@ -131,38 +189,36 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* buf) {
 
 // One slice of kLocalIds ids per block: its top_k keys and its finite count.
 __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
-    __shared__ unsigned long long keys[kLocalIds];
-    __shared__ uint32_t red[kT / 64];
+    constexpr int R = kLocalIds / kT;
+    __shared__ unsigned long long red[2][kT / 64];
+    __shared__ uint32_t nred[kT / 64];
     const uint32_t tid = threadIdx.x, base = blockIdx.x * kLocalIds;
     uint32_t nf = 0;
-    for (uint32_t j = tid; j < static_cast<uint32_t>(kLocalIds); j += kT) {
-        const uint32_t id = base + j;
-        unsigned long long key = 0ull;
+    unsigned long long v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t id = base + tid + r * kT;  // coalesced
+        v[r] = 0ull;
         if (id < a.vocab) {
             const float s = adjusted(a.logits[id], a.counts ? a.counts[id] : 0u, a.repeat_penalty);
             if (isfinite(s)) {
-                key = (static_cast<unsigned long long>(order_key(s)) << 32) | (0xffffffffu - id);
+                v[r] = (static_cast<unsigned long long>(order_key(s)) << 32) | (0xffffffffu - id);
                 ++nf;
             }
         }
-        keys[j] = key;
     }
     for (int off = 32; off > 0; off >>= 1) nf += __shfl_xor(nf, off, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = nf;
-    __syncthreads();
-    bitonic_desc(keys, kLocalIds);
-    const uint32_t m = a.top_k;
-    for (uint32_t j = tid; j < m; j += kT) a.cand_buf[static_cast<size_t>(blockIdx.x) * m + j] = keys[j];
+    if ((tid & 63) == 0) nred[tid >> 6] = nf;
+    block_topk(v, a.top_k, a.cand_buf + static_cast<size_t>(blockIdx.x) * a.top_k, red);
     if (tid == 0) {
         uint32_t total = 0;
-        for (int w = 0; w < kT / 64; ++w) total += red[w];
+        for (int w = 0; w < kT / 64; ++w) total += nred[w];
         a.cand_nf[blockIdx.x] = total;
     }
 }
 
 __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
     __shared__ SampleShared sh;
-    __shared__ unsigned long long surv[kSurvivors];  // two-stage path: the slices' top_k keys
     const uint32_t tid = threadIdx.x;
     const uint32_t V = a.vocab;
     const uint32_t chunk = (V + kT - 1) / kT;
@@ -217,14 +273,25 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             tok = sh.token;
         } else {
           if (two_stage) {
-            // The slices' survivors, sorted: the first count are the candidates.
+            // The slices' lists (each top_k keys, descending, zero padded): the
+            // first wave merges them, lane s holding list s's head; the top
+            // count heads taken are the candidates, in order.
             const uint32_t total = slices * a.top_k;
-            uint32_t n = 1;
-            while (n < total) n <<= 1;
-            for (uint32_t j = tid; j < n; j += kT) surv[j] = j < total ? a.cand_buf[j] : 0ull;
+            for (uint32_t j = tid; j < total; j += kT) sh.surv[j] = a.cand_buf[j];
+            for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = 0ull;
             __syncthreads();
-            bitonic_desc(surv, n);
-            for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = j < count ? surv[j] : 0ull;
+            if (tid < 64) {
+                uint32_t pos = 0;
+                unsigned long long head = tid < slices ? sh.surv[tid * a.top_k] : 0ull;
+                for (uint32_t i = 0; i < count; ++i) {
+                    const unsigned long long b = wave_max_dpp(head);
+                    if (tid == 0) sh.cand[i] = b;
+                    if (b != 0ull && head == b) {
+                        ++pos;
+                        head = pos < a.top_k ? sh.surv[tid * a.top_k + pos] : 0ull;
+                    }
+                }
+            }
             __syncthreads();
           } else {
             // Radix select: the key of the count-th largest finite score.
@@ -377,7 +444,7 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
     SampleArgs b = a;
     const uint32_t slices = (a.vocab + kLocalIds - 1) / kLocalIds;
     const bool two_stage = a.cand_buf && a.cand_nf && a.temperature > 0.0f && a.top_k <= kFastTopK &&
-                           slices * a.top_k <= static_cast<uint32_t>(kSurvivors);
+                           slices <= 64u && slices * a.top_k <= static_cast<uint32_t>(kSurvivors);
     if (!two_stage) {
         b.cand_buf = nullptr;
         b.cand_nf = nullptr;
