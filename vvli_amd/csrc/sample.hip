@@ -18,9 +18,10 @@
 // Two-stage top-k (top_k <= 128, at most 64 slices, scratch given):
 // sample_local_kernel cuts the vocab into slices of 4096 ids, one block each,
 // and writes a slice's top_k keys (score key << 32 | ~id; 0 for a non-finite
-// score), descending, with its finite count: top_k rounds of a block max over
-// keys held in registers. The keys are distinct, so every member of the global
-// top_k is in its slice's top_k; the sampling block's first wave then merges
+// score), descending, with its finite count: each wave takes the top_k of its
+// 256 ids (top_k rounds of a wave max over keys held in registers) and the
+// first wave merges the 16 lists. The keys are distinct, so every member of
+// the global top_k is in its slice's top_k; the sampling block's first wave then merges
 // the slices' sorted lists (one list head per lane) instead of scanning the
 // vocab (one block's scan is ~1 ms at a 128K vocab).
 #include "device_common.hpp"
@@ -126,30 +127,22 @@ __device__ inline unsigned long long wave_max_dpp(unsigned long long v) {
     return m3 > m ? m3 : m;
 }
 
-// The k largest of the block's keys (R per thread, distinct, 0 = none),
-// descending, into out[0 .. k) (written by thread 0): k rounds of a block max
-// -- registers, then wave shuffles, then 16 wave maxima in LDS (red holds two
-// rounds, so one barrier per round) -- the winner's owner zeroing its copy.
-template <int R>
-__device__ inline void block_topk(unsigned long long (&v)[R], uint32_t k, unsigned long long* out,
-                                  unsigned long long (*red)[kT / 64]) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Merges up to 64 descending lists (list s at lists[s * len], zero padded;
+// keys distinct) with one fully active wave, lane s holding list s's head:
+// the k largest keys, descending, to out[0 .. k) (written by lane 0).
+__device__ inline void wave_merge(const unsigned long long* lists, uint32_t n_lists, uint32_t len, uint32_t k,
+                                  unsigned long long* out) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t pos = 0;
+    unsigned long long head = lane < n_lists ? lists[lane * len] : 0ull;
     for (uint32_t i = 0; i < k; ++i) {
-        unsigned long long mx = 0ull;
-#pragma unroll
-        for (int r = 0; r < R; ++r) mx = v[r] > mx ? v[r] : mx;
-        mx = wave_max_dpp(mx);
-        if (lane == 0) red[i & 1][wave] = mx;
-        __syncthreads();
-        unsigned long long b = 0ull;
-#pragma unroll
-        for (int w = 0; w < kT / 64; ++w) b = red[i & 1][w] > b ? red[i & 1][w] : b;
-        if (threadIdx.x == 0) out[i] = b;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (v[r] == b) v[r] = 0ull;
+        const unsigned long long b = wave_max_dpp(head);
+        if (lane == 0) out[i] = b;
+        if (b != 0ull && head == b) {  // the one owner (lanes past n_lists hold 0)
+            ++pos;
+            head = pos < len ? lists[lane * len + pos] : 0ull;
+        }
     }
-    __syncthreads();
 }
 
 struct SampleShared {
@@ -189,15 +182,17 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* buf) {
 
 // One slice of kLocalIds ids per block: its top_k keys and its finite count.
 __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
-    constexpr int R = kLocalIds / kT;
-    __shared__ unsigned long long red[2][kT / 64];
-    __shared__ uint32_t nred[kT / 64];
-    const uint32_t tid = threadIdx.x, base = blockIdx.x * kLocalIds;
+    constexpr int R = kLocalIds / kT;  // keys per lane
+    constexpr int W = kT / 64;
+    __shared__ unsigned long long lists[W * kFastTopK];
+    __shared__ uint32_t nred[W];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t base = blockIdx.x * kLocalIds + wave * (64 * R), k = a.top_k;
     uint32_t nf = 0;
     unsigned long long v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t id = base + tid + r * kT;  // coalesced
+        const uint32_t id = base + r * 64 + lane;  // the wave's 256 ids, coalesced
         v[r] = 0ull;
         if (id < a.vocab) {
             const float s = adjusted(a.logits[id], a.counts ? a.counts[id] : 0u, a.repeat_penalty);
@@ -207,13 +202,27 @@ __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
             }
         }
     }
+    // The wave's top k, descending: k rounds of a wave max, the owner zeroing its copy.
+    for (uint32_t i = 0; i < k; ++i) {
+        unsigned long long mx = v[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r) mx = v[r] > mx ? v[r] : mx;
+        const unsigned long long b = wave_max_dpp(mx);
+        if (lane == 0) lists[wave * k + i] = b;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (v[r] == b) v[r] = 0ull;
+    }
     for (int off = 32; off > 0; off >>= 1) nf += __shfl_xor(nf, off, 64);
-    if ((tid & 63) == 0) nred[tid >> 6] = nf;
-    block_topk(v, a.top_k, a.cand_buf + static_cast<size_t>(blockIdx.x) * a.top_k, red);
-    if (tid == 0) {
-        uint32_t total = 0;
-        for (int w = 0; w < kT / 64; ++w) total += nred[w];
-        a.cand_nf[blockIdx.x] = total;
+    if (lane == 0) nred[wave] = nf;
+    __syncthreads();
+    if (wave == 0) {
+        wave_merge(lists, W, k, k, a.cand_buf + static_cast<size_t>(blockIdx.x) * k);
+        if (lane == 0) {
+            uint32_t total = 0;
+            for (int w = 0; w < W; ++w) total += nred[w];
+            a.cand_nf[blockIdx.x] = total;
+        }
     }
 }
 
@@ -280,18 +289,7 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             for (uint32_t j = tid; j < total; j += kT) sh.surv[j] = a.cand_buf[j];
             for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = 0ull;
             __syncthreads();
-            if (tid < 64) {
-                uint32_t pos = 0;
-                unsigned long long head = tid < slices ? sh.surv[tid * a.top_k] : 0ull;
-                for (uint32_t i = 0; i < count; ++i) {
-                    const unsigned long long b = wave_max_dpp(head);
-                    if (tid == 0) sh.cand[i] = b;
-                    if (b != 0ull && head == b) {
-                        ++pos;
-                        head = pos < a.top_k ? sh.surv[tid * a.top_k + pos] : 0ull;
-                    }
-                }
-            }
+            if (tid < 64) wave_merge(sh.surv, slices, a.top_k, count, sh.cand);
             __syncthreads();
           } else {
             // Radix select: the key of the count-th largest finite score.
