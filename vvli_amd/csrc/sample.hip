@@ -98,33 +98,28 @@ __device__ inline void bitonic_desc(unsigned long long* k, uint32_t n) {
 }
 
 // Max over a fully active wave: DPP within each 16-lane row (quad swaps, then
-// half-row and row mirrors), then the four row maxima read out of lanes 0, 16,
-// 32, 48. No LDS round trips, unlike a shuffle butterfly.
-template <int CTRL>
-__device__ inline unsigned long long dpp_max_step(unsigned long long v) {
-    const int lo = static_cast<int>(static_cast<uint32_t>(v)), hi = static_cast<int>(static_cast<uint32_t>(v >> 32));
-    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false));
-    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false));
-    const unsigned long long o = (static_cast<unsigned long long>(ohi) << 32) | olo;
-    return o > v ? o : v;
+// half-row and row mirrors; the moves fold into v_max_u32's DPP operand),
+// then the four row maxima read out of lanes 0, 16, 32, 48. No LDS round
+// trips, unlike a shuffle butterfly.
+__device__ inline uint32_t wave_max_u32_dpp(uint32_t x) {
+    x = max(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xf, 0xf, true)));   // quad_perm [1,0,3,2]
+    x = max(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xf, 0xf, true)));   // quad_perm [2,3,0,1]
+    x = max(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xf, 0xf, true)));  // row_half_mirror
+    x = max(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xf, 0xf, true)));  // row_mirror
+    const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 0));
+    const uint32_t m1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 16));
+    const uint32_t m2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 32));
+    const uint32_t m3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 48));
+    return max(max(m0, m1), max(m2, m3));
 }
 
-__device__ inline unsigned long long readlane_u64(unsigned long long v, int lane) {
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
-    return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
+// 64-bit max as two 32-bit ones: the high halves, then the low halves of the
+// lanes holding the maximal high half.
 __device__ inline unsigned long long wave_max_dpp(unsigned long long v) {
-    v = dpp_max_step<0xB1>(v);   // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E>(v);   // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x141>(v);  // row_half_mirror
-    v = dpp_max_step<0x140>(v);  // row_mirror: every lane holds its row's max
-    unsigned long long m = readlane_u64(v, 0);
-    const unsigned long long m1 = readlane_u64(v, 16), m2 = readlane_u64(v, 32), m3 = readlane_u64(v, 48);
-    m = m1 > m ? m1 : m;
-    m = m2 > m ? m2 : m;
-    return m3 > m ? m3 : m;
+    const uint32_t hi = static_cast<uint32_t>(v >> 32);
+    const uint32_t h = wave_max_u32_dpp(hi);
+    const uint32_t l = wave_max_u32_dpp(hi == h ? static_cast<uint32_t>(v) : 0u);
+    return (static_cast<unsigned long long>(h) << 32) | l;
 }
 
 // Merges up to 64 descending lists (list s at lists[s * len], zero padded;
