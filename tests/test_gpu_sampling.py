@@ -57,6 +57,37 @@ def test_sampler_next_matches_oracle(k, vocab, oracle_mod):
         assert np.array_equal(st_gpu, st_orc), f"trial {trial}: PRNG state"
 
 
+# Two-stage top-k boundaries (slices of 4096 ids, at most 64 slices, slices * top_k <= 4096):
+# 38 slices with a 512-id last slice; exactly 64 slices of 64 survivors (every merge lane holds a
+# list); 65 slices (the single-block path instead).
+@pytest.mark.parametrize("vocab,top_k", [(152064, 100), (262144, 64), (262145, 40)])
+@pytest.mark.parametrize("layout", ["spread", "one_slice", "few_finite"])
+def test_sampler_slice_boundaries(vocab, top_k, layout, oracle_mod):
+    o = opts(top_k=top_k, top_p=1.0, temperature=1.1)
+    rng = np.random.default_rng(vocab % 1000 + top_k)
+    st_gpu = R.prng_seed(7)
+    st_orc = st_gpu.copy()
+    print(f"sampler vocab={vocab} top_k={top_k} layout={layout}", flush=True)
+    for trial in range(6):
+        logits = rng.normal(0, 2, vocab).astype(np.float32)
+        if layout == "one_slice":  # the whole top_k (and more) in one slice: its list runs out
+            s0 = int(rng.integers(0, vocab // 4096)) * 4096
+            logits[s0 + rng.permutation(4096)[: top_k + 20]] += 25.0
+        elif layout == "few_finite":  # fewer finite scores than top_k: zero-padded lists
+            keep = rng.integers(0, vocab, top_k // 2)
+            vals = logits[keep].copy()
+            logits[:] = -np.inf
+            logits[rng.integers(0, vocab, 100)] = np.nan
+            logits[keep] = vals
+        if trial % 2:  # the last id among the leaders (the ragged last slice)
+            logits[vocab - 1] = np.nanmax(np.where(np.isfinite(logits), logits, -1e30)) + 1.0
+        prompt = rng.integers(0, vocab, 16)
+        t_gpu = R.sampler_next(logits, prompt, [], o, st_gpu)
+        t_orc = oracle_mod.sampler_next(logits, prompt, [], o, st_orc)
+        assert t_gpu == t_orc, f"trial {trial}"
+        assert np.array_equal(st_gpu, st_orc), f"trial {trial}: PRNG state"
+
+
 def test_sampler_edge_cases(oracle_mod):
     o = opts(top_k=5)
     st = R.prng_seed(3)
