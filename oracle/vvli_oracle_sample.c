@@ -9,11 +9,12 @@
  * outputs) and Random.float(f32) (23 random mantissa bits, the exponent from
  * the leading zeros of the remaining bits). Zig's standard library is not in
  * the reference tree; these are restated from their published algorithms.
- * Pinned: SplitMix64 against its published first outputs for seed 0; the
+ * Pinned: SplitMix64 against its published first outputs for seed 0;
+ * xoshiro256++ against Blackman and Vigna's published known-answer vector
+ * (state {1, 2, 3, 4}); float(f32) by closed forms on that stream; the
  * deterministic steps (penalties, candidates, probabilities, top-p cut, the
  * cumulative pick) against the reference's own tests (src/generator.zig:
- * 491-512) and closed forms. The xoshiro256++ stream and float(f32) beyond
- * that are "parity unpinned": nothing in the reference tree fixes them.
+ * 491-512) and closed forms.
  */
 #include <math.h>
 #include <stdlib.h>

@@ -1,7 +1,7 @@
 """The oracle's sampler (oracle/vvli_oracle_sample.c) against the reference's
-own sampler tests (src/generator.zig:491-512), closed forms, and the published
-SplitMix64 sequence. The xoshiro256++ stream beyond its SplitMix64 seeding is
-parity unpinned (Zig's std is not in the reference tree)."""
+own sampler tests (src/generator.zig:491-512), closed forms, the published
+SplitMix64 sequence and the published xoshiro256++ known-answer vector (Zig's
+std, which holds DefaultPrng, is not in the reference tree)."""
 import ctypes
 import math
 
@@ -24,6 +24,31 @@ def test_splitmix64_published_sequence(oracle_mod):
     assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
     # DefaultPrng.init: the state is four SplitMix64 outputs.
     assert [int(x) for x in oracle_mod.prng_seed(0)] == got
+
+
+# xoshiro256++ from state {1, 2, 3, 4}: the first ten outputs of Blackman and Vigna's reference
+# implementation (the known-answer vector Rust's rand_xoshiro also checks).
+XOSHIRO256PP_1234 = [41943041, 58720359, 3588806011781223, 3591011842654386, 9228616714210784205,
+                     9973669472204895162, 14011001112246962877, 12406186145184390807, 15849039046786891736,
+                     10450023813501588000]
+
+
+def test_xoshiro256pp_published_vector(oracle_mod):
+    st = np.array([1, 2, 3, 4], dtype=np.uint64)
+    got = [int(oracle_mod.lib().orc_prng_next(oracle_mod._p(st))) for _ in range(10)]
+    assert got == XOSHIRO256PP_1234
+
+
+def test_float_f32_on_the_published_stream(oracle_mod):
+    """Random.float(f32): 23 mantissa bits from the output's low bits, exponent 126 - clz(output).
+    The first five outputs have 38, 38, 12, 12 and 0 leading zeros: 0x2800001 -> 2^-39 * (1 + 2^-23),
+    0x3800067 -> exponent 88 with mantissa 0x67, and the fifth (>= 2^63) lands in [0.5, 1)."""
+    st = np.array([1, 2, 3, 4], dtype=np.uint64)
+    bits = [int(np.float32(oracle_mod.lib().orc_prng_float(oracle_mod._p(st))).view(np.uint32)) for _ in range(5)]
+    assert bits == [0x2C000001, 0x2C000067, 0x39000067, 0x394400B2, 0x3F4433CD]
+    assert np.float32(np.uint32(0x2C000001).view(np.float32)) == np.float32(2.0**-39 * (1 + 2.0**-23))
+    # Each draw consumed exactly one output: the state now yields the sixth.
+    assert int(oracle_mod.lib().orc_prng_next(oracle_mod._p(st))) == XOSHIRO256PP_1234[5]
 
 
 def test_library_seed_mapping_matches_oracle(oracle_mod):
