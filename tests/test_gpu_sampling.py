@@ -57,10 +57,11 @@ def test_sampler_next_matches_oracle(k, vocab, oracle_mod):
         assert np.array_equal(st_gpu, st_orc), f"trial {trial}: PRNG state"
 
 
-# Two-stage top-k boundaries (slices of 4096 ids, at most 64 slices, slices * top_k <= 4096):
-# 38 slices with a 512-id last slice; exactly 64 slices of 64 survivors (every merge lane holds a
-# list); 65 slices (the single-block path instead).
-@pytest.mark.parametrize("vocab,top_k", [(152064, 100), (262144, 64), (262145, 40)])
+# Two-stage top-k boundaries (slices of 4096 ids, at most 64 slices; lists staged in LDS up to
+# 4096 keys, merged from the scratch beyond): 38 slices with a 512-id last slice, staged (100) and
+# not (128); exactly 64 slices (every merge lane holds a list) of 64 (staged) and 128 keys; 65
+# slices (the single-block path instead).
+@pytest.mark.parametrize("vocab,top_k", [(152064, 100), (152064, 128), (262144, 64), (262144, 128), (262145, 40)])
 @pytest.mark.parametrize("layout", ["spread", "one_slice", "few_finite"])
 def test_sampler_slice_boundaries(vocab, top_k, layout, oracle_mod):
     o = opts(top_k=top_k, top_p=1.0, temperature=1.1)

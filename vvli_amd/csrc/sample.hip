@@ -15,7 +15,8 @@
 //            (sampleCandidate, :451-463).
 // Sequential f32 sums in candidate order keep the reference's rounding.
 //
-// Two-stage top-k (top_k <= 128, at most 64 slices, scratch given):
+// Two-stage top-k (top_k <= 128, at most 64 slices, scratch of
+// sample_cand_elems keys given):
 // sample_local_kernel cuts the vocab into slices of 4096 ids, one block each,
 // and writes a slice's top_k keys (score key << 32 | ~id; 0 for a non-finite
 // score), descending, with its finite count: each wave takes the top_k of its
@@ -75,7 +76,7 @@ __device__ inline float prng_float(uint64_t* s) {
 
 constexpr int kLocalIds = 4096;  // vocab slice of a local top-k block
 constexpr int kFastTopK = 128;   // largest top_k of the two-stage path
-constexpr int kSurvivors = 4096; // slices * top_k the sampling block merges (slices <= 64)
+constexpr int kSurvivors = 4096; // slice lists the sampling block stages in LDS (more: merged from scratch)
 
 // Descending bitonic sort of n (a power of two) keys in LDS by the block.
 __device__ inline void bitonic_desc(unsigned long long* k, uint32_t n) {
@@ -280,11 +281,14 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             // The slices' lists (each top_k keys, descending, zero padded): the
             // first wave merges them, lane s holding list s's head; the top
             // count heads taken are the candidates, in order.
+            // Lists staged in LDS when they fit, else merged from the scratch.
             const uint32_t total = slices * a.top_k;
-            for (uint32_t j = tid; j < total; j += kT) sh.surv[j] = a.cand_buf[j];
+            const bool staged = total <= static_cast<uint32_t>(kSurvivors);
+            if (staged)
+                for (uint32_t j = tid; j < total; j += kT) sh.surv[j] = a.cand_buf[j];
             for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = 0ull;
             __syncthreads();
-            if (tid < 64) wave_merge(sh.surv, slices, a.top_k, count, sh.cand);
+            if (tid < 64) wave_merge(staged ? sh.surv : a.cand_buf, slices, a.top_k, count, sh.cand);
             __syncthreads();
           } else {
             // Radix select: the key of the count-th largest finite score.
@@ -430,14 +434,17 @@ __global__ __launch_bounds__(kT) void sample_counts_kernel(uint32_t* counts, uin
 
 }  // namespace
 
-size_t sample_cand_elems(uint32_t vocab) { return static_cast<size_t>(kSurvivors); }
+size_t sample_cand_elems(uint32_t vocab) {
+    const size_t slices = (vocab + kLocalIds - 1) / kLocalIds;
+    return (slices <= 64 ? slices : 1) * kFastTopK;
+}
 size_t sample_nf_elems(uint32_t vocab) { return (vocab + kLocalIds - 1) / kLocalIds; }
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
     SampleArgs b = a;
     const uint32_t slices = (a.vocab + kLocalIds - 1) / kLocalIds;
     const bool two_stage = a.cand_buf && a.cand_nf && a.temperature > 0.0f && a.top_k <= kFastTopK &&
-                           slices <= 64u && slices * a.top_k <= static_cast<uint32_t>(kSurvivors);
+                           slices <= 64u;
     if (!two_stage) {
         b.cand_buf = nullptr;
         b.cand_nf = nullptr;
