@@ -163,7 +163,10 @@ int vvli_gpu_forward_token(vvli_gpu_model* model, uint32_t token, uint32_t pos, 
 int vvli_gpu_forward_embedding(vvli_gpu_model* model, const float* embedding, uint32_t pos, float* logits_out,
                                uint32_t* argmax_out);
 /* forwardToken that also returns the residual stream after every layer
- * (hidden_out: layers*hidden floats, layer-major) for per-layer parity. */
+ * (hidden_out: layers*hidden floats, layer-major) for per-layer parity. It
+ * runs on the path forward_token takes (vvli_gpu_set_decode_path): the
+ * persistent step, whose down-projection phases then also write the rows, or
+ * the per-kernel step. */
 int vvli_gpu_forward_token_debug(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* logits_out,
                                  float* hidden_out);
 /* Read back one KV-cache row (kv_heads*head_dim floats each; either output
@@ -260,6 +263,13 @@ int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t 
  * for prefill its one launch. VVLI_INVALID_CONFIG if no persistent launch
  * has run. Waits for the launch to finish. */
 int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
+/* Test hook for the persistent step's failure path (no reference
+ * counterpart): the n-th persistent launch from now (n >= 1; 0 cancels)
+ * starts with its device error flag raised, as if a poll of an earlier launch
+ * had timed out. Its blocks leave before any phase, and the call that waits
+ * for it returns VVLI_HIP_ERROR; the flag is cleared once the host has read
+ * it. */
+int vvli_gpu_test_inject_step_error(vvli_gpu_model* model, uint32_t n);
 
 /* ---------------------------------------------------------------------- */
 /* Isolated matmul op (device pointers)                                    */

@@ -106,6 +106,7 @@ def lib() -> ctypes.CDLL:
             "orc_kv_clear": (None, [c_void_p]),
             "orc_set_rope_table": (c_int, [c_void_p, c_void_p, c_uint32]),
             "orc_forward_token": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+            "orc_prefill": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
             "orc_forward_embedding": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
             "orc_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
             "orc_generate_greedy": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_int64, c_void_p, P(c_uint32),
@@ -310,6 +311,13 @@ class OracleRunner:
                   if want_hidden else None)
         _check(lib().orc_forward_embedding(self._h, _p(emb), pos, _p(self.logits), _p(hidden)))
         return (self.logits.copy(), hidden) if want_hidden else self.logits.copy()
+
+    def prefill(self, tokens, start_pos: int = 0) -> np.ndarray:
+        """The prompt loop with its loops interchanged (orc_prefill): same KV
+        rows and last logits as one forward_token per token."""
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        _check(lib().orc_prefill(self._h, _p(toks), toks.size, start_pos, _p(self.logits)))
+        return self.logits.copy()
 
     def kv_read(self, layer: int, pos: int):
         kv = self.cfg.kv_dim() if hasattr(self.cfg, "kv_dim") else None

@@ -639,6 +639,177 @@ int orc_forward_embedding(orc_runner* r, const float* embedding, uint32_t pos, f
     return forward_current(r, pos, logits_out, hidden_out);
 }
 
+/* ------------------------------------------------------------------------ */
+/* prompt pass: the prompt loop of src/generator.zig:243-251 (one           */
+/* forwardToken per prompt token) with its loops interchanged so that a     */
+/* weight row is read once per block of tokens instead of once per token.   */
+/* Every value is computed by the same functions in the same order as       */
+/* orc_forward_token computes it for that token, so the KV rows and the     */
+/* last token's logits are bit-identical to the token loop's (only the      */
+/* work order across tokens and rows differs). A token's attention reads    */
+/* rows 0..its pos, all written before any attention of the layer runs.     */
+/* ------------------------------------------------------------------------ */
+
+#define PF_TOKEN_BLOCK 16
+
+typedef struct pf_linear_job {
+    const orc_runner* r;
+    float* out; /* [n][rows] */
+    size_t w_off, bias_off, rows, cols;
+    const float* x; /* [n][cols] */
+    size_t n;
+    size_t row0, row1;
+} pf_linear_job;
+
+static void* pf_linear_worker(void* arg) {
+    pf_linear_job* j = (pf_linear_job*)arg;
+    const orc_runner* r = j->r;
+    const uint32_t kind = r->c.weight_kind;
+    const void* w = kind == 1 ? (const void*)((const uint16_t*)r->blob + j->w_off)
+                              : (const void*)((const float*)r->blob + j->w_off);
+    const void* bias = j->bias_off == (size_t)-1 ? NULL
+                       : (kind == 1 ? (const void*)((const uint16_t*)r->blob + j->bias_off)
+                                    : (const void*)((const float*)r->blob + j->bias_off));
+    for (size_t t0 = 0; t0 < j->n; t0 += PF_TOKEN_BLOCK) {
+        size_t t1 = t0 + PF_TOKEN_BLOCK < j->n ? t0 + PF_TOKEN_BLOCK : j->n;
+        for (size_t row = j->row0; row < j->row1; ++row)
+            for (size_t t = t0; t < t1; ++t) /* linear_range's expression for one row */
+                j->out[t * j->rows + row] =
+                    (kind == 1 ? orc_dot_bf16((const uint16_t*)w + row * j->cols, j->x + t * j->cols, j->cols, r->lanes)
+                               : orc_dot_f32((const float*)w + row * j->cols, j->x + t * j->cols, j->cols, r->lanes)) +
+                    (bias ? weight_at(bias, kind, row) : 0.0f);
+    }
+    return NULL;
+}
+
+static int pf_threads(const orc_runner* r) {
+    long t = r->threads == 0 ? sysconf(_SC_NPROCESSORS_ONLN) : r->threads;
+    return t < 1 ? 1 : (t > MAX_WORKERS ? MAX_WORKERS : (int)t);
+}
+
+static int pf_linear(const orc_runner* r, float* out, size_t w_off, size_t rows, size_t cols, const float* x, size_t n,
+                     size_t bias_off) {
+    int nt = pf_threads(r);
+    pthread_t tid[MAX_WORKERS];
+    pf_linear_job jobs[MAX_WORKERS];
+    size_t per = (rows + (size_t)nt - 1) / (size_t)nt;
+    int spawned = 0;
+    for (int i = 0; i < nt; ++i) {
+        size_t a = (size_t)i * per, b = a + per < rows ? a + per : rows;
+        jobs[i] = (pf_linear_job){r, out, w_off, bias_off, rows, cols, x, n, a < rows ? a : rows, b};
+    }
+    for (; spawned + 1 < nt; ++spawned)
+        if (pthread_create(&tid[spawned], NULL, pf_linear_worker, &jobs[spawned]) != 0) {
+            for (int i = 0; i < spawned; ++i) pthread_join(tid[i], NULL);
+            return ORC_THREAD_SPAWN_FAILED;
+        }
+    pf_linear_worker(&jobs[nt - 1]);
+    for (int i = 0; i < spawned; ++i) pthread_join(tid[i], NULL);
+    return ORC_OK;
+}
+
+typedef struct pf_attn_job {
+    const orc_runner* r;
+    float* attn;     /* [n][h] */
+    const float* q;  /* [n][h], rotated */
+    const float* kl; /* this layer's cache */
+    const float* vl;
+    size_t n, start, first, stride;
+    float* scores;   /* max_seq floats of this worker */
+} pf_attn_job;
+
+static void* pf_attn_worker(void* arg) {
+    pf_attn_job* j = (pf_attn_job*)arg;
+    const orc_config* c = &j->r->c;
+    size_t h = c->hidden, hd = head_dim(c);
+    for (size_t t = j->first; t < j->n; t += j->stride)
+        orc_attention(j->attn + t * h, j->q + t * h, j->kl, j->vl, c->heads, c->kv_heads, hd, j->start + t, j->scores,
+                      j->r->lanes);
+    return NULL;
+}
+
+int orc_prefill(orc_runner* r, const uint32_t* tokens, uint32_t n, uint32_t start_pos, float* logits_out) {
+    if (!r || !tokens) return ORC_NULL_ARG;
+    if (n == 0) return ORC_EMPTY_PROMPT;
+    if ((uint64_t)start_pos + n > r->max_seq) return ORC_CONTEXT_FULL;
+    const orc_config* c = &r->c;
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= c->vocab) return ORC_INVALID_TOKEN;
+    size_t h = c->hidden, kv = kv_dim(c), hd = head_dim(c), inter = c->inter;
+    int nt = pf_threads(r);
+    float* x = aligned_floats((size_t)n * h);
+    float* res = aligned_floats((size_t)n * h);
+    float* nrm = aligned_floats((size_t)n * h);
+    float* q = aligned_floats((size_t)n * h);
+    float* k = aligned_floats((size_t)n * kv);
+    float* v = aligned_floats((size_t)n * kv);
+    float* attn = aligned_floats((size_t)n * h);
+    float* proj = aligned_floats((size_t)n * h);
+    float* gate = aligned_floats((size_t)n * inter);
+    float* up = aligned_floats((size_t)n * inter);
+    float* scores = aligned_floats((size_t)nt * r->max_seq);
+    float* bufs[] = {x, res, nrm, q, k, v, attn, proj, gate, up, scores};
+    int rc = ORC_OK;
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
+        if (!bufs[i]) rc = ORC_OUT_OF_MEMORY;
+    for (uint32_t t = 0; rc == ORC_OK && t < n; ++t) { /* copyEmbeddingToken (src/llm.zig:1373-1380) */
+        size_t start = r->embed + (size_t)tokens[t] * h;
+        for (size_t i = 0; i < h; ++i) x[t * h + i] = weight_at(r->blob, c->weight_kind, start + i);
+    }
+    for (uint32_t l = 0; rc == ORC_OK && l < c->layers; ++l) { /* forwardLayer (src/llm.zig:732-766) per token */
+        const orc_layer_offsets* o = &r->lo[l];
+        memcpy(res, x, (size_t)n * h * sizeof(float));
+        for (uint32_t t = 0; t < n; ++t)
+            orc_rmsnorm(nrm + t * h, x + t * h, wptr(r, o->input_norm), c->weight_kind, h, c->rms_eps, r->lanes);
+        if ((rc = pf_linear(r, q, o->q, h, h, nrm, n, o->q_bias))) break;
+        if ((rc = pf_linear(r, k, o->k, kv, h, nrm, n, o->k_bias))) break;
+        if ((rc = pf_linear(r, v, o->v, kv, h, nrm, n, o->v_bias))) break;
+        float* kl = r->keys + (size_t)l * r->max_seq * kv;
+        float* vl = r->values + (size_t)l * r->max_seq * kv;
+        for (uint32_t t = 0; t < n; ++t) {
+            orc_rope(q + t * h, c->heads, hd, start_pos + t, c->rope_theta, c->rope_layout, r->inv_freq);
+            orc_rope(k + t * kv, c->kv_heads, hd, start_pos + t, c->rope_theta, c->rope_layout, r->inv_freq);
+            memcpy(kl + (size_t)(start_pos + t) * kv, k + t * kv, kv * sizeof(float));
+            memcpy(vl + (size_t)(start_pos + t) * kv, v + t * kv, kv * sizeof(float));
+        }
+        {
+            pthread_t tid[MAX_WORKERS];
+            pf_attn_job jobs[MAX_WORKERS];
+            int spawned = 0;
+            for (int i = 0; i < nt; ++i)
+                jobs[i] = (pf_attn_job){r, attn, q, kl, vl, n, start_pos, (size_t)i, (size_t)nt,
+                                        scores + (size_t)i * r->max_seq};
+            for (; spawned + 1 < nt; ++spawned)
+                if (pthread_create(&tid[spawned], NULL, pf_attn_worker, &jobs[spawned]) != 0) {
+                    rc = ORC_THREAD_SPAWN_FAILED;
+                    break;
+                }
+            if (rc == ORC_OK) pf_attn_worker(&jobs[nt - 1]);
+            for (int i = 0; i < spawned; ++i) pthread_join(tid[i], NULL);
+            if (rc) break;
+        }
+        if ((rc = pf_linear(r, proj, o->o, h, h, attn, n, (size_t)-1))) break;
+        for (uint32_t t = 0; t < n; ++t) orc_add(x + t * h, res + t * h, proj + t * h, h);
+        memcpy(res, x, (size_t)n * h * sizeof(float));
+        for (uint32_t t = 0; t < n; ++t)
+            orc_rmsnorm(nrm + t * h, x + t * h, wptr(r, o->post_norm), c->weight_kind, h, c->rms_eps, r->lanes);
+        if ((rc = pf_linear(r, gate, o->gate, inter, h, nrm, n, (size_t)-1))) break;
+        if ((rc = pf_linear(r, up, o->up, inter, h, nrm, n, (size_t)-1))) break;
+        for (uint32_t t = 0; t < n; ++t) orc_silu_mul(gate + t * inter, gate + t * inter, up + t * inter, inter);
+        if ((rc = pf_linear(r, proj, o->down, h, inter, gate, n, (size_t)-1))) break;
+        for (uint32_t t = 0; t < n; ++t) orc_add(x + t * h, res + t * h, proj + t * h, h);
+    }
+    if (rc == ORC_OK) { /* the last token's forwardCurrentEmbedding tail (src/llm.zig:727-728) */
+        memcpy(r->x, x + (size_t)(n - 1) * h, h * sizeof(float));
+        orc_rmsnorm(r->norm, r->x, wptr(r, r->final_norm), c->weight_kind, h, c->rms_eps, r->lanes);
+        size_t head = c->tie ? r->embed : r->lm_head;
+        rc = linear(r, r->logits, head, c->vocab, h, r->norm, (size_t)-1);
+        if (rc == ORC_OK && logits_out) memcpy(logits_out, r->logits, (size_t)c->vocab * sizeof(float));
+    }
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i) free(bufs[i]);
+    return rc;
+}
+
 int orc_kv_read(const orc_runner* r, uint32_t layer, uint32_t pos, float* k_out, float* v_out) {
     if (!r) return ORC_NULL_ARG;
     if (layer >= r->c.layers || pos >= r->max_seq) return ORC_INVALID_CONFIG;

@@ -21,6 +21,7 @@
  *   silu-mul, add, argmax                     : closed forms, tie/NaN special cases
  *   whole forward (split-half, interleaved)   : HF transformers f32 golden fixtures (tests/golden)
  *   greedy generator loop                     : token-by-token replay against orc_forward_token
+ *   prompt pass (orc_prefill)                 : bit equality with the orc_forward_token loop
  * Bit-level agreement with Zig's std.math (pow/cos/sin/exp) and with the
  * host-dependent SIMD width is "parity unpinned"; tolerance-level parity is
  * pinned by the checks above.
@@ -124,6 +125,12 @@ int orc_set_rope_table(orc_runner* r, const float* inv_freq, uint32_t n);
 int orc_forward_token(orc_runner* r, uint32_t token, uint32_t pos, float* logits_out, float* hidden_out);
 int orc_forward_embedding(orc_runner* r, const float* embedding, uint32_t pos, float* logits_out,
                           float* hidden_out);
+/* The prompt loop (src/generator.zig:243-251): tokens at positions
+ * start_pos.. through every layer with the loops interchanged (weight rows
+ * shared by blocks of tokens, attention spread over threads by token). KV
+ * rows and the last token's logits are bit-identical to n orc_forward_token
+ * calls (checked by tests/test_oracle.py). */
+int orc_prefill(orc_runner* r, const uint32_t* tokens, uint32_t n, uint32_t start_pos, float* logits_out);
 int orc_kv_read(const orc_runner* r, uint32_t layer, uint32_t pos, float* k_out, float* v_out);
 
 /* ---- generator: src/generator.zig:142-175, 221-293 ---- */

@@ -66,16 +66,23 @@ def built():
     return True
 
 
-@pytest.mark.parametrize("name", list(CASES))
-def test_token_steps_match_oracle(name, built, oracle_mod, host_threads):
+STEP_CASES = [(n, "graph") for n in CASES] + [(n, "persistent") for n in CASES if CASES[n][1] == C.WEIGHT_BF16]
+
+
+@pytest.mark.parametrize("name,path", STEP_CASES)
+def test_token_steps_match_oracle(name, path, built, oracle_mod, host_threads):
+    """Per-layer residuals and logits of every step, on the per-kernel step
+    ('graph': the kernels launched eagerly) and on the persistent step (its
+    down-projection phases write the residual rows)."""
     cfg, kind, how, steps = CASES[name]
     max_seq = min(cfg.max_position_embeddings, 128)
     blob = make_blob(cfg, kind, how)
     orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
     rng = np.random.default_rng(1)
     toks = rng.integers(0, cfg.vocab_size, size=steps)
-    print(f"case={name} steps={steps}", flush=True)
+    print(f"case={name} path={path} steps={steps}", flush=True)
     with R.Runner(cfg, blob, max_seq) as gpu:
+        gpu.set_decode_path(path)
         for pos, tok in enumerate(toks):
             ref_logits, ref_hidden = orc.forward_token(int(tok), pos, want_hidden=True)
             logits, hidden = gpu.forward_token_debug(int(tok), pos)
@@ -102,6 +109,7 @@ def test_graph_step_equals_debug_step(name, built):
     toks = np.random.default_rng(2).integers(0, cfg.vocab_size, size=min(steps, 12))
     with R.Runner(cfg, blob, max_seq) as a, R.Runner(cfg, blob, max_seq) as b:
         a.set_decode_path("graph")
+        b.set_decode_path("graph")  # forward_token_debug then launches the same kernels eagerly
         for pos, tok in enumerate(toks):
             la = a.forward_token(int(tok), pos).copy()
             am = a.last_argmax
@@ -227,3 +235,53 @@ def test_llama3_rope_table_matches_oracle(path, built, oracle_mod, host_threads)
         for pos, tok in enumerate(toks[:8]):
             ref_plain = orc2.forward_token(int(tok), pos)
         assert rel_err(plain, ref_plain) <= TOL
+
+
+def test_persistent_error_flag_is_reported(built, oracle_mod, host_threads):
+    """The persistent step's failure path, forced from the host
+    (vvli_gpu_test_inject_step_error): a launch that starts with its error
+    flag raised leaves before any phase and the waiting call returns
+    VVLI_HIP_ERROR; the runner works afterwards. In the sampled generation
+    loop, which checks the flag only at its end, a flag raised in a middle
+    launch is still reported (later launches must not clear it)."""
+    cfg, kind, how, _ = CASES["qwen_small"]
+    blob = make_blob(cfg, kind, how)
+    lib = R._lib.lib()
+    toks = [5, 77, 300, 12]
+    orc = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+    print("inject: forward_token", flush=True)
+    with R.Runner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path("persistent")
+        gpu.forward_token(toks[0], 0)
+        R._lib.check(lib.vvli_gpu_test_inject_step_error(gpu._h, 1))
+        with pytest.raises(VvliError) as e:
+            gpu.forward_token(toks[1], 1)
+        assert e.value.rc == 8 and "injected" in str(e.value)
+        # The flag was read and cleared: the step runs again and the runner continues.
+        for pos in range(len(toks)):
+            ref = orc.forward_token(toks[pos], pos)
+            if pos == 0:
+                continue
+            got = gpu.forward_token(toks[pos], pos)
+            assert rel_err(got, ref) <= TOL and gpu.last_argmax == oracle_mod.argmax(ref)
+    print("inject: sampled generation, third per-token launch", flush=True)
+    prompt = np.array(toks, dtype=np.uint32)
+    opts = R.Sampling(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=7)
+    with R.Runner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path("persistent")
+        R._lib.check(lib.vvli_gpu_test_inject_step_error(gpu._h, 3))
+        with pytest.raises(VvliError) as e:
+            gpu.generate(prompt, 8, opts, batched_prefill=True)
+        assert e.value.rc == 8
+        gpu.kv_clear()
+        got, _ = gpu.generate(prompt, 8, opts, batched_prefill=True)
+    ref_orc = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+    want = ref_orc.generate_sampled(prompt, 8, opts)
+    np.testing.assert_array_equal(got, want)
+    print("inject: greedy generation, decode launch", flush=True)
+    with R.Runner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path("persistent")
+        R._lib.check(lib.vvli_gpu_test_inject_step_error(gpu._h, 2))  # 1: the prompt launch, 2: decode
+        with pytest.raises(VvliError) as e:
+            gpu.generate_greedy_measured(prompt, 8)
+        assert e.value.rc == 8

@@ -361,6 +361,50 @@ def test_generator_loop_replays_forward_steps(oracle_mod):
     assert list(toks2) == manual[: manual.index(eos) + 1]
 
 
+@pytest.mark.parametrize("case", ["tiny_f32", "qwen_bf16", "llama_bf16_untied"])
+def test_prefill_pass_equals_token_loop(oracle_mod, case):
+    """orc_prefill (the prompt loop with its loops interchanged, used for the
+    long-prompt GPU cases) leaves bit-identical KV rows and last logits to one
+    orc_forward_token per token, over two calls (start_pos > 0) that cross
+    token blocks and thread boundaries unevenly."""
+    if case == "tiny_f32":
+        import dataclasses
+
+        cfg, kind = dataclasses.replace(C.tiny_test(), max_position_embeddings=64), C.WEIGHT_F32
+        blob = R.deterministic_blob(cfg, kind)
+    else:
+        kw = dict(vocab_size=300, hidden_size=128, intermediate_size=192, num_hidden_layers=2,
+                  num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=128, rope_theta=1e6,
+                  rms_norm_eps=1e-6, tie_word_embeddings=True, architecture="qwen2", qkv_bias=True,
+                  rope_layout=C.ROPE_SPLIT_HALF)
+        if case == "llama_bf16_untied":
+            kw.update(qkv_bias=False, tie_word_embeddings=False, architecture="llama",
+                      rope_layout=C.ROPE_INTERLEAVED, rms_norm_eps=1e-5, num_attention_heads=8)
+        cfg, kind = C.Config(**kw), C.WEIGHT_BF16
+        blob = R.synthetic_blob(cfg, kind, seed=5)
+    toks = np.random.default_rng(9).integers(0, cfg.vocab_size, size=53)
+    n1 = 37
+    loop = oracle_mod.OracleRunner(cfg, blob, 64, threads=3)
+    for pos, t in enumerate(toks):
+        want = loop.forward_token(int(t), pos)
+        if pos == n1 - 1:
+            want_mid = want
+    batch = oracle_mod.OracleRunner(cfg, blob, 64, threads=5)
+    got_mid = batch.prefill(toks[:n1], 0)
+    got = batch.prefill(toks[n1:], n1)
+    assert np.array_equal(got_mid.view(np.uint32), want_mid.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for layer in range(cfg.num_hidden_layers):
+        for pos in range(len(toks)):
+            a, b = batch.kv_read(layer, pos), loop.kv_read(layer, pos)
+            assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32)), (layer, pos)
+            assert np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32)), (layer, pos)
+    # The next token step continues from the same state.
+    nxt = oracle_mod.argmax(want)
+    assert np.array_equal(batch.forward_token(nxt, len(toks)).view(np.uint32),
+                          loop.forward_token(nxt, len(toks)).view(np.uint32))
+
+
 def test_llama3_rope_table_matches_hf_fixture(oracle_mod):
     """Llama-3 RoPE scaling (no reference counterpart): the oracle's table and
     the library's vvli_host_llama3_inv_freq against Hugging Face's

@@ -100,7 +100,7 @@ __device__ __forceinline__ bool poll_tw(const tword* p, uint32_t tag, tword& w, 
     uint32_t spins = 0;
     while (tw_tag(w) != tag) {
         if (++spins > kSpinLimit) {
-            st_a(err, 1u);
+            st_a(err, kDecodeErrTimeout);
             return false;
         }
         if ((spins & 63u) == 0 && ld_a(err) != 0) return false;
@@ -118,7 +118,7 @@ __device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint3
     uint32_t spins = 0;
     while (tw_tag(w0) != tag || tw_tag(w1) != tag) {
         if (++spins > kSpinLimit) {
-            st_a(err, 1u);
+            st_a(err, kDecodeErrTimeout);
             return false;
         }
         if ((spins & 63u) == 0 && ld_a(err) != 0) return false;
@@ -398,7 +398,7 @@ __device__ __forceinline__ void mk_glds_compute(const GLds& gl, const MkGemv& g,
 __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
                                         uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
                                         uint32_t tag, const MkResid& rs, uint32_t t0, const float* park,
-                                        uint32_t lds_first, uint32_t n_lds, uint32_t* err) {
+                                        uint32_t lds_first, uint32_t n_lds, uint32_t* err, float* dbg) {
     const int lane = w.lane;
     const uint32_t U = mk_units(g);
     const uint32_t per_item = kNJC * kWave;
@@ -460,6 +460,10 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
                     tword* o = mode == kGemvPlain ? seg_out(g, sa) : g.o0;
                     if (va) st_a(o + ra, tw_make(oa + ea, tag));
                     if (vb) st_a(o + rb, tw_make(ob + eb, tag));
+                    if (dbg) {  // residual stream after the layer (parity dumps only)
+                        if (va) dbg[ra] = oa + ea;
+                        if (vb) dbg[rb] = ob + eb;
+                    }
                 }
             }
             pending = 0;
@@ -573,7 +577,7 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
                     if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
                 if (done) break;
                 if (++spins > kSpinLimit) {
-                    st_a(err, 1u);
+                    st_a(err, kDecodeErrTimeout);
                     ok = false;
                     break;
                 }
@@ -891,7 +895,7 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 good = good && tw_tag(wv[s2]) == tag_out;                                                   \
             if (good) break;                                                                                \
             if (spins > kSpinLimit) {                                                                       \
-                st_a(p.error, 1u);                                                                          \
+                st_a(p.error, kDecodeErrTimeout);                                                           \
                 ok = false;                                                                                 \
                 break;                                                                                      \
             }                                                                                               \
@@ -1037,8 +1041,12 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     if (tid == 0) {
         s_ctl[0] = ld_a(&p.state->token);
         s_ctl[1] = ld_a(&p.state->pos);
+        s_ctl[3] = ld_a(p.error);
     }
     __syncthreads();
+    // A flag still raised (an earlier launch of an unchecked sequence failed,
+    // or the host raised it): leave before any phase.
+    if (s_ctl[3] != 0) return;
     uint32_t token = s_ctl[0];
     const uint32_t pos0 = s_ctl[1];
     bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
@@ -1057,7 +1065,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             if (token >= 0xfffffffeu) break;  // stop (EOS / context full) or error
         }
         if (pos >= p.max_seq || token >= p.vocab) {  // host validated; defensive stop
-            if (blockIdx.x == 0 && tid == 0) st_a(p.error, 2u);
+            if (blockIdx.x == 0 && tid == 0) st_a(p.error, kDecodeErrState);
             return;
         }
         const uint32_t T = pos + 1;
@@ -1116,7 +1124,9 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     ok = ok && mk_gemv(g, mode, smem, w, buf, tile, have, best, tag, rs, gl.n,
                                        reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) + p.g_lds_park),
                                        n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0, n_lds,
-                                       p.error);
+                                       p.error,
+                                       (f.kind == kPhD && p.hidden_dbg) ? p.hidden_dbg + (size_t)f.layer * H
+                                                                        : nullptr);
                 }
                 if (f.logits && w.lane == 0) {
                     st_a(p.tkeys + 2 * w.wid, tw_make_u((uint32_t)(best >> 32), tag));

@@ -143,6 +143,10 @@ struct DecodeGemv {
     uint32_t split;  // one row per tile, its two halves streamed side by side (long rows, few of them)
 };
 
+// Values of DecodeStepParams::error: a poll passed its spin limit, the step
+// state was out of range, or the host raised it before the launch (test hook).
+enum : uint32_t { kDecodeErrTimeout = 1, kDecodeErrState = 2, kDecodeErrInjected = 3 };
+
 // Activations of the persistent step are arrays of tagged 64-bit words: the
 // f32 value (or u32) in the low half, the epoch of the phase that wrote it in
 // the high half.
@@ -192,6 +196,10 @@ struct DecodeStepParams {
     uint32_t g_lds_offset2;
     uint32_t g_lds_tiles;
     uint32_t g_lds_park;  // byte offset of [8 waves][64] f32: LDS tile results until they are written
+    // Nullable: the down-projection phase of layer l also writes the residual
+    // stream after the layer to hidden_dbg[l * hidden ..] (plain f32 stores;
+    // with n_steps > 1 the last step's values remain).
+    float* hidden_dbg;
 };
 
 // LDS bytes of one gate/up tile (gate row + up row of K bf16 weights, in

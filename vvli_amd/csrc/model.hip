@@ -69,6 +69,7 @@ struct vvli_gpu_model {
     uint32_t mk_epoch = 1;                // epoch of the next launch's first phase
     uint32_t* h_err = nullptr;    // pinned
     bool mk_pending = false;      // a persistent launch ran since the last error check
+    uint32_t mk_inject = 0;       // test hook: the mk_inject-th next persistent launch starts flagged
     hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last persistent launch
     bool mk_timed = false;
     // Mixture-of-experts model (vvli_gpu_moe_model_create).
@@ -440,7 +441,7 @@ TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t b
 }
 
 int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned long long* timing = nullptr,
-                   uint32_t timing_stride = 0) {
+                   uint32_t timing_stride = 0, float* hidden_dbg = nullptr) {
     const vvli_gpu_config& c = m->cfg;
     // Epochs only grow; before they would wrap, clear every tag (stale words
     // then carry epoch 0, which no phase uses).
@@ -499,8 +500,15 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.g_lds_offset2 = m->mk_glds_off2;
     p.g_lds_tiles = m->mk_glds_tiles;
     p.g_lds_park = m->mk_glds_park;
+    p.hidden_dbg = hidden_dbg;
     m->mk_epoch += static_cast<uint32_t>(need);
-    HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
+    // The error word is cleared only once the host has read it: a launch
+    // that follows an unchecked one (the sampled generation loop) keeps a
+    // raised flag -- its blocks leave at once -- and the loop's final check
+    // reports it.
+    if (!m->mk_pending) HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
+    if (m->mk_inject && --m->mk_inject == 0)
+        HIP_TRY(hipMemsetAsync(m->mk_err, kDecodeErrInjected, 1, m->stream));
     HIP_TRY(hipEventRecord(m->mk_ev0, m->stream));
     HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
     HIP_TRY(hipEventRecord(m->mk_ev1, m->stream));
@@ -515,9 +523,11 @@ int check_persistent_error(vvli_gpu_model* m) {
     HIP_TRY(hipMemcpyAsync(m->h_err, m->mk_err, sizeof(uint32_t),
                            hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
-    if (*m->h_err != 0)
-        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (input wait timed out)",
-                         *m->h_err);
+    const uint32_t e = *m->h_err;
+    if (e != 0)
+        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (%s)", e,
+                         e == kDecodeErrTimeout ? "input wait timed out"
+                                                : (e == kDecodeErrState ? "invalid step state" : "injected by test hook"));
     return VVLI_OK;
 }
 
@@ -1252,7 +1262,9 @@ int vvli_gpu_forward_token_debug(vvli_gpu_model* m, uint32_t token, uint32_t pos
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
-    int rc = enqueue_step(m, m->stream, m->hidden);
+    // The path forward_token takes: the persistent step's down-projection
+    // phases write the residual rows, or the per-kernel step runs eagerly.
+    int rc = use_persistent(m) ? run_persistent(m, 1, -1, nullptr, 0, m->hidden) : enqueue_step(m, m->stream, m->hidden);
     if (rc) return rc;
     if (hidden_out)
         HIP_TRY(hipMemcpyAsync(hidden_out, m->hidden, static_cast<size_t>(m->cfg.layers) * m->cfg.hidden * sizeof(float),
@@ -1324,6 +1336,12 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* m, float* ms_out) {
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(hipEventSynchronize(m->mk_ev1));
     HIP_TRY(hipEventElapsedTime(ms_out, m->mk_ev0, m->mk_ev1));
+    return VVLI_OK;
+}
+
+int vvli_gpu_test_inject_step_error(vvli_gpu_model* m, uint32_t n) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    m->mk_inject = n;
     return VVLI_OK;
 }
 
