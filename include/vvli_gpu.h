@@ -286,6 +286,22 @@ int vvli_gpu_test_inject_step_error(vvli_gpu_model* model, uint32_t n);
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream);
 
+/* vvli_gpu_linear without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results as vvli_gpu_linear. Where that call splits
+ * the activations into a stream-ordered scratch (M >= 4: 4*M*ceil32(K)
+ * bytes), this one uses a static device array of
+ * VVLI_LINEAR_NOALLOC_SCRATCH_BYTES on each GPU it runs on, held until the
+ * process ends; a larger M*K returns VVLI_INVALID_CONFIG before any launch.
+ * The array of the current device is used (stream must belong to it). Every
+ * call on one GPU shares that array and nothing in it needs clearing, but
+ * calls that overlap on one GPU (other streams, other threads) race on it:
+ * serialise them. */
+#define VVLI_LINEAR_NOALLOC_SCRATCH_BYTES (16u << 20)
+int vvli_gpu_linear_noalloc(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M,
+                            uint32_t N, uint32_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -138,6 +138,8 @@ PROTOTYPES = {
     "vvli_gpu_last_launch_time": (c_int, [c_void_p, POINTER(ctypes.c_float)]),
     "vvli_gpu_test_inject_step_error": (c_int, [c_void_p, c_uint32]),
     "vvli_gpu_linear": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_void_p]),
+    "vvli_gpu_linear_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
+                                        c_void_p]),
     "vvli_host_fill_deterministic": (None, [c_void_p, c_size_t, c_uint32]),
     "vvli_host_fill_synthetic": (c_int, [POINTER(CConfig), c_uint64, c_float, c_void_p, c_size_t, c_uint32]),
     "vvli_host_synthetic_normal": (c_double, [c_uint64, c_uint64, c_uint64]),

@@ -1453,9 +1453,6 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
     return VVLI_OK;
 }
 
-// Rows from which vvli_gpu_linear runs one GEMM instead of a GEMV per row.
-constexpr uint32_t kLinearGemmMinRows = 4;
-
 int vvli_gpu_generate(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new, int64_t eos,
                       uint32_t flags, const vvli_gpu_sampling* opts, uint32_t* out_tokens, uint32_t* n_out,
                       vvli_gpu_stats* stats) {
@@ -1541,62 +1538,6 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
     if (e != hipSuccess)
         return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR, "sampler: %s",
                          hipGetErrorString(e));
-    return VVLI_OK;
-}
-
-int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
-                    uint32_t K, void* stream) {
-    if (!dW || !dX || !dY) return set_error(VVLI_NULL_ARG, "NULL device pointer to vvli_gpu_linear");
-    if (M == 0 || N == 0 || K == 0 || K % 8 != 0)
-        return set_error(VVLI_INVALID_CONFIG, "bad linear shape M=%u N=%u K=%u (K %% 8 == 0 required)", M, N, K);
-    int rc = init_once();
-    if (rc) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (M >= kLinearGemmMinRows) {
-        // One MFMA GEMM reads W once for all rows (activations split hi/lo
-        // into stream-ordered scratch).
-        GemmArgs g;
-        g.a = dX, g.lda = K, g.w[0] = dW, g.bias[0] = dBias;
-        g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
-        g.out = dY, g.ldo = N, g.M = M, g.N = N, g.K = K;
-        // The split scratch is kept per stream and grows stream-ordered; the
-        // lock covers the enqueue, so calls on one stream use it in turn.
-        struct Scratch {
-            hipStream_t stream;
-            void* p;
-            size_t bytes;
-        };
-        static std::mutex mu;
-        static std::vector<Scratch> cache;
-        const size_t need = gemm_split_elems(M, K) * sizeof(uint16_t);
-        std::lock_guard<std::mutex> lock(mu);
-        Scratch* sc = nullptr;
-        for (Scratch& c : cache)
-            if (c.stream == s) sc = &c;
-        if (!sc) {
-            cache.push_back(Scratch{s, nullptr, 0});
-            sc = &cache.back();
-        }
-        if (sc->bytes < need) {
-            if (sc->p) HIP_TRY(hipFreeAsync(sc->p, s));
-            sc->p = nullptr, sc->bytes = 0;
-            HIP_TRY(hipMallocAsync(&sc->p, need, s));
-            sc->bytes = need;
-        }
-        g.a_hl = static_cast<uint16_t*>(sc->p);
-        HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
-        return VVLI_OK;
-    }
-    for (uint32_t mi = 0; mi < M; ++mi) {
-        GemvArgs g;
-        g.w[0] = dW;
-        g.bias[0] = dBias;
-        g.out[0] = dY + static_cast<size_t>(mi) * N;
-        g.rows[0] = N;
-        g.x = dX + static_cast<size_t>(mi) * K;
-        g.K = K;
-        HIP_TRY(launch_gemv(VVLI_WEIGHT_BF16, kGemvPlain, g, s));
-    }
     return VVLI_OK;
 }
 

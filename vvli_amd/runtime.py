@@ -342,3 +342,11 @@ def linear(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None 
     """vvli_gpu_linear on raw device pointers (e.g. torch ``tensor.data_ptr()``)."""
     _lib.check(_lib.lib().vvli_gpu_linear(c_void_p(dW), c_void_p(dX), None if dBias is None else c_void_p(dBias),
                                           c_void_p(dY), M, N, K, None if stream is None else c_void_p(stream)))
+
+
+def linear_noalloc(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None = None,
+                   stream: int | None = None) -> None:
+    """vvli_gpu_linear_noalloc: the same op with its scratch in a static device
+    array (no allocation; at most VVLI_LINEAR_NOALLOC_SCRATCH_BYTES of split planes)."""
+    _lib.check(_lib.lib().vvli_gpu_linear_noalloc(c_void_p(dW), c_void_p(dX), None if dBias is None else c_void_p(dBias),
+                                                  c_void_p(dY), M, N, K, None if stream is None else c_void_p(stream)))
