@@ -77,30 +77,49 @@ def profile_kernels(runner, cfg, token: int, pos: int, reps: int = 3) -> dict:
 
 
 def measured_traffic(symbol: str, model: str):
-    """HBM bytes per launch of `symbol` on `model` from the committed rocprofv3
-    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 256 MiB copy);
+    """The committed rocprofv3 PMC measurement of `symbol` on `model`
+    (FETCH_SIZE + WRITE_SIZE of one launch, calibrated on a 256 MiB copy):
+    dict(traffic, algorithmic, steps, pos) -- the launch's measured HBM bytes,
+    its algorithmic bytes, and the decode steps / first position it ran -- or
     None where no summary covers that kernel and workload."""
     path = ROOT / "profiles" / "pmc_traffic_llama1b_decode.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
         parts = line.strip().split("\t")
-        if len(parts) == 4 and parts[0] == "traffic" and parts[1] == symbol and parts[2] == model:
-            return int(parts[3])
+        if len(parts) == 7 and parts[0] == "traffic" and parts[1] == symbol and parts[2] == model:
+            return {"traffic": int(parts[3]), "algorithmic": int(parts[4]), "steps": int(parts[5]),
+                    "pos": int(parts[6])}
     return None
 
 
-def cpu_baseline(cfg, blob, budget_s: float, max_tokens: int) -> dict:
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, blob, prompt, budget_s: float, max_tokens: int) -> dict:
     """Decode tok/s of the oracle (C restatement of the reference CPU path:
-    per-call thread fan-out over rows, single-threaded attention) on this host."""
+    per-call thread fan-out over rows, single-threaded attention) on this
+    host, at the positions the GPU decodes: the prompt goes through the
+    oracle's prompt pass (bit-identical to its token loop, untimed), then
+    greedy decode steps are timed for about budget_s seconds."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
     threads = oracle.cpu_count()
-    r = oracle.OracleRunner(cfg, blob, max_tokens + 16, threads=threads, lanes=16)
-    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=8)
-    for pos, t in enumerate(prompt):
-        logits = r.forward_token(int(t), pos)
+    r = oracle.OracleRunner(cfg, blob, len(prompt) + max_tokens + 16, threads=threads, lanes=16)
+    t0 = time.perf_counter()
+    logits = r.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
     tokens = []
     t0 = time.perf_counter()
     pos = len(prompt)
@@ -111,7 +130,137 @@ def cpu_baseline(cfg, blob, budget_s: float, max_tokens: int) -> dict:
         pos += 1
     dt = time.perf_counter() - t0
     r.close()
-    return {"tokens": tokens, "seconds": dt, "threads": threads, "prompt": prompt}
+    return {"tokens": tokens, "seconds": dt, "threads": threads, "prefill_s": prefill_s}
+
+
+def gemv_sweep(shapes, ms, log=True) -> list:
+    """vvli_gpu_linear over (N, K) x M: bf16 W [N, K] ~ N(0, 0.02), f32 X [M, K]
+    ~ N(0, 1), f32 Y [M, N]. Each shape rotates over enough weight copies
+    (>= 1 GiB) that W is read from HBM, not from the 256 MB memory-side cache.
+    Algorithmic bytes 2NK + 4MK + 4MN, flops 2MNK; time per call = HIP events
+    around the calls on one stream."""
+    import torch
+
+    from vvli_amd import runtime as R
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    stream = torch.cuda.current_stream()
+    rows = []
+    for n, k in shapes:
+        wbytes = 2 * n * k
+        copies = max(2, -(-(1 << 30) // wbytes))
+        ws = [(torch.randn(n, k, device="cuda", generator=gen) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+        for m in ms:
+            x = torch.randn(m, k, device="cuda", generator=gen)
+            y = torch.empty(m, n, device="cuda")
+            reps = max(copies, 20)
+            for i in range(3):
+                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            nbytes = 2 * n * k + 4 * m * k + 4 * m * n
+            rows.append({"N": n, "K": k, "M": m, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                         "tflops": round(2 * m * n * k / us / 1e6, 1)})
+            if log:
+                print(f"[bench] linear N={n} K={k} M={m}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s, "
+                      f"{2 * m * n * k / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+LINEAR_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (128256, 2048)]
+
+
+PHASE_KINDS = ("Q", "A", "O", "G", "D")
+PHASE_BYTES = {"Q": "qkv", "A": "attention", "O": "o_proj", "G": "gate_up", "D": "down"}
+
+
+def phases_main(args, cfg, blob) -> int:
+    """Per-phase critical path of the persistent decode step
+    (vvli_gpu_profile_persistent, s_memrealtime marks at 100 MHz): after a
+    batched prefill of --prompt tokens, one profiled step at every position of
+    the decode range. A phase's time is the end of its last wave minus the end
+    of the previous phase's last wave; `staged` is when the median block had
+    its input in LDS, measured from that same previous end (the hop). Bytes per
+    phase are the algorithmic bytes of the matching per-kernel launch
+    (kernel_bytes) at the step's position."""
+    import ctypes
+
+    from vvli_amd import _lib
+    from vvli_amd import runtime as R
+
+    runner = R.Runner(cfg, blob, args.ctx)
+    runner.set_decode_path("persistent")
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
+    runner.prefill(prompt)
+    L = cfg.num_hidden_layers
+    NP = 5 * L + 2
+    S = 16
+    stride = S * NP
+    nb = ctypes.c_uint32()
+    buf = np.zeros((1024 + 1) * stride, dtype=np.uint64)
+    positions = list(range(args.prompt, args.prompt + args.steps))
+    dur = {k: [] for k in PHASE_KINDS + ("logits",)}
+    hop = {k: [] for k in PHASE_KINDS + ("logits",)}
+    gbs = {k: [] for k in PHASE_KINDS + ("logits",)}
+    step_us = []
+    for pos in positions:
+        buf[:] = 0
+        _lib.check(_lib.lib().vvli_gpu_profile_persistent(runner._h, 5, pos, ctypes.c_void_p(buf.ctypes.data), stride,
+                                                          ctypes.byref(nb)))
+        n = nb.value
+        t = buf[: (n + 1) * stride].reshape(n + 1, NP, S).astype(np.int64)
+        prev = t[n, 0, 0]  # kernel start
+        start = prev
+        kb = kernel_bytes(cfg, pos)
+        for ph in range(5 * L + 1):
+            kind = "logits" if ph == 5 * L else PHASE_KINDS[ph % 5]
+            ends = t[:n, ph, 1:9]
+            end = ends[ends > 0].max()
+            st = t[:n, ph, 0]
+            st = st[st > 0]
+            us = (end - prev) * 1e-2
+            dur[kind].append(us)
+            hop[kind].append((np.median(st) - prev) * 1e-2 if st.size else np.nan)
+            gbs[kind].append(kb[PHASE_BYTES.get(kind, "logits")] / (us * 1e-6) / 1e9)
+            prev = end
+        step_us.append((prev - start) * 1e-2)
+    rows = {}
+    for k in PHASE_KINDS + ("logits",):
+        per = 1 if k == "logits" else L
+        b = kernel_bytes(cfg, positions[len(positions) // 2])[PHASE_BYTES.get(k, "logits")]
+        rows[k] = {"us": round(float(np.median(dur[k])), 2), "hop_us": round(float(np.nanmedian(hop[k])), 2),
+                   "bytes": int(b), "gbs": round(float(np.median(gbs[k])), 1), "per_token": per,
+                   "us_per_token": round(float(np.median(dur[k])) * per, 1)}
+    names = {"Q": "q/k/v (RMSNorm + GEMV + bias)", "A": "attention (RoPE, KV append, split merge)",
+             "O": "o_proj + residual", "G": "gate/up + SwiGLU", "D": "down + residual",
+             "logits": "final RMSNorm + lm_head + argmax keys"}
+    md = ["| phase | median us | staged after (us) | algorithmic bytes | GB/s | % of 8 TB/s | per token | us per token |",
+          "|---|---|---|---|---|---|---|---|"]
+    for k, r in rows.items():
+        md.append(f"| {names[k]} | {r['us']:.2f} | {r['hop_us']:.2f} | {r['bytes']:,} | {r['gbs']:.0f} | "
+                  f"{100 * r['gbs'] / HBM_PEAK_GBS:.1f} | x{r['per_token']} | {r['us_per_token']:.1f} |")
+    med_step = float(np.median(step_us))
+    md.append(f"| whole step (kernel start to logits end) | {med_step:.1f} | | "
+              f"{token_bytes(cfg, positions[len(positions) // 2]):,} | "
+              f"{token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3:.0f} | "
+              f"{100 * token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3 / HBM_PEAK_GBS:.1f} | | |")
+    print("\n".join(md), file=sys.stderr, flush=True)
+    line = {"metric": "persistent decode step: per-phase critical path", "value": round(med_step, 1), "unit": "us",
+            "n_gpus": 1, "steps": len(positions), "warmup": 0, "ms_per_step": round(med_step / 1e3, 4),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": f"{args.model} bf16 decode step, profiled at pos {positions[0]}-{positions[-1]}",
+                       "ctx": args.ctx}, "phases": rows, "cpu_baseline": None}
+    print(json.dumps(line), flush=True)
+    runner.close()
+    return 0
 
 
 def make_blob(cfg):
@@ -268,44 +417,9 @@ def sampled_main(args, cfg, blob) -> int:
 
 
 def linear_main(args) -> int:
-    """Isolated op sweep (vvli_gpu_linear) on the Llama-3.2-1B projection shapes:
-    bf16 W [N, K] ~ N(0, 0.02), f32 X [M, K] ~ N(0, 1), f32 Y [M, N]. Each
-    shape rotates over enough weight copies (>= 1 GiB) that W is read from HBM,
-    not from the 256 MB memory-side cache. Algorithmic bytes 2NK + 4MK + 4MN,
-    flops 2MNK; time per call = HIP events around `reps` calls on one stream."""
-    import torch
-
-    from vvli_amd import runtime as R
-
-    shapes = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (128256, 2048)]
-    ms = [1, 4, 16, 128, 512]
-    gen = torch.Generator(device="cuda").manual_seed(0)
-    stream = torch.cuda.current_stream()
-    rows = []
-    for n, k in shapes:
-        wbytes = 2 * n * k
-        copies = max(2, -(-(1 << 30) // wbytes))
-        ws = [(torch.randn(n, k, device="cuda", generator=gen) * 0.02).to(torch.bfloat16) for _ in range(copies)]
-        for m in ms:
-            x = torch.randn(m, k, device="cuda", generator=gen)
-            y = torch.empty(m, n, device="cuda")
-            reps = max(copies, 20)
-            for i in range(3):
-                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(reps):
-                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
-            e1.record(stream)
-            e1.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / reps
-            nbytes = 2 * n * k + 4 * m * k + 4 * m * n
-            rows.append({"N": n, "K": k, "M": m, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
-                         "tflops": round(2 * m * n * k / us / 1e6, 1)})
-            print(f"[bench] linear N={n} K={k} M={m}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s, "
-                  f"{2 * m * n * k / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
-        del ws
-        torch.cuda.empty_cache()
+    """Isolated op sweep (vvli_gpu_linear) on the Llama-3.2-1B projection shapes
+    at M in {1, 4, 16, 128, 512} (gemv_sweep)."""
+    rows = gemv_sweep(LINEAR_SHAPES, [1, 4, 16, 128, 512])
     gemv = [r for r in rows if r["M"] == 1]
     agg = sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv) / sum(r["us"] for r in gemv) / 1e3
     line = {
@@ -313,8 +427,8 @@ def linear_main(args) -> int:
         "n_gpus": 1, "steps": len(rows), "warmup": 3, "ms_per_step": None, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 weights, f32 activations", "data": "synthetic",
         "config": {"workload": "Llama-3.2-1B projection shapes x M in {1, 4, 16, 128, 512}, cold weights"},
-        "roofline": {"bound": "hbm", "achieved": round(agg, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(agg / 8000.0, 4), "traffic": None, "kernel": "vvli_gpu_linear, M = 1"},
+        "roofline": {"bound": "hbm", "achieved": round(agg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(agg / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "vvli_gpu_linear, M = 1"},
         "sweep": rows, "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
@@ -330,13 +444,15 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemv-sweep", action="store_true", help="decode mode: skip the M = 1 op sweep")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],
                     help="prompt processing: batched GEMM prefill, or one token step per prompt token (the reference's loop)")
-    ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "linear"],
+    ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "linear", "phases"],
                     help="decode: the headline decode benchmark; prefill: batched-prefill throughput sweep; "
-                         "linear: the isolated op sweep (vvli_gpu_linear)")
+                         "linear: the isolated op sweep (vvli_gpu_linear); phases: per-phase timing of the "
+                         "persistent decode step")
     ap.add_argument("--model", default="llama-3.2-1b",
                     choices=["llama-3.2-1b", "qwen2.5-0.5b", "qwen2.5-7b", "olmoe-1b-7b"],
                     help="decoder shape (synthetic bf16 weights); the default is the headline workload")
@@ -367,6 +483,8 @@ def main() -> int:
           flush=True)
     if args.mode == "prefill":
         return prefill_main(args, cfg, blob)
+    if args.mode == "phases":
+        return phases_main(args, cfg, blob)
     if cfg.num_experts:
         return moe_decode_main(args, cfg, blob)
     if args.sampling:
@@ -433,11 +551,27 @@ def main() -> int:
                          "bytes_per_launch": step_bytes, "gbs": step_bytes / (decode_launch_ms * 1e-3) / 1e9}}
     dom = max(kernels, key=lambda k: kernels[k]["total_us"])
     d = kernels[dom]
-    traffic = measured_traffic(dom.split(" (")[0], args.model)
+    # HBM bytes of this launch from the committed PMC measurement of the same
+    # kernel and workload: its measured / algorithmic ratio applied to this
+    # launch's algorithmic bytes (the raw figure when the steps and positions
+    # are the profiled ones).
+    prof_traffic = measured_traffic(dom.split(" (")[0], args.model)
+    traffic, traffic_src = None, None
+    if prof_traffic and persistent:
+        ratio = prof_traffic["traffic"] / prof_traffic["algorithmic"]
+        same = prof_traffic["steps"] == args.steps and prof_traffic["pos"] == args.prompt
+        traffic = prof_traffic["traffic"] if same else int(round(ratio * d["bytes_per_launch"]))
+        traffic_src = (f"profiles/pmc_traffic_llama1b_decode.md: FETCH_SIZE + WRITE_SIZE of the decode launch "
+                       f"over {prof_traffic['steps']} steps at pos {prof_traffic['pos']}-"
+                       f"{prof_traffic['pos'] + prof_traffic['steps'] - 1}, {ratio:.3f} x its algorithmic bytes"
+                       + ("" if same else "; scaled to this launch's algorithmic bytes"))
     roofline = {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": round(d["avg_us"], 2),
                 "launches_per_step": d["launches"]}
+    if traffic_src:
+        roofline["traffic_ratio"] = round(traffic / d["bytes_per_launch"], 4)
+        roofline["traffic_source"] = traffic_src
     if persistent:
         roofline["tokens_per_launch"] = args.steps
         roofline["us_per_token"] = round(d["avg_us"] / args.steps, 2)
@@ -452,20 +586,34 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
 
+    # GEMV half of the metric: the isolated op at M = 1 on the five projection
+    # shapes of the model (cold weights), HBM GB/s per shape.
+    gemv_rows = [] if args.no_gemv_sweep else gemv_sweep(LINEAR_SHAPES, [1], log=False)
+    gemv = {f"{r['N']}x{r['K']}": {"us": r["us"], "gbs": r["gbs"], "frac": r["frac"]} for r in gemv_rows}
+    if gemv_rows:
+        agg = (sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv_rows) / sum(r["us"] for r in gemv_rows)
+               / 1e3)
+        gemv["all_shapes"] = {"gbs": round(agg, 1), "frac": round(agg / HBM_PEAK_GBS, 4)}
+        print("[bench] gemv M=1: " + ", ".join(f"{k} {v['gbs']:.0f}GB/s" for k, v in gemv.items()), file=sys.stderr,
+              flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(cfg, blob, args.cpu_budget, 512)
-        # Parity spot check: the GPU's greedy continuation of the same 8-token prompt.
+        cb = cpu_baseline(cfg, blob, prompt, args.cpu_budget, 512)
+        # Parity spot check: the GPU's greedy continuation of the same prompt.
         runner.kv_clear()
-        g_tokens, _ = runner.generate_greedy_measured(cb["prompt"].astype(np.uint32), len(cb["tokens"]))
+        g_tokens, _ = runner.generate_greedy_measured(prompt, len(cb["tokens"]), batched_prefill=batched)
         same = bool(np.array_equal(g_tokens, np.array(cb["tokens"], dtype=np.uint32)))
-        cpu = {"value": round(len(cb["tokens"]) / cb["seconds"], 3), "unit": "tok/s", "cores": cb["threads"],
-               "kind": "port",
+        n_cpu = len(cb["tokens"])
+        cpu = {"value": round(n_cpu / cb["seconds"], 3), "unit": "tok/s", "cores": cb["threads"],
+               "kind": "port", "cpu_model": cpu_model(),
                "sample": f"oracle (C restatement of the reference CPU path, {cb['threads']} threads, 16-lane f32 "
-                         f"accumulators) greedy decode of {len(cb['tokens'])} tokens after an 8-token prompt, "
-                         f"same weights; GPU tokens identical: {same}"}
-        print(f"[bench] cpu baseline {cpu['value']} tok/s on {cb['threads']} threads; tokens identical: {same}",
-              file=sys.stderr, flush=True)
+                         f"accumulators, per-call thread fan-out as linearInto) greedy decode of {n_cpu} tokens at "
+                         f"positions {len(prompt)}-{len(prompt) + n_cpu - 1} after the same {len(prompt)}-token "
+                         f"prompt (run untimed through the oracle's prompt pass), same weights; "
+                         f"GPU tokens identical: {same}"}
+        print(f"[bench] cpu baseline {cpu['value']} tok/s on {cb['threads']} threads ({cpu['cpu_model']}); "
+              f"tokens identical: {same}", file=sys.stderr, flush=True)
 
     line = {
         "metric": "decode tok/s @bs1 + GEMV HBM GB/s (% of peak), Llama-3.2-1B bf16",
@@ -488,6 +636,7 @@ def main() -> int:
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "kernels": {k: {"avg_us": round(v["avg_us"], 2), "gbs": round(v["gbs"], 1)} for k, v in kernels.items()},
+        "gemv_m1": gemv or None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
