@@ -211,6 +211,7 @@ def phases_main(args, cfg, blob) -> int:
     hop = {k: [] for k in PHASE_KINDS + ("logits",)}
     gbs = {k: [] for k in PHASE_KINDS + ("logits",)}
     step_us = []
+    stg = {k: {"begin": [], "first": [], "retries": [], "own": [], "bar": [], "pre": []} for k in PHASE_KINDS + ("logits",)}
     for pos in positions:
         buf[:] = 0
         _lib.check(_lib.lib().vvli_gpu_profile_persistent(runner._h, 5, pos, ctypes.c_void_p(buf.ctypes.data), stride,
@@ -226,6 +227,20 @@ def phases_main(args, cfg, blob) -> int:
             end = ends[ends > 0].max()
             st = t[:n, ph, 0]
             st = st[st > 0]
+            ent, fst, rty = t[:n, ph, 9], t[:n, ph, 10], t[:n, ph, 11]
+            okb = (ent > 0) & (fst > 0)
+            if okb.any():  # thread 0 of each staging block: entry after the previous end, first attempt, retries
+                stg[kind]["begin"] += list((ent[okb] - prev) * 1e-2)
+                stg[kind]["first"] += list((fst[okb] - ent[okb]) * 1e-2)
+                stg[kind]["retries"] += list(rty[okb])
+                if ph > 0:  # entry after the block's own last wave of the previous phase
+                    own = t[:n, ph - 1, 1:9].max(axis=1)
+                    sel = okb & (own > 0)
+                    stg[kind]["own"] += list((ent[sel] - own[sel]) * 1e-2)
+                    bar, pre = t[:n, ph - 1, 12], t[:n, ph - 1, 13]
+                    sel2 = sel & (bar > 0) & (pre > 0)
+                    stg[kind]["bar"] += list((bar[sel2] - own[sel2]) * 1e-2)  # closing barrier
+                    stg[kind]["pre"] += list((pre[sel2] - bar[sel2]) * 1e-2)  # next weights issued
             us = (end - prev) * 1e-2
             dur[kind].append(us)
             hop[kind].append((np.median(st) - prev) * 1e-2 if st.size else np.nan)
@@ -253,6 +268,18 @@ def phases_main(args, cfg, blob) -> int:
               f"{token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3:.0f} | "
               f"{100 * token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3 / HBM_PEAK_GBS:.1f} | | |")
     print("\n".join(md), file=sys.stderr, flush=True)
+    for k in PHASE_KINDS + ("logits",):
+        d = stg[k]
+        if d["begin"]:
+            b, f, r = np.array(d["begin"]), np.array(d["first"]), np.array(d["retries"])
+            print(f"[bench] staging {k}: entry after prev end p50 {np.median(b):.2f} p90 {np.percentile(b, 90):.2f} "
+                  f"max {b.max():.2f} us; first attempt p50 {np.median(f):.2f} p90 {np.percentile(f, 90):.2f} us; "
+                  f"retries p50 {np.median(r):.0f} p90 {np.percentile(r, 90):.0f} max {r.max():.0f}"
+                  + (f"; entry after the block's own previous end p50 {np.median(d['own']):.2f} "
+                     f"p90 {np.percentile(d['own'], 90):.2f} max {np.max(d['own']):.2f} us" if d["own"] else "")
+                  + (f" = barrier p50 {np.median(d['bar']):.2f} + weight issue p50 {np.median(d['pre']):.2f} + rest"
+                     if d["bar"] else ""),
+                  file=sys.stderr, flush=True)
     line = {"metric": "persistent decode step: per-phase critical path", "value": round(med_step, 1), "unit": "us",
             "n_gpus": 1, "steps": len(positions), "warmup": 0, "ms_per_step": round(med_step / 1e3, 4),
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",

@@ -252,7 +252,11 @@ int vvli_gpu_set_prefill_path(vvli_gpu_model* model, uint32_t path);
  * (n_blocks + 1) * stride values. With stride >= 16 * (5 * layers + 2), phase
  * k of the step (per layer q/k/v, attention, o, gate/up, down; then logits)
  * fills ticks_out[b * stride + 16 k] with block b's staged input and
- * [b * stride + 16 k + 1 + w] with wave w's end of the phase;
+ * [b * stride + 16 k + 1 + w] with wave w's end of the phase, [.. + 9], [.. +
+ * 10] with thread 0's entry into the input staging and the return of its
+ * first attempt, [.. + 11] with its retry count, [.. + 12], [.. + 13] with
+ * thread 0 past the phase's closing barrier and past the next phase's first
+ * weight loads;
  * ticks_out[n_blocks * stride] is the kernel start. *n_blocks = blocks of the
  * persistent launch. */
 int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t pos, uint64_t* ticks_out,

@@ -130,7 +130,9 @@ __device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint3
 }
 
 // Detail timing mark (16-slot timing only): slot 0 the block's staged input,
-// 1 + w wave w's end of the phase.
+// 1 + w wave w's end of the phase; slots 9-11 (thread 0 in the input staging):
+// its entry, the return of its first attempt, its retry count; 12, 13 (thread
+// 0): past the phase's closing barrier, past the next phase's weight issue.
 __device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
     if (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
         p.timing[blockIdx.x * p.timing_stride + ph * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
@@ -542,8 +544,11 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
 // same batch as the activation (into nws = xs + n). False: a poll failed.
 __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src, uint32_t tag,
                                          const uint16_t* src_bf16, const uint16_t* norm_w, float eps, uint32_t n,
-                                         uint32_t* err) {
+                                         uint32_t* err, unsigned long long* tmark = nullptr) {
     const int tid = threadIdx.x;
+    // Detail timing (profiling runs only): thread 0 records its entry, the
+    // return of its first attempt, and its retry count.
+    if (tmark && tid == 0) tmark[0] = __builtin_amdgcn_s_memrealtime();
     constexpr int B = 8;  // word pairs issued before any is consumed
     float* nws = xs + n;
     float ss = 0.f;
@@ -575,6 +580,10 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
 #pragma unroll
                 for (int k = 0; k < B; ++k)
                     if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
+                if (tmark && tid == 0) {
+                    if (spins == 0) tmark[1] = __builtin_amdgcn_s_memrealtime();
+                    tmark[2] = spins;
+                }
                 if (done) break;
                 if (++spins > kSpinLimit) {
                     st_a(err, kDecodeErrTimeout);
@@ -1108,7 +1117,10 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     const tword* src = f.kind == kPhO ? p.tattn
                                                       : (f.kind == kPhD ? p.tff : (f.kind == kPhG ? p.tx + H : p.tx));
                     ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
-                                  f.kind == kPhD ? p.inter : H, p.error);
+                                  f.kind == kPhD ? p.inter : H, p.error,
+                                  (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
+                                      ? p.timing + blockIdx.x * p.timing_stride + ph * 16 + 9
+                                      : nullptr);
                     if (tid == 0) mk_mark(p, ph, 0);
                     // Residual rows: O reads x of the previous layer's D (or the
                     // embedding), D reads x of this layer's O.
@@ -1135,6 +1147,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             }
             if (w.lane == 0) mk_mark(p, ph, 1 + (int)wave);
             if (__syncthreads_or(!ok)) return;
+            if (tid == 0) mk_mark(p, ph, 12);
             // Issue the first weights of the next GEMV phase (the next step's
             // first phase after the logits) before waiting for its input.
             // (Not when the next phase starts with LDS tiles: those cover the
@@ -1151,6 +1164,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             } else if (step + 1 < p.n_steps) {
                 have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
+            if (tid == 0) mk_mark(p, ph, 13);
         }
 
         // ---- argmax + step advance (block 0) ----
