@@ -281,23 +281,31 @@ int vvli_gpu_test_inject_step_error(vvli_gpu_model* model, uint32_t n);
 /* linearInto (src/llm.zig:1228-1275) generalised to M rows of activations:
  * Y[m,n] = sum_k bf16 W[n,k] * X[m,k] (+ bias[n]) with f32 accumulation.
  * dW: N*K bf16, dX: M*K f32, dBias: N bf16 or NULL, dY: M*N f32, all device
- * pointers; K must be a multiple of 8. stream: hipStream_t or NULL for the
- * null stream. Asynchronous: returns after the launch. M < 4 runs one GEMV per
- * row; M >= 4 one MFMA GEMM (X split into two bf16 halves, so the products
- * keep about 16 bits of each f32 activation) through a per-stream scratch of
- * about 4*M*K bytes, allocated stream-ordered, grown when needed and kept
- * until the process ends (calls on one stream use it in turn). */
+ * pointers; K must be a multiple of 8; dY must be device memory (hipMalloc:
+ * the K-split paths publish partials with write-through stores). stream:
+ * hipStream_t or NULL for the null stream. Asynchronous: returns after the
+ * launch. M < 4 runs one GEMV per row; 4 <= M <= 64 one skinny MFMA kernel (W
+ * read once, X split into two bf16 halves in registers so the products keep
+ * about 16 bits of each f32 activation; few row tiles split K across blocks
+ * and the last block of a tile sums the partials in a fixed order); M > 64 one
+ * MFMA GEMM through planes of the split X. Results are deterministic except on
+ * the GEMM path, whose split-K partial sums are added with atomics (the last
+ * bits may vary run to run). Scratch (K-split partials and counters, or the
+ * GEMM's planes: about 4*M*K bytes) is kept per stream, allocated
+ * stream-ordered, grown when needed and kept until the process ends (calls on
+ * one stream use it in turn). */
 int vvli_gpu_linear(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                     uint32_t K, void* stream);
 
 /* vvli_gpu_linear without any allocation. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops and harnesses that forbid hipMalloc). Same
- * arguments, kernels and results as vvli_gpu_linear. Where that call splits
- * the activations into a stream-ordered scratch (M >= 4: 4*M*ceil32(K)
- * bytes), this one uses a static device array of
- * VVLI_LINEAR_NOALLOC_SCRATCH_BYTES on each GPU it runs on, held until the
- * process ends; a larger M*K returns VVLI_INVALID_CONFIG before any launch.
+ * arguments, kernels and results as vvli_gpu_linear. Where that call keeps a
+ * stream-ordered scratch (M > 64: the activation planes, 4*M*ceil32(K)
+ * bytes; 4 <= M <= 64 with few row tiles: K-split partials), this one uses a
+ * static device array of VVLI_LINEAR_NOALLOC_SCRATCH_BYTES (plus 64 KiB of
+ * counters) on each GPU it runs on, held until the process ends; a call
+ * needing more returns VVLI_INVALID_CONFIG before any launch.
  * The array of the current device is used (stream must belong to it). Every
  * call on one GPU shares that array and nothing in it needs clearing, but
  * calls that overlap on one GPU (other streams, other threads) race on it:

@@ -31,6 +31,11 @@ SHAPES = [
     (512, 2048, 2048, True),
     (300, 8192, 128, False),
     (33, 257, 4864, True),
+    # Skinny MFMA path (4 <= M <= 64): 32-row blocks with a ragged last block,
+    # K not a multiple of the 32-wide step, M just past a 16-row tile.
+    (5, 8200, 2056, True),
+    (63, 100, 40, False),
+    (16, 8192, 896, False),
 ]
 
 
@@ -104,3 +109,41 @@ def test_linear_two_streams_growing_scratch(oracle_mod):
             ref = oracle_mod.linear(w, x[m], None)
             e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
             assert e <= TOL, f"M={x.shape[0]} row {m}: rel err {e:.3e}"
+
+
+_BENCH_W = {}
+
+
+def _bench_weights(N, K):
+    if (N, K) not in _BENCH_W:
+        _BENCH_W.clear()
+        rng = np.random.default_rng(N + K)
+        w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        _BENCH_W[(N, K)] = bf16_bits(w)
+    return _BENCH_W[(N, K)]
+
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (128256, 2048)])
+@pytest.mark.parametrize("M", [1, 4, 16, 128, 512])
+def test_linear_benchmark_shapes(N, K, M, oracle_mod):
+    """The op-sweep shapes the benchmark times (gate/up and lm_head of
+    Llama-3.2-1B) at every M it times: GEMV (M = 1), skinny MFMA (4, 16) and
+    GEMM (128, 512) paths; sampled rows against the oracle."""
+    import torch
+
+    w = _bench_weights(N, K)
+    rng = np.random.default_rng(M)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    dev = torch.device("cuda", 0)
+    dw = torch.from_numpy(w.view(np.int16)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    print(f"linear bench shape M={M} N={N} K={K}", flush=True)
+    R.linear(dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy()
+    assert np.isfinite(y).all()
+    for m in sorted({0, 1 % M, M // 2, M - 1}):
+        ref = oracle_mod.linear(w, x[m], None)
+        e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+        assert e <= TOL, f"M={M} N={N} row {m}: rel err {e:.3e}"
