@@ -415,7 +415,7 @@ def sampled_main(args, cfg, blob) -> int:
     runner.set_decode_path(args.path)
     runner.set_prefill_path("auto")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
-    opts = R.Sampling(seed=7)
+    opts = R.Sampling(seed=7, top_k=args.top_k)
     runner.generate(prompt[:16], max(1, args.warmup), opts, batched_prefill=True)
     runner.kv_clear()
     tokens, stats = runner.generate(prompt, args.steps, opts, batched_prefill=True)
@@ -427,7 +427,8 @@ def sampled_main(args, cfg, blob) -> int:
     path = "persistent" if args.path != "graph" and runner.persistent_available() else "graph"
     print(f"[bench] sampled decode {tok_s:.1f} tok/s ({path})", file=sys.stderr, flush=True)
     line = {
-        "metric": "decode tok/s @bs1, sampled (T 0.8, top-k 40, top-p 0.95, repeat penalty 1.1)", "value": round(tok_s, 2),
+        "metric": f"decode tok/s @bs1, sampled (T 0.8, top-k {args.top_k}, top-p 0.95, repeat penalty 1.1)",
+        "value": round(tok_s, 2),
         "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(decode_s * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
@@ -485,6 +486,7 @@ def main() -> int:
                     help="decoder shape (synthetic bf16 weights); the default is the headline workload")
     ap.add_argument("--sampling", action="store_true",
                     help="decode mode: sample with the generator's default options instead of greedy")
+    ap.add_argument("--top-k", type=int, default=40, help="--sampling: top_k (0: every finite candidate)")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()

@@ -198,7 +198,7 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* model, const uint32_t* prompt, uint
 typedef struct vvli_gpu_sampling {
     float temperature;       /* <= 0: greedy with the repeat penalty */
     float top_p;             /* (0, 1] */
-    uint32_t top_k;          /* 0 = no limit; on the device at most 1024 candidates */
+    uint32_t top_k;          /* 0 = no limit (every finite candidate) */
     float repeat_penalty;    /* >= 1; 1 disables it */
     uint32_t repeat_last_n;  /* window of prompt + generated tokens, <= 65535 */
     uint64_t seed;           /* DefaultPrng seed; 0 -> 0x9e3779b97f4a7c15 as Sampler.init */
@@ -213,8 +213,10 @@ typedef struct vvli_gpu_sampling {
  * first token is sampled from the prompt's last logits; every sampled token is
  * forwarded (the last one too), so max_new tokens take max_new forwards, as
  * in the reference. Greedy without a penalty runs vvli_gpu_generate_greedy.
- * Candidate lists over 1024 (top_k 0 or > 1024 with a larger vocab) return
- * VVLI_INVALID_SAMPLING. */
+ * Candidate lists over 1024 (top_k 0 or > 1024 with a larger vocab) are
+ * sorted whole on the device (a stable radix sort: ties to the lower id,
+ * where the reference's unstable sort leaves their order open) and summed in
+ * one sequential pass; scratch for them is allocated on first use. */
 int vvli_gpu_generate(vvli_gpu_model* model, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                       int64_t eos, uint32_t flags, const vvli_gpu_sampling* opts, uint32_t* out_tokens,
                       uint32_t* n_out, vvli_gpu_stats* stats);

@@ -108,12 +108,60 @@ def test_sampler_edge_cases(oracle_mod):
 def test_sampler_rejects_bad_options():
     st = R.prng_seed(1)
     lg = np.zeros(2000, np.float32)
-    for bad in (opts(temperature=-1.0), opts(top_p=0.0), opts(repeat_penalty=0.9), opts(top_k=0),
-                opts(top_k=1025), opts(repeat_last_n=70000)):
+    for bad in (opts(temperature=-1.0), opts(top_p=0.0), opts(repeat_penalty=0.9), opts(repeat_last_n=70000)):
         with pytest.raises(VvliError) as e:
             R.sampler_next(lg, [0], [], bad, st)
         assert e.value.name == "InvalidSamplingOptions"
-    R.sampler_next(lg[:1000], [0], [], opts(top_k=0), st)  # unlimited is fine when the vocab fits
+
+
+# Whole-vocabulary candidates (top_k 0, or above 1024 with a larger vocab):
+# sorted whole on the device, one sequential pass of prefix sums.
+FULL_OPTIONS = [
+    opts(top_k=0),
+    opts(top_k=0, top_p=1.0, temperature=1.3, repeat_penalty=1.0),
+    opts(top_k=0, top_p=0.5, temperature=0.5, repeat_penalty=1.5, repeat_last_n=8),
+    opts(top_k=2000, top_p=0.9, temperature=2.0),
+    opts(top_k=0, top_p=0.95, temperature=1e-7),
+]
+
+
+@pytest.mark.parametrize("k", range(len(FULL_OPTIONS)))
+@pytest.mark.parametrize("vocab", [5000, 128256, 152064])
+def test_sampler_whole_vocab_matches_oracle(k, vocab, oracle_mod):
+    o = FULL_OPTIONS[k]
+    rng = np.random.default_rng(300 + k + vocab % 97)
+    st_gpu = R.prng_seed(5 + k)
+    st_orc = st_gpu.copy()
+    print(f"sampler whole vocab k={k} vocab={vocab}", flush=True)
+    for trial in range(6):
+        scale = (0.05, 3.0)[trial % 2]  # nearly flat (every id counts in the sums) and spread
+        logits = rng.normal(0, scale, vocab).astype(np.float32)
+        if trial % 3 == 1:  # ties, signed zeros and non-finite entries
+            logits[rng.integers(0, vocab, 300)] = logits.max()
+            logits[rng.integers(0, vocab, 40)] = 0.0
+            logits[rng.integers(0, vocab, 40)] = -0.0
+            logits[rng.integers(0, vocab, 30)] = np.nan
+            logits[rng.integers(0, vocab, 30)] = np.inf if trial % 2 else -np.inf
+        if trial == 5:  # fewer finite candidates than the limit
+            keep = rng.integers(0, vocab, 700)
+            vals = logits[keep].copy()
+            logits[:] = -np.inf
+            logits[keep] = vals
+        prompt = rng.integers(0, vocab, 20)
+        gen = rng.integers(0, vocab, trial * 7)
+        t_gpu = R.sampler_next(logits, prompt, gen, o, st_gpu)
+        t_orc = oracle_mod.sampler_next(logits, prompt, gen, o, st_orc)
+        assert t_gpu == t_orc, f"trial {trial}"
+        assert np.array_equal(st_gpu, st_orc), f"trial {trial}: PRNG state"
+
+
+def test_sampler_whole_vocab_no_finite(oracle_mod):
+    """No finite candidate on the whole-vocabulary path: llm.argmax of the logits."""
+    st = R.prng_seed(8)
+    so = st.copy()
+    for lg in (np.full(3000, -np.inf, np.float32), np.array([np.nan] + [np.inf] * 2999, np.float32)):
+        assert R.sampler_next(lg, [0], [], opts(top_k=0), st) == oracle_mod.sampler_next(lg, [0], [], opts(top_k=0), so)
+        assert np.array_equal(st, so)
 
 
 def cfg_small(**kw) -> C.Config:
@@ -148,3 +196,20 @@ def test_generate_matches_oracle(k, batched, path, oracle_mod, host_threads):
         gpu.kv_clear()
         got2, _ = gpu.generate(prompt, 48, o, eos_token_id=eos, batched_prefill=batched)
         np.testing.assert_array_equal(got2, ref[: first + 1])
+
+
+@pytest.mark.parametrize("path", ["persistent", "graph"])
+def test_generate_whole_vocab_matches_oracle(path, oracle_mod, host_threads):
+    """Sampled generation with top_k 0 (every finite candidate) on a 4096-id
+    vocabulary: the same tokens as the oracle on both decode paths."""
+    cfg = cfg_small(vocab_size=4096)
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=2, stddev=0.05)
+    o = opts(top_k=0, top_p=0.9, temperature=0.9, seed=21)
+    prompt = np.random.default_rng(6).integers(0, cfg.vocab_size, 24).astype(np.uint32)
+    orc = oracle_mod.OracleRunner(cfg, blob, 128, threads=host_threads)
+    ref = orc.generate_sampled(prompt, 40, o)
+    print(f"generate whole vocab path={path}", flush=True)
+    with R.Runner(cfg, blob, 128) as gpu:
+        gpu.set_decode_path(path)
+        got, st = gpu.generate(prompt, 40, o, batched_prefill=True)
+    np.testing.assert_array_equal(got, ref)

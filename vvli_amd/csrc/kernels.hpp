@@ -357,9 +357,16 @@ struct SampleArgs {
     // sample_cand_elems(vocab) keys and sample_nf_elems(vocab) counts.
     unsigned long long* cand_buf = nullptr;
     uint32_t* cand_nf = nullptr;
+    // Scratch of the whole-vocabulary path (candidate limits over 1024: top_k
+    // 0 or > 1024), sample_full_bytes(vocab) bytes (nullable: such limits are
+    // an error).
+    void* full = nullptr;
 };
 size_t sample_cand_elems(uint32_t vocab);
 size_t sample_nf_elems(uint32_t vocab);
+// Scratch bytes of the whole-vocabulary path (sort keys and ids twice,
+// probabilities, prefix sums, the sort's temporary storage); 0 on failure.
+size_t sample_full_bytes(uint32_t vocab);
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
 hipError_t launch_sample_counts(uint32_t* counts, uint32_t vocab, const uint32_t* prompt, uint32_t n_prompt,
                                 uint32_t last_n, hipStream_t s);

@@ -84,6 +84,7 @@ struct vvli_gpu_model {
     unsigned long long* sample_prng = nullptr;  // xoshiro256++ state [4]
     unsigned long long* sample_cand = nullptr;  // two-stage top-k survivors
     uint32_t* sample_nf = nullptr;              // finite counts of the vocab slices
+    void* sample_full = nullptr;                // whole-vocabulary candidates (limits over 1024)
     hipGraphExec_t graph_sample = nullptr;    // token step ending in the sampler
     // Batched prefill (bf16 only): chunk buffers, allocated on first use.
     bool pf_ok = false;
@@ -380,8 +381,8 @@ int capture_sample_graph(vvli_gpu_model* m, const SampleArgs& sa) {
     return VVLI_OK;
 }
 
-// validateSamplingOptions (src/generator.zig:329-333) plus the device limits:
-// at most 1024 candidates, a repeat window that fits 16-bit counts.
+// validateSamplingOptions (src/generator.zig:329-333) plus the device limit:
+// a repeat window that fits 16-bit counts.
 int validate_sampling(const vvli_gpu_sampling& o, uint32_t vocab) {
     if (o.temperature < 0.0f || std::isnan(o.temperature))
         return set_error(VVLI_INVALID_SAMPLING, "temperature %g", o.temperature);
@@ -389,10 +390,7 @@ int validate_sampling(const vvli_gpu_sampling& o, uint32_t vocab) {
         return set_error(VVLI_INVALID_SAMPLING, "top_p %g not in (0, 1]", o.top_p);
     if (o.repeat_penalty < 1.0f || std::isnan(o.repeat_penalty))
         return set_error(VVLI_INVALID_SAMPLING, "repeat_penalty %g < 1", o.repeat_penalty);
-    const uint32_t limit = (o.top_k == 0 || o.top_k > vocab) ? vocab : o.top_k;
-    if (o.temperature > 0.0f && limit > static_cast<uint32_t>(kMaxSampleTopK))
-        return set_error(VVLI_INVALID_SAMPLING, "device sampling takes at most %d candidates (top_k %u, vocab %u)",
-                         kMaxSampleTopK, o.top_k, vocab);
+    (void)vocab;
     if (o.repeat_last_n > 65535) return set_error(VVLI_INVALID_SAMPLING, "repeat_last_n %u > 65535", o.repeat_last_n);
     return VVLI_OK;
 }
@@ -688,7 +686,7 @@ void free_model(vvli_gpu_model* m) {
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
                     m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
-                    m->sample_prng, m->sample_cand, m->sample_nf};
+                    m->sample_prng, m->sample_cand, m->sample_nf, m->sample_full};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -966,6 +964,13 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     if (!m->sample_prng && (rc = dmalloc(&m->sample_prng, 4))) return rc;
     if (!m->sample_cand && (rc = dmalloc(&m->sample_cand, sample_cand_elems(c.vocab)))) return rc;
     if (!m->sample_nf && (rc = dmalloc(&m->sample_nf, sample_nf_elems(c.vocab)))) return rc;
+    const uint32_t limit = (o.top_k == 0 || o.top_k > c.vocab) ? c.vocab : o.top_k;
+    const bool full = o.temperature > 0.0f && limit > static_cast<uint32_t>(kMaxSampleTopK);
+    if (full && !m->sample_full) {
+        const size_t bytes = sample_full_bytes(c.vocab);
+        if (bytes == 0) return set_error(VVLI_HIP_ERROR, "sort storage size query failed");
+        HIP_TRY(hipMalloc(&m->sample_full, bytes));
+    }
     const bool penalty = o.repeat_penalty > 1.0f && o.repeat_last_n > 0;
     SampleArgs sa;
     sa.logits = m->logits;
@@ -979,6 +984,7 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     sa.prng = m->sample_prng;
     sa.cand_buf = m->sample_cand;
     sa.cand_nf = m->sample_nf;
+    sa.full = m->sample_full;
     sa.state = m->state;
     sa.prompt = m->prompt;
     sa.n_prompt = n_prompt;
@@ -991,7 +997,12 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     const bool persistent = use_persistent(m);
     SampleArgs after_step = sa;
     after_step.advance_pos = 0;
-    if (!persistent && (rc = capture_sample_graph(m, sa))) return rc;
+    // The whole-vocabulary sampler (a library sort among its launches) is not
+    // captured: the per-kernel path then replays the plain step graph and
+    // samples after it, as the persistent path does.
+    const bool eager_sampler = persistent || full;
+    if (!persistent && full && (rc = ensure_graph(m))) return rc;
+    if (!eager_sampler && (rc = capture_sample_graph(m, sa))) return rc;
     const int64_t t0 = now_ns();
     HIP_TRY(hipMemcpyAsync(m->prompt, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
     if (batched) {
@@ -1008,12 +1019,16 @@ int generate_sampled(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_promp
     if (persistent && (rc = check_persistent_error(m))) return rc;
     const int64_t t1 = now_ns();
     auto forward_and_sample = [&]() -> int {
-        if (!persistent) {
+        if (!eager_sampler) {
             HIP_TRY(hipGraphLaunch(m->graph_sample, m->stream));
             return VVLI_OK;
         }
-        int r = run_persistent(m, 1, -1);
-        if (r) return r;
+        if (persistent) {
+            int r = run_persistent(m, 1, -1);
+            if (r) return r;
+        } else {
+            HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+        }
         HIP_TRY(launch_sample(after_step, m->stream));
         return VVLI_OK;
     };
@@ -1499,7 +1514,13 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
     float* d_logits = nullptr;
     uint32_t *d_counts = nullptr, *d_result = nullptr, *d_nf = nullptr;
     unsigned long long *d_prng = nullptr, *d_cand = nullptr;
+    void* d_full = nullptr;
+    const uint32_t limit = (opts->top_k == 0 || opts->top_k > n) ? n : opts->top_k;
+    const bool full = opts->temperature > 0.0f && limit > static_cast<uint32_t>(kMaxSampleTopK);
+    const size_t full_bytes = full ? sample_full_bytes(n) : 0;
+    if (full && full_bytes == 0) return set_error(VVLI_HIP_ERROR, "sort storage size query failed");
     auto release = [&] {
+        if (d_full) (void)hipFree(d_full);
         if (d_logits) (void)hipFree(d_logits);
         if (d_counts) (void)hipFree(d_counts);
         if (d_result) (void)hipFree(d_result);
@@ -1510,6 +1531,7 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
     hipError_t e = hipMalloc(&d_logits, n * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&d_cand, sample_cand_elems(n) * sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMalloc(&d_nf, sample_nf_elems(n) * sizeof(uint32_t));
+    if (e == hipSuccess && full) e = hipMalloc(&d_full, full_bytes);
     if (e == hipSuccess) e = hipMalloc(&d_counts, n * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d_result, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d_prng, 4 * sizeof(unsigned long long));
@@ -1530,6 +1552,7 @@ int vvli_gpu_sampler_next(const float* logits, uint32_t n, const uint32_t* promp
         sa.result = d_result;
         sa.cand_buf = d_cand;
         sa.cand_nf = d_nf;
+        sa.full = d_full;
         e = launch_sample(sa, nullptr);
     }
     if (e == hipSuccess) e = hipMemcpy(token_out, d_result, sizeof(uint32_t), hipMemcpyDeviceToHost);

@@ -15,6 +15,18 @@
 //            (sampleCandidate, :451-463).
 // Sequential f32 sums in candidate order keep the reference's rounding.
 //
+// Whole-vocabulary candidates (limit over 1024: top_k 0, which buildCandidates
+// treats as "every finite score, sorted", :376-391, or top_k > 1024):
+// sample_full_keys_kernel writes each id's order-preserving score key (0 for
+// a non-finite score), rocPRIM's stable radix sort orders the (key, id) pairs
+// descending -- ties keep ascending ids, the order insertTopCandidate gives
+// and the oracle uses for the reference's unstable sort -- and
+// sample_full_kernel takes the first min(limit, finite) of them: the
+// probabilities in parallel, then one lane's single pass of sequential f32
+// prefix sums in candidate order (the running sum of prepareProbabilities'
+// total, of its top-p scan and of sampleCandidate's sums are the same
+// sequence), then the top-p cut and the pick as searches over those sums.
+//
 // Two-stage top-k (top_k <= 128, at most 64 slices, scratch of
 // sample_cand_elems keys given):
 // sample_local_kernel cuts the vocab into slices of 4096 ids, one block each,
@@ -25,6 +37,8 @@
 // the global top_k is in its slice's top_k; the sampling block's first wave then merges
 // the slices' sorted lists (one list head per lane) instead of scanning the
 // vocab (one block's scan is ~1 ms at a 128K vocab).
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -222,6 +236,8 @@ __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
     }
 }
 
+__device__ __noinline__ void sample_finish(const SampleArgs& a, uint32_t tok);
+
 __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
     __shared__ SampleShared sh;
     const uint32_t tid = threadIdx.x;
@@ -401,10 +417,136 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
         }
     }
     if (tid != 0) return;
+    sample_finish(a, tok);
+}
+
+// Whole-vocabulary path, pass 1: sort keys and ids (the ids in ascending
+// order, so the stable sort keeps ties by ascending id).
+__global__ __launch_bounds__(256) void sample_full_keys_kernel(SampleArgs a, uint32_t* keys, uint32_t* ids) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.vocab) return;
+    const float s = adjusted(a.logits[i], a.counts ? a.counts[i] : 0u, a.repeat_penalty);
+    keys[i] = isfinite(s) ? order_key(s) : 0u;
+    ids[i] = i;
+}
+
+// Whole-vocabulary path, pass 3 (one block): the candidates are the first
+// min(limit, finite) sorted pairs (finite keys are >= 1, so the finite ones
+// come first).
+__global__ __launch_bounds__(kT) void sample_full_kernel(SampleArgs a, const uint32_t* keys, const uint32_t* ids,
+                                                         float* prob, float* prefix) {
+    __shared__ unsigned long long red[kT / 64];
+    __shared__ uint32_t s_n, s_cut, s_pick, s_tok;
+    const uint32_t tid = threadIdx.x, V = a.vocab;
+    // Finite count: the first zero key (binary search; keys are descending).
+    if (tid == 0) {
+        uint32_t lo = 0, hi = V;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) / 2;
+            if (keys[mid] != 0u) lo = mid + 1;
+            else hi = mid;
+        }
+        s_n = lo;
+    }
+    __syncthreads();
+    const uint32_t limit = min(a.top_k == 0 ? V : a.top_k, V);
+    const uint32_t count = min(limit, s_n);
+    uint32_t tok;
+    if (count == 0) {
+        // llm.argmax of the raw logits (:111).
+        unsigned long long best = 0ull;
+        for (uint32_t i = tid; i < V; i += kT) {
+            const unsigned long long k = argmax_key(a.logits[i], i);
+            best = k > best ? k : best;
+        }
+        best = wave_max_u64(best);
+        if ((tid & 63) == 0) red[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 0; w < kT / 64; ++w) best = red[w] > best ? red[w] : best;
+            s_tok = (a.logits[0] != a.logits[0]) ? 0u : argmax_key_index(best);
+        }
+        __syncthreads();
+        tok = s_tok;
+    } else {
+        const float temperature = fmaxf(a.temperature, 1e-6f);
+        const float s0 = key_value(keys[0]);
+        for (uint32_t j = tid; j < count; j += kT) {
+            const float p = expf(__fdiv_rn(__fsub_rn(key_value(keys[j]), s0), temperature));
+            prob[j] = isfinite(p) ? p : 0.0f;
+        }
+        __syncthreads();
+        if (tid == 0) {  // sequential sums in candidate order, 16 loads ahead of the adds
+            float c = 0.0f;
+            uint32_t j = 0;
+            for (; j + 16 <= count; j += 16) {
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v[q] = prob[j + q];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    c = __fadd_rn(c, v[q]);
+                    prefix[j + q] = c;
+                }
+            }
+            for (; j < count; ++j) {
+                c = __fadd_rn(c, prob[j]);
+                prefix[j] = c;
+            }
+            s_cut = count;
+            s_pick = 0xffffffffu;
+        }
+        __syncthreads();
+        const float total = prefix[count - 1];
+        // prepareProbabilities' top-p cut: the first j with prefix[j] / total >= top_p.
+        const bool bad_total = total <= 0.0f || !isfinite(total);
+        if (!bad_total && a.top_p < 1.0f) {
+            uint32_t first = count;
+            for (uint32_t j = tid; j < count; j += kT)
+                if (__fdiv_rn(prefix[j], total) >= a.top_p) {
+                    first = j;
+                    break;
+                }
+            atomicMin(&s_cut, first == count ? count : first + 1);
+        }
+        __syncthreads();
+        const uint32_t k = bad_total ? 1u : s_cut;
+        // sampleCandidate with one draw of Random.float(f32).
+        __shared__ float s_target;
+        __shared__ uint32_t s_ok;
+        if (tid == 0) {
+            uint64_t st4[4] = {a.prng[0], a.prng[1], a.prng[2], a.prng[3]};
+            const float u = prng_float(st4);
+            for (int q = 0; q < 4; ++q) a.prng[q] = st4[q];
+            const float t2 = prefix[k - 1];
+            s_ok = t2 > 0.0f && isfinite(t2);
+            s_target = __fmul_rn(fminf(u, 0.99999994f), t2);
+        }
+        __syncthreads();
+        if (s_ok) {
+            const float target = s_target;
+            uint32_t first = 0xffffffffu;
+            for (uint32_t j = tid; j < k; j += kT)
+                if (target <= prefix[j]) {
+                    first = j;
+                    break;
+                }
+            atomicMin(&s_pick, first);
+        }
+        __syncthreads();
+        const uint32_t pick = !s_ok ? 0u : (s_pick == 0xffffffffu ? k - 1 : s_pick);
+        tok = ids[pick];
+    }
+    if (tid != 0) return;
+    sample_finish(a, tok);
+}
+
+// Advance the step state as the greedy finish does, then the repeat window
+// (the sampling block's thread 0, with the sampled token).
+__device__ __noinline__ void sample_finish(const SampleArgs& a, uint32_t tok) {
     if (a.result) *a.result = tok;
     StepState* st = a.state;
     if (!st) return;
-    // Advance the step state as the greedy finish does, then the repeat window.
     const uint32_t next_pos = st->pos + (a.advance_pos ? 1u : 0u);
     st->argmax = tok;
     st->pos = next_pos;
@@ -440,7 +582,45 @@ size_t sample_cand_elems(uint32_t vocab) {
 }
 size_t sample_nf_elems(uint32_t vocab) { return (vocab + kLocalIds - 1) / kLocalIds; }
 
+// Whole-vocabulary scratch: [keys in | keys out | ids in | ids out | prob |
+// prefix] of vocab words each (256-byte aligned), then the sort's storage.
+namespace {
+size_t full_word_bytes(uint32_t vocab) { return ((size_t)vocab * 4 + 255) / 256 * 256; }
+size_t full_sort_bytes(uint32_t vocab) {
+    size_t bytes = 0;
+    const hipError_t e = rocprim::radix_sort_pairs_desc(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
+                                                        static_cast<uint32_t*>(nullptr),
+                                                        static_cast<const uint32_t*>(nullptr),
+                                                        static_cast<uint32_t*>(nullptr), vocab, 0, 32);
+    return e == hipSuccess ? bytes : 0;
+}
+}  // namespace
+
+size_t sample_full_bytes(uint32_t vocab) {
+    const size_t sort = full_sort_bytes(vocab);
+    return sort ? 6 * full_word_bytes(vocab) + sort : 0;
+}
+
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
+    if (a.temperature > 0.0f && (a.top_k == 0 ? a.vocab : a.top_k) > static_cast<uint32_t>(kMaxCand)) {
+        if (!a.full) return hipErrorInvalidValue;
+        const size_t wb = full_word_bytes(a.vocab);
+        char* base = static_cast<char*>(a.full);
+        uint32_t* k_in = reinterpret_cast<uint32_t*>(base);
+        uint32_t* k_out = reinterpret_cast<uint32_t*>(base + wb);
+        uint32_t* i_in = reinterpret_cast<uint32_t*>(base + 2 * wb);
+        uint32_t* i_out = reinterpret_cast<uint32_t*>(base + 3 * wb);
+        float* prob = reinterpret_cast<float*>(base + 4 * wb);
+        float* prefix = reinterpret_cast<float*>(base + 5 * wb);
+        size_t sort_bytes = full_sort_bytes(a.vocab);
+        hipError_t e = vlaunch(sample_full_keys_kernel, dim3((a.vocab + 255) / 256), dim3(256), 0, s, a, k_in, i_in);
+        if (e == hipSuccess)
+            e = rocprim::radix_sort_pairs_desc(static_cast<void*>(base + 6 * wb), sort_bytes,
+                                               static_cast<const uint32_t*>(k_in), k_out,
+                                               static_cast<const uint32_t*>(i_in), i_out, a.vocab, 0, 32, s);
+        if (e == hipSuccess) e = vlaunch(sample_full_kernel, dim3(1), dim3(kT), 0, s, a, k_out, i_out, prob, prefix);
+        return e;
+    }
     SampleArgs b = a;
     const uint32_t slices = (a.vocab + kLocalIds - 1) / kLocalIds;
     const bool two_stage = a.cand_buf && a.cand_nf && a.temperature > 0.0f && a.top_k <= kFastTopK &&
