@@ -326,11 +326,13 @@ def moe_decode_main(args, cfg, blob) -> int:
     from vvli_amd import runtime as R
 
     runner = R.MoeRunner(cfg, blob, args.ctx)
+    batched = args.prefill == "batched"
+    runner.set_prefill_path("auto" if batched else "loop")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
-    runner.generate_greedy_measured(prompt[:8], max(1, args.warmup))
+    runner.generate_greedy_measured(prompt[:8], max(1, args.warmup), batched_prefill=batched)
     runner.kv_clear()
     torch.cuda.synchronize()
-    _, stats = runner.generate_greedy_measured(prompt, args.steps)
+    _, stats = runner.generate_greedy_measured(prompt, args.steps, batched_prefill=batched)
     torch.cuda.synchronize()
     decode_s = stats.decode_nanoseconds / 1e9
     tok_s = args.steps / decode_s
@@ -343,6 +345,7 @@ def moe_decode_main(args, cfg, blob) -> int:
         "config": {"workload": f"{args.model} bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
                    "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32", "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(stats.prefill_tokens_per_second(), 2),
+        "prefill": "batched (grouped expert GEMMs)" if batched else "token loop",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "MoE token step (per-kernel HIP graph, one replay per token)",

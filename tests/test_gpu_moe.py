@@ -101,3 +101,66 @@ def test_moe_greedy_generation(name, oracle_mod, host_threads):
         got, stats = gpu.generate_greedy_measured(prompt, 30)
         assert stats.generated_tokens == 30
         np.testing.assert_array_equal(got, ref)
+
+
+# Batched MoE prefill (route every row, group the (row, slot) pairs by expert,
+# grouped MFMA GEMMs, combine in ascending expert id) against the oracle's
+# token loop. name -> (config, prompt lengths: one prefill call each).
+PREFILL_CASES = {
+    "olmoe_small": (CASES["olmoe_small"][0], [24]),
+    # start_pos > 0 and one-row calls
+    "olmoe_small_split": (CASES["olmoe_small"][0], [5, 64, 1, 30]),
+    # GQA, q/k/v bias, top-2 of 8, no QK-norm, intermediate 96 (one ragged column tile)
+    "gqa_bias_tied": (CASES["gqa_bias_tied"][0], [37]),
+    # 600 rows x top-4 over 16 experts: about 150 pairs per expert, two row tiles each
+    "olmoe_small_long": (moe_cfg(max_position_embeddings=1024), [600]),
+    # more rows than one chunk (2048): the second chunk attends to the first's cache rows
+    "olmoe_two_chunks": (moe_cfg(max_position_embeddings=4096, vocab_size=300), [2100]),
+    # OLMoE-1B-7B layer shape with its 64-token prompt
+    "olmoe_1b_7b_2layers": (CASES["olmoe_1b_7b_2layers"][0], [64]),
+}
+
+
+@pytest.mark.parametrize("name", list(PREFILL_CASES))
+def test_moe_batched_prefill_matches_oracle(name, oracle_mod, host_threads):
+    cfg, parts = PREFILL_CASES[name]
+    total = sum(parts)
+    max_seq = total + 8
+    blob = moe_blob(oracle_mod, cfg)
+    orc = oracle_mod.OracleMoeRunner(cfg, blob, max_seq, threads=host_threads)
+    toks = np.random.default_rng(11).integers(0, cfg.vocab_size, size=total).astype(np.uint32)
+    print(f"case={name} parts={parts}", flush=True)
+    with R.MoeRunner(cfg, blob, max_seq) as gpu:
+        gpu.set_prefill_path("batched")
+        start = 0
+        for n in parts:
+            logits, am = gpu.prefill(toks[start:start + n], start)
+            logits = logits.copy()
+            for i in range(start, start + n):
+                ref = orc.forward_token(int(toks[i]), i)
+            e = rel_err(logits, ref)
+            assert e <= TOL, f"{name} prefill [{start}, {start + n}): logits rel err {e:.3e}"
+            assert am == oracle_mod.argmax(ref)
+            start += n
+        for layer in range(cfg.num_hidden_layers):
+            for pos in sorted({0, 1, total // 3, total // 2, total - 2, total - 1}):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"{name} kv layer {layer} pos {pos}"
+        nxt = int(toks[0])
+        e = rel_err(gpu.forward_token(nxt, total), orc.forward_token(nxt, total))
+        assert e <= TOL, f"{name} step after prefill: {e:.3e}"
+
+
+@pytest.mark.parametrize("name", ["olmoe_small", "gqa_bias_tied"])
+def test_moe_generation_with_batched_prefill(name, oracle_mod, host_threads):
+    cfg, _ = CASES[name]
+    blob = moe_blob(oracle_mod, cfg, seed=1)
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, size=40).astype(np.uint32)
+    orc = oracle_mod.OracleMoeRunner(cfg, blob, 96, threads=host_threads)
+    ref = orc.generate_greedy(prompt, 30)
+    print(f"case={name}", flush=True)
+    with R.MoeRunner(cfg, blob, 96) as gpu:
+        got, stats = gpu.generate_greedy_measured(prompt, 30, batched_prefill=True)
+        assert stats.prompt_tokens == 40 and stats.generated_tokens == 30
+        np.testing.assert_array_equal(got, ref)

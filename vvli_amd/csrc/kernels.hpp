@@ -255,6 +255,15 @@ struct GemmArgs {
     // gate and up sums are added there atomically (the launcher zeroes it) and
     // a SwiGLU pass writes out / out_hl.
     float* gu_acc = nullptr;
+    // Gather: A row m of the split planes is a[a_rows[m]], normalised with
+    // row_scale[a_rows[m]] (launch_gemm_grouped's gate/up input).
+    const uint32_t* a_rows = nullptr;
+    // launch_gemm_grouped: row tiles from a device table, tiles[0].x = count,
+    // tiles[1 + t] = {expert, first row, end row, 0} (rows of the A planes and
+    // of the output); the expert's W is w[0] (and w_up) + expert * w_expert.
+    const uint4* tiles = nullptr;
+    uint32_t max_tiles = 0;
+    size_t w_expert = 0;
 };
 __host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + 31) / 32 * 32; }
 size_t gemm_split_elems(uint32_t M, uint32_t K);
@@ -262,6 +271,13 @@ size_t gemm_split_elems(uint32_t M, uint32_t K);
 // rows * 2N floats is then needed).
 uint32_t gemm_gateup_split_rows(uint32_t N);
 hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s);
+// Rows of one grouped GEMM tile; a table for M grouped rows over E experts
+// holds at most grouped_gemm_max_tiles(M, E) tiles.
+uint32_t grouped_gemm_tile_rows();
+uint32_t grouped_gemm_max_tiles(uint32_t M, uint32_t E);
+// Per-expert GEMMs over grouped rows (kGemmGateUp or kGemmPlain; no K split,
+// no bias): each tile of g.tiles multiplies its rows by its expert's W.
+hipError_t launch_gemm_grouped(int mode, const GemmArgs& g, hipStream_t s);
 
 hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s);
 hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
@@ -274,6 +290,11 @@ struct PrefillRopeArgs {
     const float* rope_cs;    // [max_seq][hd/2][2]
     float* kcache;           // this layer's [max_seq][kvdim]
     float* vcache;
+    // QK-norm (models that carry it): q = q_norm * (q * 1/sqrt(mean(q^2) + eps))
+    // over the row's full q, the same for k, before the rotation.
+    const uint16_t* q_norm = nullptr;
+    const uint16_t* k_norm = nullptr;
+    float norm_eps = 0.f;
 };
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s);
 
@@ -334,6 +355,30 @@ struct MoeRouterArgs {
 };
 // Router GEMV + softmax + top-k in one launch.
 hipError_t launch_moe_router(const MoeRouterArgs& a, hipStream_t s);
+
+// Batched (prefill) routing of `rows` residual rows: per row the router
+// logits of norm(x_r) (row_scale from launch_row_rms), softmax, top-k into
+// idx[r * top_k ..] and weight[r * top_k ..].
+struct MoeRouteRowsArgs {
+    const uint16_t* w = nullptr;       // [E][H] router
+    const float* x = nullptr;          // [rows][H]
+    const float* row_scale = nullptr;  // [rows]
+    const uint16_t* norm_w = nullptr;  // post-attention RMSNorm weight
+    uint32_t rows = 0, H = 0, E = 0, top_k = 0;
+    uint32_t* idx = nullptr;
+    float* weight = nullptr;
+};
+hipError_t launch_moe_route_rows(const MoeRouteRowsArgs& a, hipStream_t s);
+// Groups the rows * top_k (row, slot) pairs by expert, pairs of one expert
+// in pair order: grouped_rows[g] = the row of grouped pair g, pair_pos[p] =
+// where pair p went, tiles = the grouped GEMM's tile table (tile_rows rows per
+// tile, at most grouped_gemm_max_tiles entries).
+hipError_t launch_moe_group(const uint32_t* idx, uint32_t rows, uint32_t top_k, uint32_t E, uint32_t tile_rows,
+                            uint32_t* grouped_rows, uint32_t* pair_pos, uint4* tiles, hipStream_t s);
+// x[r] += sum over row r's experts in ascending expert id of
+// eout[pair_pos[p]] * weight[p] (eout rows of H floats).
+hipError_t launch_moe_combine(const float* eout, const uint32_t* pair_pos, const uint32_t* idx, const float* weight,
+                              uint32_t rows, uint32_t top_k, uint32_t H, float* x, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Token sampling (sample.hip): Sampler.next on device logits.

@@ -100,6 +100,15 @@ struct vvli_gpu_model {
     uint32_t pf_gu_rows = 0;
     void* pf_kvp = nullptr;     // packed K/V tiles of one layer for the attention kernel
     size_t pf_kvp_bytes = 0;
+    // MoE prefill, per (row, slot) pair of a chunk (pf_rows * top_k pairs).
+    uint32_t* pf_eidx = nullptr;   // expert of each pair
+    float* pf_ew = nullptr;        // its router probability
+    uint32_t* pf_grows = nullptr;  // grouped pair -> row
+    uint32_t* pf_ppos = nullptr;   // pair -> grouped position
+    uint4* pf_tiles = nullptr;     // grouped GEMM tile table
+    uint16_t* pf_ehl = nullptr;    // gate/up input planes over the grouped pairs
+    uint16_t* pf_eact = nullptr;   // SwiGLU planes (the down GEMM's input)
+    float* pf_eout = nullptr;      // [pairs][H] expert outputs
 };
 
 namespace {
@@ -554,7 +563,7 @@ bool prefill_supported(const vvli_gpu_config& c) {
 }
 
 bool use_batched_prefill(const vvli_gpu_model* m) {
-    return m->prefill_path != 1 && !m->moe && prefill_supported(m->cfg);
+    return m->prefill_path != 1 && prefill_supported(m->cfg);
 }
 
 int ensure_prefill_buffers(vvli_gpu_model* m) {
@@ -589,12 +598,75 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
     }
     m->pf_kvp_bytes = kvp;
     m->pf_rows = static_cast<uint32_t>(rows);
+    if (m->moe) return VVLI_OK;
     const uint32_t gu_rows = std::min<uint32_t>(m->pf_rows, gemm_gateup_split_rows(c.inter));
     if (gu_rows > 0 && hipMalloc(reinterpret_cast<void**>(&m->pf_gu), static_cast<size_t>(gu_rows) * 2 * I *
                                                                           sizeof(float)) == hipSuccess)
         m->pf_gu_rows = gu_rows;
     else
         m->pf_gu = nullptr;  // short chunks then run gate/up unsplit
+    return VVLI_OK;
+}
+
+int ensure_moe_prefill_buffers(vvli_gpu_model* m) {
+    if (m->pf_eout) return VVLI_OK;
+    const vvli_gpu_config& c = m->cfg;
+    const size_t n = static_cast<size_t>(m->pf_rows) * c.experts_per_tok;
+    void** bufs[] = {reinterpret_cast<void**>(&m->pf_eidx), reinterpret_cast<void**>(&m->pf_ew),
+                     reinterpret_cast<void**>(&m->pf_grows), reinterpret_cast<void**>(&m->pf_ppos),
+                     reinterpret_cast<void**>(&m->pf_tiles), reinterpret_cast<void**>(&m->pf_ehl),
+                     reinterpret_cast<void**>(&m->pf_eact), reinterpret_cast<void**>(&m->pf_eout)};
+    const size_t tiles = 1 + grouped_gemm_max_tiles(static_cast<uint32_t>(n), c.num_experts);
+    const size_t bytes[] = {n * 4, n * 4, n * 4, n * 4, tiles * sizeof(uint4), gemm_split_elems(static_cast<uint32_t>(n), c.hidden) * 2,
+                            gemm_split_elems(static_cast<uint32_t>(n), c.inter) * 2, n * c.hidden * sizeof(float)};
+    for (int i = 0; i < 8; ++i) {
+        hipError_t e = hipMalloc(bufs[i], bytes[i]);
+        if (e != hipSuccess) {
+            for (void** b : bufs) {
+                if (*b) (void)hipFree(*b);
+                *b = nullptr;
+            }
+            return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR,
+                             "MoE prefill buffers (%zu pairs): %s", n, hipGetErrorString(e));
+        }
+    }
+    return VVLI_OK;
+}
+
+// Mixture-of-experts half of a prefill layer for the chunk's P rows: route
+// every row, group the (row, slot) pairs by expert, run the experts' gate/up
+// and down as grouped GEMMs over their rows, combine into pf_x.
+int enqueue_prefill_moe_ffn(vvli_gpu_model* m, uint32_t l, uint32_t P, hipStream_t s) {
+    const vvli_gpu_config& c = m->cfg;
+    const MoeLayerSlices& L = m->moe_layout.layers[l];
+    const uint32_t H = c.hidden, I = c.inter, E = c.num_experts, K = c.experts_per_tok, n = P * K;
+    auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+    LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+    MoeRouteRowsArgs ra;
+    ra.w = w16(L.router), ra.x = m->pf_x, ra.row_scale = m->pf_scale, ra.norm_w = w16(L.post_norm);
+    ra.rows = P, ra.H = H, ra.E = E, ra.top_k = K, ra.idx = m->pf_eidx, ra.weight = m->pf_ew;
+    LAUNCH(launch_moe_route_rows(ra, s));
+    LAUNCH(launch_moe_group(m->pf_eidx, P, K, E, grouped_gemm_tile_rows(), m->pf_grows, m->pf_ppos, m->pf_tiles, s));
+    // act = silu(norm(x_row) . Wg_e^T) * (norm(x_row) . Wu_e^T) per pair, as split planes
+    GemmArgs gu;
+    gu.a = m->pf_x, gu.lda = H, gu.a_rows = m->pf_grows, gu.row_scale = m->pf_scale, gu.norm_w = w16(L.post_norm);
+    gu.w[0] = w16(L.gate_up), gu.w_up = w16(L.gate_up) + static_cast<size_t>(I) * H;
+    gu.w_expert = static_cast<size_t>(2) * I * H;
+    gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
+    gu.M = n, gu.N = I, gu.K = H;
+    gu.a_hl = m->pf_ehl;
+    gu.out_hl = m->pf_eact, gu.out_plane = static_cast<size_t>(n) * gemm_kp(I);
+    gu.tiles = m->pf_tiles, gu.max_tiles = grouped_gemm_max_tiles(n, E);
+    LAUNCH(launch_gemm_grouped(kGemmGateUp, gu, s));
+    // out_pair = act . Wd_e^T
+    GemmArgs gd;
+    gd.w[0] = w16(L.down), gd.w_expert = static_cast<size_t>(H) * I;
+    gd.seg_end[0] = gd.seg_end[1] = gd.seg_end[2] = H;
+    gd.out = m->pf_eout, gd.ldo = H, gd.M = n, gd.N = H, gd.K = I;
+    gd.a_hl = m->pf_eact, gd.a_ready = true, gd.a_plane = static_cast<size_t>(n) * gemm_kp(I);
+    gd.tiles = m->pf_tiles, gd.max_tiles = gu.max_tiles;
+    LAUNCH(launch_gemm_grouped(kGemmPlain, gd, s));
+    LAUNCH(launch_moe_combine(m->pf_eout, m->pf_ppos, m->pf_eidx, m->pf_ew, P, K, H, m->pf_x, s));
     return VVLI_OK;
 }
 
@@ -605,6 +677,7 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
 int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint32_t last_token, uint32_t counting) {
     int rc = ensure_prefill_buffers(m);
     if (rc) return rc;
+    if (m->moe && (rc = ensure_moe_prefill_buffers(m))) return rc;
     const vvli_gpu_config& c = m->cfg;
     hipStream_t s = m->stream;
     const uint32_t H = c.hidden, kv = kv_dim(c), I = c.inter, hd = head_dim(c), ldqkv = H + 2 * kv;
@@ -615,7 +688,14 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
         const uint32_t pos0 = start + c0;
         LAUNCH(launch_prefill_embed(embed, m->prompt + pos0, P, H, m->pf_x, s));
         for (uint32_t l = 0; l < c.layers; ++l) {
-            const LayerSlices& L = m->layout.layers[l];
+            AttnSlices L;
+            if (m->moe) {
+                const MoeLayerSlices& M = m->moe_layout.layers[l];
+                L = AttnSlices{M.input_norm, M.q, M.q_bias, M.k, M.k_bias, M.v, M.v_bias, M.q_norm, M.k_norm, M.o};
+            } else {
+                const LayerSlices& D = m->layout.layers[l];
+                L = AttnSlices{D.input_norm, D.q, D.q_bias, D.k, D.k_bias, D.v, D.v_bias, kNone, kNone, D.o};
+            }
             float* kc = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
             float* vc = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
             // input RMSNorm fused into the q|k|v GEMM (+ bias)
@@ -631,6 +711,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             // RoPE on q and k, k/v appended at positions pos0 ..
             PrefillRopeArgs ra{m->pf_qkv, ldqkv, P, pos0, c.heads, c.kv_heads, hd, kv, c.rope_layout,
                                m->rope_cs, kc, vc};
+            if (L.q_norm != kNone) ra.q_norm = w16(L.q_norm), ra.k_norm = w16(L.k_norm), ra.norm_eps = c.rms_eps;
             LAUNCH(launch_prefill_rope_kv(ra, s));
             PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
                                1.0f / sqrtf(static_cast<float>(hd))};
@@ -647,11 +728,16 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             go.a_hl = reinterpret_cast<uint16_t*>(fused_o ? m->pf_ahl2 : m->pf_ahl);
             if (fused_o) go.a_ready = true, go.a_plane = m->pf_rows * gemm_kp(H);
             LAUNCH(launch_gemm_bf16(kGemmResid, go, s));
+            if (m->moe) {
+                if ((rc = enqueue_prefill_moe_ffn(m, l, P, s))) return rc;
+                continue;
+            }
+            const LayerSlices& D = m->layout.layers[l];
             // post-attention RMSNorm fused into gate/up + SwiGLU
             LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
             GemmArgs gu;
-            gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(L.post_norm);
-            gu.w[0] = w16(L.gate), gu.w_up = w16(L.up);
+            gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(D.post_norm);
+            gu.w[0] = w16(D.gate), gu.w_up = w16(D.up);
             gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
             gu.M = P, gu.N = I, gu.K = H;
             gu.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
@@ -661,7 +747,7 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             LAUNCH(launch_gemm_bf16(kGemmGateUp, gu, s));
             // x += ff . Wd^T
             GemmArgs gd;
-            gd.w[0] = w16(L.down);
+            gd.w[0] = w16(D.down);
             gd.seg_end[0] = gd.seg_end[1] = gd.seg_end[2] = H;
             gd.out = m->pf_x, gd.ldo = H, gd.M = P, gd.N = H, gd.K = I;
             gd.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2);
@@ -685,7 +771,8 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
-                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
+                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->pf_eidx, m->pf_ew, m->pf_grows, m->pf_ppos, m->pf_tiles, m->pf_ehl, m->pf_eact,
+                    m->pf_eout, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng, m->sample_cand, m->sample_nf, m->sample_full};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -1252,7 +1339,7 @@ int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
 int vvli_gpu_set_prefill_path(vvli_gpu_model* m, uint32_t path) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     if (path > 2) return set_error(VVLI_INVALID_CONFIG, "prefill path %u not in 0..2", path);
-    if (path == 2 && (m->moe || !prefill_supported(m->cfg)))
+    if (path == 2 && !prefill_supported(m->cfg))
         return set_error(VVLI_INVALID_CONFIG, "batched prefill needs bf16 weights and head_dim 32, 64 or 128");
     m->prefill_path = path;
     return VVLI_OK;

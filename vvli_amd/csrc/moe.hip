@@ -323,7 +323,174 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeGemvArgs a, float
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batched (prefill) pieces: the P rows of a chunk are routed together, their
+// P * top_k (row, slot) pairs grouped by expert, the experts run as grouped
+// GEMMs over their rows (launch_gemm_grouped, prefill.hip) and the outputs
+// combined per row in ascending expert id -- the oracle's order, so the
+// combine adds exactly what the token step's combine adds.
+// ---------------------------------------------------------------------------
+
+// One block per row: norm(x_r) staged in LDS, one router row per wave at a
+// time, then wave 0 takes the softmax and top-k (route_wave).
+__global__ __launch_bounds__(kThreads) void moe_route_rows_kernel(MoeRouteRowsArgs a) {
+    extern __shared__ float smem[];
+    float* xs = smem;  // [H]
+    __shared__ float row_logit[256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r = blockIdx.x;
+    const float* x = a.x + static_cast<size_t>(r) * a.H;
+    const float scale = a.row_scale[r];
+    for (uint32_t i = tid; i < a.H; i += kThreads) xs[i] = x[i] * bf(a.norm_w[i]) * scale;
+    __syncthreads();
+    const uint32_t U = a.H / 8;
+    for (uint32_t e = wave; e < a.E; e += kWavesPerBlock) {
+        const uint16_t* row = a.w + static_cast<size_t>(e) * a.H;
+        float acc = 0.f;
+        for (uint32_t u = lane; u < U; u += 64) {
+            const uint4 q = load_unit(row + static_cast<size_t>(u) * 8);
+            float wf[8];
+            WeightTraits<uint16_t>::expand(q, wf);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = fmaf(wf[j], xs[u * 8 + j], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) row_logit[e] = acc;
+    }
+    __syncthreads();
+    if (wave == 0)
+        route_wave(row_logit, a.E, a.top_k, a.idx + static_cast<size_t>(r) * a.top_k,
+                   a.weight + static_cast<size_t>(r) * a.top_k);
+}
+
+// Counting sort of the n = rows * top_k pairs by expert in one 1024-thread
+// block. The expert ids are staged in LDS as bytes; thread (g, e) owns expert
+// e in pair range g (G = 1024 / E ranges): it counts, the counts become
+// offsets (per expert over ranges, then over experts in id order), and a
+// second pass writes the pairs of its range at its offset, so the pairs of an
+// expert keep their pair order. Every expert's rows are then cut into tiles
+// of tile_rows for the grouped GEMM.
+constexpr int kGroupThreads = 1024;
+constexpr uint32_t kGroupMaxPairs = 32768;  // 2048 rows x top-16
+
+__global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const uint32_t* __restrict__ idx, uint32_t n,
+                                                                 uint32_t top_k, uint32_t E, uint32_t tile_rows,
+                                                                 uint32_t* __restrict__ grouped_rows,
+                                                                 uint32_t* __restrict__ pair_pos,
+                                                                 uint4* __restrict__ tiles) {
+    __shared__ uint8_t ids[kGroupMaxPairs];
+    __shared__ uint32_t cnt[kGroupThreads];  // [g][e], then the pair offsets
+    __shared__ uint32_t eoff[256], toff[257];
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t p = tid; p < n; p += kGroupThreads) ids[p] = static_cast<uint8_t>(idx[p]);
+    const uint32_t G = kGroupThreads / E;
+    const uint32_t g = tid / E, e = tid % E;
+    const uint32_t span = (n + G - 1) / G;
+    const uint32_t p0 = g * span, p1 = min(n, p0 + span);
+    __syncthreads();
+    uint32_t c = 0;
+    if (g < G)
+        for (uint32_t p = p0; p < p1; ++p) c += ids[p] == e;
+    cnt[tid] = c;
+    __syncthreads();
+    if (tid < E) {  // exclusive offsets over the ranges of expert tid
+        uint32_t run = 0;
+        for (uint32_t gg = 0; gg < G; ++gg) {
+            const uint32_t v = cnt[gg * E + tid];
+            cnt[gg * E + tid] = run;
+            run += v;
+        }
+        eoff[tid] = run;  // the expert's total, for now
+    }
+    __syncthreads();
+    if (tid == 0) {  // totals -> offsets over experts; tile counts -> tile offsets
+        uint32_t run = 0, tr = 0;
+        for (uint32_t ee = 0; ee < E; ++ee) {
+            const uint32_t tot = eoff[ee];
+            eoff[ee] = run;
+            toff[ee] = tr;
+            run += tot;
+            tr += (tot + tile_rows - 1) / tile_rows;
+        }
+        toff[E] = tr;
+        tiles[0] = make_uint4(tr, 0, 0, 0);
+    }
+    __syncthreads();
+    if (g < G) {
+        uint32_t at = eoff[e] + cnt[tid];
+        for (uint32_t p = p0; p < p1; ++p)
+            if (ids[p] == e) {
+                grouped_rows[at] = p / top_k;
+                pair_pos[p] = at;
+                ++at;
+            }
+    }
+    if (tid < E) {
+        const uint32_t b = eoff[tid], end = tid + 1 < E ? eoff[tid + 1] : n;
+        uint32_t t = toff[tid];
+        for (uint32_t r0 = b; r0 < end; r0 += tile_rows) tiles[1 + t++] = make_uint4(tid, r0, min(end, r0 + tile_rows), 0);
+    }
+}
+
+// One block per row: its (expert, weight, grouped position) triples sorted
+// by expert id in LDS, then x[r][i] += sum_j eout[pos_j][i] * w_j in that
+// order (products rounded, then added: the oracle's moe += out * w).
+__global__ __launch_bounds__(kThreads) void moe_combine_kernel(const float* __restrict__ eout,
+                                                              const uint32_t* __restrict__ pair_pos,
+                                                              const uint32_t* __restrict__ idx,
+                                                              const float* __restrict__ weight, uint32_t top_k,
+                                                              uint32_t H, float* __restrict__ x) {
+    __shared__ uint32_t se[kMaxTopK], sp[kMaxTopK];
+    __shared__ float sw[kMaxTopK];
+    const uint32_t r = blockIdx.x;
+    if (threadIdx.x == 0) {
+        for (uint32_t j = 0; j < top_k; ++j) {  // insertion sort by expert id (ids of a row are distinct)
+            const size_t p = static_cast<size_t>(r) * top_k + j;
+            const uint32_t ej = idx[p], pj = pair_pos[p];
+            const float wj = weight[p];
+            uint32_t k = j;
+            while (k > 0 && se[k - 1] > ej) {
+                se[k] = se[k - 1], sp[k] = sp[k - 1], sw[k] = sw[k - 1];
+                --k;
+            }
+            se[k] = ej, sp[k] = pj, sw[k] = wj;
+        }
+    }
+    __syncthreads();
+    float* xr = x + static_cast<size_t>(r) * H;
+    for (uint32_t i = threadIdx.x; i < H; i += kThreads) {
+        float acc = 0.f;
+        for (uint32_t j = 0; j < top_k; ++j)
+            acc = __fadd_rn(acc, __fmul_rn(eout[static_cast<size_t>(sp[j]) * H + i], sw[j]));
+        xr[i] = __fadd_rn(xr[i], acc);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_moe_route_rows(const MoeRouteRowsArgs& a, hipStream_t s) {
+    if (a.rows == 0) return hipSuccess;
+    if (a.E == 0 || a.E > 256 || a.top_k == 0 || a.top_k > a.E || a.top_k > static_cast<uint32_t>(kMaxTopK) ||
+        a.H % 8 != 0 || a.H > 16384 || !a.row_scale)
+        return hipErrorInvalidValue;
+    return vlaunch(moe_route_rows_kernel, dim3(a.rows), dim3(kThreads), static_cast<size_t>(a.H) * sizeof(float), s,
+                   a);
+}
+
+hipError_t launch_moe_group(const uint32_t* idx, uint32_t rows, uint32_t top_k, uint32_t E, uint32_t tile_rows,
+                            uint32_t* grouped_rows, uint32_t* pair_pos, uint4* tiles, hipStream_t s) {
+    const size_t n = static_cast<size_t>(rows) * top_k;
+    if (n == 0 || n > kGroupMaxPairs || E == 0 || E > 256 || tile_rows == 0) return hipErrorInvalidValue;
+    return vlaunch(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, idx, static_cast<uint32_t>(n), top_k, E,
+                   tile_rows, grouped_rows, pair_pos, tiles);
+}
+
+hipError_t launch_moe_combine(const float* eout, const uint32_t* pair_pos, const uint32_t* idx, const float* weight,
+                              uint32_t rows, uint32_t top_k, uint32_t H, float* x, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (top_k == 0 || top_k > static_cast<uint32_t>(kMaxTopK)) return hipErrorInvalidValue;
+    return vlaunch(moe_combine_kernel, dim3(rows), dim3(kThreads), 0, s, eout, pair_pos, idx, weight, top_k, H, x);
+}
 
 hipError_t moe_gemv_init_attributes() {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemv_kernel<kGemvGateUp>),
@@ -336,7 +503,9 @@ hipError_t moe_gemv_init_attributes() {
     // vector) is capped at 64 KiB, hidden <= 16384.
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_router_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-    return e;
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_route_rows_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
 }
 
 hipError_t launch_moe_gemv(int mode, const MoeGemvArgs& a, hipStream_t s) {

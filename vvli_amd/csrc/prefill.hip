@@ -78,19 +78,20 @@ static_assert(kBK == 32, "gemm_kp rounds to 32");
 
 // Row of W feeding B-tile row r of block column n0 (GateUp interleaves gate and
 // up rows in groups of 16 so one lane holds both halves of an output).
+// eoff: element offset of the expert's matrix (grouped launches; else 0).
 template <int MODE>
-__device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int r, bool& valid) {
+__device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int r, size_t eoff, bool& valid) {
     if (MODE == kGemmGateUp) {
         const uint32_t n = n0 / 2 + (r / 32) * 16 + (r % 16);
         valid = n < g.N;
-        return ((r / 16) & 1 ? g.w_up : g.w[0]) + static_cast<size_t>(valid ? n : 0) * g.K;
+        return ((r / 16) & 1 ? g.w_up : g.w[0]) + eoff + static_cast<size_t>(valid ? n : 0) * g.K;
     }
     const uint32_t n = n0 + r;
     valid = n < g.N;
     const uint32_t nn = valid ? n : 0;
-    if (nn < g.seg_end[0]) return g.w[0] + static_cast<size_t>(nn) * g.K;
-    if (nn < g.seg_end[1]) return g.w[1] + static_cast<size_t>(nn - g.seg_end[0]) * g.K;
-    return g.w[2] + static_cast<size_t>(nn - g.seg_end[1]) * g.K;
+    if (nn < g.seg_end[0]) return g.w[0] + eoff + static_cast<size_t>(nn) * g.K;
+    if (nn < g.seg_end[1]) return g.w[1] + eoff + static_cast<size_t>(nn - g.seg_end[0]) * g.K;
+    return g.w[2] + eoff + static_cast<size_t>(nn - g.seg_end[1]) * g.K;
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -130,7 +131,8 @@ __device__ __forceinline__ void gemm_lds_wait(bf16x8 (&a)[4], bf16x8 (&l)[4], bf
 // A into hi | lo bf16 planes (a_hl[0][m][kp], a_hl[1][m][kp]) with the
 // RMSNorm prologue when norm_w is set: v = (a * w) * scale in rmsNormInto's
 // order (src/llm.zig:1297), hi = bf16(v), lo = bf16(v - hi); columns K .. kp
-// are zeros. 8 columns per thread.
+// are zeros. 8 columns per thread. With a_rows, row m is gathered from a
+// row a_rows[m].
 __global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs g) {
     const uint32_t kp = gemm_kp(g.K);
     const uint32_t groups = kp / 8;
@@ -139,13 +141,14 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs g) {
     const uint32_t m = static_cast<uint32_t>(i / groups), k = static_cast<uint32_t>(i % groups) * 8;
     u16x8 hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = hi;
     if (k < g.K) {  // K % 8 == 0: the group is all in or all out
-        const float* ap = g.a + static_cast<size_t>(m) * g.lda + k;
+        const uint32_t src = g.a_rows ? g.a_rows[m] : m;
+        const float* ap = g.a + static_cast<size_t>(src) * g.lda + k;
         const float4 v0 = *reinterpret_cast<const float4*>(ap);
         const float4 v1 = *reinterpret_cast<const float4*>(ap + 4);
         float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if (g.norm_w) {
             const u16x8 w = *reinterpret_cast<const u16x8*>(g.norm_w + k);
-            const float scale = g.row_scale[m];
+            const float scale = g.row_scale[src];
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(__fmul_rn(v[j], from_bf16(w[j])), scale);
         }
@@ -165,24 +168,46 @@ __device__ inline float silu_mul(float gv, float uv) {
     return __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), uv);  // siluMulInto, src/llm.zig:1382-1387
 }
 
-template <int MODE>
+// GROUPED: the block's rows and expert come from the tile table (block b:
+// tile b / tn, column tile b % tn); 16-row groups past the tile's end skip
+// their MFMAs (their copies still run, reading the tile's first row, so
+// every wave issues the same copies per stage).
+template <int MODE, bool GROUPED = false>
 __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
     extern __shared__ __attribute__((aligned(1024))) char gemm_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
-    // Tile of this block. Consecutive blocks go to the 8 XCDs in turn and each
-    // XCD has its own L2: block b is mapped to tile u = offset(xcd) + b / 8, so
-    // every XCD walks a contiguous run of tiles, ordered in panels of 8 W
-    // columns (M fastest inside a panel): the blocks an XCD runs together
-    // cover about 8 x 8 tiles and share their A and W slabs through its L2.
     const uint32_t cols = MODE == kGemmGateUp ? 2 * g.N : g.N;
-    const uint32_t tm = (g.M + kBM - 1) / kBM, tn = (cols + kBN - 1) / kBN;
-    const uint32_t ntile = gridDim.x;
-    const uint32_t xcd = blockIdx.x % 8, per = ntile / 8, rem = ntile % 8;
-    const uint32_t u = xcd * per + min(xcd, rem) + blockIdx.x / 8;
-    const uint32_t panel = u / (tm * 8), pw = min(8u, tn - 8 * panel), within = u - panel * tm * 8;
-    const uint32_t m0 = (within / pw) * kBM;
-    const uint32_t n0 = (8 * panel + within % pw) * kBN;
+    const uint32_t tn = (cols + kBN - 1) / kBN;
+    uint32_t m0, n0, mlim;
+    size_t eoff = 0;
+    if (GROUPED) {
+        const uint32_t t = blockIdx.x / tn;
+        if (t >= g.tiles[0].x) return;  // uniform per block
+        const uint4 td = g.tiles[1 + t];
+        m0 = td.y, mlim = td.z;
+        n0 = (blockIdx.x % tn) * kBN;
+        eoff = static_cast<size_t>(td.x) * g.w_expert;
+    } else {
+        // Tile of this block. Consecutive blocks go to the 8 XCDs in turn and each
+        // XCD has its own L2: block b is mapped to tile u = offset(xcd) + b / 8, so
+        // every XCD walks a contiguous run of tiles, ordered in panels of 8 W
+        // columns (M fastest inside a panel): the blocks an XCD runs together
+        // cover about 8 x 8 tiles and share their A and W slabs through its L2.
+        const uint32_t tm = (g.M + kBM - 1) / kBM;
+        const uint32_t ntile = gridDim.x;
+        const uint32_t xcd = blockIdx.x % 8, per = ntile / 8, rem = ntile % 8;
+        const uint32_t u = xcd * per + min(xcd, rem) + blockIdx.x / 8;
+        const uint32_t panel = u / (tm * 8), pw = min(8u, tn - 8 * panel), within = u - panel * tm * 8;
+        m0 = (within / pw) * kBM;
+        n0 = (8 * panel + within % pw) * kBN;
+        mlim = g.M;
+    }
+    // Live 16-row groups of this wave (grouped tiles only).
+    bool live[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        live[i] = !GROUPED || m0 + static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wm)) * 64 + i * 16 < mlim;
     // Split K across gridDim.z blocks (partial sums added atomically).
     const uint32_t nk_all = (g.K + kBK - 1) / kBK;
     const uint32_t per_split = (nk_all + gridDim.z - 1) / gridDim.z;
@@ -216,12 +241,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
         chunk[i] = (static_cast<uint32_t>(lane & 3) ^ gemm_swz(row)) * 8;
         is_w[i] = q >= 16;
         if (q < 16) {
-            const uint32_t gm = m0 + row < g.M ? m0 + row : 0;
+            const uint32_t gm = m0 + row < mlim ? m0 + row : (GROUPED ? m0 : 0);
             const size_t plane = g.a_plane ? g.a_plane : static_cast<size_t>(g.M) * kp;
             src[i] = g.a_hl + (q >= 8 ? plane : 0) + static_cast<size_t>(gm) * kp;
         } else {
             bool valid;
-            src[i] = gemm_w_row<MODE>(g, n0, static_cast<int>(row), valid);
+            src[i] = gemm_w_row<MODE>(g, n0, static_cast<int>(row), eoff, valid);
         }
     }
     auto issue_one = [&](int kt, int stage, int i) {
@@ -276,11 +301,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
 #pragma unroll
-            for (int i = (q & 1) * 2; i < (q & 1) * 2 + 2; ++i)
+            for (int i = (q & 1) * 2; i < (q & 1) * 2 + 2; ++i) {
+                if (!live[i]) continue;
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q < 2 ? fh[cur][i] : fl[cur][i], fw[cur][j],
                                                                         acc[i][j], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
             if (more) issue_one(kn, kn % kStages, q);
             if (next) {
@@ -305,7 +332,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
         for (int jr = 0; jr < 4; ++jr) {
             const uint32_t row = m0 + wm * 64 + i * 16 + rq + jr;
-            if (row >= g.M) continue;
+            if (row >= mlim) continue;
             float* orow = g.out + static_cast<size_t>(row) * g.ldo;
             if (MODE == kGemmGateUp) {
 #pragma unroll
@@ -397,7 +424,8 @@ __device__ inline void rot(float* v, int a, int b, float c, float s) {
 }
 
 // One block per token row t (position start + t): rotate its q heads in place
-// and its k head vectors, then write k and v to the cache rows of that position.
+// and its k head vectors (after the QK-norm when the model has one), then
+// write k and v to the cache rows of that position.
 __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRopeArgs a) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = a.start + t;
@@ -407,6 +435,22 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
     const uint32_t qpairs = a.heads * half, kpairs = a.kv_heads * half;
     float* kc = a.kcache + static_cast<size_t>(pos) * a.kvdim;
     float* vc = a.vcache + static_cast<size_t>(pos) * a.kvdim;
+    float scq = 1.f, sck = 1.f;
+    if (a.q_norm) {
+        __shared__ float red[2][kRowThreads / 64];
+        const uint32_t qw = a.heads * a.hd;
+        float sq = 0.f, sk = 0.f;
+        for (uint32_t i = threadIdx.x; i < qw; i += kRowThreads) sq = fmaf(row[i], row[i], sq);
+        for (uint32_t i = threadIdx.x; i < a.kvdim; i += kRowThreads) sk = fmaf(row[qw + i], row[qw + i], sk);
+        sq = wave_sum(sq), sk = wave_sum(sk);
+        if ((threadIdx.x & 63) == 0) red[0][threadIdx.x >> 6] = sq, red[1][threadIdx.x >> 6] = sk;
+        __syncthreads();
+        float tq = 0.f, tk = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRowThreads / 64; ++w) tq += red[0][w], tk += red[1][w];
+        scq = 1.0f / sqrtf(tq / static_cast<float>(qw) + a.norm_eps);
+        sck = 1.0f / sqrtf(tk / static_cast<float>(a.kvdim) + a.norm_eps);
+    }
     for (uint32_t p = threadIdx.x; p < qpairs + kpairs; p += kRowThreads) {
         const bool is_q = p < qpairs;
         const uint32_t pp = is_q ? p : p - qpairs;
@@ -414,6 +458,12 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
         float* v = row + (is_q ? 0 : a.heads * a.hd) + h * a.hd;
         const int f = a.rope_layout == 0 ? 2 * i : i;
         const int s = a.rope_layout == 0 ? 2 * i + 1 : i + half;
+        if (a.q_norm) {  // weight * (x * s), OlmoeRMSNorm's order
+            const uint16_t* nw = (is_q ? a.q_norm : a.k_norm) + h * a.hd;
+            const float sc = is_q ? scq : sck;
+            v[f] = from_bf16(nw[f]) * (v[f] * sc);
+            v[s] = from_bf16(nw[s]) * (v[s] * sc);
+        }
         rot(v, f, s, cs[2 * i], cs[2 * i + 1]);
         if (!is_q) {
             kc[h * a.hd + f] = v[f];
@@ -1019,6 +1069,37 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     }
 }
 
+uint32_t grouped_gemm_tile_rows() { return kBM; }
+uint32_t grouped_gemm_max_tiles(uint32_t M, uint32_t E) { return M / kBM + E; }
+
+hipError_t launch_gemm_grouped(int mode, const GemmArgs& g, hipStream_t s) {
+    if (g.M == 0 || g.N == 0) return hipSuccess;
+    if (!g.a_hl || !g.tiles || g.max_tiles == 0 || g.K % 8 != 0 || (g.norm_w && !g.row_scale) ||
+        (mode != kGemmGateUp && mode != kGemmPlain) || (mode == kGemmGateUp && !g.out_hl) ||
+        (mode == kGemmPlain && (g.out_hl || !g.out || g.bias[0] || g.seg_end[0] != g.N)) ||
+        (g.a_plane && g.a_plane < static_cast<size_t>(g.M) * gemm_kp(g.K)) ||
+        (g.out_hl && g.out_plane < static_cast<size_t>(g.M) * gemm_kp(g.N)))
+        return hipErrorInvalidValue;
+    if (!g.a_ready) {
+        const size_t n = static_cast<size_t>(g.M) * (gemm_kp(g.K) / 8);
+        hipError_t e = vlaunch(gemm_split_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, g);
+        if (e != hipSuccess) return e;
+    }
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_kernel<kGemmPlain, true>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_kernel<kGemmGateUp, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
+    const dim3 grid((cols + kBN - 1) / kBN * g.max_tiles);
+    if (mode == kGemmGateUp) return vlaunch(gemm_bf16_kernel<kGemmGateUp, true>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+    return vlaunch(gemm_bf16_kernel<kGemmPlain, true>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+}
+
 hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s) {
     const uint32_t waves_per_block = kRowThreads / 64;
     return vlaunch(row_rms_kernel, dim3((rows + waves_per_block - 1) / waves_per_block), dim3(kRowThreads), 0, s, x,
@@ -1032,6 +1113,7 @@ hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, u
 }
 
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
+    if ((a.q_norm == nullptr) != (a.k_norm == nullptr)) return hipErrorInvalidValue;
     return vlaunch(prefill_rope_kv_kernel, dim3(a.rows), dim3(kRowThreads), 0, s, a);
 }
 
