@@ -38,12 +38,17 @@ def kernel_bytes(cfg, pos: int) -> dict:
     H, I, V, kv = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.kv_dim()
     T = pos + 1
     bias = (H + 2 * kv) * 2 if cfg.qkv_bias else 0
+    # MoE: the top-k experts' gate/up and down (I per expert), the router and
+    # the QK-norm weights.
+    K = cfg.num_experts_per_token if cfg.num_experts else 1
+    router = cfg.num_experts * H * 2 if cfg.num_experts else 0
+    qkn = (H + kv) * 2 if cfg.num_experts and cfg.qk_norm else 0
     return {
         "qkv": (H * H + 2 * kv * H) * 2 + bias + H * 2 + H * 4 + (H + 2 * kv) * 4,
-        "attention": 2 * T * kv * 4 + 2 * kv * 4 + (H + 2 * kv) * 4 + H * 4,
+        "attention": 2 * T * kv * 4 + 2 * kv * 4 + (H + 2 * kv) * 4 + H * 4 + qkn,
         "o_proj": H * H * 2 + H * 4 + 2 * H * 4,
-        "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
-        "down": H * I * 2 + I * 4 + 2 * H * 4,
+        "gate_up": K * 2 * I * H * 2 + router + H * 2 + H * 4 + K * I * 4,
+        "down": K * H * I * 2 + K * I * 4 + 2 * H * 4,
         "logits": V * H * 2 + H * 2 + H * 4 + V * 4,
     }
 
@@ -196,7 +201,7 @@ def phases_main(args, cfg, blob) -> int:
     from vvli_amd import _lib
     from vvli_amd import runtime as R
 
-    runner = R.Runner(cfg, blob, args.ctx)
+    runner = (R.MoeRunner if cfg.num_experts else R.Runner)(cfg, blob, args.ctx)
     runner.set_decode_path("persistent")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
     runner.prefill(prompt)
@@ -211,6 +216,7 @@ def phases_main(args, cfg, blob) -> int:
     hop = {k: [] for k in PHASE_KINDS + ("logits",)}
     gbs = {k: [] for k in PHASE_KINDS + ("logits",)}
     step_us = []
+    moe_marks = {"route": [], "publish": [], "last_pub": [], "after_last": []}  # MoE gate/up: slots 14, 15
     stg = {k: {"begin": [], "first": [], "retries": [], "own": [], "bar": [], "pre": []} for k in PHASE_KINDS + ("logits",)}
     for pos in positions:
         buf[:] = 0
@@ -241,6 +247,15 @@ def phases_main(args, cfg, blob) -> int:
                     sel2 = sel & (bar > 0) & (pre > 0)
                     stg[kind]["bar"] += list((bar[sel2] - own[sel2]) * 1e-2)  # closing barrier
                     stg[kind]["pre"] += list((pre[sel2] - bar[sel2]) * 1e-2)  # next weights issued
+            if cfg.num_experts and kind == "G":
+                s0, s14, s15 = t[:n, ph, 0], t[:n, ph, 14], t[:n, ph, 15]
+                sel = (s0 > 0) & (s14 > 0)
+                moe_marks["route"] += list((s14[sel] - s0[sel]) * 1e-2)
+                pr = (s0 > 0) & (s15 > 0)
+                if pr.any():
+                    moe_marks["publish"] += list((s15[pr] - s0[pr]) * 1e-2)
+                    moe_marks["last_pub"].append((s15[pr].max() - np.median(s0[s0 > 0])) * 1e-2)
+                    moe_marks["after_last"] += list((s14[sel] - s15[pr].max()) * 1e-2)
             us = (end - prev) * 1e-2
             dur[kind].append(us)
             hop[kind].append((np.median(st) - prev) * 1e-2 if st.size else np.nan)
@@ -256,6 +271,9 @@ def phases_main(args, cfg, blob) -> int:
                    "us_per_token": round(float(np.median(dur[k])) * per, 1)}
     names = {"Q": "q/k/v (RMSNorm + GEMV + bias)", "A": "attention (RoPE, KV append, split merge)",
              "O": "o_proj + residual", "G": "gate/up + SwiGLU", "D": "down + residual",
+             **({"A": "attention (QK-norm, RoPE, KV append, split merge)",
+                 "G": "router + top-k + experts' gate/up + SwiGLU",
+                 "D": "experts' down + weighted sum + residual"} if cfg.num_experts else {}),
              "logits": "final RMSNorm + lm_head + argmax keys"}
     md = ["| phase | median us | staged after (us) | algorithmic bytes | GB/s | % of 8 TB/s | per token | us per token |",
           "|---|---|---|---|---|---|---|---|"]
@@ -268,6 +286,13 @@ def phases_main(args, cfg, blob) -> int:
               f"{token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3:.0f} | "
               f"{100 * token_bytes(cfg, positions[len(positions) // 2]) / med_step / 1e3 / HBM_PEAK_GBS:.1f} | | |")
     print("\n".join(md), file=sys.stderr, flush=True)
+    if cfg.num_experts and moe_marks["route"]:
+        r = np.array(moe_marks["route"])
+        print(f"[bench] MoE gate/up: routed p50 {np.median(r):.2f} p90 {np.percentile(r, 90):.2f} us after the "
+              f"staged input; router row published p50 {np.median(moe_marks['publish']):.2f} us after a producer's "
+              f"staged input, the last one p50 {np.median(moe_marks['last_pub']):.2f} us after the median block's; "
+              f"routed p50 {np.median(moe_marks['after_last']):.2f} us after the last publication",
+              file=sys.stderr, flush=True)
     for k in PHASE_KINDS + ("logits",):
         d = stg[k]
         if d["begin"]:
@@ -326,6 +351,8 @@ def moe_decode_main(args, cfg, blob) -> int:
     from vvli_amd import runtime as R
 
     runner = R.MoeRunner(cfg, blob, args.ctx)
+    runner.set_decode_path(args.path)
+    persistent = args.path == "persistent" or (args.path == "auto" and runner.persistent_available())
     batched = args.prefill == "batched"
     runner.set_prefill_path("auto" if batched else "loop")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, size=args.prompt).astype(np.uint32)
@@ -348,7 +375,8 @@ def moe_decode_main(args, cfg, blob) -> int:
         "prefill": "batched (grouped expert GEMMs)" if batched else "token loop",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "MoE token step (per-kernel HIP graph, one replay per token)",
+                     "kernel": ("MoE persistent decode step (one cooperative launch for the decode loop)"
+                                if persistent else "MoE token step (per-kernel HIP graph, one replay per token)"),
                      "bytes_per_launch": step_bytes // args.steps},
         "cpu_baseline": None,
     }

@@ -57,14 +57,17 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", list(CASES))
-def test_moe_steps_match_oracle(name, oracle_mod, host_threads):
+def test_moe_steps_match_oracle(name, path, oracle_mod, host_threads):
     cfg, steps = CASES[name]
     blob = moe_blob(oracle_mod, cfg)
     orc = oracle_mod.OracleMoeRunner(cfg, blob, 64, threads=host_threads)
     toks = np.random.default_rng(7).integers(0, cfg.vocab_size, size=steps)
-    print(f"case={name} steps={steps}", flush=True)
+    print(f"case={name} path={path} steps={steps}", flush=True)
     with R.MoeRunner(cfg, blob, 64) as gpu:
+        assert gpu.persistent_available()
+        gpu.set_decode_path(path)
         for pos, tok in enumerate(toks):
             ref_logits, ref_hidden, _ = orc.forward_token(int(tok), pos, want_hidden=True)
             logits, hidden = gpu.forward_token_debug(int(tok), pos)
@@ -89,15 +92,17 @@ def test_moe_matches_hf_olmoe_fixture(oracle_mod):
             assert e <= TOL, f"pos {pos}: vs HF {e:.3e}"
 
 
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", ["olmoe_small", "gqa_bias_tied"])
-def test_moe_greedy_generation(name, oracle_mod, host_threads):
+def test_moe_greedy_generation(name, path, oracle_mod, host_threads):
     cfg, _ = CASES[name]
     blob = moe_blob(oracle_mod, cfg, seed=1)
     prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, size=6).astype(np.uint32)
     orc = oracle_mod.OracleMoeRunner(cfg, blob, 64, threads=host_threads)
     ref = orc.generate_greedy(prompt, 30)
-    print(f"case={name}", flush=True)
+    print(f"case={name} path={path}", flush=True)
     with R.MoeRunner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path(path)
         got, stats = gpu.generate_greedy_measured(prompt, 30)
         assert stats.generated_tokens == 30
         np.testing.assert_array_equal(got, ref)
@@ -152,15 +157,17 @@ def test_moe_batched_prefill_matches_oracle(name, oracle_mod, host_threads):
         assert e <= TOL, f"{name} step after prefill: {e:.3e}"
 
 
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", ["olmoe_small", "gqa_bias_tied"])
-def test_moe_generation_with_batched_prefill(name, oracle_mod, host_threads):
+def test_moe_generation_with_batched_prefill(name, path, oracle_mod, host_threads):
     cfg, _ = CASES[name]
     blob = moe_blob(oracle_mod, cfg, seed=1)
     prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, size=40).astype(np.uint32)
     orc = oracle_mod.OracleMoeRunner(cfg, blob, 96, threads=host_threads)
     ref = orc.generate_greedy(prompt, 30)
-    print(f"case={name}", flush=True)
+    print(f"case={name} path={path}", flush=True)
     with R.MoeRunner(cfg, blob, 96) as gpu:
+        gpu.set_decode_path(path)
         got, stats = gpu.generate_greedy_measured(prompt, 30, batched_prefill=True)
         assert stats.prompt_tokens == 40 and stats.generated_tokens == 30
         np.testing.assert_array_equal(got, ref)

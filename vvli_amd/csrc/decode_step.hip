@@ -39,6 +39,7 @@
 #include "device_common.hpp"
 #include "gemv_tile.hpp"
 #include "kernels.hpp"
+#include "moe_route.hpp"
 
 namespace vvli {
 
@@ -132,7 +133,8 @@ __device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint3
 // Detail timing mark (16-slot timing only): slot 0 the block's staged input,
 // 1 + w wave w's end of the phase; slots 9-11 (thread 0 in the input staging):
 // its entry, the return of its first attempt, its retry count; 12, 13 (thread
-// 0): past the phase's closing barrier, past the next phase's weight issue.
+// 0): past the phase's closing barrier, past the next phase's weight issue;
+// 14, 15 (thread 0, MoE gate/up): routed, its router row published (producers).
 __device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
     if (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
         p.timing[blockIdx.x * p.timing_stride + ph * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
@@ -159,8 +161,12 @@ struct MkTile {
     bool valid[2];         // output row exists
 };
 
+template <bool MOE = false>
 __device__ __forceinline__ uint32_t mk_tiles(const MkGemv& g, int mode) {
     const uint32_t total = g.r0 + g.r1 + g.r2;
+    if constexpr (MOE) {
+        if (g.moe == 2) return total;  // MoE down: one output row per tile
+    }
     return (mode == kGemvGateUp || g.split) ? total : (total + 1) / 2;
 }
 
@@ -170,8 +176,41 @@ __device__ __forceinline__ uint32_t mk_units(const MkGemv& g) { return g.split ?
 // Tile `tile`: gate row t and up row t (SwiGLU), else rows 2t, 2t+1 of the
 // stacked segments (segments hold an even number of rows, so a tile never
 // straddles two; an odd last row re-reads its own row as the second).
-__device__ __forceinline__ void mk_make_tile(const MkGemv& g, int mode, uint32_t tile, MkTile& t) {
+// MOE phases take the expert of a slot from ex (LDS): gate/up tile t is row
+// t % r_slot of slot t / r_slot's expert; down tile t is output row t, its
+// item `slot` streams that row of the experts of slots 2 slot and 2 slot + 1
+// (p[0], p[1]; an odd last pair repeats its first slot).
+template <bool MOE = false>
+__device__ __forceinline__ void mk_make_tile(const MkGemv& g, int mode, uint32_t tile, MkTile& t, uint32_t slot = 0,
+                                             const uint32_t* ex = nullptr) {
     const uint32_t K = g.K;
+    if constexpr (MOE) {
+        if (g.moe == 1) {
+            const bool v = tile < g.r0;
+            const uint32_t tt = v ? tile : 0;
+            const uint32_t sl = tt / g.r_slot, r = tt - sl * g.r_slot;
+            const size_t off = (size_t)ex[sl] * g.w_expert + (size_t)r * K;
+            t.p[0] = g.w0 + off;
+            t.p[1] = g.w_up + off;
+            t.row[0] = t.row[1] = tt;
+            t.seg = 0;
+            t.valid[0] = v;
+            t.valid[1] = false;
+            return;
+        }
+        if (g.moe == 2) {
+            const uint32_t s0 = 2 * slot, s1 = s0 + 1 < g.r_slot ? s0 + 1 : s0;
+            const bool v = tile < g.r0;
+            const size_t r = v ? tile : 0;
+            t.p[0] = g.w0 + (size_t)ex[s0] * g.w_expert + r * K;
+            t.p[1] = g.w0 + (size_t)ex[s1] * g.w_expert + r * K;
+            t.row[0] = t.row[1] = (uint32_t)r;
+            t.seg = 0;
+            t.valid[0] = v;
+            t.valid[1] = false;
+            return;
+        }
+    }
     if (g.split) {  // row t: first half in p[0], second half in p[1]
         const bool v = tile < g.r0;
         const uint32_t r = v ? tile : 0;
@@ -231,11 +270,12 @@ __device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
 // Issue the first item of this wave's first tile (weights only: may run
 // before the phase input exists). Defines buf and t on every path, so they are
 // dead between a phase's last item and the next prefetch.
+template <bool MOE = false>
 __device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkWave& w, uint4 (&buf)[2][kNJC],
-                                            MkTile& t, uint32_t t0 = 0) {
-    const uint32_t ntiles = mk_tiles(g, mode) - t0;
+                                            MkTile& t, uint32_t t0 = 0, const uint32_t* ex = nullptr) {
+    const uint32_t ntiles = mk_tiles<MOE>(g, mode) - t0;
     const uint32_t me = mk_owner(w, ntiles);
-    mk_make_tile(g, mode, t0 + (me < ntiles ? me : 0), t);
+    mk_make_tile<MOE>(g, mode, t0 + (me < ntiles ? me : 0), t, 0, ex);
     if (me >= ntiles) {
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -397,23 +437,33 @@ __device__ __forceinline__ void mk_glds_compute(const GLds& gl, const MkGemv& g,
 // make every following weight wait for that store's acknowledgement. Each lane
 // also loads its tile's addend (residual row or bias) when the batch opens and
 // checks the residual's tag only when it writes.
+// MOE down phase (g.moe == 2): a tile (one output row) has an item per pair
+// of slots (and chunk of the row); slots s, s + 1 multiply their experts'
+// rows with xs + s * K and xs + (s + 1) * K and add wsl[s], wsl[s + 1] times
+// the dot products, per lane, before the wave sum.
+template <bool MOE = false>
 __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
                                         uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
                                         uint32_t tag, const MkResid& rs, uint32_t t0, const float* park,
-                                        uint32_t lds_first, uint32_t n_lds, uint32_t* err, float* dbg) {
+                                        uint32_t lds_first, uint32_t n_lds, uint32_t* err, float* dbg,
+                                        const uint32_t* ex = nullptr, const float* wsl = nullptr) {
     const int lane = w.lane;
     const uint32_t U = mk_units(g);
     const uint32_t per_item = kNJC * kWave;
     const float* xs1 = g.split ? xs + g.K / 2 : xs;  // x of the second streamed row
-    const uint32_t nchunk = (U + per_item - 1) / per_item;
-    const uint32_t ntiles = mk_tiles(g, mode) - t0;
+    const uint32_t cps = (U + per_item - 1) / per_item;  // items per row
+    bool md = false;
+    if constexpr (MOE) md = g.moe == 2;
+    const uint32_t npair = md ? (g.r_slot + 1) / 2 : 1;
+    const uint32_t nchunk = cps * npair;
+    const uint32_t ntiles = mk_tiles<MOE>(g, mode) - t0;
     const uint32_t me = mk_owner(w, ntiles);
     const uint32_t my_tiles = me < ntiles ? (ntiles - 1 - me) / w.nw + 1 : 0;
     const uint32_t n_items = my_tiles * nchunk;
     bool ok = true;
     if (n_items) {
         if (!have) {
-            mk_make_tile(g, mode, t0 + me, tA);
+            mk_make_tile<MOE>(g, mode, t0 + me, tA, 0, ex);
             issue<uint16_t, 2>(bufA, tA.p, 0, U, lane);
         }
         // Lane state of the open batch: rows, segment, addends, parked results.
@@ -427,7 +477,7 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
             const uint32_t k = base + (uint32_t)lane;
             const bool mine = k < my_tiles;
             MkTile t;
-            mk_make_tile(g, mode, t0 + (mine ? me + k * w.nw : me), t);
+            mk_make_tile<MOE>(g, mode, t0 + (mine ? me + k * w.nw : me), t, 0, ex);
             ra = t.row[0];
             rb = t.row[1];
             sa = t.seg;
@@ -474,21 +524,49 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
         uint4 bufB[2][kNJC];
         MkTile tc = tA, tn = tA;  // tiles of the item being consumed / in flight
         float acc0 = 0.f, acc1 = 0.f;
+        float tot0 = 0.f;  // MOE down: router-weighted sum over the slots
         for (uint32_t it = 0; it < n_items; ++it) {
             const uint32_t chunk = it % nchunk;
             const bool more = it + 1 < n_items;
-            if (more && chunk == nchunk - 1) mk_make_tile(g, mode, t0 + me + ((it + 1) / nchunk) * w.nw, tn);
-            const uint32_t nbase = (chunk == nchunk - 1 ? 0 : chunk + 1) * per_item;
+            const uint32_t nchunk_next = chunk == nchunk - 1 ? 0 : chunk + 1;
+            if (more && chunk == nchunk - 1)
+                mk_make_tile<MOE>(g, mode, t0 + me + ((it + 1) / nchunk) * w.nw, tn, 0, ex);
+            uint32_t nbase = nchunk_next * per_item, ubase = chunk * per_item;
+            const float* xa = xs;
+            const float* xb = xs1;
+            if constexpr (MOE) {
+                if (md) {
+                    if (more && nchunk_next != 0 && nchunk_next % cps == 0)  // next slot pair of the same tile
+                        mk_make_tile<MOE>(g, mode, t0 + me + (it / nchunk) * w.nw, tn, nchunk_next / cps, ex);
+                    nbase = (nchunk_next % cps) * per_item;
+                    ubase = (chunk % cps) * per_item;
+                    const uint32_t s0 = 2 * (chunk / cps), s1 = s0 + 1 < g.r_slot ? s0 + 1 : s0;
+                    xa = xs + (size_t)s0 * g.K;
+                    xb = xs + (size_t)s1 * g.K;
+                }
+            }
             float acc[2] = {acc0, acc1};
             if (it & 1) {
                 if (more) issue<uint16_t, 2>(bufA, tn.p, nbase, U, lane);
-                consume_rows(bufB, xs, xs1, chunk * per_item, U, lane, acc);
+                consume_rows(bufB, xa, xb, ubase, U, lane, acc);
             } else {
                 if (more) issue<uint16_t, 2>(bufB, tn.p, nbase, U, lane);
-                consume_rows(bufA, xs, xs1, chunk * per_item, U, lane, acc);
+                consume_rows(bufA, xa, xb, ubase, U, lane, acc);
             }
             acc0 = acc[0];
             acc1 = acc[1];
+            if constexpr (MOE) {
+                if (md && chunk % cps == cps - 1) {  // end of a slot pair's rows
+                    const uint32_t s0 = 2 * (chunk / cps);
+                    tot0 = fmaf(wsl[s0], acc0, tot0);
+                    if (s0 + 1 < g.r_slot) tot0 = fmaf(wsl[s0 + 1], acc1, tot0);
+                    acc0 = acc1 = 0.f;
+                    if (chunk == nchunk - 1) {
+                        acc0 = tot0;
+                        tot0 = 0.f;
+                    }
+                }
+            }
             if (chunk == nchunk - 1) {
                 float v0, v1 = 0.f;
                 if (g.split) {
@@ -663,7 +741,67 @@ struct AttnLds {
 // (flash-decoding: out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s).
 // The K/V rows of the first tile are loaded before q is waited for. EXACT:
 // hd == HDMAX (loops fully unrolled), else hd <= HDMAX at run time.
-template <int HDMAX, bool EXACT>
+// QK-norm scales (MOE models that carry it): s_q = 1/sqrt(mean(q^2) + eps)
+// over the full q, s_k the same over the full k, from the q | k words of
+// phase `tag` (polled as one batch per thread, like the input staging).
+// Block-uniform; false: a poll failed.
+__device__ __forceinline__ bool mk_qk_scales(const DecodeStepParams& p, uint32_t tag, float& scq, float& sck) {
+    __shared__ float red2[2][kMkWaves];
+    const int tid = threadIdx.x;
+    const uint32_t nq = p.heads * p.hd, n2 = (nq + p.kvdim) / 2;  // word pairs of q | k (nq is even)
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(p.tqkv, n2 * 16);
+    constexpr int B = 4;
+    float sq = 0.f, sk = 0.f;
+    bool ok = true;
+    for (uint32_t i0 = tid; i0 < n2 && ok; i0 += B * kMkThreads) {
+        tword a[B], b[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) ld_coh_tw2(r, (i0 + k * kMkThreads) * 16, a[k], b[k]);
+        for (uint32_t spins = 0;;) {
+            bool done = true;
+#pragma unroll
+            for (int k = 0; k < B; ++k)
+                if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
+            if (done) break;
+            if (++spins > kSpinLimit) {
+                st_a(p.error, kDecodeErrTimeout);
+                ok = false;
+                break;
+            }
+            if ((spins & 63u) == 0 && ld_a(p.error) != 0) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < B; ++k) ld_coh_tw2(r, (i0 + k * kMkThreads) * 16, a[k], b[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            const uint32_t i = i0 + k * kMkThreads;
+            if (i < n2) {
+                const float v0 = tw_val(a[k]), v1 = tw_val(b[k]);
+                const float s2 = fmaf(v1, v1, v0 * v0);
+                if (2 * i < nq) sq += s2;
+                else sk += s2;
+            }
+        }
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    if ((tid & 63) == 0) red2[0][tid >> 6] = sq, red2[1][tid >> 6] = sk;
+    if (__syncthreads_or(!ok)) return false;
+    float tq = 0.f, tk = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMkWaves; ++i) tq += red2[0][i], tk += red2[1][i];
+    scq = 1.0f / sqrtf(tq / (float)nq + p.eps);
+    sck = 1.0f / sqrtf(tk / (float)p.kvdim + p.eps);
+    return true;
+}
+
+__device__ __forceinline__ float bf_val(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+template <int HDMAX, bool EXACT, bool MOE = false>
 __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t layer, uint32_t pos, uint32_t chunk,
                                              uint32_t ns, float* smem, uint32_t tag_in, uint32_t tag_out) {
     using LY = AttnLds<HDMAX>;
@@ -734,6 +872,15 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         }                                                                             \
     }
         VVLI_TILE_LOAD(t0, (int)min((uint32_t)TILE, t1 - t0));
+        // QK-norm (weight * (x * s), OlmoeRMSNorm's order) before the rotation.
+        const uint16_t* qn = nullptr;
+        const uint16_t* kn = nullptr;
+        float scq = 1.f, sck = 1.f;
+        if constexpr (MOE) {
+            qn = p.layer[layer].q_norm;
+            kn = p.layer[layer].k_norm;
+            if (qn && !mk_qk_scales(p, tag_in, scq, sck)) return false;
+        }
         // q (and the owner's new k / v) of this kv head, RoPE'd into LDS.
         for (int idx = tid; idx < G * half; idx += kMkThreads) {
             const int g = idx / half, i = idx - g * half;
@@ -741,7 +888,14 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const tword* src = q + (size_t)(h * G + g) * hd;
             tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
             ok = ok && poll_tw2(src + f, src + sc, tag_in, w0, w1, p.error);
-            const float x0 = tw_val(w0), x1 = tw_val(w1);
+            float x0 = tw_val(w0), x1 = tw_val(w1);
+            if constexpr (MOE) {
+                if (qn) {
+                    const uint16_t* nw = qn + (size_t)(h * G + g) * hd;
+                    x0 = bf_val(nw[f]) * (x0 * scq);
+                    x1 = bf_val(nw[sc]) * (x1 * scq);
+                }
+            }
             const float c = cs[2 * i], sn = cs[2 * i + 1];
             qs[g * HDMAX + f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
             qs[g * HDMAX + sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
@@ -761,7 +915,13 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             if (hk) ok = ok && poll_tw2(ksrc + f, ksrc + sc, tag_in, w0, w1, p.error);
             if (hv) ok = ok && poll_tw(vsrc, tag_in, wv, p.error);
             if (hk) {
-                const float x0 = tw_val(w0), x1 = tw_val(w1);
+                float x0 = tw_val(w0), x1 = tw_val(w1);
+                if constexpr (MOE) {
+                    if (kn) {
+                        x0 = bf_val(kn[(size_t)h * hd + f]) * (x0 * sck);
+                        x1 = bf_val(kn[(size_t)h * hd + sc]) * (x1 * sck);
+                    }
+                }
                 const float c = cs[2 * tid], sn = cs[2 * tid + 1];
                 knew[f] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
                 knew[sc] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
@@ -1022,12 +1182,83 @@ __device__ __forceinline__ const uint16_t* mk_norm_of(const DecodeStepParams& p,
     return f.kind == kPhQ ? t.norm[f.layer * 2] : (f.kind == kPhG ? t.norm[f.layer * 2 + 1] : nullptr);
 }
 
-template <int HDMAX, bool EXACT>
+// MOE routing in the gate/up phase. Router row e is computed by wave
+// e / grid of block grid - 1 - e % grid (the last blocks: the first ones run
+// the attention units and reach the phase later) on its block's staged
+// norm(x) and published as a tagged word; every block that runs
+// gate/up or down tiles then polls the E logits (one hop: the router stays
+// one 8 KiB row per producing wave instead of the whole matrix per block)
+// and the block takes the softmax + top-k into ex / wsl (`need`: the block
+// has tiles in this layer's gate/up or down). The gate/up and down
+// phases of the layer take their experts from there. Block-uniform; false:
+// a poll failed.
+// The producing wave's first router row, loaded at the end of the previous
+// phase into `pre` (the gate/up phase has no weight prefetch of its own).
+__device__ __forceinline__ uint32_t mk_router_row(const MkWave& w) {
+    return w.wave * gridDim.x + (gridDim.x - 1 - blockIdx.x);
+}
+
+__device__ __forceinline__ void mk_router_prefetch(const DecodeStepParams& p, uint32_t layer, const MkWave& w,
+                                                   uint4 (&pre)[kNJC]) {
+    const uint32_t e = mk_router_row(w);
+    if (e >= p.experts) return;
+    const uint16_t* rp[1] = {p.layer[layer].router + (size_t)e * p.hidden};
+    uint4 b[1][kNJC];
+    issue<uint16_t, 1>(b, rp, 0, p.hidden / 8, w.lane);
+#pragma unroll
+    for (int j = 0; j < kNJC; ++j) pre[j] = b[0][j];
+}
+
+__device__ __forceinline__ bool mk_route(const DecodeStepParams& p, uint32_t layer, const float* xs, uint32_t tag,
+                                         bool need, float* s_rl, unsigned long long* s_key, uint32_t* s_rank,
+                                         uint32_t* ex, float* wsl, const MkWave& w, const uint4 (&pre)[kNJC],
+                                         uint32_t ph) {
+    const uint16_t* rw = p.layer[layer].router;
+    const uint32_t E = p.experts, H = p.hidden, U = H / 8;
+    const uint32_t e0 = mk_router_row(w);
+    for (uint32_t e = e0; e < E; e += w.nw) {
+        const uint16_t* rp[1] = {rw + (size_t)e * H};
+        float acc[1] = {0.f};
+        for (uint32_t ub = 0; ub < U; ub += kNJC * kWave) {
+            uint4 b[1][kNJC];
+            if (e == e0 && ub == 0) {
+#pragma unroll
+                for (int j = 0; j < kNJC; ++j) b[0][j] = pre[j];
+            } else {
+                issue<uint16_t, 1>(b, rp, ub, U, w.lane);
+            }
+            consume<uint16_t, 1>(b, xs, ub, U, w.lane, acc);
+        }
+        const float v = wave_sum(acc[0]);
+        if (w.lane == 0) st_a(p.trl + e, tw_make(v, tag));
+        if (threadIdx.x == 0) mk_mark(p, ph, 15);
+    }
+    if (!need) return true;
+    bool ok = true;
+    const int tid = threadIdx.x;
+    if ((uint32_t)tid < E) {
+        tword wv = ld_a(p.trl + tid);
+        ok = poll_tw(p.trl + tid, tag, wv, p.error);
+        s_rl[tid] = tw_val(wv);
+    }
+    if (__syncthreads_or(!ok)) return false;
+    route_block<kMkThreads>(s_rl, E, p.top_k, ex, wsl, s_key, s_rank);
+    __syncthreads();
+    return true;
+}
+
+template <int HDMAX, bool EXACT, bool MOE = false>
 __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParams p) {
     extern __shared__ float smem[];
     __shared__ float red[kMkWaves];
     __shared__ unsigned long long kred[kMkWaves];
     __shared__ uint32_t s_ctl[4];
+    // MOE: the layer's routed experts and their weights, router logits.
+    __shared__ uint32_t s_ex[MOE ? kMaxTopK : 1];
+    __shared__ float s_w[MOE ? kMaxTopK : 1];
+    __shared__ float s_rl[MOE ? 256 : 1];
+    __shared__ unsigned long long s_key[MOE ? 256 : 1];
+    __shared__ uint32_t s_rank[MOE ? 256 : 1];
     const int tid = threadIdx.x;
     MkWave w;
     w.lane = tid & 63;
@@ -1089,8 +1320,8 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             const uint32_t tag = e0 + ph;
             bool ok = true;
             if (f.kind == kPhA && !f.logits) {
-                ok = mk_attention<HDMAX, EXACT>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag);
-                if (p.g_lds_tiles) {  // blocks without a unit: this layer's first gate/up tiles into LDS
+                ok = mk_attention<HDMAX, EXACT, MOE>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag);
+                if (!MOE && p.g_lds_tiles) {  // blocks without a unit: this layer's first gate/up tiles into LDS
                     const MkGemv& gg = tb.gemv[f.layer * 4 + 2];
                     const GLds q = mk_glds(p, units, gg);
                     if (mk_glds_count(q, w.wave)) {
@@ -1107,13 +1338,16 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 const int mode = mk_mode(f);
                 if (f.logits) best = 0ull;
                 // LDS tiles: gate/up phases only (gl.n = 0 otherwise).
-                const GLds gl = mk_glds(p, units, g, f.kind == kPhG && !f.logits && p.g_lds_tiles);
+                const GLds gl = mk_glds(p, units, g, !MOE && f.kind == kPhG && !f.logits && p.g_lds_tiles);
                 // The block has tiles (streamed: block < their count; or LDS
                 // tiles): stage the input.
-                const uint32_t n_streamed = mk_tiles(g, mode) - gl.n;
+                const uint32_t n_streamed = mk_tiles<MOE>(g, mode) - gl.n;
                 const bool has_lds =
                     gl.n && blockIdx.x >= gl.first_block && (blockIdx.x - gl.first_block) * gl.per_block < gl.n;
-                if (blockIdx.x < n_streamed || has_lds) {
+                // MOE gate/up: every block stages (the router rows are spread over
+                // the grid's waves); blocks with gate/up or down tiles route.
+                const bool routes = MOE && f.kind == kPhG && !f.logits;
+                if (blockIdx.x < n_streamed || has_lds || routes) {
                     const tword* src = f.kind == kPhO ? p.tattn
                                                       : (f.kind == kPhD ? p.tff : (f.kind == kPhG ? p.tx + H : p.tx));
                     ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
@@ -1122,6 +1356,14 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                                       ? p.timing + blockIdx.x * p.timing_stride + ph * 16 + 9
                                       : nullptr);
                     if (tid == 0) mk_mark(p, ph, 0);
+                    if constexpr (MOE) {
+                        if (routes && ok) {
+                            const uint32_t nd = mk_tiles<MOE>(tb.gemv[f.layer * 4 + 3], kGemvResid);
+                            const bool need = blockIdx.x < n_streamed || has_lds || blockIdx.x < nd;
+                            ok = mk_route(p, f.layer, smem, tag, need, s_rl, s_key, s_rank, s_ex, s_w, w, buf[0], ph);
+                            if (tid == 0) mk_mark(p, ph, 14);
+                        }
+                    }
                     // Residual rows: O reads x of the previous layer's D (or the
                     // embedding), D reads x of this layer's O.
                     MkResid rs;
@@ -1133,12 +1375,14 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                         have = mk_prefetch(g, mode, w, buf, tile, gl.n);
                         mk_glds_compute(gl, g, smem, reinterpret_cast<char*>(smem), p.g_lds_park, w);
                     }
-                    ok = ok && mk_gemv(g, mode, smem, w, buf, tile, have, best, tag, rs, gl.n,
-                                       reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) + p.g_lds_park),
-                                       n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0, n_lds,
-                                       p.error,
-                                       (f.kind == kPhD && p.hidden_dbg) ? p.hidden_dbg + (size_t)f.layer * H
-                                                                        : nullptr);
+                    ok = ok && mk_gemv<MOE>(g, mode, smem, w, buf, tile, have, best, tag, rs, gl.n,
+                                            reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) +
+                                                                           p.g_lds_park),
+                                            n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0,
+                                            n_lds, p.error,
+                                            (f.kind == kPhD && p.hidden_dbg) ? p.hidden_dbg + (size_t)f.layer * H
+                                                                             : nullptr,
+                                            s_ex, s_w);
                 }
                 if (f.logits && w.lane == 0) {
                     st_a(p.tkeys + 2 * w.wid, tw_make_u((uint32_t)(best >> 32), tag));
@@ -1156,11 +1400,15 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             if (ph < logits_ph) {
                 const MkPhase nf = mk_phase(ph + 1, p.layers);
                 const MkGemv& ng = mk_gemv_of(p, tb, nf);
-                if (nf.kind == kPhG && !nf.logits && p.g_lds_tiles &&
+                if (MOE && nf.kind == kPhG && !nf.logits) {  // experts not routed yet: the router row instead
+                    have = false;
+                    mk_router_prefetch(p, nf.layer, w, buf[0]);
+                }
+                else if (nf.kind == kPhG && !nf.logits && p.g_lds_tiles &&
                     mk_glds(p, units, ng).n > 0)
                     have = false;
                 else if (nf.kind != kPhA || nf.logits)
-                    have = mk_prefetch(ng, mk_mode(nf), w, buf, tile);
+                    have = mk_prefetch<MOE>(ng, mk_mode(nf), w, buf, tile, 0, s_ex);
             } else if (step + 1 < p.n_steps) {
                 have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
@@ -1250,15 +1498,22 @@ uint32_t decode_step_glds_plan(uint32_t hidden, uint32_t inter, uint32_t hd, siz
     return static_cast<uint32_t>(n1 + n2);
 }
 
-static const void* decode_step_fn(uint32_t hd) {
+bool decode_step_moe_supported(uint32_t hd) { return hd == 64 || hd == 128; }
+
+static const void* decode_step_fn(uint32_t hd, bool moe) {
+    if (moe) {
+        if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true, true>);
+        return reinterpret_cast<const void*>(&decode_step_kernel<128, true, true>);
+    }
     if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true>);
     if (hd == 128) return reinterpret_cast<const void*>(&decode_step_kernel<128, true>);
     if (hd <= 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, false>);
     return reinterpret_cast<const void*>(&decode_step_kernel<128, false>);
 }
 
-hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu) {
-    const void* f = decode_step_fn(hd);
+hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu, bool moe) {
+    if (moe && !decode_step_moe_supported(hd)) return hipErrorInvalidValue;
+    const void* f = decode_step_fn(hd, moe);
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kMkThreads, lds);
@@ -1277,8 +1532,13 @@ hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t
         const char* e = getenv("VVLI_PLAIN_LAUNCH");
         return e && e[0] == '1';
     }();
-    if (plain) return hipLaunchKernel(decode_step_fn(p.hd), dim3(blocks), dim3(kMkThreads), args, lds, s);
-    return hipLaunchCooperativeKernel(decode_step_fn(p.hd), dim3(blocks), dim3(kMkThreads), args, (unsigned)lds, s);
+    const bool moe = p.experts > 0;
+    if (moe && (!decode_step_moe_supported(p.hd) || p.experts > 256 || p.top_k == 0 || p.top_k > kMaxTopK ||
+                p.top_k > p.experts || p.hidden % 8 != 0))
+        return hipErrorInvalidValue;
+    if (plain) return hipLaunchKernel(decode_step_fn(p.hd, moe), dim3(blocks), dim3(kMkThreads), args, lds, s);
+    return hipLaunchCooperativeKernel(decode_step_fn(p.hd, moe), dim3(blocks), dim3(kMkThreads), args, (unsigned)lds,
+                                      s);
 }
 
 }  // namespace vvli

@@ -127,6 +127,8 @@ hipError_t launch_set_state(StepState* st, uint32_t token, uint32_t pos, uint32_
 // ---------------------------------------------------------------------------
 struct DecodeLayer {
     const uint16_t *input_norm, *q, *q_bias, *k, *k_bias, *v, *v_bias, *o, *post_norm, *gate, *up, *down;
+    // Mixture-of-experts layers: router [E][H], QK-norm weights (null: none).
+    const uint16_t *router, *q_norm, *k_norm;
 };
 
 // One GEMV phase of the persistent step: up to three stacked row segments
@@ -141,6 +143,12 @@ struct DecodeGemv {
     const uint16_t* w_up;
     uint32_t K;
     uint32_t split;  // one row per tile, its two halves streamed side by side (long rows, few of them)
+    // Mixture-of-experts phases: 1 = gate/up of the routed experts (tile t:
+    // slot t / r_slot, row t % r_slot of that slot's expert), 2 = down (a tile
+    // of rows 2t, 2t+1 streams them from every slot's expert and adds the
+    // router-weighted sum); w_expert elements lie between experts' matrices.
+    uint32_t moe, r_slot;
+    size_t w_expert;
 };
 
 // Values of DecodeStepParams::error: a poll passed its spin limit, the step
@@ -200,6 +208,12 @@ struct DecodeStepParams {
     // stream after the layer to hidden_dbg[l * hidden ..] (plain f32 stores;
     // with n_steps > 1 the last step's values remain).
     float* hidden_dbg;
+    // Mixture-of-experts step (experts > 0): the gate/up phase routes (router
+    // logits as tagged words trl[experts], one row per producing wave; every
+    // block with tiles takes the softmax + top-k) and runs the top_k experts;
+    // `inter` is then top_k * the expert width (the down phase's staged input).
+    uint32_t experts, top_k;
+    unsigned long long* trl;
 };
 
 // LDS bytes of one gate/up tile (gate row + up row of K bf16 weights, in
@@ -213,7 +227,9 @@ uint32_t decode_step_glds_plan(uint32_t hidden, uint32_t inter, uint32_t hd, siz
 size_t decode_step_table_offset(uint32_t hidden, uint32_t inter, uint32_t hd);
 size_t decode_step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t layers, uint32_t hd);
 uint32_t decode_step_phases_per_step(uint32_t layers);
-hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu);
+// moe: the mixture-of-experts instantiation (head_dim 64 or 128 only).
+bool decode_step_moe_supported(uint32_t hd);
+hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu, bool moe = false);
 hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t lds, hipStream_t s);
 
 // ---------------------------------------------------------------------------

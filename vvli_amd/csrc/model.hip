@@ -422,9 +422,13 @@ void prng_seed(uint64_t seed, uint64_t out[4]) {
 // graph's 921.
 bool use_persistent(const vvli_gpu_model* m) { return m->mk_ok && m->path != 1; }
 
+// Width of the persistent step's feed-forward activation (the down phase's
+// input): the intermediate size, or top_k expert widths in an MoE model.
+uint32_t mk_ff_width(const vvli_gpu_config& c) { return c.num_experts ? c.experts_per_tok * c.inter : c.inter; }
+
 // Offsets (in words) of the tagged activation arrays inside mk_tw.
 struct TaggedLayout {
-    size_t tx, tqkv, tattn, tff, ml, acc, keys, step, total;
+    size_t tx, tqkv, tattn, tff, ml, acc, keys, step, rl, total;
 };
 TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t blocks) {
     const size_t H = c.hidden, kv = kv_dim(c), G = c.heads / c.kv_heads, hd = head_dim(c);
@@ -438,11 +442,12 @@ TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t b
     t.tx = take(2 * H);
     t.tqkv = take(H + 2 * kv);
     t.tattn = take(H);
-    t.tff = take(c.inter);
+    t.tff = take(mk_ff_width(c));
     t.ml = take(static_cast<size_t>(c.kv_heads) * nsplit * G * 2);
     t.acc = take(static_cast<size_t>(c.kv_heads) * nsplit * G * hd);
     t.keys = take(static_cast<size_t>(blocks) * 8 * 2);
     t.step = take(1);
+    t.rl = take(c.num_experts);  // MoE router logits
     t.total = cur;
     return t;
 }
@@ -460,7 +465,7 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     DecodeStepParams p{};
     p.vocab = c.vocab;
     p.hidden = c.hidden;
-    p.inter = c.inter;
+    p.inter = mk_ff_width(c);
     p.layers = c.layers;
     p.heads = c.heads;
     p.kv_heads = c.kv_heads;
@@ -501,13 +506,14 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.timing = timing;
     p.timing_stride = timing_stride;
     p.timing_slots = timing_stride >= 16u * decode_step_phases_per_step(c.layers) ? 16u : 1u;
-    p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, c.inter, p.hd));
+    p.table_lds_offset = static_cast<uint32_t>(decode_step_table_offset(c.hidden, mk_ff_width(c), p.hd));
     p.g_lds_offset1 = m->mk_glds_off1;
     p.g_lds_tiles1 = m->mk_glds_tiles1;
     p.g_lds_offset2 = m->mk_glds_off2;
     p.g_lds_tiles = m->mk_glds_tiles;
     p.g_lds_park = m->mk_glds_park;
     p.hidden_dbg = hidden_dbg;
+    if (m->moe) p.experts = c.num_experts, p.top_k = c.experts_per_tok, p.trl = m->mk_tw + tl.rl;
     m->mk_epoch += static_cast<uint32_t>(need);
     // The error word is cleared only once the host has read it: a launch
     // that follows an unchecked one (the sampled generation loop) keeps a
@@ -835,23 +841,26 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     const size_t kvlen = static_cast<size_t>(cfg->layers) * max_seq_len * kv;
     m->nsplit = attn_nsplit(max_seq_len, hd);
     m->nkeys = gemv_num_keys(cfg->vocab);
-    // Persistent step: bf16 only, one 512-thread block per CU if it fits.
-    if (cfg->weight_kind == VVLI_WEIGHT_BF16 && !moe) {
+    // Persistent step: bf16 only, one 512-thread block per CU if it fits
+    // (MoE: head_dim 64 or 128).
+    if (cfg->weight_kind == VVLI_WEIGHT_BF16 && (!moe || decode_step_moe_supported(hd))) {
         int cus = 0, bpc = 0;
-        m->mk_lds = decode_step_lds_bytes(H, cfg->inter, cfg->layers, hd);
+        m->mk_lds = decode_step_lds_bytes(H, mk_ff_width(*cfg), cfg->layers, hd);
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
-            m->mk_lds <= 160 * 1024 && decode_step_max_blocks(hd, m->mk_lds, &bpc) == hipSuccess && bpc >= 1 &&
+            m->mk_lds <= 160 * 1024 && decode_step_max_blocks(hd, m->mk_lds, &bpc, moe) == hipSuccess && bpc >= 1 &&
             cus > 0 && static_cast<uint64_t>(max_seq_len) * kv * sizeof(float) < (1ull << 31)) {  // 32-bit KV offsets
             m->mk_ok = true;
             m->mk_blocks = static_cast<uint32_t>(cus);
             m->mk_nsplit = std::max<uint32_t>(1, std::min<uint32_t>(16, (max_seq_len + 63) / 64));  // <= kMaxSplitMk
-            // The rest of the CU's LDS holds gate/up tiles (VVLI_DECODE_GLDS=0: off).
+            // The rest of the CU's LDS holds gate/up tiles (VVLI_DECODE_GLDS=0: off;
+            // MoE: none, the experts are known only once the gate/up phase routes).
             const char* env = getenv("VVLI_DECODE_GLDS");
             uint32_t off1 = 0, n1 = 0, off2 = 0, park = 0;
             size_t lds2 = m->mk_lds;
-            const uint32_t tiles =
-                (env && env[0] == '0') ? 0 : decode_step_glds_plan(H, cfg->inter, hd, &lds2, &off1, &n1, &off2, &park);
-            if (tiles > 0 && decode_step_max_blocks(hd, lds2, &bpc) == hipSuccess && bpc >= 1) {
+            const uint32_t tiles = (moe || (env && env[0] == '0'))
+                                       ? 0
+                                       : decode_step_glds_plan(H, cfg->inter, hd, &lds2, &off1, &n1, &off2, &park);
+            if (tiles > 0 && decode_step_max_blocks(hd, lds2, &bpc, moe) == hipSuccess && bpc >= 1) {
                 m->mk_glds_off1 = off1;
                 m->mk_glds_tiles1 = n1;
                 m->mk_glds_off2 = off2;
@@ -859,7 +868,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
                 m->mk_glds_park = park;
                 m->mk_lds = lds2;
             } else {
-                (void)decode_step_max_blocks(hd, m->mk_lds, &bpc);  // restore the attribute for the smaller size
+                (void)decode_step_max_blocks(hd, m->mk_lds, &bpc, moe);  // restore the attribute for the smaller size
             }
         }
         (void)hipGetLastError();
@@ -939,11 +948,20 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
     TRY_ALLOC(upload_rope(m));
     if (m->mk_ok) {
         std::vector<DecodeLayer> dl(cfg->layers);
+        auto w = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+        const size_t IH = static_cast<size_t>(cfg->inter) * H;
         for (uint32_t l = 0; l < cfg->layers; ++l) {
+            if (moe) {  // gate = the fused gate|up of expert 0, up = its up rows
+                const MoeLayerSlices& L = m->moe_layout.layers[l];
+                dl[l] = DecodeLayer{w(L.input_norm), w(L.q), w(L.q_bias), w(L.k), w(L.k_bias), w(L.v),
+                                    w(L.v_bias),     w(L.o), w(L.post_norm), w(L.gate_up), w(L.gate_up) + IH,
+                                    w(L.down),       w(L.router), w(L.q_norm), w(L.k_norm)};
+                continue;
+            }
             const LayerSlices& L = m->layout.layers[l];
-            auto w = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
             dl[l] = DecodeLayer{w(L.input_norm), w(L.q), w(L.q_bias), w(L.k), w(L.k_bias), w(L.v), w(L.v_bias),
-                                w(L.o),          w(L.post_norm), w(L.gate), w(L.up), w(L.down)};
+                                w(L.o),          w(L.post_norm), w(L.gate), w(L.up), w(L.down),
+                                nullptr,         nullptr,        nullptr};
         }
         TRY_ALLOC(fail_hip(hipMemcpy(m->mk_layers, dl.data(), dl.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice),
                            "layer table"));
@@ -970,6 +988,10 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
             // Down rows are long (inter) and few (hidden): split each row in
             // two halves so that every wave of the grid streams.
             gd.split = (cfg->inter % 16 == 0 && cfg->inter >= 2 * H) ? 1u : 0u;
+            if (moe) {  // routed experts: top_k slots of inter rows / columns
+                gg.moe = 1, gg.r_slot = cfg->inter, gg.w_expert = 2 * IH, gg.r0 = cfg->experts_per_tok * cfg->inter;
+                gd.moe = 2, gd.r_slot = cfg->experts_per_tok, gd.w_expert = IH, gd.split = 0;
+            }
         }
         DecodeGemv& gl = dg[static_cast<size_t>(cfg->layers) * 4];
         gl.w0 = static_cast<const uint16_t*>(wslice(m, cfg->tie ? m->layout.embed : m->layout.lm_head));

@@ -16,6 +16,7 @@
 #include "device_common.hpp"
 #include "gemv_tile.hpp"
 #include "kernels.hpp"
+#include "moe_route.hpp"
 
 namespace vvli {
 
@@ -28,55 +29,15 @@ __device__ inline float bf(uint16_t h) { return __uint_as_float(static_cast<uint
 
 // Router: logits = W_r . norm(x), one row per wave over ceil(E / 4) blocks;
 // the last block to finish (atomic ticket) runs the softmax and top-k on the
-// logits (route_wave) and resets the ticket.
-
-__device__ inline void route_wave(const float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight) {
-    const int lane = threadIdx.x & 63;
-    float p[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t e = lane + 64 * j;
-        p[j] = e < E ? logits[e] : -INFINITY;
-        mx = fmaxf(mx, p[j]);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t e = lane + 64 * j;
-        p[j] = e < E ? expf(p[j] - mx) : 0.f;
-        sum += p[j];
-    }
-    sum = wave_sum(sum);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] = p[j] / sum;
-    uint32_t taken = 0;
-    for (uint32_t r = 0; r < top_k; ++r) {
-        unsigned long long best = 0ull;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64 * j;
-            if (e >= E || (taken >> j) & 1u) continue;
-            const unsigned long long key =
-                (static_cast<unsigned long long>(__float_as_uint(p[j]) + 1u) << 32) | (0xffffffffu - e);
-            best = key > best ? key : best;
-        }
-        best = wave_max_u64(best);
-        const uint32_t e = 0xffffffffu - static_cast<uint32_t>(best & 0xffffffffull);
-        if (lane == 0) {
-            idx[r] = e;
-            weight[r] = __uint_as_float(static_cast<uint32_t>(best >> 32) - 1u);
-        }
-        if (static_cast<uint32_t>(lane) == e % 64) taken |= 1u << (e / 64);
-    }
-}
+// logits (route_block) and resets the ticket.
 
 __global__ __launch_bounds__(kThreads) void moe_router_kernel(MoeRouterArgs a) {
     extern __shared__ float smem[];
     float* xs = smem;                // [H] normalised input
     float* red = smem + a.H;         // [waves]
     __shared__ int last;
+    __shared__ unsigned long long route_keys[256];
+    __shared__ uint32_t route_rank[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Stage (x * w) * s.
     float ss = 0.f;
@@ -125,21 +86,12 @@ __global__ __launch_bounds__(kThreads) void moe_router_kernel(MoeRouterArgs a) {
     }
     __syncthreads();
     if (!last) return;
-    if (wave == 0) {
-        float lg[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64 * j;
-            lg[j] = e < a.E ? __hip_atomic_load(a.logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-        }
-        // route_wave reads logits through LDS.
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64 * j;
-            if (e < a.E) xs[e] = lg[j];
-        }
-        route_wave(xs, a.E, a.top_k, a.idx, a.weight);
-        if (lane == 0) __hip_atomic_store(a.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // The last block routes (route_block reads the logits from LDS).
+    for (uint32_t e = tid; e < a.E; e += kThreads)
+        xs[e] = __hip_atomic_load(a.logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    route_block<kThreads>(xs, a.E, a.top_k, a.idx, a.weight, route_keys, route_rank);
+    if (tid == 0) __hip_atomic_store(a.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Stages x (x_len floats) in LDS, optionally RMS-normalised (x * w) * s.
@@ -332,11 +284,13 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeGemvArgs a, float
 // ---------------------------------------------------------------------------
 
 // One block per row: norm(x_r) staged in LDS, one router row per wave at a
-// time, then wave 0 takes the softmax and top-k (route_wave).
+// time, then the block takes the softmax and top-k (route_block).
 __global__ __launch_bounds__(kThreads) void moe_route_rows_kernel(MoeRouteRowsArgs a) {
     extern __shared__ float smem[];
     float* xs = smem;  // [H]
     __shared__ float row_logit[256];
+    __shared__ unsigned long long route_keys[256];
+    __shared__ uint32_t route_rank[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r = blockIdx.x;
     const float* x = a.x + static_cast<size_t>(r) * a.H;
@@ -358,9 +312,8 @@ __global__ __launch_bounds__(kThreads) void moe_route_rows_kernel(MoeRouteRowsAr
         if (lane == 0) row_logit[e] = acc;
     }
     __syncthreads();
-    if (wave == 0)
-        route_wave(row_logit, a.E, a.top_k, a.idx + static_cast<size_t>(r) * a.top_k,
-                   a.weight + static_cast<size_t>(r) * a.top_k);
+    route_block<kThreads>(row_logit, a.E, a.top_k, a.idx + static_cast<size_t>(r) * a.top_k,
+                          a.weight + static_cast<size_t>(r) * a.top_k, route_keys, route_rank);
 }
 
 // Counting sort of the n = rows * top_k pairs by expert in one 1024-thread
