@@ -142,8 +142,10 @@ int vvli_gpu_read_weights(vvli_gpu_model* model, uint64_t elem_offset, uint64_t 
  * post_norm, router [E][hidden], gate_up [E][2*inter][hidden] (gate rows then
  * up rows, HF's fused layout), down [E][hidden][inter]; final_norm; lm_head
  * unless tied; every slice 64-byte aligned. The handle works with every token
- * entry point below (the per-kernel graph path; prefill runs the token loop).
- * Limits: <= 256 experts, experts_per_tok <= 16. */
+ * entry point below: decode on the persistent step (head_dim 64 or 128) or
+ * the per-kernel graph, prompts through the batched prefill (head_dim 32, 64
+ * or 128; the (row, slot) pairs grouped by expert on the device) or the
+ * token loop. Limits: <= 256 experts, experts_per_tok <= 16. */
 uint64_t vvli_gpu_moe_storage_element_count(const vvli_gpu_config* cfg);
 int vvli_gpu_moe_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* host_blob,
                               size_t blob_elems, vvli_gpu_model** out);
