@@ -26,8 +26,8 @@ def bf16_bits(a: np.ndarray) -> np.ndarray:
     return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
 
 
-def moe_blob(oracle_mod, cfg, seed=0):
-    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=seed, stddev=0.02)
+def moe_blob(oracle_mod, cfg, seed=0, stddev=0.02):
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=seed, stddev=stddev)
     lay = oracle_mod.moe_layout(cfg, C.WEIGHT_BF16)
     rng = np.random.default_rng(seed + 100)
     n = cfg.num_experts * cfg.hidden_size
@@ -170,4 +170,39 @@ def test_moe_generation_with_batched_prefill(name, path, oracle_mod, host_thread
         gpu.set_decode_path(path)
         got, stats = gpu.generate_greedy_measured(prompt, 30, batched_prefill=True)
         assert stats.prompt_tokens == 40 and stats.generated_tokens == 30
+        np.testing.assert_array_equal(got, ref)
+
+
+def moe_generate_sampled_ref(oracle_mod, orc, prompt, max_new, opts):
+    """generateGreedyMeasuredInternal's loop with the Sampler
+    (src/generator.zig:230-280, Sampler.init's seed mapping :75) over the MoE
+    oracle's token step and the oracle sampler."""
+    pos, logits = 0, None
+    for t in prompt:
+        logits = orc.forward_token(int(t), pos)
+        pos += 1
+    prng = oracle_mod.prng_seed(opts.seed if opts.seed else 0x9E3779B97F4A7C15)
+    out = []
+    for _ in range(max_new):
+        tok = oracle_mod.sampler_next(logits, prompt, np.array(out, dtype=np.uint32), opts, prng)
+        out.append(tok)
+        logits = orc.forward_token(tok, pos)
+        pos += 1
+    return np.array(out, dtype=np.uint32)
+
+
+@pytest.mark.parametrize("path", ["persistent", "graph"])
+def test_moe_sampled_generation(path, oracle_mod, host_threads):
+    cfg, _ = CASES["olmoe_small"]
+    # N(0, 0.05) weights: logits spread enough that the top-k and top-p cuts sit in clear gaps.
+    blob = moe_blob(oracle_mod, cfg, seed=3, stddev=0.05)
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, size=20).astype(np.uint32)
+    o = R.Sampling(temperature=0.8, top_p=0.95, top_k=40, repeat_penalty=1.1, repeat_last_n=64, seed=7)
+    orc = oracle_mod.OracleMoeRunner(cfg, blob, 96, threads=host_threads)
+    ref = moe_generate_sampled_ref(oracle_mod, orc, prompt, 40, o)
+    print(f"case=olmoe_small sampled path={path}", flush=True)
+    with R.MoeRunner(cfg, blob, 96) as gpu:
+        gpu.set_decode_path(path)
+        got, stats = gpu.generate(prompt, 40, o, batched_prefill=True)
+        assert stats.generated_tokens == 40
         np.testing.assert_array_equal(got, ref)
