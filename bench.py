@@ -111,7 +111,7 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(cfg, blob, prompt, budget_s: float, max_tokens: int) -> dict:
+def cpu_baseline(cfg, blob, prompt, budget_s: float, max_tokens: int, inv_freq=None) -> dict:
     """Decode tok/s of the oracle (C restatement of the reference CPU path:
     per-call thread fan-out over rows, single-threaded attention) on this
     host, at the positions the GPU decodes: the prompt goes through the
@@ -122,6 +122,8 @@ def cpu_baseline(cfg, blob, prompt, budget_s: float, max_tokens: int) -> dict:
 
     threads = oracle.cpu_count()
     r = oracle.OracleRunner(cfg, blob, len(prompt) + max_tokens + 16, threads=threads, lanes=16)
+    if inv_freq is not None:
+        r.set_rope_table(inv_freq)
     t0 = time.perf_counter()
     logits = r.prefill(prompt)
     prefill_s = time.perf_counter() - t0
@@ -136,6 +138,42 @@ def cpu_baseline(cfg, blob, prompt, budget_s: float, max_tokens: int) -> dict:
     dt = time.perf_counter() - t0
     r.close()
     return {"tokens": tokens, "seconds": dt, "threads": threads, "prefill_s": prefill_s}
+
+
+def open_runner(args, cfg, blob):
+    """The decode runner over blob: uploaded directly (--source synthetic) or
+    written as a bf16 GGUF file and loaded through the device GGUF loader
+    (mmap -> HBM, vvli_gpu_model_create_from_gguf), the form the Llama-3.2-1B
+    workload specifies. Returns (runner, description of the source)."""
+    from vvli_amd import runtime as R
+
+    if args.source != "gguf":
+        return R.Runner(cfg, blob, args.ctx), "synthetic blob uploaded from host memory"
+    import tempfile
+
+    from vvli_amd import gguf_write
+    from vvli_amd import loaders as L
+
+    tmpd = tempfile.mkdtemp(prefix="vvli_bench_")
+    path = os.path.join(tmpd, f"{args.model}.gguf")
+    try:
+        t = time.perf_counter()
+        size = gguf_write.write_dense_gguf(path, cfg, blob)
+        tw = time.perf_counter() - t
+        t = time.perf_counter()
+        gcfg, runner = L.device_load_gguf(path, args.ctx)
+        tl = time.perf_counter() - t
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(tmpd)
+    for f in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+              "num_key_value_heads", "tie_word_embeddings", "rope_layout"):
+        if getattr(gcfg, f) != getattr(cfg, f):
+            raise RuntimeError(f"GGUF round trip changed {f}: {getattr(gcfg, f)} != {getattr(cfg, f)}")
+    print(f"[bench] bf16 GGUF {size / 1e9:.2f} GB written in {tw:.1f}s, loaded to the device in {tl:.1f}s",
+          file=sys.stderr, flush=True)
+    return runner, f"bf16 GGUF file ({size / 1e9:.2f} GB) through the device GGUF loader (mmap -> HBM)"
 
 
 def gemv_sweep(shapes, ms, log=True) -> list:
@@ -518,9 +556,17 @@ def main() -> int:
     ap.add_argument("--sampling", action="store_true",
                     help="decode mode: sample with the generator's default options instead of greedy")
     ap.add_argument("--top-k", type=int, default=40, help="--sampling: top_k (0: every finite candidate)")
+    ap.add_argument("--source", default=None, choices=["gguf", "synthetic"],
+                    help="decode mode: weights through a bf16 GGUF file and the device loader (default for "
+                         "llama-3.2-1b, the workload's form) or uploaded from the synthetic host blob")
+    ap.add_argument("--rope", default=None, choices=["llama3", "base"],
+                    help="decode mode: llama3-scaled RoPE table (default for llama-3.2-1b) or plain theta")
     ap.add_argument("--path", default="auto", choices=["auto", "graph", "persistent"],
                     help="decode implementation: one persistent launch per step (auto) or per-kernel HIP graph")
     args = ap.parse_args()
+    llama = args.model == "llama-3.2-1b"
+    args.source = args.source or ("gguf" if llama else "synthetic")
+    args.rope = args.rope or ("llama3" if llama else "base")
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (multi-GPU sharding is not built)",
@@ -549,7 +595,11 @@ def main() -> int:
         return moe_decode_main(args, cfg, blob)
     if args.sampling:
         return sampled_main(args, cfg, blob)
-    runner = R.Runner(cfg, blob, args.ctx)
+    runner, source = open_runner(args, cfg, blob)
+    inv_freq = None
+    if args.rope == "llama3":  # Llama-3.2's rope_scaling: factor 32, low/high freq factors 1 / 4, original ctx 8192
+        inv_freq = R.llama3_inv_freq(cfg.head_dim(), cfg.rope_theta)
+        runner.set_rope_table(inv_freq)
     runner.set_decode_path(args.path)
     runner.set_prefill_path("auto" if args.prefill == "batched" else "loop")
     batched = args.prefill == "batched"
@@ -682,7 +732,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(cfg, blob, prompt, args.cpu_budget, 512)
+        cb = cpu_baseline(cfg, blob, prompt, args.cpu_budget, 512, inv_freq)
         # Parity spot check: the GPU's greedy continuation of the same prompt.
         runner.kv_clear()
         g_tokens, _ = runner.generate_greedy_measured(prompt, len(cb["tokens"]), batched_prefill=batched)
@@ -713,6 +763,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": f"{args.model} bf16 greedy decode, bs1", "prompt_tokens": args.prompt,
                    "decode_tokens": args.steps, "ctx": args.ctx, "kv_cache": "f32", "prefill": args.prefill,
+                   "weights": source,
+                   "rope": ("llama3 scaling (factor 32, low/high freq factors 1/4, original ctx 8192)"
+                            if inv_freq is not None else f"theta {cfg.rope_theta:g}"),
                    "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(prefill_tok_s, 2),
         "step_roofline": {"bytes_per_token_avg": step_bytes // args.steps, "achieved": round(step_gbs, 1),

@@ -560,3 +560,28 @@ def test_gguf_metadata_value_types():
     w.meta = [m for m in w.meta if b"rope.freq_base" not in m]
     w.kv("llama.rope.freq_base", I16, struct.pack("<h", 5000))
     assert C.Config.from_gguf(w.build()).rope_theta == 5000.0
+
+
+@pytest.mark.parametrize("tie", [True, False])
+def test_written_gguf_loads_back_bit_exact(tmp_path, tie):
+    """vvli_amd.gguf_write (the benchmark's GGUF workload) read back by the host
+    GGUF loader: the same config and the same blob, bit for bit."""
+    from vvli_amd import gguf_write
+    from vvli_amd import runtime as R
+
+    cfg = tiny("llama", tie, False)
+    cfg.rope_layout = C.ROPE_INTERLEAVED
+    cfg.rms_norm_eps = float(np.float32(1e-5))
+    cfg.rope_theta = float(np.float32(5e5))
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=3, stddev=0.02)
+    path = tmp_path / "m.gguf"
+    size = gguf_write.write_dense_gguf(path, cfg, blob)
+    assert path.stat().st_size == size
+    got_cfg, got = L.load_gguf(path, C.WEIGHT_BF16)
+    for f in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+              "num_key_value_heads", "max_position_embeddings", "tie_word_embeddings", "qkv_bias", "rope_layout"):
+        assert getattr(got_cfg, f) == getattr(cfg, f), f
+    assert got_cfg.rope_theta == cfg.rope_theta and got_cfg.rms_norm_eps == cfg.rms_norm_eps
+    np.testing.assert_array_equal(got, blob)
+    with pytest.raises(ValueError):
+        gguf_write.write_dense_gguf(path, cfg, blob.astype(np.float32))

@@ -54,6 +54,36 @@ def llama3_inv_freq(head_dim: int, theta: float, factor: float = 32.0, low_freq_
     return out
 
 
+def dense_slices(cfg: Config, weight_kind: int = WEIGHT_BF16) -> list:
+    """(slot, layer or None, element offset, element count) of every slice of
+    the dense blob, in vvli_gpu_storage_element_count's layout (assignSlices,
+    src/llm.zig:488-522: embed; per layer input_norm, q, (q_bias), k,
+    (k_bias), v, (v_bias), o, post_norm, gate, up, down; final_norm; lm_head
+    unless tied; each slice 64-byte aligned)."""
+    ea = 64 // (2 if weight_kind == WEIGHT_BF16 else 4)
+    H, kv, I = cfg.hidden_size, cfg.kv_dim(), cfg.intermediate_size
+    out, cur = [], 0
+
+    def take(slot, layer, n):
+        nonlocal cur
+        cur = (cur + ea - 1) // ea * ea
+        out.append((slot, layer, cur, n))
+        cur += n
+
+    take("embed", None, cfg.vocab_size * H)
+    for l in range(cfg.num_hidden_layers):
+        for slot, n in [("input_norm", H), ("q", H * H), ("q_bias", H if cfg.qkv_bias else None), ("k", kv * H),
+                        ("k_bias", kv if cfg.qkv_bias else None), ("v", kv * H),
+                        ("v_bias", kv if cfg.qkv_bias else None), ("o", H * H), ("post_norm", H),
+                        ("gate", I * H), ("up", I * H), ("down", H * I)]:
+            if n is not None:
+                take(slot, l, n)
+    take("final_norm", None, H)
+    if not cfg.tie_word_embeddings:
+        take("lm_head", None, cfg.vocab_size * H)
+    return out
+
+
 def moe_slice_offset(cfg: Config, layer: int, slot: str, weight_kind: int = WEIGHT_BF16) -> int:
     """Element offset of one slice of the MoE blob (vvli_gpu_moe_storage_element_count's
     layout: per layer input_norm, q, (q_bias), k, (k_bias), v, (v_bias), (q_norm,
