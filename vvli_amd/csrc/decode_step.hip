@@ -1189,7 +1189,13 @@ __device__ __forceinline__ const uint16_t* mk_norm_of(const DecodeStepParams& p,
 // gate/up or down tiles then polls the E logits (one hop: the router stays
 // one 8 KiB row per producing wave instead of the whole matrix per block)
 // and the block takes the softmax + top-k into ex / wsl (`need`: the block
-// has tiles in this layer's gate/up or down). The gate/up and down
+// has tiles in this layer's gate/up or down).
+// Why the next layer's write of trl cannot overtake a reader: a block that
+// polls trl here has gate/up or down tiles, so its gate/up outputs (staged
+// by every down block) or its down outputs (staged by the next q/k/v phase)
+// lie upstream of the next layer's gate/up staging, which precedes any write
+// of trl for that layer. Blocks without tiles do not poll, so a late one
+// never waits for words that have moved on to a later epoch. The gate/up and down
 // phases of the layer take their experts from there. Block-uniform; false:
 // a poll failed.
 // The producing wave's first router row, loaded at the end of the previous
