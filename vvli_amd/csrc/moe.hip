@@ -283,37 +283,45 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeGemvArgs a, float
 // combine adds exactly what the token step's combine adds.
 // ---------------------------------------------------------------------------
 
-// One block per row: norm(x_r) staged in LDS, one router row per wave at a
-// time, then the block takes the softmax and top-k (route_block).
-__global__ __launch_bounds__(kThreads) void moe_route_rows_kernel(MoeRouteRowsArgs a) {
+// One 512-thread block per row: norm(x_r) staged in LDS, then each wave
+// takes four router rows at a time (their loads in flight together: the
+// router sits in L2, so a row costs a round trip, not bandwidth), then the
+// block's softmax and top-k (route_block).
+constexpr int kRouteThreads = 512;
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_rows_kernel(MoeRouteRowsArgs a) {
     extern __shared__ float smem[];
     float* xs = smem;  // [H]
     __shared__ float row_logit[256];
     __shared__ unsigned long long route_keys[256];
     __shared__ uint32_t route_rank[256];
+    constexpr int kWaves = kRouteThreads / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r = blockIdx.x;
     const float* x = a.x + static_cast<size_t>(r) * a.H;
     const float scale = a.row_scale[r];
-    for (uint32_t i = tid; i < a.H; i += kThreads) xs[i] = x[i] * bf(a.norm_w[i]) * scale;
+    for (uint32_t i = tid; i < a.H; i += kRouteThreads) xs[i] = x[i] * bf(a.norm_w[i]) * scale;
     __syncthreads();
     const uint32_t U = a.H / 8;
-    for (uint32_t e = wave; e < a.E; e += kWavesPerBlock) {
-        const uint16_t* row = a.w + static_cast<size_t>(e) * a.H;
-        float acc = 0.f;
-        for (uint32_t u = lane; u < U; u += 64) {
-            const uint4 q = load_unit(row + static_cast<size_t>(u) * 8);
-            float wf[8];
-            WeightTraits<uint16_t>::expand(q, wf);
+    for (uint32_t e0 = wave * 4; e0 < a.E; e0 += kWaves * 4) {
+        const uint16_t* rp[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc = fmaf(wf[j], xs[u * 8 + j], acc);
+        for (int q = 0; q < 4; ++q) rp[q] = a.w + static_cast<size_t>(e0 + q < a.E ? e0 + q : a.E - 1) * a.H;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t ub = 0; ub < U; ub += kNJC * 64) {
+            uint4 b[4][kNJC];
+            issue<uint16_t, 4>(b, rp, ub, U, lane);
+            consume<uint16_t, 4>(b, xs, ub, U, lane, acc);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) row_logit[e] = acc;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float v = wave_sum(acc[q]);
+            if (lane == 0 && e0 + q < a.E) row_logit[e0 + q] = v;
+        }
     }
     __syncthreads();
-    route_block<kThreads>(row_logit, a.E, a.top_k, a.idx + static_cast<size_t>(r) * a.top_k,
-                          a.weight + static_cast<size_t>(r) * a.top_k, route_keys, route_rank);
+    route_block<kRouteThreads>(row_logit, a.E, a.top_k, a.idx + static_cast<size_t>(r) * a.top_k,
+                               a.weight + static_cast<size_t>(r) * a.top_k, route_keys, route_rank);
 }
 
 // Counting sort of the n = rows * top_k pairs by expert in one 1024-thread
@@ -356,17 +364,30 @@ __global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const uint32_t
         eoff[tid] = run;  // the expert's total, for now
     }
     __syncthreads();
-    if (tid == 0) {  // totals -> offsets over experts; tile counts -> tile offsets
-        uint32_t run = 0, tr = 0;
-        for (uint32_t ee = 0; ee < E; ++ee) {
-            const uint32_t tot = eoff[ee];
-            eoff[ee] = run;
-            toff[ee] = tr;
-            run += tot;
-            tr += (tot + tile_rows - 1) / tile_rows;
-        }
-        toff[E] = tr;
-        tiles[0] = make_uint4(tr, 0, 0, 0);
+    // Totals -> offsets over experts, tile counts -> tile offsets: inclusive
+    // scans over the E entries (Hillis-Steele in LDS), made exclusive below.
+    __shared__ uint32_t scan_a[256], scan_b[256];
+    if (tid < 256) {
+        const uint32_t tot = tid < E ? eoff[tid] : 0u;
+        scan_a[tid] = tot;
+        scan_b[tid] = (tot + tile_rows - 1) / tile_rows;
+    }
+    __syncthreads();
+    for (uint32_t d = 1; d < 256; d <<= 1) {
+        uint32_t va = 0, vb = 0;
+        if (tid < 256 && tid >= d) va = scan_a[tid - d], vb = scan_b[tid - d];
+        __syncthreads();
+        if (tid < 256) scan_a[tid] += va, scan_b[tid] += vb;
+        __syncthreads();
+    }
+    if (tid < E) {
+        const uint32_t tot = eoff[tid];
+        eoff[tid] = scan_a[tid] - tot;
+        toff[tid] = scan_b[tid] - (tot + tile_rows - 1) / tile_rows;
+    }
+    if (tid == 0) {
+        toff[E] = scan_b[E - 1];
+        tiles[0] = make_uint4(scan_b[E - 1], 0, 0, 0);
     }
     __syncthreads();
     if (g < G) {
@@ -412,9 +433,14 @@ __global__ __launch_bounds__(kThreads) void moe_combine_kernel(const float* __re
     __syncthreads();
     float* xr = x + static_cast<size_t>(r) * H;
     for (uint32_t i = threadIdx.x; i < H; i += kThreads) {
+        float v[kMaxTopK];  // every slot's load in flight before the ordered sum
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j)
+            v[j] = j < static_cast<int>(top_k) ? eout[static_cast<size_t>(sp[j]) * H + i] : 0.f;
         float acc = 0.f;
-        for (uint32_t j = 0; j < top_k; ++j)
-            acc = __fadd_rn(acc, __fmul_rn(eout[static_cast<size_t>(sp[j]) * H + i], sw[j]));
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j)
+            if (j < static_cast<int>(top_k)) acc = __fadd_rn(acc, __fmul_rn(v[j], sw[j]));
         xr[i] = __fadd_rn(xr[i], acc);
     }
 }
@@ -426,8 +452,8 @@ hipError_t launch_moe_route_rows(const MoeRouteRowsArgs& a, hipStream_t s) {
     if (a.E == 0 || a.E > 256 || a.top_k == 0 || a.top_k > a.E || a.top_k > static_cast<uint32_t>(kMaxTopK) ||
         a.H % 8 != 0 || a.H > 16384 || !a.row_scale)
         return hipErrorInvalidValue;
-    return vlaunch(moe_route_rows_kernel, dim3(a.rows), dim3(kThreads), static_cast<size_t>(a.H) * sizeof(float), s,
-                   a);
+    return vlaunch(moe_route_rows_kernel, dim3(a.rows), dim3(kRouteThreads), static_cast<size_t>(a.H) * sizeof(float),
+                   s, a);
 }
 
 hipError_t launch_moe_group(const uint32_t* idx, uint32_t rows, uint32_t top_k, uint32_t E, uint32_t tile_rows,

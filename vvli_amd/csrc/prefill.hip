@@ -416,13 +416,6 @@ __global__ __launch_bounds__(kRowThreads) void prefill_embed_kernel(const uint16
     x[static_cast<size_t>(t) * n + i] = from_bf16(embed[static_cast<size_t>(tokens[t]) * n + i]);
 }
 
-__device__ inline void rot(float* v, int a, int b, float c, float s) {
-    // rotatePair, src/llm.zig:1360-1371: x0*c - x1*s, x0*s + x1*c (unfused)
-    const float x0 = v[a], x1 = v[b];
-    v[a] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-    v[b] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
-}
-
 // One block per token row t (position start + t): rotate its q heads in place
 // and its k head vectors (after the QK-norm when the model has one), then
 // write k and v to the cache rows of that position.
@@ -451,23 +444,56 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
         scq = 1.0f / sqrtf(tq / static_cast<float>(qw) + a.norm_eps);
         sck = 1.0f / sqrtf(tk / static_cast<float>(a.kvdim) + a.norm_eps);
     }
-    for (uint32_t p = threadIdx.x; p < qpairs + kpairs; p += kRowThreads) {
-        const bool is_q = p < qpairs;
-        const uint32_t pp = is_q ? p : p - qpairs;
-        const uint32_t h = pp / half, i = pp % half;
-        float* v = row + (is_q ? 0 : a.heads * a.hd) + h * a.hd;
-        const int f = a.rope_layout == 0 ? 2 * i : i;
-        const int s = a.rope_layout == 0 ? 2 * i + 1 : i + half;
-        if (a.q_norm) {  // weight * (x * s), OlmoeRMSNorm's order
-            const uint16_t* nw = (is_q ? a.q_norm : a.k_norm) + h * a.hd;
-            const float sc = is_q ? scq : sck;
-            v[f] = from_bf16(nw[f]) * (v[f] * sc);
-            v[s] = from_bf16(nw[s]) * (v[s] * sc);
+    // Four pairs per thread per pass, their loads issued before any store (the
+    // stores go to the same row, so one pair at a time would serialise the
+    // round trips).
+    constexpr int kPairs = 4;
+    const uint32_t total = qpairs + kpairs;
+    for (uint32_t p0 = threadIdx.x; p0 < total; p0 += kPairs * kRowThreads) {
+        float x0[kPairs], x1[kPairs], c[kPairs], sn[kPairs], w0[kPairs], w1[kPairs];
+#pragma unroll
+        for (int u = 0; u < kPairs; ++u) {
+            const uint32_t p = p0 + u * kRowThreads;
+            const uint32_t pc = p < total ? p : 0;
+            const bool is_q = pc < qpairs;
+            const uint32_t pp = is_q ? pc : pc - qpairs;
+            const uint32_t h = pp / half, i = pp % half;
+            const float* v = row + (is_q ? 0 : a.heads * a.hd) + h * a.hd;
+            const int f = a.rope_layout == 0 ? 2 * i : i;
+            const int sidx = a.rope_layout == 0 ? 2 * i + 1 : i + half;
+            x0[u] = v[f], x1[u] = v[sidx];
+            c[u] = cs[2 * i], sn[u] = cs[2 * i + 1];
+            w0[u] = w1[u] = 1.f;
+            if (a.q_norm) {
+                const uint16_t* nw = (is_q ? a.q_norm : a.k_norm) + h * a.hd;
+                w0[u] = from_bf16(nw[f]), w1[u] = from_bf16(nw[sidx]);
+            }
         }
-        rot(v, f, s, cs[2 * i], cs[2 * i + 1]);
-        if (!is_q) {
-            kc[h * a.hd + f] = v[f];
-            kc[h * a.hd + s] = v[s];
+#pragma unroll
+        for (int u = 0; u < kPairs; ++u) {
+            const uint32_t p = p0 + u * kRowThreads;
+            if (p >= total) break;
+            const bool is_q = p < qpairs;
+            const uint32_t pp = is_q ? p : p - qpairs;
+            const uint32_t h = pp / half, i = pp % half;
+            float* v = row + (is_q ? 0 : a.heads * a.hd) + h * a.hd;
+            const int f = a.rope_layout == 0 ? 2 * i : i;
+            const int sidx = a.rope_layout == 0 ? 2 * i + 1 : i + half;
+            float a0 = x0[u], a1 = x1[u];
+            if (a.q_norm) {  // weight * (x * s), OlmoeRMSNorm's order
+                const float sc = is_q ? scq : sck;
+                a0 = w0[u] * (a0 * sc);
+                a1 = w1[u] * (a1 * sc);
+            }
+            // rotatePair, src/llm.zig:1360-1371: x0*c - x1*s, x0*s + x1*c (unfused)
+            const float r0 = __fsub_rn(__fmul_rn(a0, c[u]), __fmul_rn(a1, sn[u]));
+            const float r1 = __fadd_rn(__fmul_rn(a0, sn[u]), __fmul_rn(a1, c[u]));
+            v[f] = r0;
+            v[sidx] = r1;
+            if (!is_q) {
+                kc[h * a.hd + f] = r0;
+                kc[h * a.hd + sidx] = r1;
+            }
         }
     }
     const float* vsrc = row + (a.heads + a.kv_heads) * a.hd;
