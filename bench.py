@@ -256,6 +256,7 @@ def phases_main(args, cfg, blob) -> int:
     step_us = []
     moe_marks = {"route": [], "publish": [], "last_pub": [], "after_last": []}  # MoE gate/up: slots 14, 15
     stg = {k: {"begin": [], "first": [], "retries": [], "own": [], "bar": [], "pre": []} for k in PHASE_KINDS + ("logits",)}
+    attn = {k: [] for k in ("q", "pass", "partials stored", "partials polled", "merged", "published")}
     for pos in positions:
         buf[:] = 0
         _lib.check(_lib.lib().vvli_gpu_profile_persistent(runner._h, 5, pos, ctypes.c_void_p(buf.ctypes.data), stride,
@@ -273,6 +274,15 @@ def phases_main(args, cfg, blob) -> int:
             st = st[st > 0]
             ent, fst, rty = t[:n, ph, 9], t[:n, ph, 10], t[:n, ph, 11]
             okb = (ent > 0) & (fst > 0)
+            if kind == "A":  # attention units: their own marks (slots 9, 10, 11, 14, 15, 0), no input staging
+                own = t[:n, ph, 0] > 0  # the splits that merge publish (slot 0)
+                oth = (t[:n, ph, 11] > 0) & ~own
+                for key, sl, sel in (("q", 9, own | oth), ("pass", 10, own | oth), ("partials stored", 11, oth),
+                                     ("partials polled", 11, own), ("merged", 15, own), ("published", 0, own)):
+                    v = t[:n, ph, sl][sel]
+                    attn[key] += list((v[v > 0] - prev) * 1e-2)
+                st = np.zeros(0)
+                okb = np.zeros_like(okb)
             if okb.any():  # thread 0 of each staging block: entry after the previous end, first attempt, retries
                 stg[kind]["begin"] += list((ent[okb] - prev) * 1e-2)
                 stg[kind]["first"] += list((fst[okb] - ent[okb]) * 1e-2)
@@ -331,6 +341,9 @@ def phases_main(args, cfg, blob) -> int:
               f"staged input, the last one p50 {np.median(moe_marks['last_pub']):.2f} us after the median block's; "
               f"routed p50 {np.median(moe_marks['after_last']):.2f} us after the last publication",
               file=sys.stderr, flush=True)
+    if attn["q"]:
+        print("[bench] attention units, us after the q/k/v phase's end (p50): " +
+              ", ".join(f"{k} {np.median(v):.2f}" for k, v in attn.items() if v), file=sys.stderr, flush=True)
     for k in PHASE_KINDS + ("logits",):
         d = stg[k]
         if d["begin"]:

@@ -135,6 +135,10 @@ __device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint3
 // its entry, the return of its first attempt, its retry count; 12, 13 (thread
 // 0): past the phase's closing barrier, past the next phase's weight issue;
 // 14, 15 (thread 0, MoE gate/up): routed, its router row published (producers).
+// Attention units: 9 q (and the new k / v) in LDS, 10 the split's pass done,
+// 11 partials stored (other splits) or polled (the split that merges), 14
+// merge weights computed, 15 K/V row stores acknowledged, 0 the merged output
+// published.
 __device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
     if (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
         p.timing[blockIdx.x * p.timing_stride + ph * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
@@ -262,9 +266,26 @@ struct MkWave {
 };
 
 // Wave index that owns tiles wid, wid + nw, ... of a phase with `ntiles` tiles.
-// Either way block b owns a tile of the phase iff b < ntiles.
+// Either way block b owns a tile of the phase iff b < ntiles (b - fb < ntiles
+// for a wave from mk_wave_from(w, fb)).
 __device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
     return ntiles > w.nw ? w.wid_c : w.wid;
+}
+
+// The wave as a phase sees it whose tiles run on blocks [fb, grid) only
+// (blocks below fb own none).
+__device__ __forceinline__ MkWave mk_wave_from(const MkWave& w, uint32_t fb) {
+    if (fb == 0) return w;
+    MkWave v = w;
+    const uint32_t nb = gridDim.x - fb;
+    v.nw = nb * kMkWaves;
+    if (blockIdx.x < fb) {
+        v.wid = v.wid_c = 0xffffffffu;
+    } else {
+        v.wid = w.wave * nb + (blockIdx.x - fb);
+        v.wid_c = (blockIdx.x - fb) * kMkWaves + w.wave;
+    }
+    return v;
 }
 
 // Issue the first item of this wave's first tile (weights only: may run
@@ -619,10 +640,13 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
 // (rmsNormInto, src/llm.zig:1287-1300). src is a tagged activation of phase
 // `tag` (polled until every word carries it) or (src_bf16) a bf16 embedding
 // row (copyEmbeddingToken, :1373-1380). The norm weights are loaded in the
-// same batch as the activation (into nws = xs + n). False: a poll failed.
+// same batch as the activation (into nws = xs + n). arrived() runs on every
+// thread once its share of the input is in registers, before the block-wide
+// normalisation. False: a poll failed.
+template <typename F>
 __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src, uint32_t tag,
                                          const uint16_t* src_bf16, const uint16_t* norm_w, float eps, uint32_t n,
-                                         uint32_t* err, unsigned long long* tmark = nullptr) {
+                                         uint32_t* err, unsigned long long* tmark, F&& arrived) {
     const int tid = threadIdx.x;
     // Detail timing (profiling runs only): thread 0 records its entry, the
     // return of its first attempt, and its retry count.
@@ -693,6 +717,7 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
             }
         }
     }
+    arrived();
     if (__syncthreads_or(!ok)) return false;
     if (norm_w) {
         ss = wave_sum(ss);
@@ -803,7 +828,8 @@ __device__ __forceinline__ float bf_val(uint16_t h) { return __uint_as_float((ui
 
 template <int HDMAX, bool EXACT, bool MOE = false>
 __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t layer, uint32_t pos, uint32_t chunk,
-                                             uint32_t ns, float* smem, uint32_t tag_in, uint32_t tag_out) {
+                                             uint32_t ns, float* smem, uint32_t tag_in, uint32_t tag_out,
+                                             uint32_t ph) {
     using LY = AttnLds<HDMAX>;
     constexpr int TILE = LY::TILE, KS = LY::KS;
     constexpr int NP = (kMaxGroupMk * HDMAX + kMkThreads - 1) / kMkThreads;
@@ -837,7 +863,17 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
     bool ok = true;
 
     for (uint32_t unit = blockIdx.x; unit < p.kv_heads * ns; unit += gridDim.x) {
-        const uint32_t h = unit / ns, s = unit - h * ns;
+        // Units [0, kv_heads) are the splits that merge (each head's last),
+        // the others follow head by head.
+        uint32_t h, s;
+        if (unit < p.kv_heads) {
+            h = unit;
+            s = ns - 1;
+        } else {
+            const uint32_t u = unit - p.kv_heads;
+            h = u / (ns - 1);
+            s = u - h * (ns - 1);
+        }
         const uint32_t t0 = s * chunk, t1 = min(t0 + chunk, pos + 1);
         const bool owns = s == ns - 1;  // the last split ends at pos
         // K/V rows of a tile travel through registers (rk, rv) so the next
@@ -933,12 +969,26 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             l_s[tid] = 0.f;
         }
         if (__syncthreads_or(!ok)) return false;
+        if (tid == 0) mk_mark(p, ph, 9);
         if (owns) {
             for (int d = tid; d < hd; d += kMkThreads) {
                 st_a(kc + (size_t)pos * kvw + (size_t)h * hd + d, knew[d]);
                 st_a(vc + (size_t)pos * kvw + (size_t)h * hd + d, vnew[d]);
             }
         }
+        // P.V work items: (slice sl, q head g, dim d); with G * hd <= 256 the
+        // tile's rows are cut into nsl slices of span rows each (nsl * G * hd
+        // <= kMkThreads, span a multiple of 16) so every thread works, and the
+        // slices are summed after the last tile.
+        constexpr int kPvBatch = 8;
+        // (Slices only where registers allow: not in the dense hd-128 kernel,
+        // whose groups are wide enough for every thread anyway.)
+        constexpr bool kPvSlices = HDMAX <= 64 || MOE;
+        const int god = G * hd;
+        int nsl = 1;
+        if constexpr (kPvSlices)
+            while (nsl < TILE / 16 && 2 * nsl * god <= kMkThreads) nsl *= 2;
+        const int span = TILE / nsl;
         float acc[NP];
 #pragma unroll
         for (int i = 0; i < NP; ++i) acc[i] = 0.f;
@@ -999,27 +1049,50 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 }
             }
             __syncthreads();
+            // Rows in batches of kPvBatch (every LDS read of a batch issued
+            // before its FMAs, one wait per batch).
 #pragma unroll
             for (int i = 0; i < NP; ++i) {
                 const int idx = tid + i * kMkThreads;
-                if (idx < G * hd) {
-                    const int g = idx / hd, d = idx - g * hd;
+                if (idx < god * nsl) {
+                    // (Recomputed per tile: registers are scarce here.)
+                    const int sl = nsl > 1 ? idx / god : 0;  // i > 0 only when nsl == 1
+                    const int o = idx - sl * god;
+                    const int g = o / hd, d = o - g * hd;
                     const float* pr = ps + g * TILE;
+                    const int j0 = sl * span, j1 = min(j0 + span, tlen);
                     float v0 = acc[i] * c_s[g], v1 = 0.f, v2 = 0.f, v3 = 0.f;
-                    int j = 0;
-                    for (; j + 4 <= tlen; j += 4) {
-                        const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
-                        v0 = fmaf(p4.x, vs[(j + 0) * HDMAX + d], v0);
-                        v1 = fmaf(p4.y, vs[(j + 1) * HDMAX + d], v1);
-                        v2 = fmaf(p4.z, vs[(j + 2) * HDMAX + d], v2);
-                        v3 = fmaf(p4.w, vs[(j + 3) * HDMAX + d], v3);
+                    int j = j0;
+                    for (; j + kPvBatch <= j1; j += kPvBatch) {
+                        float4 p4[kPvBatch / 4];
+                        float vv[kPvBatch];
+#pragma unroll
+                        for (int k = 0; k < kPvBatch / 4; ++k) p4[k] = *reinterpret_cast<const float4*>(pr + j + 4 * k);
+#pragma unroll
+                        for (int k = 0; k < kPvBatch; ++k) vv[k] = vs[(j + k) * HDMAX + d];
+#pragma unroll
+                        for (int k = 0; k < kPvBatch / 4; ++k) {
+                            v0 = fmaf(p4[k].x, vv[4 * k + 0], v0);
+                            v1 = fmaf(p4[k].y, vv[4 * k + 1], v1);
+                            v2 = fmaf(p4[k].z, vv[4 * k + 2], v2);
+                            v3 = fmaf(p4[k].w, vv[4 * k + 3], v3);
+                        }
                     }
-                    for (; j < tlen; ++j) v0 = fmaf(pr[j], vs[j * HDMAX + d], v0);
+                    for (; j < j1; ++j) v0 = fmaf(pr[j], vs[j * HDMAX + d], v0);
                     acc[i] = (v0 + v1) + (v2 + v3);
                 }
             }
             __syncthreads();
         }
+        if (nsl > 1) {  // slices 1.. through the (now free) K tile, added in slice order
+            float* sred = ks;
+            if (tid >= god && tid < god * nsl) sred[tid - god] = acc[0];
+            __syncthreads();
+            if (tid < god)
+                for (int k = 1; k < nsl; ++k) acc[0] += sred[(k - 1) * god + tid];
+            // (The next write of the K tile follows a block barrier.)
+        }
+        if (tid == 0) mk_mark(p, ph, 10);
         const size_t pbase = (size_t)h * p.nsplit;
         if (!owns) {
             // Partials of this split: (m, l) per q head and the unnormalised output.
@@ -1034,6 +1107,7 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 st_a(pml + 2 * tid, tw_make(m_s[tid], tag_out));
                 st_a(pml + 2 * tid + 1, tw_make(l_s[tid], tag_out));
             }
+            if (tid == 0) mk_mark(p, ph, 11);
             continue;
         }
         // Owner: fetch the other splits' partials -- (m, l) together with the
@@ -1044,7 +1118,8 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         const int npe = (G * hd + kMkThreads - 1) / kMkThreads;  // output batches in use
         const tword* mls = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
         const tword* accs = p.tpart_acc + pbase * G * hd;
-        tword wv[kMaxSplitMk - 1];
+        tword wv[kMaxSplitMk - 1] = {};
+        static_assert((kMaxSplitMk - 1) * kMaxGroupMk <= kMaxGroupMk * TILE, "merge weights fit in ps");
 #define VVLI_POLL_PARTIALS(i_, with_ml_)                                                                    \
     {                                                                                                       \
         const int idx_ = tid + (i_) * kMkThreads;                                                           \
@@ -1085,6 +1160,7 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             pl[(ns - 1) * G + tid] = l_s[tid];
         }
         if (__syncthreads_or(!ok)) return false;
+        if (tid == 0) mk_mark(p, ph, 11);
         float* wsp = ps;  // [split][group] merge weights
         for (int g = wave; g < G; g += kMkWaves) {
             const bool in = (uint32_t)lane < ns;
@@ -1095,8 +1171,10 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const float L = wave_sum(lv * e);
             if (in) wsp[lane * G + g] = e / L;
         }
+        if (tid == 0) mk_mark(p, ph, 14);
         wait_all_mem();  // the K/V row stores (wave 0) land before any wave publishes the output
         __syncthreads();
+        if (tid == 0) mk_mark(p, ph, 15);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             if (i >= npe) break;
@@ -1104,10 +1182,18 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const int idx = tid + i * kMkThreads;
             if (idx < G * hd) {
                 const int g = idx / hd;
+                // Every weight is read (in bounds: ps holds kMaxGroupMk * TILE
+                // floats), so the reads go out together; splits past ns are
+                // dropped by a select.
+                float wt[kMaxSplitMk - 1];
+#pragma unroll
+                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) wt[s2] = wsp[s2 * G + g];
                 float o = 0.f;
 #pragma unroll
-                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2)
-                    if (s2 < (int)ns - 1) o = fmaf(tw_val(wv[s2]), wsp[s2 * G + g], o);
+                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) {
+                    const float t = fmaf(tw_val(wv[s2]), wt[s2], o);
+                    o = s2 < (int)ns - 1 ? t : o;
+                }
                 o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
                 // (An opaque copy of idx: hoisted out of every loop, the
                 // 64-bit store addresses would hold registers all kernel long.)
@@ -1118,6 +1204,7 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         }
 #undef VVLI_POLL_PARTIALS
         if (__syncthreads_or(!ok)) return false;
+        if (tid == 0) mk_mark(p, ph, 0);
     }
     return true;
 #undef VVLI_TILE_LOAD
@@ -1296,6 +1383,13 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     uint32_t token = s_ctl[0];
     const uint32_t pos0 = s_ctl[1];
     bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
+    // The o phases leave out blocks [0, kv_heads) -- they run the merging
+    // attention units, the last to finish the attention phase -- when the
+    // other blocks' waves cover the tiles.
+    const uint32_t o_fb =
+        (p.kv_heads < gridDim.x && mk_tiles<MOE>(tb.gemv[1], kGemvResid) <= (gridDim.x - p.kv_heads) * kMkWaves)
+            ? p.kv_heads
+            : 0;
 
     for (uint32_t step = 0; step < p.n_steps; ++step) {
         const uint32_t e0 = p.epoch0 + step * nps;  // epoch of this step's phase 0
@@ -1326,7 +1420,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             const uint32_t tag = e0 + ph;
             bool ok = true;
             if (f.kind == kPhA && !f.logits) {
-                ok = mk_attention<HDMAX, EXACT, MOE>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag);
+                ok = mk_attention<HDMAX, EXACT, MOE>(p, f.layer, pos, chunk, ns, smem, tag - 1, tag, ph);
                 if (!MOE && p.g_lds_tiles) {  // blocks without a unit: this layer's first gate/up tiles into LDS
                     const MkGemv& gg = tb.gemv[f.layer * 4 + 2];
                     const GLds q = mk_glds(p, units, gg);
@@ -1353,14 +1447,23 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 // MOE gate/up: every block stages (the router rows are spread over
                 // the grid's waves); blocks with gate/up or down tiles route.
                 const bool routes = MOE && f.kind == kPhG && !f.logits;
-                if (blockIdx.x < n_streamed || has_lds || routes) {
+                const uint32_t fb = (f.kind == kPhO && !f.logits) ? o_fb : 0;
+                const MkWave wp = mk_wave_from(w, fb);
+                if ((blockIdx.x >= fb && blockIdx.x - fb < n_streamed) || has_lds || routes) {
                     const tword* src = f.kind == kPhO ? p.tattn
                                                       : (f.kind == kPhD ? p.tff : (f.kind == kPhG ? p.tx + H : p.tx));
+                    // The phase's first weights, once the wave's share of the
+                    // input is in (not with LDS tiles, which cover that
+                    // latency, nor before the MoE routing picks the experts).
+                    auto first_weights = [&]() {
+                        if (!have && !gl.n && !routes) have = mk_prefetch<MOE>(g, mode, wp, buf, tile, 0, s_ex);
+                    };
                     ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
                                   f.kind == kPhD ? p.inter : H, p.error,
                                   (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
                                       ? p.timing + blockIdx.x * p.timing_stride + ph * 16 + 9
-                                      : nullptr);
+                                      : nullptr,
+                                  first_weights);
                     if (tid == 0) mk_mark(p, ph, 0);
                     if constexpr (MOE) {
                         if (routes && ok) {
@@ -1381,7 +1484,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                         have = mk_prefetch(g, mode, w, buf, tile, gl.n);
                         mk_glds_compute(gl, g, smem, reinterpret_cast<char*>(smem), p.g_lds_park, w);
                     }
-                    ok = ok && mk_gemv<MOE>(g, mode, smem, w, buf, tile, have, best, tag, rs, gl.n,
+                    ok = ok && mk_gemv<MOE>(g, mode, smem, wp, buf, tile, have, best, tag, rs, gl.n,
                                             reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) +
                                                                            p.g_lds_park),
                                             n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0,
@@ -1413,8 +1516,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 else if (nf.kind == kPhG && !nf.logits && p.g_lds_tiles &&
                     mk_glds(p, units, ng).n > 0)
                     have = false;
-                else if (nf.kind != kPhA || nf.logits)
-                    have = mk_prefetch<MOE>(ng, mk_mode(nf), w, buf, tile, 0, s_ex);
+                else have = false;
             } else if (step + 1 < p.n_steps) {
                 have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
