@@ -294,7 +294,7 @@ def phases_main(args, cfg, blob) -> int:
                     bar, pre = t[:n, ph - 1, 12], t[:n, ph - 1, 13]
                     sel2 = sel & (bar > 0) & (pre > 0)
                     stg[kind]["bar"] += list((bar[sel2] - own[sel2]) * 1e-2)  # closing barrier
-                    stg[kind]["pre"] += list((pre[sel2] - bar[sel2]) * 1e-2)  # next weights issued
+                    stg[kind]["pre"] += list((pre[sel2] - bar[sel2]) * 1e-2)  # the end-of-phase marks (MoE: the router row prefetch)
             if cfg.num_experts and kind == "G":
                 s0, s14, s15 = t[:n, ph, 0], t[:n, ph, 14], t[:n, ph, 15]
                 sel = (s0 > 0) & (s14 > 0)
@@ -353,7 +353,7 @@ def phases_main(args, cfg, blob) -> int:
                   f"retries p50 {np.median(r):.0f} p90 {np.percentile(r, 90):.0f} max {r.max():.0f}"
                   + (f"; entry after the block's own previous end p50 {np.median(d['own']):.2f} "
                      f"p90 {np.percentile(d['own'], 90):.2f} max {np.max(d['own']):.2f} us" if d["own"] else "")
-                  + (f" = barrier p50 {np.median(d['bar']):.2f} + weight issue p50 {np.median(d['pre']):.2f} + rest"
+                  + (f" = barrier p50 {np.median(d['bar']):.2f} + {np.median(d['pre']):.2f} to the set-up of the next phase + rest"
                      if d["bar"] else ""),
                   file=sys.stderr, flush=True)
     line = {"metric": "persistent decode step: per-phase critical path", "value": round(med_step, 1), "unit": "us",
