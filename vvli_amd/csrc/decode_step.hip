@@ -258,18 +258,21 @@ __device__ __forceinline__ void mk_make_tile(const MkGemv& g, int mode, uint32_t
 }
 
 struct MkWave {
-    uint32_t wid;    // wave (t mod blocks) ... : spreads a short phase over every CU
-    uint32_t wid_c;  // block-contiguous wave index: long phases sweep memory together
+    uint32_t wid;    // wave (t mod blocks) ... : tile t goes to block t mod blocks
     uint32_t nw;
     uint32_t wave;   // wave of the block
     int lane;
 };
 
-// Wave index that owns tiles wid, wid + nw, ... of a phase with `ntiles` tiles.
-// Either way block b owns a tile of the phase iff b < ntiles (b - fb < ntiles
-// for a wave from mk_wave_from(w, fb)).
+// Wave index that owns tiles wid, wid + nw, ... of a phase with `ntiles` tiles:
+// consecutive tiles go to consecutive blocks, so a phase with fewer tiles than
+// waves still uses every CU and the tiles of a partial last round spread over
+// all blocks (one more tile for some waves, never a whole block's waves more).
+// Block b owns a tile of the phase iff b < ntiles (b - fb < ntiles for a wave
+// from mk_wave_from(w, fb)).
 __device__ __forceinline__ uint32_t mk_owner(const MkWave& w, uint32_t ntiles) {
-    return ntiles > w.nw ? w.wid_c : w.wid;
+    (void)ntiles;
+    return w.wid;
 }
 
 // The wave as a phase sees it whose tiles run on blocks [fb, grid) only
@@ -280,10 +283,9 @@ __device__ __forceinline__ MkWave mk_wave_from(const MkWave& w, uint32_t fb) {
     const uint32_t nb = gridDim.x - fb;
     v.nw = nb * kMkWaves;
     if (blockIdx.x < fb) {
-        v.wid = v.wid_c = 0xffffffffu;
+        v.wid = 0xffffffffu;
     } else {
         v.wid = w.wave * nb + (blockIdx.x - fb);
-        v.wid_c = (blockIdx.x - fb) * kMkWaves + w.wave;
     }
     return v;
 }
@@ -1356,10 +1358,10 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     MkWave w;
     w.lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
-    // Tile t goes to wave (t mod blocks) of ... so consecutive tiles land on
-    // different CUs and a phase with fewer tiles than waves still uses them all.
+    // Tile t goes to block t mod blocks, wave (t / blocks) mod 8: consecutive
+    // tiles land on different CUs and a phase with fewer tiles than waves
+    // still uses them all.
     w.wid = wave * gridDim.x + blockIdx.x;
-    w.wid_c = blockIdx.x * kMkWaves + wave;
     w.nw = gridDim.x * kMkWaves;
     w.wave = wave;
     uint4 buf[2][kNJC];
