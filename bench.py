@@ -256,7 +256,7 @@ def phases_main(args, cfg, blob) -> int:
     step_us = []
     moe_marks = {"route": [], "publish": [], "last_pub": [], "after_last": []}  # MoE gate/up: slots 14, 15
     stg = {k: {"begin": [], "first": [], "retries": [], "own": [], "bar": [], "pre": []} for k in PHASE_KINDS + ("logits",)}
-    attn = {k: [] for k in ("q", "pass", "partials stored", "partials polled", "merged", "published")}
+    attn = {k: [] for k in ("q", "pass", "partials stored", "partials polled", "weights", "published")}
     for pos in positions:
         buf[:] = 0
         _lib.check(_lib.lib().vvli_gpu_profile_persistent(runner._h, 5, pos, ctypes.c_void_p(buf.ctypes.data), stride,
@@ -275,11 +275,10 @@ def phases_main(args, cfg, blob) -> int:
             ent, fst, rty = t[:n, ph, 9], t[:n, ph, 10], t[:n, ph, 11]
             okb = (ent > 0) & (fst > 0)
             if kind == "A":  # attention units: their own marks (slots 9, 10, 11, 14, 15, 0), no input staging
-                own = t[:n, ph, 0] > 0  # the splits that merge publish (slot 0)
-                oth = (t[:n, ph, 11] > 0) & ~own
-                for key, sl, sel in (("q", 9, own | oth), ("pass", 10, own | oth), ("partials stored", 11, oth),
-                                     ("partials polled", 11, own), ("merged", 15, own), ("published", 0, own)):
-                    v = t[:n, ph, sl][sel]
+                unit = t[:n, ph, 9] > 0
+                for key, sl in (("q", 9), ("pass", 10), ("partials stored", 11), ("partials polled", 14),
+                                ("weights", 15), ("published", 0)):
+                    v = t[:n, ph, sl][unit]
                     attn[key] += list((v[v > 0] - prev) * 1e-2)
                 st = np.zeros(0)
                 okb = np.zeros_like(okb)

@@ -13,7 +13,8 @@ geometries of the two long-context workloads:
   reference RoPE and with the llama3-scaled table.
 * Qwen2.5-7B heads (hidden 3584, 28 q / 4 kv heads, head_dim 128, group 7,
   qkv bias, untied): 4096-token prompt, then 256 decode steps at ctx 8192, so
-  every step merges 16 splits of 257..272 positions.
+  every step merges 43..46 splits of 96 positions (each split merging at most
+  21 of its head's 896 outputs; at 46 splits one merges none).
 
 Two layers, and a reduced intermediate size and vocabulary, keep the oracle's
 CPU time to seconds; the attention shapes, the split counts and the KV lengths
@@ -52,12 +53,16 @@ def cfg_qwen7b_heads() -> C.Config:
                     rope_layout=C.ROPE_SPLIT_HALF)
 
 
-def splits_at(pos: int, max_seq: int) -> int:
+def splits_at(pos: int, max_seq: int, kv_heads: int, head_dim: int, blocks: int = 256) -> int:
     """Attention splits the persistent step merges at `pos` (its split rule:
-    min(16, ceil(max_seq / 64)) splits of at least 64 positions)."""
-    nsplit = max(1, min(16, (max_seq + 63) // 64))
+    at most min(64, ceil(max_seq / 64), blocks / kv_heads) splits of at least
+    64 positions, a whole number of K/V tiles each -- 64 rows at head_dim <= 64,
+    32 at 128; blocks: one per CU, 256 on an MI355X)."""
+    nsplit = max(1, min(64, (max_seq + 63) // 64, blocks // kv_heads))
+    tile = 64 if head_dim <= 64 else 32
     t = pos + 1
     chunk = max(64, -(-t // nsplit))
+    chunk = -(-chunk // tile) * tile
     return -(-t // chunk)
 
 
@@ -76,7 +81,8 @@ def test_persistent_decode_long_context(name, oracle_mod, host_threads):
     L = cfg.num_hidden_layers
     blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02)
     prompt = np.random.default_rng(11).integers(0, cfg.vocab_size, size=n_prompt).astype(np.uint32)
-    want_splits = sorted({splits_at(p, ctx) for p in range(n_prompt, n_prompt + steps)})
+    want_splits = sorted({splits_at(p, ctx, cfg.num_key_value_heads, cfg.head_dim())
+                          for p in range(n_prompt, n_prompt + steps)})
     print(f"case={name} prompt={n_prompt} steps={steps} ctx={ctx} splits={want_splits}", flush=True)
     orc = oracle_mod.OracleRunner(cfg, blob, ctx, threads=host_threads)
     with R.Runner(cfg, blob, ctx) as gpu:

@@ -48,7 +48,9 @@ namespace {
 constexpr int kMkThreads = 512;
 constexpr int kMkWaves = kMkThreads / kWave;
 constexpr int kMaxGroupMk = 16;
-constexpr int kMaxSplitMk = 16;  // attention splits per kv head
+constexpr int kMaxSplitMk = 64;  // attention splits per kv head
+constexpr int kOwnerMergeMax = 16;  // splits merged by one block (the one that appends the K/V row)
+static_assert(kMaxSplitMk <= 64, "the split merge weights are one wave's lanes");
 constexpr uint32_t kSpinLimit = 1u << 22;  // polls of one word (each after a short sleep): seconds
 
 typedef unsigned long long tword;
@@ -136,9 +138,9 @@ __device__ __forceinline__ bool poll_tw2(const tword* p0, const tword* p1, uint3
 // 0): past the phase's closing barrier, past the next phase's weight issue;
 // 14, 15 (thread 0, MoE gate/up): routed, its router row published (producers).
 // Attention units: 9 q (and the new k / v) in LDS, 10 the split's pass done,
-// 11 partials stored (other splits) or polled (the split that merges), 14
-// merge weights computed, 15 K/V row stores acknowledged, 0 the merged output
-// published.
+// 11 its partials stored, 14 the partials it merges polled, 15 merge weights
+// computed (and the K/V row stores acknowledged), 0 its merged outputs
+// published (a split that stores partials for another to merge: 9-11 only).
 __device__ __forceinline__ void mk_mark(const DecodeStepParams& p, uint32_t ph, int slot) {
     if (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
         p.timing[blockIdx.x * p.timing_stride + ph * p.timing_slots + slot] = __builtin_amdgcn_s_memrealtime();
@@ -740,8 +742,9 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
 // ---------------------------------------------------------------------------
 // LDS layout of the attention phase (floats): q [16][HDMAX], K tile
 // [TILE][HDMAX+4] (16-byte aligned rows), V tile [TILE][HDMAX], probabilities
-// [16][TILE] (also the split merge weights), new k / v rows, running max /
-// sum / correction per q head, split (m, l) for the merge.
+// [16][TILE], new k / v rows, running max / sum / correction per q head.
+// The merge of the splits reuses the K tile (every split's (m, l) and merge
+// weights) and the V tile with the probabilities (the slice's partial values).
 template <int HDMAX>
 struct AttnLds {
     static constexpr int TILE = 4096 / HDMAX;  // 64 rows at hd 64, 32 at hd 128
@@ -755,17 +758,17 @@ struct AttnLds {
     static constexpr int kM = kVnew + HDMAX;
     static constexpr int kL = kM + kMaxGroupMk;
     static constexpr int kC = kL + kMaxGroupMk;
-    static constexpr int kPm = kC + kMaxGroupMk;
-    static constexpr int kPl = kPm + kMaxSplitMk * kMaxGroupMk;
-    static constexpr int kTotal = kPl + kMaxSplitMk * kMaxGroupMk;
+    static constexpr int kTotal = kC + kMaxGroupMk;
 };
 
 // One (kv head, split) unit per block: RoPE of q and of the new k (applyRoPE,
 // src/llm.zig:1337-1371), K/V append at pos (:744-745), and an online-softmax
 // pass over the split's positions for the `group` q heads sharing the kv head
-// (computeAttentionInto, :1302-1335). The split holding pos (always the last)
-// merges the others' partials (m, l, acc) into the attention output
+// (computeAttentionInto, :1302-1335). The splits of a head then merge their
+// partials (m, l, acc) into the attention output, each split one slice of it
 // (flash-decoding: out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s).
+// Every split waits for the others, so the kv_heads * ns units must all hold
+// a block at once (the host caps the splits at blocks / kv_heads).
 // The K/V rows of the first tile are loaded before q is waited for. EXACT:
 // hd == HDMAX (loops fully unrolled), else hd <= HDMAX at run time.
 // QK-norm scales (MOE models that carry it): s_q = 1/sqrt(mean(q^2) + eps)
@@ -851,8 +854,6 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
     float* m_s = smem + LY::kM;
     float* l_s = smem + LY::kL;
     float* c_s = smem + LY::kC;
-    float* pm = smem + LY::kPm;
-    float* pl = smem + LY::kPl;
     const float* cs = p.rope_cs + (size_t)pos * hd;
     float* kc = p.kcache + (size_t)layer * p.max_seq * kvw;
     float* vc = p.vcache + (size_t)layer * p.max_seq * kvw;
@@ -865,8 +866,8 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
     bool ok = true;
 
     for (uint32_t unit = blockIdx.x; unit < p.kv_heads * ns; unit += gridDim.x) {
-        // Units [0, kv_heads) are the splits that merge (each head's last),
-        // the others follow head by head.
+        // Units [0, kv_heads) are the splits that append the new K/V row
+        // (each head's last), the others follow head by head.
         uint32_t h, s;
         if (unit < p.kv_heads) {
             h = unit;
@@ -978,6 +979,16 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 st_a(vc + (size_t)pos * kvw + (size_t)h * hd + d, vnew[d]);
             }
         }
+        // Work split of a tile (TILE * HDMAX = 4096 floats):
+        // scores: thread (row qj, chunk qc) -- HDMAX / 8 chunks of 8 floats
+        // per row, one pair per thread -- holds its 8 floats of K_j and forms
+        // q_g . K_j over the chunk for every q head g, summed across the
+        // row's chunk lanes by DPP: the K tile is read from LDS once per tile
+        // (the q reads are broadcasts).
+        // P.V: thread (slice psl, dim pd) -- slices of 8 rows -- keeps the
+        // running outputs of all G heads for its slice (pa), rescaled with the
+        // running max like the whole; the V tile is read once per tile and the
+        // slices are summed after the last tile.
         // P.V work items: (slice sl, q head g, dim d); with G * hd <= 256 the
         // tile's rows are cut into nsl slices of span rows each (nsl * G * hd
         // <= kMkThreads, span a multiple of 16) so every thread works, and the
@@ -1092,12 +1103,43 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             __syncthreads();
             if (tid < god)
                 for (int k = 1; k < nsl; ++k) acc[0] += sred[(k - 1) * god + tid];
-            // (The next write of the K tile follows a block barrier.)
+            __syncthreads();  // the merge reuses the K tile
         }
         if (tid == 0) mk_mark(p, ph, 10);
+        if (ns == 1) {  // one split: normalise its own outputs
+            if (owns) wait_all_mem();  // the K/V row stores land before the output is published
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int idx = tid + i * kMkThreads;
+                if (idx < G * hd) {
+                    const int g = idx / hd;
+                    int idx_o = idx;  // (opaque: see below)
+                    asm volatile("" : "+v"(idx_o));
+                    st_a(p.tattn + (size_t)h * G * hd + idx_o, tw_make(fmaf(acc[i], 1.0f / l_s[g], 0.f), tag_out));
+                }
+            }
+            if (__syncthreads_or(!ok)) return false;
+            if (tid == 0) mk_mark(p, ph, 0);
+            continue;
+        }
+        // Flash-decoding merge: out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s
+        // (splits in ascending order). With 3..kOwnerMergeMax splits the
+        // split that appended the K/V row merges them all and the others store
+        // their partials and leave (their blocks start the next phase early);
+        // with 2 or more than kOwnerMergeMax splits every split stores its
+        // partials and merges a slice of the outputs from all of them, so no
+        // block reads more than its slice of the partials. (Measured: the
+        // former at Llama-3.2-1B heads with 9-10 splits, the latter at 2 and
+        // at 43-46 splits.) The merge tables live in the K tile, free after
+        // the last tile.
+        const bool owner_merge = ns > 2 && ns <= kOwnerMergeMax;
         const size_t pbase = (size_t)h * p.nsplit;
-        if (!owns) {
-            // Partials of this split: (m, l) per q head and the unnormalised output.
+        float* pm = ks;                              // [split][group]
+        float* pl = pm + kMaxSplitMk * kMaxGroupMk;  // [split][group]
+        float* wsp = pl + kMaxSplitMk * kMaxGroupMk; // merge weights [split][group]
+        static_assert(3 * kMaxSplitMk * kMaxGroupMk <= TILE * KS, "merge tables fit in the K tile");
+        if (!owner_merge || !owns) {  // partials: (m, l) per q head and the unnormalised outputs
             tword* pml = p.tpart_ml + (pbase + s) * G * 2;
             tword* pacc = p.tpart_acc + (pbase + s) * G * hd;
 #pragma unroll
@@ -1110,18 +1152,18 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 st_a(pml + 2 * tid + 1, tw_make(l_s[tid], tag_out));
             }
             if (tid == 0) mk_mark(p, ph, 11);
-            continue;
         }
-        // Owner: fetch the other splits' partials -- (m, l) together with the
-        // first batch of outputs, re-polled as a whole until every word
-        // carries the tag (one memory round trip when they are there) -- then
-        // merge, own split last.
-        const int nml = (int)(ns - 1) * G;
-        const int npe = (G * hd + kMkThreads - 1) / kMkThreads;  // output batches in use
-        const tword* mls = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
-        const tword* accs = p.tpart_acc + pbase * G * hd;
-        tword wv[kMaxSplitMk - 1] = {};
-        static_assert((kMaxSplitMk - 1) * kMaxGroupMk <= kMaxGroupMk * TILE, "merge weights fit in ps");
+        if (owner_merge) {
+            if (!owns) continue;
+            // Owner: fetch the other splits' partials -- (m, l) together with the
+            // first batch of outputs, re-polled as a whole until every word
+            // carries the tag (one memory round trip when they are there) -- then
+            // merge, own split last.
+            const int nml = (int)(ns - 1) * G;
+            const int npe = (G * hd + kMkThreads - 1) / kMkThreads;  // output batches in use
+            const tword* mls = p.tpart_ml + (pbase * G + (size_t)tid) * 2;  // split tid / G, head tid % G
+            const tword* accs = p.tpart_acc + pbase * G * hd;
+            tword wv[kOwnerMergeMax - 1] = {};
 #define VVLI_POLL_PARTIALS(i_, with_ml_)                                                                    \
     {                                                                                                       \
         const int idx_ = tid + (i_) * kMkThreads;                                                           \
@@ -1134,10 +1176,10 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 wm_ = ld_a(mls);                                                                            \
                 wl_ = ld_a(mls + 1);                                                                        \
             }                                                                                               \
-            _Pragma("unroll") for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) if (mine_ && s2 < (int)ns - 1)   \
+            _Pragma("unroll") for (int s2 = 0; s2 < kOwnerMergeMax - 1; ++s2) if (mine_ && s2 < (int)ns - 1)\
                 wv[s2] = ld_a(accs + (size_t)s2 * G * hd + idx_);                                           \
             if (ml_) good = tw_tag(wm_) == tag_out && tw_tag(wl_) == tag_out;                               \
-            _Pragma("unroll") for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) if (mine_ && s2 < (int)ns - 1)   \
+            _Pragma("unroll") for (int s2 = 0; s2 < kOwnerMergeMax - 1; ++s2) if (mine_ && s2 < (int)ns - 1)\
                 good = good && tw_tag(wv[s2]) == tag_out;                                                   \
             if (good) break;                                                                                \
             if (spins > kSpinLimit) {                                                                       \
@@ -1156,16 +1198,106 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             pl[tid] = tw_val(wl_);                                                                          \
         }                                                                                                   \
     }
-        VVLI_POLL_PARTIALS(0, true)
-        if (tid < G) {
-            pm[(ns - 1) * G + tid] = m_s[tid];
-            pl[(ns - 1) * G + tid] = l_s[tid];
+            VVLI_POLL_PARTIALS(0, true)
+            if (tid < G) {
+                pm[(ns - 1) * G + tid] = m_s[tid];
+                pl[(ns - 1) * G + tid] = l_s[tid];
+            }
+            if (__syncthreads_or(!ok)) return false;
+            if (tid == 0) mk_mark(p, ph, 14);
+            for (int g = wave; g < G; g += kMkWaves) {
+                const bool in = (uint32_t)lane < ns;
+                const float mv = in ? pm[lane * G + g] : -INFINITY;
+                const float lv = in ? pl[lane * G + g] : 0.f;
+                const float M = wave_max(mv);
+                const float e = in ? expf(mv - M) : 0.f;
+                const float L = wave_sum(lv * e);
+                if (in) wsp[lane * G + g] = e / L;
+            }
+            wait_all_mem();  // the K/V row stores (wave 0) land before any wave publishes the output
+            __syncthreads();
+            if (tid == 0) mk_mark(p, ph, 15);
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                if (i >= npe) break;
+                if (i > 0) VVLI_POLL_PARTIALS(i, false)
+                const int idx = tid + i * kMkThreads;
+                if (idx < G * hd) {
+                    const int g = idx / hd;
+                    // Every weight is read (in bounds: the weight table holds
+                    // kMaxSplitMk * kMaxGroupMk floats), so the reads go out
+                    // together; splits past ns are dropped by a select.
+                    float wt[kOwnerMergeMax - 1];
+#pragma unroll
+                    for (int s2 = 0; s2 < kOwnerMergeMax - 1; ++s2) wt[s2] = wsp[s2 * G + g];
+                    float o = 0.f;
+#pragma unroll
+                    for (int s2 = 0; s2 < kOwnerMergeMax - 1; ++s2) {
+                        const float t = fmaf(tw_val(wv[s2]), wt[s2], o);
+                        o = s2 < (int)ns - 1 ? t : o;
+                    }
+                    o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
+                    // (An opaque copy of idx: hoisted out of every loop, the
+                    // 64-bit store addresses would hold registers all kernel long.)
+                    int idx_o = idx;
+                    asm volatile("" : "+v"(idx_o));
+                    st_a(p.tattn + (size_t)h * G * hd + idx_o, tw_make(o, tag_out));
+                }
+            }
+#undef VVLI_POLL_PARTIALS
+            if (__syncthreads_or(!ok)) return false;
+            if (tid == 0) mk_mark(p, ph, 0);
+            continue;
         }
+        // Slices in reverse split order: the split that appended the K/V row
+        // (the last) takes slice 0, never empty, so its publication also
+        // orders the row stores before any reader of the output.
+        const int per = (god + (int)ns - 1) / (int)ns;
+        const int o0 = min(god, ((int)ns - 1 - (int)s) * per), nout = min(god, o0 + per) - o0;
+        float* pv = vs;                              // slice values [output][split] (V tile, probabilities)
+        static_assert(LY::kP + kMaxGroupMk * TILE - LY::kV >= kMaxGroupMk * HDMAX + kMaxSplitMk,
+                      "slice values fit in the V tile and the probabilities");
+        // Every split's (m, l) per q head and the slice's values of every
+        // split (pair q = output * ns + split, in batches of two per thread),
+        // each polled (its split may still be storing); the first batch of
+        // values is issued with the (m, l) loads, so one memory round trip
+        // fetches the lot when it is there.
+        const tword* mlb = p.tpart_ml + pbase * G * 2;     // [split][group][2]
+        const tword* accb = p.tpart_acc + pbase * G * hd;  // [split][G * hd]
+        const int nq = nout * (int)ns;
+        tword wv[2] = {};
+#define VVLI_VALUES_LOAD(qb_)                                              \
+    _Pragma("unroll") for (int k = 0; k < 2; ++k) {                        \
+        const int q = (qb_) + tid + k * kMkThreads;                        \
+        if (q < nq) {                                                      \
+            const int ol = q / (int)ns, s2 = q - ol * (int)ns;             \
+            wv[k] = ld_a(accb + (size_t)s2 * god + o0 + ol);               \
+        }                                                                  \
+    }
+        VVLI_VALUES_LOAD(0)
+        for (int i = tid; i < (int)ns * G; i += kMkThreads) {
+            tword wm = ld_a(mlb + (size_t)i * 2), wl = ld_a(mlb + (size_t)i * 2 + 1);
+            ok = ok && poll_tw2(mlb + (size_t)i * 2, mlb + (size_t)i * 2 + 1, tag_out, wm, wl, p.error);
+            pm[i] = tw_val(wm);
+            pl[i] = tw_val(wl);
+        }
+        for (int qb = 0; qb < nq; qb += 2 * kMkThreads) {
+            if (qb > 0) VVLI_VALUES_LOAD(qb)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int q = qb + tid + k * kMkThreads;
+                if (q < nq) {
+                    const int ol = q / (int)ns, s2 = q - ol * (int)ns;
+                    ok = ok && poll_tw(accb + (size_t)s2 * god + o0 + ol, tag_out, wv[k], p.error);
+                    pv[q] = tw_val(wv[k]);
+                }
+            }
+        }
+#undef VVLI_VALUES_LOAD
         if (__syncthreads_or(!ok)) return false;
-        if (tid == 0) mk_mark(p, ph, 11);
-        float* wsp = ps;  // [split][group] merge weights
+        if (tid == 0) mk_mark(p, ph, 14);
         for (int g = wave; g < G; g += kMkWaves) {
-            const bool in = (uint32_t)lane < ns;
+            const bool in = lane < (int)ns;
             const float mv = in ? pm[lane * G + g] : -INFINITY;
             const float lv = in ? pl[lane * G + g] : 0.f;
             const float M = wave_max(mv);
@@ -1173,38 +1305,27 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const float L = wave_sum(lv * e);
             if (in) wsp[lane * G + g] = e / L;
         }
-        if (tid == 0) mk_mark(p, ph, 14);
-        wait_all_mem();  // the K/V row stores (wave 0) land before any wave publishes the output
+        if (owns) wait_all_mem();  // the K/V row stores land before the output is published
         __syncthreads();
         if (tid == 0) mk_mark(p, ph, 15);
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            if (i >= npe) break;
-            if (i > 0) VVLI_POLL_PARTIALS(i, false)
-            const int idx = tid + i * kMkThreads;
-            if (idx < G * hd) {
-                const int g = idx / hd;
-                // Every weight is read (in bounds: ps holds kMaxGroupMk * TILE
-                // floats), so the reads go out together; splits past ns are
-                // dropped by a select.
-                float wt[kMaxSplitMk - 1];
-#pragma unroll
-                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) wt[s2] = wsp[s2 * G + g];
-                float o = 0.f;
-#pragma unroll
-                for (int s2 = 0; s2 < kMaxSplitMk - 1; ++s2) {
-                    const float t = fmaf(tw_val(wv[s2]), wt[s2], o);
-                    o = s2 < (int)ns - 1 ? t : o;
-                }
-                o = fmaf(acc[i], wsp[(ns - 1) * G + g], o);
-                // (An opaque copy of idx: hoisted out of every loop, the
+        // Output o0 + ol sums its ns weighted values over a segment of wdt
+        // lanes (ns rounded up to a power of two; a fixed butterfly order).
+        int wdt = 1;
+        while (wdt < (int)ns) wdt <<= 1;
+        const int sl = tid & (wdt - 1);
+        for (int ob = 0; ob < nout; ob += kMkThreads / wdt) {  // uniform over the block
+            const int ol = ob + tid / wdt;
+            float x = 0.f;
+            if (ol < nout && sl < (int)ns) x = pv[ol * (int)ns + sl] * wsp[sl * G + (o0 + ol) / hd];
+            for (int off = wdt >> 1; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+            if (sl == 0 && ol < nout) {
+                // (An opaque copy of the index: hoisted out of every loop, the
                 // 64-bit store addresses would hold registers all kernel long.)
-                int idx_o = idx;
-                asm volatile("" : "+v"(idx_o));
-                st_a(p.tattn + (size_t)h * G * hd + idx_o, tw_make(o, tag_out));
+                int o_st = o0 + ol;
+                asm volatile("" : "+v"(o_st));
+                st_a(p.tattn + (size_t)h * G * hd + o_st, tw_make(x, tag_out));
             }
         }
-#undef VVLI_POLL_PARTIALS
         if (__syncthreads_or(!ok)) return false;
         if (tid == 0) mk_mark(p, ph, 0);
     }
@@ -1411,8 +1532,13 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             return;
         }
         const uint32_t T = pos + 1;
+        // Positions per attention split: a whole number of K/V tiles (a split
+        // pays one tile's load latency per tile, so 65 rows cost as much as
+        // 96 -- fewer splits then merge, and more blocks stay free).
+        constexpr uint32_t kTile = AttnLds<HDMAX>::TILE;
         uint32_t chunk = (T + p.nsplit - 1) / p.nsplit;
         if (chunk < p.min_chunk) chunk = p.min_chunk;
+        chunk = (chunk + kTile - 1) / kTile * kTile;
         const uint32_t ns = (T + chunk - 1) / chunk;
         const uint16_t* emb = p.embed + (size_t)token * H;
         const uint32_t units = p.kv_heads * ns;  // attention units run by blocks [0, units)

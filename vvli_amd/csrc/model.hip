@@ -851,7 +851,10 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
             cus > 0 && static_cast<uint64_t>(max_seq_len) * kv * sizeof(float) < (1ull << 31)) {  // 32-bit KV offsets
             m->mk_ok = true;
             m->mk_blocks = static_cast<uint32_t>(cus);
-            m->mk_nsplit = std::max<uint32_t>(1, std::min<uint32_t>(16, (max_seq_len + 63) / 64));  // <= kMaxSplitMk
+            // Splits per kv head (<= kMaxSplitMk): every split of a head waits for
+            // the others' partials, so all kv_heads * nsplit units hold a block at once.
+            m->mk_nsplit = std::max<uint32_t>(
+                1, std::min<uint32_t>(std::min<uint32_t>(64, (max_seq_len + 63) / 64), m->mk_blocks / cfg->kv_heads));
             // The rest of the CU's LDS holds gate/up tiles (VVLI_DECODE_GLDS=0: off;
             // MoE: none, the experts are known only once the gate/up phase routes).
             const char* env = getenv("VVLI_DECODE_GLDS");
