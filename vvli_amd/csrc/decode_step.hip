@@ -83,6 +83,7 @@ __device__ __forceinline__ uint32_t tw_tag(tword w) { return (uint32_t)(w >> 32)
 // buffer loads with the sc1 cache policy, through a raw buffer resource
 // (out-of-range reads return 0).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float mk_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kCpolSc1 = 16;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -742,7 +743,8 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
 // ---------------------------------------------------------------------------
 // LDS layout of the attention phase (floats): q [16][HDMAX], K tile
 // [TILE][HDMAX+4] (16-byte aligned rows), V tile [TILE][HDMAX], probabilities
-// [16][TILE], new k / v rows, running max / sum / correction per q head.
+// [16][TILE], new k / v rows, running max / sum / correction per q head, and
+// at head_dim 128 the matrix-core tile's partials.
 // The merge of the splits reuses the K tile (every split's (m, l) and merge
 // weights) and the V tile with the probabilities (the slice's partial values).
 template <int HDMAX>
@@ -758,7 +760,10 @@ struct AttnLds {
     static constexpr int kM = kVnew + HDMAX;
     static constexpr int kL = kM + kMaxGroupMk;
     static constexpr int kC = kL + kMaxGroupMk;
-    static constexpr int kTotal = kC + kMaxGroupMk;
+    // head_dim 128 (matrix-core tile): score partials [kq][jb][16][16],
+    // then the P.V slices [js][16][HDMAX]
+    static constexpr int kRed = kC + kMaxGroupMk;
+    static constexpr int kTotal = kRed + (HDMAX == 128 ? 2048 : 0);
 };
 
 // One (kv head, split) unit per block: RoPE of q and of the new k (applyRoPE,
@@ -989,121 +994,249 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         // running outputs of all G heads for its slice (pa), rescaled with the
         // running max like the whole; the V tile is read once per tile and the
         // slices are summed after the last tile.
-        // P.V work items: (slice sl, q head g, dim d); with G * hd <= 256 the
-        // tile's rows are cut into nsl slices of span rows each (nsl * G * hd
-        // <= kMkThreads, span a multiple of 16) so every thread works, and the
-        // slices are summed after the last tile.
-        constexpr int kPvBatch = 8;
-        // (Slices only where registers allow: not in the dense hd-128 kernel,
-        // whose groups are wide enough for every thread anyway.)
-        constexpr bool kPvSlices = HDMAX <= 64 || MOE;
         const int god = G * hd;
-        int nsl = 1;
-        if constexpr (kPvSlices)
-            while (nsl < TILE / 16 && 2 * nsl * god <= kMkThreads) nsl *= 2;
-        const int span = TILE / nsl;
-        float acc[NP];
-#pragma unroll
-        for (int i = 0; i < NP; ++i) acc[i] = 0.f;
-        for (uint32_t ta = t0; ta < t1; ta += TILE) {
-            const int tlen = (int)min((uint32_t)TILE, t1 - ta);
-            VVLI_TILE_STORE(ta, tlen);
-            if (ta + TILE < t1) {
-                VVLI_TILE_LOAD(ta + TILE, (int)min((uint32_t)TILE, t1 - ta - TILE));
-            }
-            __syncthreads();
-            // scores s[g][j] = (q_g . K_j) * scale: thread pairs, each over half
-            // of the dimensions (two independent chains), summed across the pair.
-            for (int idx2 = tid; idx2 < 2 * G * TILE; idx2 += kMkThreads) {
-                const int idx = idx2 >> 1, half_d = idx2 & 1;
-                const int g = idx / TILE, j = idx - g * TILE;
-                float a0 = 0.f, a1 = 0.f;
-                if (j < tlen) {
-                    const float* qr = qs + g * HDMAX;
-                    const float* kr = ks + j * KS;
-                    if constexpr (EXACT) {
-#pragma unroll
-                        for (int d = half_d * 4; d < HDMAX; d += 8) {  // float4 chunks alternate in the pair
-                            const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
-                            const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
-                            a0 = fmaf(q4.x, k4.x, a0);
-                            a1 = fmaf(q4.y, k4.y, a1);
-                            a0 = fmaf(q4.z, k4.z, a0);
-                            a1 = fmaf(q4.w, k4.w, a1);
-                        }
-                    } else {
-                        for (int d = half_d * 4; d < hd; d += 8) {
-                            const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
-                            const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
-                            a0 = fmaf(q4.x, k4.x, a0);
-                            a1 = fmaf(q4.y, k4.y, a1);
-                            a0 = fmaf(q4.z, k4.z, a0);
-                            a1 = fmaf(q4.w, k4.w, a1);
-                        }
+        float acc[NP];  // the split's unnormalised outputs, idx = g * hd + d at thread idx % kMkThreads
+        // head_dim 128: the scores and P.V on the matrix cores (the tile's
+        // dependent LDS round trips halve: 5.3k -> 2.7k cycles per 32-row tile
+        // at group 7); head_dim <= 64: the vector units (one 64-row tile per
+        // split at the timed lengths, where the matrix-core tile measured no
+        // faster).
+        if constexpr (HDMAX == 128) {
+            // The tile's products on the matrix cores (v_mfma_f32_16x16x4f32; a
+            // wave's 64 lanes: A[m][k] from lane m + 16 k, B[k][n] from lane
+            // n + 16 k, lane l gets D[4 (l / 16) + i][l % 16], i < 4; q heads past
+            // the group give rows that are not used, rows past the tile are
+            // masked (scores) or zeroed (V)).
+            // Scores: wave (row block jb of 16 K rows, quarter kq of 32 dims)
+            // forms S_kq[g][j] over its dims -- 8 MFMAs, the K dims of a lane
+            // contiguous -- into red; the softmax wave of head g sums the kKq
+            // partials. P.V: wave (16-dim block db, 32-row slice js) keeps the
+            // running outputs O[g][d] of its slice in o4, rescaled by the running
+            // max's correction each tile; the slices are summed after the last
+            // tile.
+            constexpr int kJb = TILE / 16, kKq = 8 / kJb;  // 2 x 4 at hd 128, 4 x 2 at hd 64
+            constexpr int kDb = HDMAX / 16, kJs = 8 / kDb;
+            static_assert(kKq * 32 == HDMAX && kJs * 32 == TILE && kJb * kKq == kMkWaves, "MFMA wave split of a tile");
+            const int ml = lane & 15, mg = lane >> 4;
+            float* red = smem + LY::kRed;
+            mk_f32x4 o4 = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t ta = t0; ta < t1; ta += TILE) {
+                const int tlen = (int)min((uint32_t)TILE, t1 - ta);
+                VVLI_TILE_STORE(ta, tlen);
+                if (ta + TILE < t1) {
+                    VVLI_TILE_LOAD(ta + TILE, (int)min((uint32_t)TILE, t1 - ta - TILE));
+                }
+                __syncthreads();
+                {
+                    const int jb = wave % kJb, kq = wave / kJb;
+                    const int d0 = kq * 32 + mg * 8;
+                    const bool in0 = EXACT || d0 < hd, in1 = EXACT || d0 + 4 < hd;  // (hd % 4 == 0)
+                    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float* qr = qs + ml * HDMAX + d0;
+                    const float* kr = ks + (jb * 16 + ml) * KS + d0;
+                    const float4 qa0 = in0 ? *reinterpret_cast<const float4*>(qr) : z4;
+                    const float4 qa1 = in1 ? *reinterpret_cast<const float4*>(qr + 4) : z4;
+                    const float4 kb0 = in0 ? *reinterpret_cast<const float4*>(kr) : z4;
+                    const float4 kb1 = in1 ? *reinterpret_cast<const float4*>(kr + 4) : z4;
+                    mk_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa0.x, kb0.x, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa0.y, kb0.y, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa0.z, kb0.z, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa0.w, kb0.w, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa1.x, kb1.x, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa1.y, kb1.y, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa1.z, kb1.z, sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa1.w, kb1.w, sacc, 0, 0, 0);
+                    float* rp = red + (kq * kJb + jb) * 256 + (4 * mg) * 16 + ml;  // [kq][jb][g][j % 16]
+                    rp[0] = sacc[0];
+                    rp[16] = sacc[1];
+                    rp[32] = sacc[2];
+                    rp[48] = sacc[3];
+                }
+                __syncthreads();
+                for (int g = wave; g < G; g += kMkWaves) {
+                    // s[g][j] = (q_g . K_j) * scale, j = lane: the kKq partial products summed
+                    float sc = -INFINITY;
+                    if (lane < tlen) {
+                        const int jb = lane >> 4, jj = lane & 15;
+                        float x = 0.f;
+    #pragma unroll
+                        for (int kq = 0; kq < kKq; ++kq) x += red[(kq * kJb + jb) * 256 + g * 16 + jj];
+                        sc = x * p.scale;
+                    }
+                    const float m_old = m_s[g];
+                    const float m_new = fmaxf(m_old, wave_max(sc));
+                    const float corr = expf(m_old - m_new);
+                    const float e = lane < tlen ? expf(sc - m_new) : 0.f;
+                    if (lane < TILE) ps[g * TILE + lane] = e;
+                    const float lsum = wave_sum(e);
+                    if (lane == 0) {
+                        l_s[g] = l_s[g] * corr + lsum;
+                        m_s[g] = m_new;
+                        c_s[g] = corr;
                     }
                 }
-                const float part = a0 + a1;
-                const float dot = part + __shfl_xor(part, 1, kWave);
-                if (half_d == 0) ps[g * TILE + j] = j < tlen ? dot * p.scale : -INFINITY;
+                __syncthreads();
+                {
+                    const int db = wave % kDb, js = wave / kDb;
+                    const int d = db * 16 + ml, j0 = js * 32 + mg * 8;
+                    const float4 pa0 = *reinterpret_cast<const float4*>(ps + ml * TILE + j0);
+                    const float4 pa1 = *reinterpret_cast<const float4*>(ps + ml * TILE + j0 + 4);
+                    float vb[8];
+    #pragma unroll
+                    for (int r = 0; r < 8; ++r) vb[r] = j0 + r < tlen ? vs[(j0 + r) * HDMAX + d] : 0.f;
+                    o4[0] *= c_s[4 * mg + 0];
+                    o4[1] *= c_s[4 * mg + 1];
+                    o4[2] *= c_s[4 * mg + 2];
+                    o4[3] *= c_s[4 * mg + 3];
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.x, vb[0], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.y, vb[1], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.z, vb[2], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.w, vb[3], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.x, vb[4], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.y, vb[5], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.z, vb[6], o4, 0, 0, 0);
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.w, vb[7], o4, 0, 0, 0);
+                }
+                __syncthreads();
             }
-            __syncthreads();
-            for (int g = wave; g < G; g += kMkWaves) {
-                const float sc = lane < TILE ? ps[g * TILE + lane] : -INFINITY;
-                const float m_old = m_s[g];
-                const float m_new = fmaxf(m_old, wave_max(sc));
-                const float corr = expf(m_old - m_new);
-                const float e = lane < tlen ? expf(sc - m_new) : 0.f;
-                if (lane < TILE) ps[g * TILE + lane] = e;
-                const float lsum = wave_sum(e);
-                if (lane == 0) {
-                    l_s[g] = l_s[g] * corr + lsum;
-                    m_s[g] = m_new;
-                    c_s[g] = corr;
+            // The slices' outputs, summed in slice order into the layout of the
+            // merge (output idx = g * hd + d at thread idx % kMkThreads).
+            {
+                const int db = wave % kDb, js = wave / kDb;
+                const int d = db * 16 + ml;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (4 * mg + i < G) red[(js * 16 + 4 * mg + i) * HDMAX + d] = o4[i];  // [js][g][d]
+                __syncthreads();
+    #pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int idx = tid + i * kMkThreads;
+                    acc[i] = 0.f;
+                    if (idx < god) {
+                        const int g = idx / hd, dd = idx - g * hd;
+                        float o = 0.f;
+    #pragma unroll
+                        for (int sl = 0; sl < kJs; ++sl) o += red[(sl * 16 + g) * HDMAX + dd];
+                        acc[i] = o;
+                    }
                 }
             }
-            __syncthreads();
-            // Rows in batches of kPvBatch (every LDS read of a batch issued
-            // before its FMAs, one wait per batch).
-#pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                const int idx = tid + i * kMkThreads;
-                if (idx < god * nsl) {
-                    // (Recomputed per tile: registers are scarce here.)
-                    const int sl = nsl > 1 ? idx / god : 0;  // i > 0 only when nsl == 1
-                    const int o = idx - sl * god;
-                    const int g = o / hd, d = o - g * hd;
-                    const float* pr = ps + g * TILE;
-                    const int j0 = sl * span, j1 = min(j0 + span, tlen);
-                    float v0 = acc[i] * c_s[g], v1 = 0.f, v2 = 0.f, v3 = 0.f;
-                    int j = j0;
-                    for (; j + kPvBatch <= j1; j += kPvBatch) {
-                        float4 p4[kPvBatch / 4];
-                        float vv[kPvBatch];
-#pragma unroll
-                        for (int k = 0; k < kPvBatch / 4; ++k) p4[k] = *reinterpret_cast<const float4*>(pr + j + 4 * k);
-#pragma unroll
-                        for (int k = 0; k < kPvBatch; ++k) vv[k] = vs[(j + k) * HDMAX + d];
-#pragma unroll
-                        for (int k = 0; k < kPvBatch / 4; ++k) {
-                            v0 = fmaf(p4[k].x, vv[4 * k + 0], v0);
-                            v1 = fmaf(p4[k].y, vv[4 * k + 1], v1);
-                            v2 = fmaf(p4[k].z, vv[4 * k + 2], v2);
-                            v3 = fmaf(p4[k].w, vv[4 * k + 3], v3);
+        } else {
+            // P.V work items: (slice sl, q head g, dim d); with G * hd <= 256 the
+            // tile's rows are cut into nsl slices of span rows each (nsl * G * hd
+            // <= kMkThreads, span a multiple of 16) so every thread works, and the
+            // slices are summed after the last tile.
+            constexpr int kPvBatch = 8;
+            // (Slices only where registers allow: not in the dense hd-128 kernel,
+            // whose groups are wide enough for every thread anyway.)
+            constexpr bool kPvSlices = HDMAX <= 64 || MOE;
+            int nsl = 1;
+            if constexpr (kPvSlices)
+                while (nsl < TILE / 16 && 2 * nsl * god <= kMkThreads) nsl *= 2;
+            const int span = TILE / nsl;
+    #pragma unroll
+            for (int i = 0; i < NP; ++i) acc[i] = 0.f;
+            for (uint32_t ta = t0; ta < t1; ta += TILE) {
+                const int tlen = (int)min((uint32_t)TILE, t1 - ta);
+                VVLI_TILE_STORE(ta, tlen);
+                if (ta + TILE < t1) {
+                    VVLI_TILE_LOAD(ta + TILE, (int)min((uint32_t)TILE, t1 - ta - TILE));
+                }
+                __syncthreads();
+                // scores s[g][j] = (q_g . K_j) * scale: thread pairs, each over half
+                // of the dimensions (two independent chains), summed across the pair.
+                for (int idx2 = tid; idx2 < 2 * G * TILE; idx2 += kMkThreads) {
+                    const int idx = idx2 >> 1, half_d = idx2 & 1;
+                    const int g = idx / TILE, j = idx - g * TILE;
+                    float a0 = 0.f, a1 = 0.f;
+                    if (j < tlen) {
+                        const float* qr = qs + g * HDMAX;
+                        const float* kr = ks + j * KS;
+                        if constexpr (EXACT) {
+    #pragma unroll
+                            for (int d = half_d * 4; d < HDMAX; d += 8) {  // float4 chunks alternate in the pair
+                                const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
+                                const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+                                a0 = fmaf(q4.x, k4.x, a0);
+                                a1 = fmaf(q4.y, k4.y, a1);
+                                a0 = fmaf(q4.z, k4.z, a0);
+                                a1 = fmaf(q4.w, k4.w, a1);
+                            }
+                        } else {
+                            for (int d = half_d * 4; d < hd; d += 8) {
+                                const float4 q4 = *reinterpret_cast<const float4*>(qr + d);
+                                const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+                                a0 = fmaf(q4.x, k4.x, a0);
+                                a1 = fmaf(q4.y, k4.y, a1);
+                                a0 = fmaf(q4.z, k4.z, a0);
+                                a1 = fmaf(q4.w, k4.w, a1);
+                            }
                         }
                     }
-                    for (; j < j1; ++j) v0 = fmaf(pr[j], vs[j * HDMAX + d], v0);
-                    acc[i] = (v0 + v1) + (v2 + v3);
+                    const float part = a0 + a1;
+                    const float dot = part + __shfl_xor(part, 1, kWave);
+                    if (half_d == 0) ps[g * TILE + j] = j < tlen ? dot * p.scale : -INFINITY;
                 }
+                __syncthreads();
+                for (int g = wave; g < G; g += kMkWaves) {
+                    const float sc = lane < TILE ? ps[g * TILE + lane] : -INFINITY;
+                    const float m_old = m_s[g];
+                    const float m_new = fmaxf(m_old, wave_max(sc));
+                    const float corr = expf(m_old - m_new);
+                    const float e = lane < tlen ? expf(sc - m_new) : 0.f;
+                    if (lane < TILE) ps[g * TILE + lane] = e;
+                    const float lsum = wave_sum(e);
+                    if (lane == 0) {
+                        l_s[g] = l_s[g] * corr + lsum;
+                        m_s[g] = m_new;
+                        c_s[g] = corr;
+                    }
+                }
+                __syncthreads();
+                // Rows in batches of kPvBatch (every LDS read of a batch issued
+                // before its FMAs, one wait per batch).
+    #pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int idx = tid + i * kMkThreads;
+                    if (idx < god * nsl) {
+                        // (Recomputed per tile: registers are scarce here.)
+                        const int sl = nsl > 1 ? idx / god : 0;  // i > 0 only when nsl == 1
+                        const int o = idx - sl * god;
+                        const int g = o / hd, d = o - g * hd;
+                        const float* pr = ps + g * TILE;
+                        const int j0 = sl * span, j1 = min(j0 + span, tlen);
+                        float v0 = acc[i] * c_s[g], v1 = 0.f, v2 = 0.f, v3 = 0.f;
+                        int j = j0;
+                        for (; j + kPvBatch <= j1; j += kPvBatch) {
+                            float4 p4[kPvBatch / 4];
+                            float vv[kPvBatch];
+    #pragma unroll
+                            for (int k = 0; k < kPvBatch / 4; ++k) p4[k] = *reinterpret_cast<const float4*>(pr + j + 4 * k);
+    #pragma unroll
+                            for (int k = 0; k < kPvBatch; ++k) vv[k] = vs[(j + k) * HDMAX + d];
+    #pragma unroll
+                            for (int k = 0; k < kPvBatch / 4; ++k) {
+                                v0 = fmaf(p4[k].x, vv[4 * k + 0], v0);
+                                v1 = fmaf(p4[k].y, vv[4 * k + 1], v1);
+                                v2 = fmaf(p4[k].z, vv[4 * k + 2], v2);
+                                v3 = fmaf(p4[k].w, vv[4 * k + 3], v3);
+                            }
+                        }
+                        for (; j < j1; ++j) v0 = fmaf(pr[j], vs[j * HDMAX + d], v0);
+                        acc[i] = (v0 + v1) + (v2 + v3);
+                    }
+                }
+                __syncthreads();
             }
-            __syncthreads();
-        }
-        if (nsl > 1) {  // slices 1.. through the (now free) K tile, added in slice order
-            float* sred = ks;
-            if (tid >= god && tid < god * nsl) sred[tid - god] = acc[0];
-            __syncthreads();
-            if (tid < god)
-                for (int k = 1; k < nsl; ++k) acc[0] += sred[(k - 1) * god + tid];
-            __syncthreads();  // the merge reuses the K tile
+            if (nsl > 1) {  // slices 1.. through the (now free) K tile, added in slice order
+                float* sred = ks;
+                if (tid >= god && tid < god * nsl) sred[tid - god] = acc[0];
+                __syncthreads();
+                if (tid < god)
+                    for (int k = 1; k < nsl; ++k) acc[0] += sred[(k - 1) * god + tid];
+                __syncthreads();  // the merge reuses the K tile
+            }
         }
         if (tid == 0) mk_mark(p, ph, 10);
         if (ns == 1) {  // one split: normalise its own outputs
