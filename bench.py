@@ -313,7 +313,8 @@ def phases_main(args, cfg, blob) -> int:
     for k in PHASE_KINDS + ("logits",):
         per = 1 if k == "logits" else L
         b = kernel_bytes(cfg, positions[len(positions) // 2])[PHASE_BYTES.get(k, "logits")]
-        rows[k] = {"us": round(float(np.median(dur[k])), 2), "hop_us": round(float(np.nanmedian(hop[k])), 2),
+        hk = [h for h in hop[k] if not np.isnan(h)]  # (the attention phase stages nothing)
+        rows[k] = {"us": round(float(np.median(dur[k])), 2), "hop_us": round(float(np.median(hk)), 2) if hk else None,
                    "bytes": int(b), "gbs": round(float(np.median(gbs[k])), 1), "per_token": per,
                    "us_per_token": round(float(np.median(dur[k])) * per, 1)}
     names = {"Q": "q/k/v (RMSNorm + GEMV + bias)", "A": "attention (RoPE, KV append, split merge)",
@@ -325,7 +326,8 @@ def phases_main(args, cfg, blob) -> int:
     md = ["| phase | median us | staged after (us) | algorithmic bytes | GB/s | % of 8 TB/s | per token | us per token |",
           "|---|---|---|---|---|---|---|---|"]
     for k, r in rows.items():
-        md.append(f"| {names[k]} | {r['us']:.2f} | {r['hop_us']:.2f} | {r['bytes']:,} | {r['gbs']:.0f} | "
+        hop_s = f"{r['hop_us']:.2f}" if r["hop_us"] is not None else "-"
+        md.append(f"| {names[k]} | {r['us']:.2f} | {hop_s} | {r['bytes']:,} | {r['gbs']:.0f} | "
                   f"{100 * r['gbs'] / HBM_PEAK_GBS:.1f} | x{r['per_token']} | {r['us_per_token']:.1f} |")
     med_step = float(np.median(step_us))
     md.append(f"| whole step (kernel start to logits end) | {med_step:.1f} | | "
