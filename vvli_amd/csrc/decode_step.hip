@@ -780,7 +780,8 @@ struct AttnLds {
 // over the full q, s_k the same over the full k, from the q | k words of
 // phase `tag` (polled as one batch per thread, like the input staging).
 // Block-uniform; false: a poll failed.
-__device__ __forceinline__ bool mk_qk_scales(const DecodeStepParams& p, uint32_t tag, float& scq, float& sck) {
+__device__ __forceinline__ bool mk_qk_scales(const DecodeStepParams& p, uint32_t tag, float& scq, float& sck,
+                                             float* qk_lds) {
     __shared__ float red2[2][kMkWaves];
     const int tid = threadIdx.x;
     const uint32_t nq = p.heads * p.hd, n2 = (nq + p.kvdim) / 2;  // word pairs of q | k (nq is even)
@@ -816,6 +817,7 @@ __device__ __forceinline__ bool mk_qk_scales(const DecodeStepParams& p, uint32_t
             const uint32_t i = i0 + k * kMkThreads;
             if (i < n2) {
                 const float v0 = tw_val(a[k]), v1 = tw_val(b[k]);
+                if (qk_lds) *reinterpret_cast<float2*>(qk_lds + 2 * i) = make_float2(v0, v1);
                 const float s2 = fmaf(v1, v1, v0 * v0);
                 if (2 * i < nq) sq += s2;
                 else sk += s2;
@@ -920,19 +922,36 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
         const uint16_t* qn = nullptr;
         const uint16_t* kn = nullptr;
         float scq = 1.f, sck = 1.f;
+        // With QK-norm the whole q | k is polled for the scales; its values
+        // land in the K and V tile space (free until the first tile), so the
+        // head's q and the new k come from LDS, and the appending split's v
+        // word goes out with that batch: one memory round trip, not two.
+        float* qkl = nullptr;
+        tword wv_pre = 0;
         if constexpr (MOE) {
             qn = p.layer[layer].q_norm;
             kn = p.layer[layer].k_norm;
-            if (qn && !mk_qk_scales(p, tag_in, scq, sck)) return false;
+            if (qn) {
+                if (p.heads * p.hd + kvw <= (uint32_t)(TILE * KS + TILE * HDMAX)) qkl = ks;
+                if (qkl && owns && tid < hd) wv_pre = ld_a(vn_all + (size_t)h * hd + tid);
+                if (!mk_qk_scales(p, tag_in, scq, sck, qkl)) return false;
+            }
         }
         // q (and the owner's new k / v) of this kv head, RoPE'd into LDS.
         for (int idx = tid; idx < G * half; idx += kMkThreads) {
             const int g = idx / half, i = idx - g * half;
             const int f = inter ? 2 * i : i, sc = inter ? 2 * i + 1 : i + half;
-            const tword* src = q + (size_t)(h * G + g) * hd;
-            tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
-            ok = ok && poll_tw2(src + f, src + sc, tag_in, w0, w1, p.error);
-            float x0 = tw_val(w0), x1 = tw_val(w1);
+            float x0, x1;
+            if (qkl) {
+                x0 = qkl[(h * G + g) * hd + f];
+                x1 = qkl[(h * G + g) * hd + sc];
+            } else {
+                const tword* src = q + (size_t)(h * G + g) * hd;
+                tword w0 = ld_a(src + f), w1 = ld_a(src + sc);
+                ok = ok && poll_tw2(src + f, src + sc, tag_in, w0, w1, p.error);
+                x0 = tw_val(w0);
+                x1 = tw_val(w1);
+            }
             if constexpr (MOE) {
                 if (qn) {
                     const uint16_t* nw = qn + (size_t)(h * G + g) * hd;
@@ -950,16 +969,17 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
             const tword* vsrc = vn_all + (size_t)h * hd + tid;
             const bool hk = tid < half, hv = tid < hd;
             const int f = inter ? 2 * tid : tid, sc = inter ? 2 * tid + 1 : tid + half;
-            tword w0 = 0, w1 = 0, wv = 0;
-            if (hk) {
+            tword w0 = 0, w1 = 0, wv = wv_pre;
+            if (hk && !qkl) {
                 w0 = ld_a(ksrc + f);
                 w1 = ld_a(ksrc + sc);
             }
-            if (hv) wv = ld_a(vsrc);
-            if (hk) ok = ok && poll_tw2(ksrc + f, ksrc + sc, tag_in, w0, w1, p.error);
+            if (hv && !qkl) wv = ld_a(vsrc);
+            if (hk && !qkl) ok = ok && poll_tw2(ksrc + f, ksrc + sc, tag_in, w0, w1, p.error);
             if (hv) ok = ok && poll_tw(vsrc, tag_in, wv, p.error);
             if (hk) {
-                float x0 = tw_val(w0), x1 = tw_val(w1);
+                const uint32_t kq = p.heads * p.hd + (uint32_t)h * hd;  // the new k in the q | k staging
+                float x0 = qkl ? qkl[kq + f] : tw_val(w0), x1 = qkl ? qkl[kq + sc] : tw_val(w1);
                 if constexpr (MOE) {
                     if (kn) {
                         x0 = bf_val(kn[(size_t)h * hd + f]) * (x0 * sck);
