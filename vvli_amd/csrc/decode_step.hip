@@ -49,6 +49,12 @@ constexpr int kMkThreads = 512;
 constexpr int kMkWaves = kMkThreads / kWave;
 constexpr int kMaxGroupMk = 16;
 constexpr int kMaxSplitMk = 64;  // attention splits per kv head
+// Delay of the gate/up LDS copies after the q/k/v words appear: two
+// s_sleep of 64 x kGldsSleep cycles, ~1.5 us at the 2.2 GHz shader clock
+// of a decode step. Measured best near 1.5 us (Llama-3.2-1B 1315 -> 1331
+// tok/s, Qwen2.5-0.5B 1259 -> 1278; delays of 0.5, 1, 2 and 3 us gave
+// 1322, 1329, 1328, 1320 at Llama-3.2-1B).
+constexpr int kGldsSleep = 26;
 constexpr int kOwnerMergeMax = 16;  // splits merged by one block (the one that appends the K/V row)
 static_assert(kMaxSplitMk <= 64, "the split merge weights are one wave's lanes");
 constexpr uint32_t kSpinLimit = 1u << 22;  // polls of one word (each after a short sleep): seconds
@@ -1712,12 +1718,18 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     const MkGemv& gg = tb.gemv[f.layer * 4 + 2];
                     const GLds q = mk_glds(p, units, gg);
                     if (mk_glds_count(q, w.wave)) {
-                        // Start the copy once the q/k/v words show up, so it
-                        // does not queue in front of them and of the units'
-                        // K/V loads.
+                        // Start the copy kGldsDelay after the q/k/v words
+                        // show up, so it does not queue in front of them, of
+                        // the units' K/V loads and of their q polls (which
+                        // return ~1.5 us after the words appear; the copies
+                        // still end well before the gate/up phase).
                         tword qw = ld_a(p.tqkv);
                         ok = ok && poll_tw(p.tqkv, tag - 1, qw, p.error);
-                        if (ok) mk_glds_issue(q, gg, reinterpret_cast<char*>(smem), w.wave, w.lane);
+                        if (ok) {
+                            __builtin_amdgcn_s_sleep(kGldsSleep);  // 64 x kGldsSleep cycles, twice
+                            __builtin_amdgcn_s_sleep(kGldsSleep);
+                            mk_glds_issue(q, gg, reinterpret_cast<char*>(smem), w.wave, w.lane);
+                        }
                     }
                 }
             } else {
