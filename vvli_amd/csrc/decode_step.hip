@@ -1273,7 +1273,7 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
                 const int idx = tid + i * kMkThreads;
                 if (idx < G * hd) {
                     const int g = idx / hd;
-                    int idx_o = idx;  // (opaque: see below)
+                    int idx_o = idx;  // (an opaque copy: hoisted, the 64-bit store address would hold registers)
                     asm volatile("" : "+v"(idx_o));
                     st_a(p.tattn + (size_t)h * G * hd + idx_o, tw_make(fmaf(acc[i], 1.0f / l_s[g], 0.f), tag_out));
                 }
