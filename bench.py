@@ -180,14 +180,22 @@ def gemv_sweep(shapes, ms, log=True) -> list:
     """vvli_gpu_linear over (N, K) x M: bf16 W [N, K] ~ N(0, 0.02), f32 X [M, K]
     ~ N(0, 1), f32 Y [M, N]. Each shape rotates over enough weight copies
     (>= 1 GiB) that W is read from HBM, not from the 256 MB memory-side cache.
-    Algorithmic bytes 2NK + 4MK + 4MN, flops 2MNK; time per call = HIP events
-    around the calls on one stream."""
+    Algorithmic bytes 2NK + 4MK + 4MN, flops 2MNK.
+
+    Time per call, two ways: `us` -- a HIP graph of `reps` back-to-back calls
+    (one per weight copy in turn), HIP events around its replay, so the GPU
+    runs the kernels back to back without waiting for the host (the op's
+    device time including the gap between launches); `us_host_loop` -- the
+    same calls issued one by one from Python through ctypes, HIP events
+    around the loop (bounded below by the host's per-call cost, about 3 us
+    here). The graph is captured on a stream whose scratch the warm-up calls
+    already sized, so the capture records kernels only."""
     import torch
 
     from vvli_amd import runtime as R
 
     gen = torch.Generator(device="cuda").manual_seed(0)
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()
     rows = []
     for n, k in shapes:
         wbytes = 2 * n * k
@@ -197,22 +205,42 @@ def gemv_sweep(shapes, ms, log=True) -> list:
             x = torch.randn(m, k, device="cuda", generator=gen)
             y = torch.empty(m, n, device="cuda")
             reps = max(copies, 20)
-            for i in range(3):
+            torch.cuda.synchronize()
+
+            def call(i):
                 R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(reps):
-                R.linear(ws[i % copies].data_ptr(), x.data_ptr(), y.data_ptr(), m, n, k, stream=stream.cuda_stream)
-            e1.record(stream)
+
+            with torch.cuda.stream(stream):
+                for i in range(3):
+                    call(i)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(reps):
+                    call(i)
+                e1.record(stream)
+            e1.synchronize()
+            us_host = e0.elapsed_time(e1) * 1e3 / reps
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(reps):
+                    call(i)
+            with torch.cuda.stream(stream):
+                g.replay()
+                stream.synchronize()
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
             e1.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / reps
+            del g
             nbytes = 2 * n * k + 4 * m * k + 4 * m * n
             rows.append({"N": n, "K": k, "M": m, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                          "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-                         "tflops": round(2 * m * n * k / us / 1e6, 1)})
+                         "tflops": round(2 * m * n * k / us / 1e6, 1), "us_host_loop": round(us_host, 2)})
             if log:
-                print(f"[bench] linear N={n} K={k} M={m}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s, "
-                      f"{2 * m * n * k / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+                print(f"[bench] linear N={n} K={k} M={m}: {us:.2f} us (graph), {nbytes / us / 1e3:.0f} GB/s, "
+                      f"{2 * m * n * k / us / 1e6:.1f} TFLOP/s; host loop {us_host:.2f} us", file=sys.stderr,
+                      flush=True)
         del ws
         torch.cuda.empty_cache()
     return rows
@@ -530,14 +558,25 @@ def sampled_main(args, cfg, blob) -> int:
 def linear_main(args) -> int:
     """Isolated op sweep (vvli_gpu_linear) on the Llama-3.2-1B projection shapes
     at M in {1, 4, 16, 128, 512} (gemv_sweep)."""
-    rows = gemv_sweep(LINEAR_SHAPES, [1, 4, 16, 128, 512])
-    gemv = [r for r in rows if r["M"] == 1]
-    agg = sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv) / sum(r["us"] for r in gemv) / 1e3
+    ms = [int(v) for v in args.linear_m.split(",")]
+    rows = gemv_sweep(LINEAR_SHAPES, ms)
+    gemv = [r for r in rows if r["M"] == 1] or rows
+    agg = sum(2 * r["N"] * r["K"] + 4 * r["K"] * r["M"] + 4 * r["N"] * r["M"] for r in gemv) / sum(r["us"] for r in gemv) / 1e3
+    if args.copy_calibration:  # a 256 MiB device copy: the HBM-counter calibration of rocprofv3 --pmc runs
+        import torch
+
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
     line = {
-        "metric": "linear op sweep: GEMV HBM GB/s (M=1, all five shapes)", "value": round(agg, 1), "unit": "GB/s",
+        "metric": f"linear op sweep: GEMV HBM GB/s (M={gemv[0]['M']}, all five shapes)", "value": round(agg, 1),
+        "unit": "GB/s",
         "n_gpus": 1, "steps": len(rows), "warmup": 3, "ms_per_step": None, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 weights, f32 activations", "data": "synthetic",
-        "config": {"workload": "Llama-3.2-1B projection shapes x M in {1, 4, 16, 128, 512}, cold weights"},
+        "config": {"workload": f"Llama-3.2-1B projection shapes x M in {{{', '.join(map(str, ms))}}}, cold weights",
+                   "timing": "HIP graph of back-to-back calls per shape and M (us); Python host loop (us_host_loop)"},
         "roofline": {"bound": "hbm", "achieved": round(agg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(agg / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "vvli_gpu_linear, M = 1"},
         "sweep": rows, "cpu_baseline": None,
@@ -556,6 +595,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv-sweep", action="store_true", help="decode mode: skip the M = 1 op sweep")
+    ap.add_argument("--linear-m", default="1,4,16,128,512", help="linear mode: comma-separated M values")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],
@@ -736,11 +776,13 @@ def main() -> int:
     # GEMV half of the metric: the isolated op at M = 1 on the five projection
     # shapes of the model (cold weights), HBM GB/s per shape.
     gemv_rows = [] if args.no_gemv_sweep else gemv_sweep(LINEAR_SHAPES, [1], log=False)
-    gemv = {f"{r['N']}x{r['K']}": {"us": r["us"], "gbs": r["gbs"], "frac": r["frac"]} for r in gemv_rows}
+    gemv = {f"{r['N']}x{r['K']}": {"us": r["us"], "gbs": r["gbs"], "frac": r["frac"],
+                                   "us_host_loop": r["us_host_loop"]} for r in gemv_rows}
     if gemv_rows:
         agg = (sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv_rows) / sum(r["us"] for r in gemv_rows)
                / 1e3)
-        gemv["all_shapes"] = {"gbs": round(agg, 1), "frac": round(agg / HBM_PEAK_GBS, 4)}
+        gemv["all_shapes"] = {"gbs": round(agg, 1), "frac": round(agg / HBM_PEAK_GBS, 4),
+                              "timing": "per shape: HIP graph of back-to-back calls over >= 1 GiB of weight copies"}
         print("[bench] gemv M=1: " + ", ".join(f"{k} {v['gbs']:.0f}GB/s" for k, v in gemv.items()), file=sys.stderr,
               flush=True)
 

@@ -123,12 +123,20 @@ def _bench_weights(N, K):
     return _BENCH_W[(N, K)]
 
 
-@pytest.mark.parametrize("N,K", [(8192, 2048), (128256, 2048)])
-@pytest.mark.parametrize("M", [1, 4, 16, 128, 512])
+# The isolated op sweep on the Llama-3.2-1B projection shapes: q/o, k/v,
+# gate/up, down and lm_head, each at every M of the sweep.
+SWEEP_SHAPES = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (128256, 2048)]
+SWEEP_M = [1, 4, 16, 128, 512]
+
+
+@pytest.mark.parametrize("M", SWEEP_M)  # M varies fastest: each weight matrix is generated once
+@pytest.mark.parametrize("N,K", SWEEP_SHAPES)
 def test_linear_benchmark_shapes(N, K, M, oracle_mod):
-    """The op-sweep shapes the benchmark times (gate/up and lm_head of
-    Llama-3.2-1B) at every M it times: GEMV (M = 1), skinny MFMA (4, 16) and
-    GEMM (128, 512) paths; sampled rows against the oracle."""
+    """Every (N, K) x M point of the op sweep the benchmark times: GEMV
+    (M = 1), skinny MFMA (4, 16) and GEMM (128, 512) paths. Every row of x
+    for M <= 16; for M = 128 / 512 the rows at the edges of the GEMM's
+    16-row fragments and 128-row block tiles, the middle and the last, each
+    compared with the oracle over all N outputs."""
     import torch
 
     w = _bench_weights(N, K)
@@ -143,7 +151,56 @@ def test_linear_benchmark_shapes(N, K, M, oracle_mod):
     torch.cuda.synchronize()
     y = dy.cpu().numpy()
     assert np.isfinite(y).all()
-    for m in sorted({0, 1 % M, M // 2, M - 1}):
+    rows = range(M) if M <= 16 else sorted({0, 1, 15, 16, 63, 64, 127, M // 2, M - 1} & set(range(M)) |
+                                          ({128, 129, 255, 256, 383, 384} & set(range(M))))
+    for m in rows:
         ref = oracle_mod.linear(w, x[m], None)
         e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
         assert e <= TOL, f"M={M} N={N} row {m}: rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", [
+    (1, 37, 40, True),      # rows of 5 units: one unit per lane, most lanes masked
+    (2, 4099, 896, False),  # 112 units per row (two per lane, a ragged second), ragged last block
+    (3, 130, 8192, True),   # three rows of x in one launch, 4 items per row
+    (2, 1, 2048, True),     # a single output row
+    (3, 512, 16384, False), # 3 x 64 KiB of x exceeds LDS: one launch per row
+    (1, 300, 40960, False), # the largest K whose x fits LDS
+])
+def test_linear_gemv_shapes(M, N, K, has_bias, oracle_mod):
+    """The M <= 3 GEMV kernel (one launch for up to three rows of x staged in
+    LDS, whole-row wave tiles walked in items of 1-4 units per lane): ragged
+    rows and tiles, bias, and the per-row fallback, against the oracle."""
+    import torch
+
+    rng = np.random.default_rng(M * 31 + N * 17 + K)
+    w = bf16_bits(rng.normal(0, 0.02, size=(N, K)))
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    bias = bf16_bits(rng.normal(0, 0.02, size=N)) if has_bias else None
+    dev = torch.device("cuda", 0)
+    dw = torch.from_numpy(w.view(np.int16)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    db = torch.from_numpy(bias.view(np.int16)).to(dev) if has_bias else None
+    print(f"linear gemv M={M} N={N} K={K} bias={has_bias}", flush=True)
+    R.linear(dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), M, N, K, None if db is None else db.data_ptr())
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy()
+    for m in range(M):
+        ref = oracle_mod.linear(w, x[m], bias)
+        e = float(np.max(np.abs(y[m] - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+        assert e <= TOL, f"M={M} N={N} K={K} row {m}: rel err {e:.3e}"
+
+
+def test_linear_gemv_rejects_k_beyond_lds():
+    """M <= 3 stages x in LDS: K beyond 40960 floats is an invalid shape for
+    those M (checked before any launch)."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    K = 40968
+    w = torch.zeros((4, K), dtype=torch.int16, device=dev)
+    x = torch.zeros((1, K), dtype=torch.float32, device=dev)
+    y = torch.zeros((1, 4), dtype=torch.float32, device=dev)
+    with pytest.raises(VvliError):
+        R.linear(w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, K)

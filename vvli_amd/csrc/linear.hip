@@ -13,15 +13,56 @@
 
 #include "internal.hpp"
 #include "kernels.hpp"
+#include "linear_gemv.hpp"
 
 using namespace vvli;
 
 namespace {
 
-// Rows from which one MFMA kernel replaces a GEMV launch per row; up to
-// kSkinnyMaxRows the skinny kernel below, beyond it the prefill GEMM.
+// Rows from which one MFMA kernel replaces the GEMV kernel (linear_gemv.hpp,
+// up to 3 rows of x in one launch); up to kSkinnyMaxRows the skinny kernel
+// below, beyond it the prefill GEMM.
 constexpr uint32_t kLinearGemmMinRows = 4;
 constexpr uint32_t kSkinnyMaxRows = 64;
+
+// ---------------------------------------------------------------------------
+// GEMV plan (M <= 3): one wave per row tile (RW = 1), UL units of 16 bytes per
+// lane per item (4, i.e. 4 KiB rows in one item at K = 2048; fewer when rows
+// are short), one block of four waves per CU. Measured on the Llama-3.2-1B
+// shapes (per-dispatch time, cold weights): more waves per CU or two-row
+// tiles are no faster on the 8-33 MB shapes and slower on the 525 MB lm_head
+// (4 waves per CU 79.6 us, 8 waves 85.6 us, 16 waves 90.3 us) -- with two
+// 4 KiB items per wave in flight, 32 KiB per CU cover the latency, and more
+// outstanding requests only add contention.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kGemvMaxLds = 160 * 1024;
+
+uint32_t gemv_ul(uint32_t K) {
+    const uint32_t U = K / 8;
+    return U > 128 ? 4 : (U > 64 ? 2 : 1);
+}
+
+template <int MR, int UL>
+hipError_t launch_gemv_t(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
+                         uint32_t K, hipStream_t s) {
+    const uint32_t blocks = std::min<uint32_t>((N + kLgWaves - 1) / kLgWaves, 256);
+    const size_t lds = (size_t)MR * K * sizeof(float);
+    return vlaunch(linear_gemv_kernel<MR, 1, UL>, dim3(blocks), dim3(kLgThreads), lds, s, dW, dX, dBias, dY, M, N, K);
+}
+
+// One launch for up to 3 rows of x (x staged in LDS: MR * K * 4 bytes).
+hipError_t launch_gemv_rows(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M,
+                            uint32_t N, uint32_t K, hipStream_t s) {
+    const uint32_t ul = gemv_ul(K);
+#define VVLI_GEMV_MR(MR_)                                                                           \
+    return ul == 4 ? launch_gemv_t<MR_, 4>(dW, dX, dBias, dY, M, N, K, s)                          \
+           : ul == 2 ? launch_gemv_t<MR_, 2>(dW, dX, dBias, dY, M, N, K, s)                        \
+                     : launch_gemv_t<MR_, 1>(dW, dX, dBias, dY, M, N, K, s);
+    if (M == 1) VVLI_GEMV_MR(1)
+    if (M == 2) VVLI_GEMV_MR(2)
+    VVLI_GEMV_MR(3)
+#undef VVLI_GEMV_MR
+}
 
 // ---------------------------------------------------------------------------
 // Skinny GEMM (4 <= M <= 64): Y[m][n] = sum_k X[m][k] W[n][k] (+ bias[n]) on
@@ -263,6 +304,17 @@ int linear_setup() {
     static hipError_t err = hipSuccess;
     std::call_once(flag, [] {
         err = gemv_init_attributes();
+        const void* gemv[] = {reinterpret_cast<const void*>(&linear_gemv_kernel<1, 1, 1>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<1, 1, 2>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<1, 1, 4>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<2, 1, 1>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<2, 1, 2>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<2, 1, 4>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 1>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 2>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 4>)};
+        for (const void* k : gemv)
+            if (err == hipSuccess) err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds);
         // Skinny variants keep up to 128 KiB of wave partials in LDS.
         const std::pair<const void*, int> skinny[] = {
             {reinterpret_cast<const void*>(&linear_skinny_kernel<1, 1, 4>), 8 * 16 * 16 * 4},
@@ -286,6 +338,9 @@ int check_linear_args(const void* dW, const void* dX, const void* dY, uint32_t M
     if (!dW || !dX || !dY) return set_error(VVLI_NULL_ARG, "NULL device pointer to %s", who);
     if (M == 0 || N == 0 || K == 0 || K % 8 != 0)
         return set_error(VVLI_INVALID_CONFIG, "bad linear shape M=%u N=%u K=%u (K %% 8 == 0 required)", M, N, K);
+    if (M < kLinearGemmMinRows && (size_t)K * sizeof(float) > kGemvMaxLds)
+        return set_error(VVLI_INVALID_CONFIG, "linear K=%u too large for M=%u (x is staged in LDS: K <= %zu)", K, M,
+                         kGemvMaxLds / sizeof(float));
     return linear_setup();
 }
 
@@ -320,16 +375,14 @@ int linear_enqueue(const uint16_t* dW, const float* dX, const uint16_t* dBias, f
         HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
         return VVLI_OK;
     }
-    for (uint32_t mi = 0; mi < M; ++mi) {
-        GemvArgs g;
-        g.w[0] = dW;
-        g.bias[0] = dBias;
-        g.out[0] = dY + static_cast<size_t>(mi) * N;
-        g.rows[0] = N;
-        g.x = dX + static_cast<size_t>(mi) * K;
-        g.K = K;
-        HIP_TRY(launch_gemv(VVLI_WEIGHT_BF16, kGemvPlain, g, s));
+    // M <= 3: one GEMV launch for all rows when their x fits LDS, else one per row.
+    if ((size_t)M * K * sizeof(float) <= kGemvMaxLds) {
+        HIP_TRY(launch_gemv_rows(dW, dX, dBias, dY, M, N, K, s));
+        return VVLI_OK;
     }
+    for (uint32_t mi = 0; mi < M; ++mi)
+        HIP_TRY(launch_gemv_rows(dW, dX + static_cast<size_t>(mi) * K, dBias, dY + static_cast<size_t>(mi) * N, 1, N, K,
+                                 s));
     return VVLI_OK;
 }
 
