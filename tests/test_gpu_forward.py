@@ -51,6 +51,11 @@ CASES = {
                                num_key_value_heads=2), C.WEIGHT_BF16, "synth", 24),
     # f32 weights through the f32 kernel variants.
     "qwen_small_f32": (cfg_small(), C.WEIGHT_F32, "synth", 20),
+    # head_dim 96 (between the 64 and 128 kernels: the head-dim-128 persistent
+    # kernel with its columns d >= 96 masked), GQA group 4, interleaved RoPE.
+    "hd96_g4": (cfg_small(vocab_size=700, hidden_size=768, intermediate_size=1024, num_attention_heads=8,
+                          num_key_value_heads=2, qkv_bias=False, architecture="llama",
+                          rope_layout=C.ROPE_INTERLEAVED), C.WEIGHT_BF16, "synth", 40),
 }
 
 
@@ -118,7 +123,7 @@ def test_graph_step_equals_debug_step(name, built):
             assert am == R.argmax(la)
 
 
-BF16_CASES = ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7", "qwen05_heads"]
+BF16_CASES = ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7", "qwen05_heads", "hd96_g4"]
 
 
 @pytest.mark.parametrize("name", BF16_CASES)
@@ -126,9 +131,11 @@ def test_persistent_steps_match_oracle(name, built, oracle_mod, host_threads):
     """The one-launch persistent step (forward_token on the 'persistent'
     path): logits, argmax and K/V rows against the oracle, token by token."""
     cfg, kind, how, steps = CASES[name]
-    # llama_small (head_dim 64) and hd128_g7 (head_dim 128, the matrix-core
-    # tile): up to 5 splits of 64 positions, merged by the appending split.
-    steps = {"llama_small": 300, "hd128_g7": 300}.get(name, steps)
+    # llama_small (head_dim 64), hd128_g7 (head_dim 128, the matrix-core
+    # tile) and hd96_g4 (the same tile with masked columns): 2 splits of 64
+    # positions (every split merges a slice of the outputs) up to 5 (the
+    # appending split merges the others).
+    steps = {"llama_small": 300, "hd128_g7": 300, "hd96_g4": 300}.get(name, steps)
     max_seq = min(cfg.max_position_embeddings, 512)
     blob = make_blob(cfg, kind, how)
     orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)

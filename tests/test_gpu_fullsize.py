@@ -7,10 +7,14 @@ within 2e-3 max relative error for the first positions, and the greedy tokens
 identical. Sequence lengths are cut to what the CPU oracle finishes in
 seconds; the GPU runs the same code paths the benchmark runs (persistent
 decode step, batched prefill)."""
+import os
+
 import numpy as np
 import pytest
 
 from vvli_amd import config as C
+from vvli_amd import gguf_write
+from vvli_amd import loaders as L
 from vvli_amd import runtime as R
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
@@ -84,3 +88,44 @@ def test_olmoe_full_size(oracle_mod, host_threads):
         ref = orc2.generate_greedy(prompt, 64)
         got, _ = gpu.generate_greedy_measured(prompt, 64)
         np.testing.assert_array_equal(got, ref)
+
+
+def test_llama1b_workload_as_benched(oracle_mod, host_threads, tmp_path):
+    """The headline decode workload exactly as bench.py times it: Llama-3.2-1B
+    shape (16 layers), seeded N(0, 0.02) bf16 weights written as a GGUF file
+    and loaded through the device GGUF loader, the llama3-scaled RoPE table,
+    a 512-token batched prefill, then 128 greedy tokens from one persistent
+    decode launch at ctx 4096 (generator.zig's loop: src/generator.zig:221-293).
+
+    Bar: the 128 tokens identical to the oracle's (its prompt runs token by
+    token, as the reference does), and the residual stream after every layer
+    and the logits within 2e-3 at positions 512, 575 and 639 (each step
+    recomputed on both sides over the KV cache the generation left)."""
+    cfg = C.llama32_1b()
+    ctx, n_prompt, n_new = 4096, 512, 128
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02, threads=host_threads)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, n_prompt).astype(np.uint32)
+    table = R.llama3_inv_freq(cfg.head_dim(), cfg.rope_theta)
+    path = os.path.join(tmp_path, "llama-3.2-1b.gguf")
+    gguf_write.write_dense_gguf(path, cfg, blob)
+    print("case=llama-3.2-1b workload: GGUF -> device loader, 512 + 128, ctx 4096", flush=True)
+    gcfg, gpu = L.device_load_gguf(path, ctx)
+    os.remove(path)
+    with gpu:
+        assert gcfg.num_hidden_layers == 16 and gcfg.rope_layout == C.ROPE_INTERLEAVED
+        gpu.set_decode_path("persistent")
+        gpu.set_rope_table(table)
+        got, stats = gpu.generate_greedy_measured(prompt, n_new, batched_prefill=True)
+        assert stats.generated_tokens == n_new
+        orc = oracle_mod.OracleRunner(cfg, blob, ctx, threads=host_threads)
+        orc.set_rope_table(table)
+        print("case=llama-3.2-1b workload: oracle 512 + 128", flush=True)
+        ref, _ = orc.generate_greedy(prompt, n_new)
+        np.testing.assert_array_equal(got, ref)
+        for pos in (512, 575, 639):  # token fed at pos: the (pos - 512)-th generated one
+            tok = int(ref[pos - n_prompt])
+            ref_logits, ref_hidden = orc.forward_token(tok, pos, want_hidden=True)
+            logits, hidden = gpu.forward_token_debug(tok, pos)
+            worst = max(rel_err(hidden[l], ref_hidden[l]) for l in range(cfg.num_hidden_layers))
+            assert worst <= TOL, f"pos {pos}: hidden rel err {worst:.3e}"
+            assert rel_err(logits, ref_logits) <= TOL, f"pos {pos}: logits"

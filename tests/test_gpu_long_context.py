@@ -15,6 +15,11 @@ geometries of the two long-context workloads:
   qkv bias, untied): 4096-token prompt, then 256 decode steps at ctx 8192, so
   every step merges 43..46 splits of 96 positions (each split merging at most
   21 of its head's 896 outputs; at 46 splits one merges none).
+* The spread merge at head_dim 64 beyond 16 splits: Llama-3.2-1B heads at
+  positions 2016-2055 (32 splits, each merging 8 of its kv head's 256
+  outputs, then 17 splits of 128 positions) with the llama3 table, and
+  Qwen2.5-0.5B heads (14 q / 2 kv, group 7) at positions 4064-4095 (64
+  splits, each merging 7 of its kv head's 448 outputs).
 
 Two layers, and a reduced intermediate size and vocabulary, keep the oracle's
 CPU time to seconds; the attention shapes, the split counts and the KV lengths
@@ -66,11 +71,24 @@ def splits_at(pos: int, max_seq: int, kv_heads: int, head_dim: int, blocks: int 
     return -(-t // chunk)
 
 
+def cfg_qwen05b_heads() -> C.Config:
+    return C.Config(vocab_size=512, hidden_size=896, intermediate_size=512, num_hidden_layers=2,
+                    num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768, rope_theta=1e6,
+                    rms_norm_eps=1e-6, tie_word_embeddings=True, architecture="qwen2", qkv_bias=True,
+                    rope_layout=C.ROPE_SPLIT_HALF)
+
+
 CASES = {
     # name: (config maker, ctx, prompt, decode steps, llama3 table)
     "llama1b_heads_512p128": (cfg_llama1b_heads, 4096, 512, 128, False),
     "llama1b_heads_512p128_llama3rope": (cfg_llama1b_heads, 4096, 512, 128, True),
     "qwen7b_heads_4096p256": (cfg_qwen7b_heads, 8192, 4096, 256, False),
+    # Llama-3.2-1B heads past position 1024: 32 splits of 64 positions up to
+    # position 2047, then 17 of 128 -- the spread merge at head_dim 64.
+    "llama1b_heads_2016p40": (cfg_llama1b_heads, 4096, 2016, 40, True),
+    # Qwen2.5-0.5B heads (14 q / 2 kv, head_dim 64, group 7): 64 splits at
+    # positions 4032-4095, the most the step uses.
+    "qwen05b_heads_4064p32": (cfg_qwen05b_heads, 8192, 4064, 32, False),
 }
 
 

@@ -90,3 +90,63 @@ def test_noalloc_linear_rejects_oversize():
     assert e.value.name == "InvalidConfig"
     torch.cuda.synchronize()
     assert bool((dy == 7.0).all())
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", [
+    (16, 512, 8192, False),  # skinny MFMA with K split across blocks (32 row tiles): counters in the scratch
+    (130, 1000, 896, True),  # the GEMM path: activation split planes in the scratch
+])
+def test_noalloc_linear_in_graph(M, N, K, has_bias, oracle_mod):
+    """vvli_gpu_linear_noalloc captured into a HIP graph (torch.cuda.CUDAGraph
+    over the entry point on the capture stream): after one eager call on the
+    device (its one-time set-up: attributes and the scratch address), the
+    capture records kernels only (neither path issues a memset), and every
+    replay -- three, with other eager calls and synchronisations between them
+    -- matches the eager result: bit-equal where the op is deterministic,
+    else within 1e-5."""
+    import torch
+
+    rng = np.random.default_rng(M + N + K)
+    w = bf16_bits(rng.normal(0, 0.02, size=(N, K)))
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    bias = bf16_bits(rng.normal(0, 0.02, size=N)) if has_bias else None
+    dev = torch.device("cuda", 0)
+    dw = torch.from_numpy(w.view(np.int16)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    bptr = None if bias is None else torch.from_numpy(bias.view(np.int16)).to(dev)
+    bp = None if bptr is None else bptr.data_ptr()
+    stream = torch.cuda.Stream(device=dev)
+    eager = []
+    for _ in range(2):
+        dy = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+        R.linear_noalloc(dw.data_ptr(), dx.data_ptr(), dy.data_ptr(), M, N, K, bp, stream=stream.cuda_stream)
+        stream.synchronize()
+        eager.append(dy.cpu().numpy())
+    deterministic = np.array_equal(eager[0].view(np.uint32), eager[1].view(np.uint32))
+    assert rel_err(eager[0][0], oracle_mod.linear(w, x[0], bias)) <= 2e-3
+    yg = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    g = torch.cuda.CUDAGraph()
+    print(f"noalloc graph capture M={M} N={N} K={K}", flush=True)
+    with torch.cuda.graph(g, stream=stream):
+        R.linear_noalloc(dw.data_ptr(), dx.data_ptr(), yg.data_ptr(), M, N, K, bp, stream=stream.cuda_stream)
+    # Between replays: an eager call that uses the same static scratch (a
+    # skinny K-split call: its counters and partials).
+    other = torch.zeros((16, 512), dtype=torch.float32, device=dev)
+    ow = torch.zeros((512, 2048), dtype=torch.int16, device=dev)
+    ox = torch.ones((16, 2048), dtype=torch.float32, device=dev)
+    for rep in range(3):
+        yg.fill_(float("nan"))
+        with torch.cuda.stream(stream):
+            g.replay()
+        stream.synchronize()
+        got = yg.cpu().numpy()
+        if deterministic:
+            assert np.array_equal(got.view(np.uint32), eager[0].view(np.uint32)), f"replay {rep}: not bit-equal"
+        else:
+            e = rel_err(got, eager[0])
+            assert e <= 1e-5, f"replay {rep}: rel err {e:.2e}"
+        # eager work between replays on the same scratch
+        R.linear_noalloc(ow.data_ptr(), ox.data_ptr(), other.data_ptr(), 16, 512, 2048)
+        torch.cuda.synchronize()
+        assert bool((other == 0).all())
+    del g

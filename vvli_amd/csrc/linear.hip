@@ -213,16 +213,23 @@ __global__ __launch_bounds__(kSkinnyThreads) void linear_skinny_kernel(const uin
         }
     }
     if (KS == 1) return;
-    // Every thread waits for its partial stores to complete before the block
-    // counts itself in (no L2 write-back fence: the stores write through);
-    // the last block to count in reads the partials with agent-scope loads,
-    // which see the other XCDs' stores.
+    // Release side, by hand: every thread waits for its partial stores to
+    // complete (s_waitcnt vmcnt(0): the agent-scope stores are issued with
+    // sc1, which on gfx950 writes them through the XCD's L2 to the memory
+    // side, so a completed store is visible to every XCD) before the block
+    // counts itself in. A release fence would add an L2 write-back
+    // (buffer_wbl2) of the whole XCD's dirty lines, which nothing here needs:
+    // measured, release/acquire fences made the op 5-7x slower.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == KS - 1;
     __syncthreads();
     if (!s_last) return;
+    // Acquire side: the last block invalidates its L1 (buffer_inv sc1, no
+    // write-back) before reading the partials, which it also reads with
+    // agent-scope (sc1) loads.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (uint32_t idx = threadIdx.x; idx < (uint32_t)(RM * RN); idx += kSkinnyThreads) {
         const uint32_t m = idx / RN, n = n0 + idx % RN;
         if (m < M && n < N) {
