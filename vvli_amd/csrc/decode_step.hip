@@ -319,6 +319,7 @@ __device__ __forceinline__ bool mk_prefetch(const MkGemv& g, int mode, const MkW
     return true;
 }
 
+
 // Where a residual-mode phase takes its residual rows: tagged words of an
 // earlier phase, or (layer 0) the bf16 embedding row of the token.
 struct MkResid {
@@ -557,6 +558,42 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
         MkTile tc = tA, tn = tA;  // tiles of the item being consumed / in flight
         float acc0 = 0.f, acc1 = 0.f;
         float tot0 = 0.f;  // MOE down: router-weighted sum over the slots
+        // The tile of the consumed item (tc) is complete: reduce, epilogue,
+        // park the result in its lane, write a full batch.
+        auto end_tile = [&]() {
+            float v0, v1 = 0.f;
+            if (g.split) {
+                v0 = wave_sum(acc0 + acc1);  // the row's two halves
+            } else {
+                v0 = wave_sum(acc0);
+                v1 = wave_sum(acc1);
+            }
+            acc0 = acc1 = 0.f;
+            if (mode == kGemvGateUp) {
+                v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
+            } else if (mode == kGemvLogits && lane == 0) {
+                // llm.argmax (src/llm.zig:778-789): a NaN logit 0 makes the
+                // result 0 (every comparison with it fails): top key, index 0.
+                if (tc.valid[0]) {
+                    const unsigned long long k0 =
+                        (tc.row[0] == 0 && v0 != v0) ? ~0ull : argmax_key(v0, tc.row[0]);
+                    best = k0 > best ? k0 : best;
+                }
+                if (tc.valid[1]) {
+                    const unsigned long long k1 = argmax_key(v1, tc.row[1]);
+                    best = k1 > best ? k1 : best;
+                }
+            }
+            if ((uint32_t)lane == pending) {
+                oa = v0;
+                ob = v1;
+            }
+            if (++pending == kWave) {
+                flush();
+                base += kWave;
+                open_batch();
+            }
+        };
         for (uint32_t it = 0; it < n_items; ++it) {
             const uint32_t chunk = it % nchunk;
             const bool more = it + 1 < n_items;
@@ -600,38 +637,7 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
                 }
             }
             if (chunk == nchunk - 1) {
-                float v0, v1 = 0.f;
-                if (g.split) {
-                    v0 = wave_sum(acc0 + acc1);  // the row's two halves
-                } else {
-                    v0 = wave_sum(acc0);
-                    v1 = wave_sum(acc1);
-                }
-                acc0 = acc1 = 0.f;
-                if (mode == kGemvGateUp) {
-                    v0 = (v0 / (1.0f + expf(-v0))) * v1;  // siluMulInto, src/llm.zig:1382-1387
-                } else if (mode == kGemvLogits && lane == 0) {
-                    // llm.argmax (src/llm.zig:778-789): a NaN logit 0 makes the
-                    // result 0 (every comparison with it fails): top key, index 0.
-                    if (tc.valid[0]) {
-                        const unsigned long long k0 =
-                            (tc.row[0] == 0 && v0 != v0) ? ~0ull : argmax_key(v0, tc.row[0]);
-                        best = k0 > best ? k0 : best;
-                    }
-                    if (tc.valid[1]) {
-                        const unsigned long long k1 = argmax_key(v1, tc.row[1]);
-                        best = k1 > best ? k1 : best;
-                    }
-                }
-                if ((uint32_t)lane == pending) {
-                    oa = v0;
-                    ob = v1;
-                }
-                if (++pending == kWave) {
-                    flush();
-                    base += kWave;
-                    open_batch();
-                }
+                end_tile();
                 tc = tn;
             }
         }
@@ -676,28 +682,32 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
     } else {
         const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * 8);
         const uint32_t n2 = n / 2;
-        for (uint32_t i0 = tid; i0 < n2; i0 += B * kMkThreads) {
-            tword a[B], b[B];
-            uint32_t nv[B];
+        // A batch: B word pairs per thread issued together (pairs past n read
+        // as zeros), with the norm weights of the same elements.
+        auto load_batch = [&](uint32_t i0, tword (&a)[B], tword (&b)[B], uint32_t (&nv)[B]) {
 #pragma unroll
             for (int k = 0; k < B; ++k) {
                 const uint32_t i = i0 + k * kMkThreads;
                 ld_coh_tw2(r, i * 16, a[k], b[k]);
                 nv[k] = (norm_w && i < n2) ? *as_global(reinterpret_cast<const uint32_t*>(norm_w + 2 * i)) : 0u;
             }
-            // The batch is polled as a whole: a retry reloads every pair that
-            // is not complete, so it ends one round trip after its last word
-            // lands (word-by-word polls would add a round trip per late word).
-            for (uint32_t spins = 0;; ) {
-                bool done = true;
+        };
+        auto complete = [&](uint32_t i0, const tword (&a)[B], const tword (&b)[B]) {
+            bool done = true;
 #pragma unroll
-                for (int k = 0; k < B; ++k)
-                    if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
-                if (tmark && tid == 0) {
-                    if (spins == 0) tmark[1] = __builtin_amdgcn_s_memrealtime();
-                    tmark[2] = spins;
-                }
-                if (done) break;
+            for (int k = 0; k < B; ++k)
+                if (i0 + k * kMkThreads < n2 && (tw_tag(a[k]) != tag || tw_tag(b[k]) != tag)) done = false;
+            return done;
+        };
+        // The batch is polled as a whole: a retry reloads every pair that is
+        // not complete, so it ends one round trip after its last word lands
+        // (word-by-word polls would add a round trip per late word). The
+        // first attempt is straight-line code (no retry loop's back edge
+        // merges into its waits). Then the values go to LDS.
+        auto finish_batch = [&](uint32_t i0, tword (&a)[B], tword (&b)[B], const uint32_t (&nv)[B]) {
+            bool done = complete(i0, a, b);
+            if (tmark && tid == 0) tmark[1] = __builtin_amdgcn_s_memrealtime();
+            for (uint32_t spins = 0; !done;) {
                 if (++spins > kSpinLimit) {
                     st_a(err, kDecodeErrTimeout);
                     ok = false;
@@ -709,9 +719,11 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
                 }
                 __builtin_amdgcn_s_sleep(1);
                 // Every pair is reloaded (a complete word stays as it is until
-                // its reader is done; pairs past n read as zeros).
+                // its reader is done).
 #pragma unroll
                 for (int k = 0; k < B; ++k) ld_coh_tw2(r, (i0 + k * kMkThreads) * 16, a[k], b[k]);
+                done = complete(i0, a, b);
+                if (tmark && tid == 0) tmark[2] = spins;
             }
 #pragma unroll
             for (int k = 0; k < B; ++k) {
@@ -726,6 +738,12 @@ __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src
                     ss = fmaf(v1, v1, ss);
                 }
             }
+        };
+        for (uint32_t i0 = tid; i0 < n2; i0 += B * kMkThreads) {
+            tword a[B], b[B];
+            uint32_t nv[B];
+            load_batch(i0, a, b, nv);
+            finish_batch(i0, a, b, nv);
         }
     }
     arrived();
