@@ -114,6 +114,9 @@ def lib() -> ctypes.CDLL:
             "orc_moe_layout": (c_size_t, [P(OrcMoeConfig), c_void_p, P(c_size_t), P(c_size_t), P(c_size_t)]),
             "orc_moe_rmsnorm": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_size_t, c_float]),
             "orc_moe_route": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+            "orc_moe_experts": (c_int, [c_void_p, c_void_p, c_uint32, c_size_t, c_size_t, c_void_p, c_size_t,
+                                        c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_int, c_int, c_int]),
+            "orc_matmul_blocked": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_int]),
             "orc_moe_runner_create": (c_int, [P(OrcMoeConfig), c_void_p, c_size_t, c_uint32, c_int, c_int,
                                               P(c_void_p)]),
             "orc_moe_runner_destroy": (None, [c_void_p]),
@@ -394,6 +397,30 @@ def moe_route(logits: np.ndarray, top_k: int):
     w = np.zeros(top_k, dtype=np.float32)
     lib().orc_moe_route(_p(lg), lg.size, top_k, _p(idx), _p(w))
     return idx, w
+
+
+def moe_experts(blob: np.ndarray, kind: int, gate_up: int, down: int, x: np.ndarray, hidden: int, inter: int,
+                experts: int, idx: np.ndarray, weights: np.ndarray, matmul: bool, lanes: int = 16,
+                threads: int = 1) -> np.ndarray:
+    """The routed experts' weighted sum of one layer (orc_moe_experts): each
+    product as linearInto (matmul False, the MoE runner's path) or as
+    tensor.zig's matmul (matmul True)."""
+    out = np.zeros(hidden, dtype=np.float32)
+    xx = np.ascontiguousarray(x, dtype=np.float32)
+    ii = np.ascontiguousarray(idx, dtype=np.uint32)
+    ww = np.ascontiguousarray(weights, dtype=np.float32)
+    _check(lib().orc_moe_experts(_p(out), _p(blob), kind, gate_up, down, _p(xx), hidden, inter, experts, ii.size,
+                                 _p(ii), _p(ww), lanes, threads, 1 if matmul else 0))
+    return out
+
+
+def matmul_blocked(a: np.ndarray, b: np.ndarray, lanes: int = 16) -> np.ndarray:
+    """src/tensor.zig matmulBlocked: a [m][k] . b [k][n], f32."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.zeros((a.shape[0], b.shape[1]), dtype=np.float32)
+    lib().orc_matmul_blocked(_p(out), _p(a), a.shape[0], a.shape[1], _p(b), b.shape[1], lanes)
+    return out
 
 
 class OracleMoeRunner:

@@ -260,6 +260,43 @@ void orc_linear(float* out, const void* w, uint32_t weight_kind, size_t rows, si
     linear_range(out, w, weight_kind, cols, x, bias, 0, rows, lanes);
 }
 
+void orc_matmul_blocked(float* out, const float* a, size_t m, size_t k, const float* b, size_t n, int lanes) {
+    /* src/tensor.zig:683-733; matmul_col_unroll = 4 (src/tensor.zig:14). A
+     * Vec of `lanes` f32 is an array here: acc[l] = acc[l] + av * b[..+l]. */
+    const size_t vec = (size_t)lanes, panel = vec * 4;
+    float acc[4][64];
+    for (size_t row = 0; row < m; ++row) {
+        const float* ar = a + row * k;
+        float* orow = out + row * n;
+        size_t col = 0;
+        for (; col + panel <= n; col += panel) {
+            for (int v = 0; v < 4; ++v)
+                for (size_t l = 0; l < vec; ++l) acc[v][l] = 0.0f;
+            for (size_t p = 0; p < k; ++p) {
+                const float av = ar[p];
+                const float* bb = b + p * n + col;
+                for (int v = 0; v < 4; ++v)
+                    for (size_t l = 0; l < vec; ++l) acc[v][l] = acc[v][l] + av * bb[v * vec + l];
+            }
+            for (int v = 0; v < 4; ++v)
+                for (size_t l = 0; l < vec; ++l) orow[col + v * vec + l] = acc[v][l];
+        }
+        for (; col + vec <= n; col += vec) {
+            for (size_t l = 0; l < vec; ++l) acc[0][l] = 0.0f;
+            for (size_t p = 0; p < k; ++p) {
+                const float av = ar[p];
+                for (size_t l = 0; l < vec; ++l) acc[0][l] = acc[0][l] + av * b[p * n + col + l];
+            }
+            for (size_t l = 0; l < vec; ++l) orow[col + l] = acc[0][l];
+        }
+        for (; col < n; ++col) {
+            float sum = 0.0f;
+            for (size_t p = 0; p < k; ++p) sum = fmaf(ar[p], b[p * n + col], sum);
+            orow[col] = sum;
+        }
+    }
+}
+
 typedef struct linear_job {
     float* out;
     const void* w;

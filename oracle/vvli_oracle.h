@@ -92,6 +92,10 @@ void orc_linear(float* out, const void* w, uint32_t weight_kind, size_t rows, si
 int orc_linear_threaded(float* out, const void* w, uint32_t weight_kind, size_t rows, size_t cols,
                         const float* x, const void* bias, int lanes, int threads, int min_rows);
 void orc_rmsnorm(float* out, const float* x, const void* w, uint32_t weight_kind, size_t n, float eps, int lanes);
+/* src/tensor.zig:683-733 matmulBlocked (f32): out[m][n] = a[m][k] . b[k][n],
+ * columns in panels of 4 vectors of `lanes`, each accumulated over p in order
+ * (unfused multiply, then add), then whole vectors, then a scalar @mulAdd tail. */
+void orc_matmul_blocked(float* out, const float* a, size_t m, size_t k, const float* b, size_t n, int lanes);
 /* inv_freq may be NULL: then the reference formula 1/pow(theta, d/hd) is used. */
 void orc_rope(float* values, size_t heads, size_t head_dim, size_t pos, float theta, uint32_t layout,
               const float* inv_freq);
@@ -159,6 +163,15 @@ size_t orc_moe_layout(const orc_moe_config* c, orc_moe_layer_offsets* layers, si
                       size_t* lm_head);
 void orc_moe_rmsnorm(float* out, const float* x, const void* w, uint32_t kind, size_t n, float eps);
 void orc_moe_route(const float* logits, size_t n, size_t top_k, uint32_t* idx, float* weights);
+/* The routed experts of one layer: moe[h] = sum over the selected experts in
+ * ascending expert index of weight * W_down,e . (silu(W_g,e . x) * (W_u,e . x)),
+ * x = the post-attention norm (hidden floats). gate_up / down: element offsets
+ * of the layer's expert matrices in the blob. matmul = 0: each product as
+ * linearInto (the runner's path); 1: as src/tensor.zig's matmul of the row x
+ * with the expert matrix transposed to f32 [K][N] (matmulBlocked). */
+int orc_moe_experts(float* moe, const void* blob, uint32_t kind, size_t gate_up, size_t down, const float* x,
+                    size_t hidden, size_t inter, size_t experts, size_t top_k, const uint32_t* idx,
+                    const float* weights, int lanes, int threads, int matmul);
 typedef struct orc_moe_runner orc_moe_runner;
 int orc_moe_runner_create(const orc_moe_config* c, const void* blob, size_t blob_elems, uint32_t max_seq_len,
                           int threads, int lanes, orc_moe_runner** out);

@@ -235,22 +235,69 @@ static int m_forward_layer(orc_moe_runner* r, uint32_t l, uint32_t pos) {
     orc_moe_rmsnorm(r->norm, r->x, m_w(r, o->post_norm), kind, h, c->rms_eps);
     if ((rc = m_linear(r, r->router, o->router, r->c.experts, h, r->norm, (size_t)-1))) return rc;
     orc_moe_route(r->router, r->c.experts, r->c.top_k, r->idx, r->rw);
-    memset(r->moe, 0, h * sizeof(float));
-    /* ascending expert index, the order of the reference implementation's index_add */
-    for (uint32_t e = 0; e < r->c.experts; ++e) {
-        int slot = -1;
-        for (uint32_t k = 0; k < r->c.top_k; ++k)
-            if (r->idx[k] == e) slot = (int)k;
-        if (slot < 0) continue;
-        const size_t gu_off = o->gate_up + (size_t)e * 2 * inter * h;
-        if ((rc = m_linear(r, r->gu, gu_off, 2 * inter, h, r->norm, (size_t)-1))) return rc;
-        orc_silu_mul(r->act, r->gu, r->gu + inter, inter);
-        if ((rc = m_linear(r, r->eout, o->down + (size_t)e * h * inter, h, inter, r->act, (size_t)-1))) return rc;
-        const float w = r->rw[slot];
-        for (size_t i = 0; i < h; ++i) r->moe[i] = r->moe[i] + r->eout[i] * w;
-    }
+    if ((rc = orc_moe_experts(r->moe, r->blob, kind, o->gate_up, o->down, r->norm, h, inter, r->c.experts,
+                              r->c.top_k, r->idx, r->rw, r->lanes, r->threads, 0)))
+        return rc;
     orc_add(r->x, r->residual, r->moe, h);
     return ORC_OK;
+}
+
+/* W rows [rows][cols] of the blob (f32 or bf16) as the f32 [cols][rows]
+ * matrix B of tensor.zig's out = x . B. */
+static float* m_transposed_f32(const void* blob, uint32_t kind, size_t off, size_t rows, size_t cols) {
+    float* t = (float*)malloc(rows * cols * sizeof(float));
+    if (!t) return NULL;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) t[c * rows + r] = m_weight_at(blob, kind, off + r * cols + c);
+    return t;
+}
+
+int orc_moe_experts(float* moe, const void* blob, uint32_t kind, size_t gate_up, size_t down, const float* x,
+                    size_t hidden, size_t inter, size_t experts, size_t top_k, const uint32_t* idx,
+                    const float* weights, int lanes, int threads, int matmul) {
+    const size_t h = hidden;
+    float* gu = m_floats(2 * inter);
+    float* act = m_floats(inter);
+    float* eout = m_floats(h);
+    int rc = (gu && act && eout) ? ORC_OK : ORC_OUT_OF_MEMORY;
+    memset(moe, 0, h * sizeof(float));
+    /* ascending expert index, the order of the reference implementation's index_add */
+    for (size_t e = 0; e < experts && rc == ORC_OK; ++e) {
+        int slot = -1;
+        for (size_t k = 0; k < top_k; ++k)
+            if (idx[k] == e) slot = (int)k;
+        if (slot < 0) continue;
+        const size_t gu_off = gate_up + e * 2 * inter * h, d_off = down + e * h * inter;
+        if (!matmul) {
+            const void* wgu = kind == 1 ? (const void*)((const uint16_t*)blob + gu_off)
+                                        : (const void*)((const float*)blob + gu_off);
+            const void* wd = kind == 1 ? (const void*)((const uint16_t*)blob + d_off)
+                                       : (const void*)((const float*)blob + d_off);
+            if ((rc = orc_linear_threaded(gu, wgu, kind, 2 * inter, h, x, NULL, lanes, threads, 64))) break;
+            orc_silu_mul(act, gu, gu + inter, inter);
+            if ((rc = orc_linear_threaded(eout, wd, kind, h, inter, act, NULL, lanes, threads, 64))) break;
+        } else {  /* src/tensor.zig:297-325 matmul -> matmulBlocked, one row of activations */
+            float* bgu = m_transposed_f32(blob, kind, gu_off, 2 * inter, h);
+            float* bd = m_transposed_f32(blob, kind, d_off, h, inter);
+            if (!bgu || !bd) {
+                free(bgu);
+                free(bd);
+                rc = ORC_OUT_OF_MEMORY;
+                break;
+            }
+            orc_matmul_blocked(gu, x, 1, h, bgu, 2 * inter, lanes);
+            orc_silu_mul(act, gu, gu + inter, inter);
+            orc_matmul_blocked(eout, act, 1, inter, bd, h, lanes);
+            free(bgu);
+            free(bd);
+        }
+        const float w = weights[slot];
+        for (size_t i = 0; i < h; ++i) moe[i] = moe[i] + eout[i] * w;
+    }
+    free(gu);
+    free(act);
+    free(eout);
+    return rc;
 }
 
 int orc_moe_forward_token(orc_moe_runner* r, uint32_t token, uint32_t pos, float* logits_out, float* hidden_out,

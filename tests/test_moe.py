@@ -159,3 +159,74 @@ def test_moe_slice_offsets_match_oracle(oracle_mod):
             for k, v in lay["layers"][l].items():
                 if v is not None:
                     assert R.moe_slice_offset(cfg, l, k) == v, (l, k)
+
+
+def test_tensor_matmul_restatement(oracle_mod):
+    """src/tensor.zig matmulBlocked restated: the reference's known answer
+    (src/tensor.zig:793-812) and, at the shape of its "no-scratch and
+    transposed scratch paths agree" test (:814-846: m 3, k lanes * 4 + 3,
+    n lanes * 4 + 5, the panel, vector and scalar column paths), agreement
+    with an f64 product within that test's 1e-5, for 4-, 8- and 16-lane hosts."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    assert np.array_equal(oracle_mod.matmul_blocked(a, b), np.array([[58, 64], [139, 154]], np.float32))
+    for lanes in (4, 8, 16):
+        m, k, n = 3, lanes * 4 + 3, lanes * 4 + 5
+        a = ((np.arange(m * k) % 11) - 5).astype(np.float32).reshape(m, k) * np.float32(0.125)
+        b = (((np.arange(k * n) * 3) % 13) - 6).astype(np.float32).reshape(k, n) * np.float32(0.0625)
+        got = oracle_mod.matmul_blocked(a, b, lanes)
+        ref = a.astype(np.float64) @ b.astype(np.float64)
+        assert np.max(np.abs(got - ref)) <= 1e-5, f"lanes {lanes}"
+        # A planted mistake (one column of b dropped from a panel) must fail.
+        b2 = b.copy()
+        b2[:, 1] = 0
+        assert np.max(np.abs(oracle_mod.matmul_blocked(a, b2, lanes) - ref)) > 1e-3
+
+
+@pytest.mark.parametrize("shape", ["fixture", "olmoe-1b-7b-experts"])
+def test_moe_experts_tensor_matmul_composition(shape, oracle_mod):
+    """The MoE oracle's routed-expert sum (each expert's gate/up and down as
+    linearInto, the runner's path) against the same composition with every
+    product as the reference's tensor.zig matmul (src/tensor.zig:297-325,
+    683-733: the row x times the expert matrix transposed to f32): both
+    within 1e-5 of an f64 evaluation and of each other -- the two differ
+    only in the f32 summation order of the dot products. Shapes: the HF
+    OLMoE fixture's layer 0 (hidden 64, 8 experts of 32, top 2) and an
+    OLMoE-1B-7B-shaped expert layer (hidden 2048, experts of 1024, top 8 --
+    the per-token expert work of OLMoE-1B-7B -- out of 16 experts instead of
+    64, to keep the blob small)."""
+    if shape == "fixture":
+        z, cfg = fixture()
+        blob = blob_from_hf(oracle_mod, cfg, z)
+    else:
+        cfg = C.olmoe_1b_7b()
+        cfg = C.Config(**{**cfg.__dict__, "num_hidden_layers": 1, "vocab_size": 64, "num_experts": 16})
+        blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=5, stddev=0.02)
+    lay = oracle_mod.moe_layout(cfg, C.WEIGHT_BF16)
+    L = lay["layers"][0]
+    H, I, E, K = cfg.hidden_size, cfg.intermediate_size, cfg.num_experts, cfg.num_experts_per_token
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(H).astype(np.float32)
+    idx, w = oracle_mod.moe_route(rng.standard_normal(E).astype(np.float32), K)
+    lin = oracle_mod.moe_experts(blob, C.WEIGHT_BF16, L["gate_up"], L["down"], x, H, I, E, idx, w, matmul=False)
+    mm = oracle_mod.moe_experts(blob, C.WEIGHT_BF16, L["gate_up"], L["down"], x, H, I, E, idx, w, matmul=True)
+    # f64 evaluation of the same composition.
+    def f64(off, n):  # bf16 bits of the blob slice -> f64
+        return (blob[off:off + n].astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float64)
+
+    ref = np.zeros(H)
+    for e in sorted(int(i) for i in idx):
+        gu = f64(L["gate_up"] + e * 2 * I * H, 2 * I * H).reshape(2 * I, H) @ x
+        act = gu[:I] / (1 + np.exp(-gu[:I])) * gu[I:]
+        out = f64(L["down"] + e * H * I, H * I).reshape(H, I) @ act
+        ref += out * float(w[list(idx).index(e)])
+    assert rel_err(lin, ref) <= 1e-5 and rel_err(mm, ref) <= 1e-5
+    assert rel_err(lin, mm) <= 1e-5
+    # A planted mistake (gate and up swapped in one expert) must fail.
+    e0 = int(idx[0])
+    g0 = L["gate_up"] + e0 * 2 * I * H
+    gate = blob[g0:g0 + I * H].copy()
+    blob[g0:g0 + I * H] = blob[g0 + I * H:g0 + 2 * I * H]
+    blob[g0 + I * H:g0 + 2 * I * H] = gate
+    mm_bad = oracle_mod.moe_experts(blob, C.WEIGHT_BF16, L["gate_up"], L["down"], x, H, I, E, idx, w, matmul=True)
+    assert rel_err(mm_bad, ref) > 1e-2
