@@ -484,7 +484,9 @@ def prefill_main(args, cfg, blob) -> int:
         return 2 * n * proj + L * 4 * cfg.num_attention_heads * cfg.head_dim() * n * (n + 1) // 2
 
     sweep = {}
-    for n in sorted({128, 512, 2048, min(4096, args.ctx), args.prompt}):
+    lengths = {int(v) for v in args.prefill_sweep.split(",")} if args.prefill_sweep else \
+        {128, 512, 2048, min(4096, args.ctx)}
+    for n in sorted(lengths | {args.prompt}):
         if n > args.ctx:
             continue
         best = 1e9
@@ -596,6 +598,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv-sweep", action="store_true", help="decode mode: skip the M = 1 op sweep")
     ap.add_argument("--linear-m", default="1,4,16,128,512", help="linear mode: comma-separated M values")
+    ap.add_argument("--prefill-sweep", default=None,
+                    help="prefill mode: comma-separated prompt lengths (default 128,512,2048,4096)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed run, copy a 256 MiB device buffer (HBM-counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill", default="batched", choices=["batched", "loop"],

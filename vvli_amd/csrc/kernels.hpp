@@ -280,7 +280,18 @@ struct GemmArgs {
     const uint4* tiles = nullptr;
     uint32_t max_tiles = 0;
     size_t w_expert = 0;
+    // Plain / Resid: when set and the launch splits K (gemm_splits > 1), each
+    // split stores its partial sums to part[split][M][N] (f32, at most
+    // gemm_part_elems(); split 0 includes the bias) instead of adding them
+    // atomically into out, which is then left for the consumer: Resid adds
+    // nothing to out, Plain does not zero it. The consumer sums the splits in
+    // order (deterministic).
+    float* part = nullptr;
 };
+// K splits a launch of launch_gemm_bf16 will use (1: no split), and the
+// capacity of the partial sums buffer any launch needs (elements).
+uint32_t gemm_splits(int mode, const GemmArgs& g);
+size_t gemm_part_elems();
 __host__ __device__ inline uint32_t gemm_kp(uint32_t K) { return (K + 31) / 32 * 32; }
 size_t gemm_split_elems(uint32_t M, uint32_t K);
 // Most rows for which a GateUp GEMM of N outputs may split K (gu_acc of
@@ -295,7 +306,10 @@ uint32_t grouped_gemm_max_tiles(uint32_t M, uint32_t E);
 // no bias): each tile of g.tiles multiplies its rows by its expert's W.
 hipError_t launch_gemm_grouped(int mode, const GemmArgs& g, hipStream_t s);
 
-hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s);
+// part / splits: the K-split partial sums of the Resid GEMM that produced x
+// ([splits][rows][n]; nullptr or splits <= 1: x is complete), added into x first.
+hipError_t launch_row_rms(float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s,
+                          const float* part = nullptr, uint32_t splits = 0);
 hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
                                 float* x, hipStream_t s);
 
@@ -311,6 +325,10 @@ struct PrefillRopeArgs {
     const uint16_t* q_norm = nullptr;
     const uint16_t* k_norm = nullptr;
     float norm_eps = 0.f;
+    // The q|k|v GEMM's K-split partial sums ([splits][rows][ld]) when it split
+    // K into a partial-sum buffer: summed into qkv first.
+    const float* part = nullptr;
+    uint32_t splits = 0;
 };
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s);
 

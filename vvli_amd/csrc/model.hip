@@ -97,6 +97,7 @@ struct vvli_gpu_model {
     float* pf_ahl = nullptr;    // GEMM activations split hi | lo (gemm_split_elems bf16)
     float* pf_ahl2 = nullptr;   // split planes written by attention (o_proj's A) and SwiGLU (down's A)
     float* pf_gu = nullptr;     // gate/up split-K sums for short chunks ([pf_gu_rows][2I])
+    float* pf_part = nullptr;   // K-split partial sums of q|k|v, o_proj and down (gemm_part_elems)
     uint32_t pf_gu_rows = 0;
     void* pf_kvp = nullptr;     // packed K/V tiles of one layer for the attention kernel
     size_t pf_kvp_bytes = 0;
@@ -604,6 +605,11 @@ int ensure_prefill_buffers(vvli_gpu_model* m) {
     }
     m->pf_kvp_bytes = kvp;
     m->pf_rows = static_cast<uint32_t>(rows);
+    e = hipMalloc(reinterpret_cast<void**>(&m->pf_part), gemm_part_elems() * sizeof(float));
+    if (e != hipSuccess) {
+        m->pf_part = nullptr;  // split GEMMs then add their partial sums atomically
+        (void)hipGetLastError();
+    }
     if (m->moe) return VVLI_OK;
     const uint32_t gu_rows = std::min<uint32_t>(m->pf_rows, gemm_gateup_split_rows(c.inter));
     if (gu_rows > 0 && hipMalloc(reinterpret_cast<void**>(&m->pf_gu), static_cast<size_t>(gu_rows) * 2 * I *
@@ -642,12 +648,13 @@ int ensure_moe_prefill_buffers(vvli_gpu_model* m) {
 // Mixture-of-experts half of a prefill layer for the chunk's P rows: route
 // every row, group the (row, slot) pairs by expert, run the experts' gate/up
 // and down as grouped GEMMs over their rows, combine into pf_x.
-int enqueue_prefill_moe_ffn(vvli_gpu_model* m, uint32_t l, uint32_t P, hipStream_t s) {
+int enqueue_prefill_moe_ffn(vvli_gpu_model* m, uint32_t l, uint32_t P, hipStream_t s, uint32_t o_splits) {
     const vvli_gpu_config& c = m->cfg;
     const MoeLayerSlices& L = m->moe_layout.layers[l];
     const uint32_t H = c.hidden, I = c.inter, E = c.num_experts, K = c.experts_per_tok, n = P * K;
     auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
-    LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+    // (completes x with o_proj's K-split partial sums first, when it split)
+    LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, o_splits));
     MoeRouteRowsArgs ra;
     ra.w = w16(L.router), ra.x = m->pf_x, ra.row_scale = m->pf_scale, ra.norm_w = w16(L.post_norm);
     ra.rows = P, ra.H = H, ra.E = E, ra.top_k = K, ra.idx = m->pf_eidx, ra.weight = m->pf_ew;
@@ -689,9 +696,22 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
     const uint32_t H = c.hidden, kv = kv_dim(c), I = c.inter, hd = head_dim(c), ldqkv = H + 2 * kv;
     const uint16_t* embed = static_cast<const uint16_t*>(wslice(m, m->layout.embed));
     auto w16 = [&](size_t off) { return static_cast<const uint16_t*>(wslice(m, off)); };
+    // K-split GEMMs leave partial sums in pf_part for their consumer (the
+    // next row RMS pass, or the RoPE pass for q|k|v), which adds them in split
+    // order: pend = the splits of the Resid GEMM whose sums x still lacks
+    // (0: the GEMM did not leave any).
+    // (Up to 8 splits: with more, the partial sums cost more traffic than the
+    // atomic adds they replace -- measured at 128 rows, where down splits 32
+    // ways: 3.11 ms with atomics, 3.30 ms with partial sums.)
+    auto use_part = [&](int mode, GemmArgs& g) {
+        const uint32_t sp = m->pf_part ? gemm_splits(mode, g) : 1u;
+        g.part = (sp > 1 && sp <= 8) ? m->pf_part : nullptr;
+        return g.part ? sp : 0u;
+    };
     for (uint32_t c0 = 0; c0 < n; c0 += m->pf_rows) {
         const uint32_t P = std::min(m->pf_rows, n - c0);
         const uint32_t pos0 = start + c0;
+        uint32_t pend = 0;
         LAUNCH(launch_prefill_embed(embed, m->prompt + pos0, P, H, m->pf_x, s));
         for (uint32_t l = 0; l < c.layers; ++l) {
             AttnSlices L;
@@ -705,7 +725,8 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             float* kc = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
             float* vc = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
             // input RMSNorm fused into the q|k|v GEMM (+ bias)
-            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
+            pend = 0;
             GemmArgs gq;
             gq.a = m->pf_x, gq.lda = H, gq.row_scale = m->pf_scale, gq.norm_w = w16(L.input_norm);
             gq.w[0] = w16(L.q), gq.w[1] = w16(L.k), gq.w[2] = w16(L.v);
@@ -713,10 +734,12 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gq.seg_end[0] = H, gq.seg_end[1] = H + kv, gq.seg_end[2] = H + 2 * kv;
             gq.out = m->pf_qkv, gq.ldo = ldqkv, gq.M = P, gq.N = ldqkv, gq.K = H;
             gq.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl);
+            const uint32_t q_splits = use_part(kGemmPlain, gq);
             LAUNCH(launch_gemm_bf16(kGemmPlain, gq, s));
             // RoPE on q and k, k/v appended at positions pos0 ..
             PrefillRopeArgs ra{m->pf_qkv, ldqkv, P, pos0, c.heads, c.kv_heads, hd, kv, c.rope_layout,
                                m->rope_cs, kc, vc};
+            if (q_splits > 1) ra.part = m->pf_part, ra.splits = q_splits;
             if (L.q_norm != kNone) ra.q_norm = w16(L.q_norm), ra.k_norm = w16(L.k_norm), ra.norm_eps = c.rms_eps;
             LAUNCH(launch_prefill_rope_kv(ra, s));
             PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
@@ -733,14 +756,17 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             go.out = m->pf_x, go.ldo = H, go.M = P, go.N = H, go.K = H;
             go.a_hl = reinterpret_cast<uint16_t*>(fused_o ? m->pf_ahl2 : m->pf_ahl);
             if (fused_o) go.a_ready = true, go.a_plane = m->pf_rows * gemm_kp(H);
+            pend = use_part(kGemmResid, go);
             LAUNCH(launch_gemm_bf16(kGemmResid, go, s));
             if (m->moe) {
-                if ((rc = enqueue_prefill_moe_ffn(m, l, P, s))) return rc;
+                if ((rc = enqueue_prefill_moe_ffn(m, l, P, s, pend))) return rc;
+                pend = 0;
                 continue;
             }
             const LayerSlices& D = m->layout.layers[l];
             // post-attention RMSNorm fused into gate/up + SwiGLU
-            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s));
+            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
+            pend = 0;
             GemmArgs gu;
             gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(D.post_norm);
             gu.w[0] = w16(D.gate), gu.w_up = w16(D.up);
@@ -758,8 +784,11 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             gd.out = m->pf_x, gd.ldo = H, gd.M = P, gd.N = H, gd.K = I;
             gd.a_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2);
             gd.a_ready = true, gd.a_plane = m->pf_rows * gemm_kp(I);
+            pend = use_part(kGemmResid, gd);
             LAUNCH(launch_gemm_bf16(kGemmResid, gd, s));
         }
+        if (pend > 1)  // the last down projection's partial sums (the scale computed with them is unused)
+            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
         if (c0 + P == n)
             HIP_TRY(hipMemcpyAsync(m->x, m->pf_x + static_cast<size_t>(P - 1) * H, H * sizeof(float),
                                    hipMemcpyDeviceToDevice, s));
@@ -777,7 +806,7 @@ void free_model(vvli_gpu_model* m) {
     void* bufs[] = {m->blob, m->kcache, m->vcache, m->rope_cs, m->x, m->qkv, m->attn, m->ff, m->logits,
                     m->hidden, m->part, m->counters, m->keys, m->state, m->prompt, m->out_tokens,
                     m->mk_layers, m->mk_gemv, m->mk_tw, m->mk_err, m->pf_x, m->pf_qkv, m->pf_attn,
-                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_kvp, m->pf_eidx, m->pf_ew, m->pf_grows, m->pf_ppos, m->pf_tiles, m->pf_ehl, m->pf_eact,
+                    m->pf_scale, m->pf_ahl, m->pf_ahl2, m->pf_gu, m->pf_part, m->pf_kvp, m->pf_eidx, m->pf_ew, m->pf_grows, m->pf_ppos, m->pf_tiles, m->pf_ehl, m->pf_eact,
                     m->pf_eout, m->moe_router, m->moe_idx, m->moe_w, m->moe_ticket, m->sample_counts,
                     m->sample_prng, m->sample_cand, m->sample_nf, m->sample_full};
     for (void* b : bufs)

@@ -96,6 +96,11 @@ __device__ inline const uint16_t* gemm_w_row(const GemmArgs& g, uint32_t n0, int
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Row `row` of this block's K split in the partial sums ([split][M][N] f32).
+__device__ __forceinline__ float* part_row(const GemmArgs& g, uint32_t row) {
+    return g.part + (static_cast<size_t>(blockIdx.z) * g.M + row) * g.N;
+}
+
 __device__ __forceinline__ uint32_t gemm_swz(uint32_t r) { return (r >> 1) & 3u; }
 
 __device__ __forceinline__ void gemm_dma16(const void* src, char* dst) {
@@ -364,7 +369,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
                     if (n >= g.N) continue;
                     float v = acc[i][j][jr];
                     if (MODE == kGemmResid) {
-                        if (split) unsafeAtomicAdd(&orow[n], v);
+                        if (split && g.part) part_row(g, row)[n] = v;  // the consumer adds the splits in order
+                        else if (split) unsafeAtomicAdd(&orow[n], v);
                         else orow[n] = __fadd_rn(orow[n], v);  // addInto (src/llm.zig:1389-1396)
                     } else {
                         const uint16_t* b = n < g.seg_end[0] ? g.bias[0] : n < g.seg_end[1] ? g.bias[1] : g.bias[2];
@@ -373,7 +379,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
                                                                                         : n - g.seg_end[1];
                             v = __fadd_rn(v, from_bf16(b[bi]));
                         }
-                        if (split) unsafeAtomicAdd(&orow[n], v);  // output zeroed before the launch
+                        if (split && g.part) part_row(g, row)[n] = v;
+                        else if (split) unsafeAtomicAdd(&orow[n], v);  // output zeroed before the launch
                         else orow[n] = v;
                     }
                 }
@@ -388,15 +395,26 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(GemmArgs g) {
 constexpr int kRowThreads = 256;
 
 // s_r = 1 / sqrt(sum(x^2) / n + eps) for each row (rmsNormInto's scale, src/llm.zig:1292-1293).
-__global__ __launch_bounds__(kRowThreads) void row_rms_kernel(const float* __restrict__ x, uint32_t n, uint32_t rows,
-                                                             float eps, float* __restrict__ scale) {
+// With K-split partial sums of the residual GEMM that produced x (part:
+// [splits][rows][n]), x_r is first completed as x_r + p_0 + p_1 + ... in split
+// order (addInto per split, src/llm.zig:1389-1396) and written back.
+__global__ __launch_bounds__(kRowThreads) void row_rms_kernel(float* __restrict__ x, uint32_t n, uint32_t rows,
+                                                             float eps, float* __restrict__ scale,
+                                                             const float* __restrict__ part, uint32_t splits) {
     const uint32_t wave = (blockIdx.x * kRowThreads + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
     if (wave >= rows) return;
-    const float* r = x + static_cast<size_t>(wave) * n;
+    float* r = x + static_cast<size_t>(wave) * n;
     float acc = 0.f;
     for (uint32_t i = lane * 4; i < n; i += 256) {
-        const float4 v = *reinterpret_cast<const float4*>(r + i);
+        float4 v = *reinterpret_cast<const float4*>(r + i);
+        if (part) {
+            for (uint32_t z = 0; z < splits; ++z) {
+                const float4 p = *reinterpret_cast<const float4*>(part + (static_cast<size_t>(z) * rows + wave) * n + i);
+                v.x = __fadd_rn(v.x, p.x), v.y = __fadd_rn(v.y, p.y), v.z = __fadd_rn(v.z, p.z), v.w = __fadd_rn(v.w, p.w);
+            }
+            *reinterpret_cast<float4*>(r + i) = v;
+        }
         acc = fmaf(v.x, v.x, acc);
         acc = fmaf(v.y, v.y, acc);
         acc = fmaf(v.z, v.z, acc);
@@ -404,6 +422,52 @@ __global__ __launch_bounds__(kRowThreads) void row_rms_kernel(const float* __res
     }
     acc = wave_sum(acc);
     if (lane == 0) scale[wave] = 1.0f / sqrtf(acc / static_cast<float>(n) + eps);
+}
+
+// Up to 8 K-split partial sums of one float4 (stride elements apart), loaded
+// together, added onto v in split order.
+constexpr uint32_t kMaxPartSplits = 8;
+__device__ __forceinline__ float4 add_parts(float4 v, const float* __restrict__ p, size_t stride, uint32_t splits) {
+    float4 q[kMaxPartSplits];
+#pragma unroll
+    for (uint32_t z = 0; z < kMaxPartSplits; ++z)
+        q[z] = z < splits ? *reinterpret_cast<const float4*>(p + z * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (uint32_t z = 0; z < kMaxPartSplits; ++z)
+        if (z < splits)
+            v.x = __fadd_rn(v.x, q[z].x), v.y = __fadd_rn(v.y, q[z].y), v.z = __fadd_rn(v.z, q[z].z),
+            v.w = __fadd_rn(v.w, q[z].w);
+    return v;
+}
+
+// As row_rms_kernel with partial sums (at most kMaxPartSplits), a block per
+// row: x_r = x_r + p_0 + p_1 + ... (split order), written back, then the
+// row's scale.
+__global__ __launch_bounds__(kRowThreads) void row_rms_part_kernel(float* __restrict__ x, uint32_t n, uint32_t rows,
+                                                                  float eps, float* __restrict__ scale,
+                                                                  const float* __restrict__ part, uint32_t splits) {
+    __shared__ float red[kRowThreads / 64];
+    const uint32_t row = blockIdx.x;
+    float* r = x + static_cast<size_t>(row) * n;
+    float acc = 0.f;
+    for (uint32_t i = threadIdx.x * 4; i < n; i += kRowThreads * 4) {
+        float4 v = add_parts(*reinterpret_cast<const float4*>(r + i), part + static_cast<size_t>(row) * n + i,
+                             static_cast<size_t>(rows) * n, splits);
+        *reinterpret_cast<float4*>(r + i) = v;
+        acc = fmaf(v.x, v.x, acc);
+        acc = fmaf(v.y, v.y, acc);
+        acc = fmaf(v.z, v.z, acc);
+        acc = fmaf(v.w, v.w, acc);
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRowThreads / 64; ++w) t += red[w];
+        scale[row] = 1.0f / sqrtf(t / static_cast<float>(n) + eps);
+    }
 }
 
 // X[t] = embed[tokens[t]] (copyEmbeddingToken, src/llm.zig:1373-1380).
@@ -423,6 +487,15 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
     const uint32_t t = blockIdx.x;
     const uint32_t pos = a.start + t;
     float* row = a.qkv + static_cast<size_t>(t) * a.ld;
+    if (a.part) {  // the q|k|v GEMM's K-split partial sums, added in split order (the bias is in split 0's)
+        const float* pr = a.part + static_cast<size_t>(t) * a.ld;
+        const size_t stride = static_cast<size_t>(a.rows) * a.ld;
+        for (uint32_t i = threadIdx.x * 4; i < a.ld; i += kRowThreads * 4) {
+            const float4 p0 = *reinterpret_cast<const float4*>(pr + i);
+            *reinterpret_cast<float4*>(row + i) = add_parts(p0, pr + stride + i, stride, a.splits - 1);
+        }
+        __syncthreads();
+    }
     const float* cs = a.rope_cs + static_cast<size_t>(pos) * a.hd;
     const uint32_t half = a.hd / 2;
     const uint32_t qpairs = a.heads * half, kpairs = a.kv_heads * half;
@@ -1025,8 +1098,18 @@ uint32_t gemm_k_splits(int mode, const GemmArgs& g, uint32_t tiles) {
     const uint32_t min_steps = tiles >= 32 ? 16 : 8;
     const uint32_t max_splits = std::min<uint32_t>(32, nk / min_steps > 0 ? nk / min_steps : 1);
     if (2 * tiles > cus) return 1;
-    return std::max<uint32_t>(1, std::min<uint32_t>(max_splits, cus / tiles));
+    uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>(max_splits, cus / tiles));
+    // Every split gets K steps: the kernel gives split z steps from z * ceil(nk / splits).
+    while (splits > 1 && (splits - 1) * ((nk + splits - 1) / splits) >= nk) --splits;
+    return splits;
 }
+
+uint32_t gemm_splits(int mode, const GemmArgs& g) {
+    const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
+    return gemm_k_splits(mode, g, ((cols + kBN - 1) / kBN) * ((g.M + kBM - 1) / kBM));
+}
+
+size_t gemm_part_elems() { return static_cast<size_t>(gemm_cus()) * kBM * kBN; }
 
 static uint32_t fa_tile_keys(uint32_t hd) { return hd == 128 ? FaShape<128>::TK : FaShape<64>::TK; }
 static_assert(FaShape<32>::Stage == 8 * 64 * 32 && FaShape<64>::Stage == 8 * 64 * 64 &&
@@ -1073,7 +1156,9 @@ hipError_t launch_gemm_bf16(int mode, const GemmArgs& g, hipStream_t s) {
     const uint32_t cols = mode == kGemmGateUp ? 2 * g.N : g.N;
     const uint32_t gx = (cols + kBN - 1) / kBN, gy = (g.M + kBM - 1) / kBM;
     const uint32_t splits = gemm_k_splits(mode, g, gx * gy);
-    if (splits > 1 && mode != kGemmResid) {
+    if (splits > 1 && g.part && static_cast<size_t>(splits) * g.M * g.N > gemm_part_elems())
+        return hipErrorInvalidValue;  // (splits * tiles <= CUs keeps every launch within it)
+    if (splits > 1 && mode != kGemmResid && !(mode == kGemmPlain && g.part)) {
         const bool gu = mode == kGemmGateUp;
         const size_t n = static_cast<size_t>(g.M) * (gu ? 2 * g.N : g.ldo);
         const uint32_t blocks = static_cast<uint32_t>(std::min<size_t>((n + 255) / 256, 4096));
@@ -1126,10 +1211,16 @@ hipError_t launch_gemm_grouped(int mode, const GemmArgs& g, hipStream_t s) {
     return vlaunch(gemm_bf16_kernel<kGemmPlain, true>, grid, dim3(kGemmThreads), kGemmLds, s, g);
 }
 
-hipError_t launch_row_rms(const float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s) {
+hipError_t launch_row_rms(float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s,
+                          const float* part, uint32_t splits) {
+    if (n % 4 != 0) return hipErrorInvalidValue;
+    if (part && splits > kMaxPartSplits) return hipErrorInvalidValue;
+    if (part && splits > 1)  // a block per row: the partial sums are splits x the row's bytes
+        return vlaunch(row_rms_part_kernel, dim3(rows), dim3(kRowThreads), 0, s, x, n, rows, eps, scale, part,
+                       splits);
     const uint32_t waves_per_block = kRowThreads / 64;
     return vlaunch(row_rms_kernel, dim3((rows + waves_per_block - 1) / waves_per_block), dim3(kRowThreads), 0, s, x,
-                   n, rows, eps, scale);
+                   n, rows, eps, scale, nullptr, 0u);
 }
 
 hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
@@ -1140,6 +1231,7 @@ hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, u
 
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
     if ((a.q_norm == nullptr) != (a.k_norm == nullptr)) return hipErrorInvalidValue;
+    if (a.part && (a.splits < 2 || a.splits > kMaxPartSplits || a.ld % 4 != 0)) return hipErrorInvalidValue;
     return vlaunch(prefill_rope_kv_kernel, dim3(a.rows), dim3(kRowThreads), 0, s, a);
 }
 
