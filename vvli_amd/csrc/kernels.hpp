@@ -310,6 +310,13 @@ hipError_t launch_gemm_grouped(int mode, const GemmArgs& g, hipStream_t s);
 // ([splits][rows][n]; nullptr or splits <= 1: x is complete), added into x first.
 hipError_t launch_row_rms(float* x, uint32_t n, uint32_t rows, float eps, float* scale, hipStream_t s,
                           const float* part = nullptr, uint32_t splits = 0);
+// launch_row_rms (with the partial sums) and the split pass of a normalising
+// GEMM in one launch: writes the GEMM's A planes of rmsnorm(x) with weight
+// norm_w (hi at a_hl, lo a_plane elements later); the GEMM then runs with
+// a_ready. For rows of n floats with row_norm_split_fits(n) (n <= 8192).
+bool row_norm_split_fits(uint32_t n);
+hipError_t launch_row_norm_split(float* x, uint32_t n, uint32_t rows, float eps, const uint16_t* norm_w,
+                                 const float* part, uint32_t splits, uint16_t* a_hl, size_t a_plane, hipStream_t s);
 hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
                                 float* x, hipStream_t s);
 

@@ -724,11 +724,19 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
             }
             float* kc = m->kcache + static_cast<size_t>(l) * m->max_seq * kv;
             float* vc = m->vcache + static_cast<size_t>(l) * m->max_seq * kv;
-            // input RMSNorm fused into the q|k|v GEMM (+ bias)
-            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
-            pend = 0;
+            // input RMSNorm into the q|k|v GEMM's A planes (+ bias in the GEMM)
             GemmArgs gq;
-            gq.a = m->pf_x, gq.lda = H, gq.row_scale = m->pf_scale, gq.norm_w = w16(L.input_norm);
+            if (row_norm_split_fits(H)) {
+                LAUNCH(launch_row_norm_split(m->pf_x, H, P, c.rms_eps, w16(L.input_norm), m->pf_part, pend,
+                                             reinterpret_cast<uint16_t*>(m->pf_ahl),
+                                             static_cast<size_t>(P) * gemm_kp(H), s));
+                gq.a_ready = true, gq.a_plane = static_cast<size_t>(P) * gemm_kp(H);
+            } else {
+                LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
+                gq.row_scale = m->pf_scale, gq.norm_w = w16(L.input_norm);
+            }
+            pend = 0;
+            gq.a = m->pf_x, gq.lda = H;
             gq.w[0] = w16(L.q), gq.w[1] = w16(L.k), gq.w[2] = w16(L.v);
             gq.bias[0] = w16(L.q_bias), gq.bias[1] = w16(L.k_bias), gq.bias[2] = w16(L.v_bias);
             gq.seg_end[0] = H, gq.seg_end[1] = H + kv, gq.seg_end[2] = H + 2 * kv;
@@ -764,11 +772,19 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
                 continue;
             }
             const LayerSlices& D = m->layout.layers[l];
-            // post-attention RMSNorm fused into gate/up + SwiGLU
-            LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
-            pend = 0;
+            // post-attention RMSNorm into the gate/up GEMM's A planes (+ SwiGLU in the GEMM)
             GemmArgs gu;
-            gu.a = m->pf_x, gu.lda = H, gu.row_scale = m->pf_scale, gu.norm_w = w16(D.post_norm);
+            if (row_norm_split_fits(H)) {
+                LAUNCH(launch_row_norm_split(m->pf_x, H, P, c.rms_eps, w16(D.post_norm), m->pf_part, pend,
+                                             reinterpret_cast<uint16_t*>(m->pf_ahl),
+                                             static_cast<size_t>(P) * gemm_kp(H), s));
+                gu.a_ready = true, gu.a_plane = static_cast<size_t>(P) * gemm_kp(H);
+            } else {
+                LAUNCH(launch_row_rms(m->pf_x, H, P, c.rms_eps, m->pf_scale, s, m->pf_part, pend));
+                gu.row_scale = m->pf_scale, gu.norm_w = w16(D.post_norm);
+            }
+            pend = 0;
+            gu.a = m->pf_x, gu.lda = H;
             gu.w[0] = w16(D.gate), gu.w_up = w16(D.up);
             gu.seg_end[0] = gu.seg_end[1] = gu.seg_end[2] = I;
             gu.M = P, gu.N = I, gu.K = H;

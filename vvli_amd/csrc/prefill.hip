@@ -470,6 +470,69 @@ __global__ __launch_bounds__(kRowThreads) void row_rms_part_kernel(float* __rest
     }
 }
 
+// Row pass in front of a normalising GEMM, a block per row: complete x_r with
+// the K-split partial sums of the GEMM that produced it (split order, written
+// back), s_r = 1 / sqrt(mean(x_r^2) + eps), then the GEMM's A planes of
+// (x_r * w) * s_r: hi = bf16(a), lo = bf16(a - hi), rows of gemm_kp(n) with a
+// zero tail (what launch_row_rms + gemm_split_kernel write, in one pass: the
+// row stays in registers). n <= kNormSplitMaxGroups * 8 * kRowThreads.
+constexpr int kNormSplitMaxGroups = 4;
+__global__ __launch_bounds__(kRowThreads) void row_norm_split_kernel(float* __restrict__ x, uint32_t n, uint32_t rows,
+                                                                    float eps, const uint16_t* __restrict__ norm_w,
+                                                                    const float* __restrict__ part, uint32_t splits,
+                                                                    uint16_t* __restrict__ a_hl, size_t a_plane) {
+    __shared__ float red[kRowThreads / 64];
+    const uint32_t row = blockIdx.x;
+    float* r = x + static_cast<size_t>(row) * n;
+    const uint32_t kp = gemm_kp(n), groups = kp / 8;
+    float v[kNormSplitMaxGroups][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kNormSplitMaxGroups; ++q) {
+        const uint32_t k = (threadIdx.x + q * kRowThreads) * 8;
+        if (k < n) {  // n % 8 == 0: a group is all in or all out
+            float4 a = *reinterpret_cast<const float4*>(r + k), b = *reinterpret_cast<const float4*>(r + k + 4);
+            if (part && splits > 1) {
+                const size_t stride = static_cast<size_t>(rows) * n;
+                a = add_parts(a, part + static_cast<size_t>(row) * n + k, stride, splits);
+                b = add_parts(b, part + static_cast<size_t>(row) * n + k + 4, stride, splits);
+                *reinterpret_cast<float4*>(r + k) = a;
+                *reinterpret_cast<float4*>(r + k + 4) = b;
+            }
+            v[q][0] = a.x, v[q][1] = a.y, v[q][2] = a.z, v[q][3] = a.w;
+            v[q][4] = b.x, v[q][5] = b.y, v[q][6] = b.z, v[q][7] = b.w;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf(v[q][j], v[q][j], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRowThreads / 64; ++w) t += red[w];
+    const float scale = 1.0f / sqrtf(t / static_cast<float>(n) + eps);  // rmsNormInto, src/llm.zig:1292-1293
+    uint16_t* out = a_hl + static_cast<size_t>(row) * kp;
+#pragma unroll
+    for (int q = 0; q < kNormSplitMaxGroups; ++q) {
+        const uint32_t gi = threadIdx.x + q * kRowThreads, k = gi * 8;
+        if (gi >= groups) continue;
+        u16x8 hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = hi;
+        if (k < n) {
+            const u16x8 w = *reinterpret_cast<const u16x8*>(norm_w + k);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float a = __fmul_rn(__fmul_rn(v[q][j], from_bf16(w[j])), scale);  // x * w * s (:1297)
+                const uint16_t h = to_bf16_rne(a);
+                hi[j] = h;
+                lo[j] = to_bf16_rne(a - from_bf16(h));
+            }
+        }
+        *reinterpret_cast<u16x8*>(out + k) = hi;
+        *reinterpret_cast<u16x8*>(out + a_plane + k) = lo;
+    }
+}
+
 // X[t] = embed[tokens[t]] (copyEmbeddingToken, src/llm.zig:1373-1380).
 __global__ __launch_bounds__(kRowThreads) void prefill_embed_kernel(const uint16_t* __restrict__ embed,
                                                                    const uint32_t* __restrict__ tokens, uint32_t n,
@@ -1221,6 +1284,19 @@ hipError_t launch_row_rms(float* x, uint32_t n, uint32_t rows, float eps, float*
     const uint32_t waves_per_block = kRowThreads / 64;
     return vlaunch(row_rms_kernel, dim3((rows + waves_per_block - 1) / waves_per_block), dim3(kRowThreads), 0, s, x,
                    n, rows, eps, scale, nullptr, 0u);
+}
+
+bool row_norm_split_fits(uint32_t n) {
+    return n % 8 == 0 && gemm_kp(n) / 8 <= static_cast<uint32_t>(kNormSplitMaxGroups * kRowThreads);
+}
+
+hipError_t launch_row_norm_split(float* x, uint32_t n, uint32_t rows, float eps, const uint16_t* norm_w,
+                                 const float* part, uint32_t splits, uint16_t* a_hl, size_t a_plane, hipStream_t s) {
+    if (!row_norm_split_fits(n) || !norm_w || !a_hl || a_plane < static_cast<size_t>(rows) * gemm_kp(n) ||
+        (part && splits > kMaxPartSplits))
+        return hipErrorInvalidValue;
+    return vlaunch(row_norm_split_kernel, dim3(rows), dim3(kRowThreads), 0, s, x, n, rows, eps, norm_w,
+                   splits > 1 ? part : nullptr, splits, a_hl, a_plane);
 }
 
 hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, uint32_t rows, uint32_t hidden,
