@@ -278,6 +278,17 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
  * for it returns VVLI_HIP_ERROR; the flag is cleared once the host has read
  * it. */
 int vvli_gpu_test_inject_step_error(vvli_gpu_model* model, uint32_t n);
+/* Test hook of the whole-vocabulary sampler (no reference counterpart):
+ * Sampler.next as vvli_gpu_sampler_next with no repeat history, restricted to
+ * candidate lists over 1024 (temperature > 0, top_k 0 or > 1024; else
+ * VVLI_INVALID_CONFIG), that also returns, in candidate order, the
+ * candidates' ids, their probabilities exp((s - s_max) / T) and the running
+ * f32 sums of those probabilities (the sums prepareProbabilities and
+ * sampleCandidate form, src/generator.zig:428-463); *count_out = candidates.
+ * ids_out, probs_out and sums_out hold n entries. */
+int vvli_gpu_test_sampler_trace(const float* logits, uint32_t n, const vvli_gpu_sampling* opts,
+                                uint64_t prng_state[4], uint32_t* token_out, uint32_t* ids_out, float* probs_out,
+                                float* sums_out, uint32_t* count_out);
 
 /* ---------------------------------------------------------------------- */
 /* Isolated matmul op (device pointers)                                    */

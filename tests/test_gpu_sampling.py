@@ -155,6 +155,99 @@ def test_sampler_whole_vocab_matches_oracle(k, vocab, oracle_mod):
         assert np.array_equal(st_gpu, st_orc), f"trial {trial}: PRNG state"
 
 
+def _oracle_candidates(oracle_mod, logits, o):
+    import ctypes
+
+    lg = np.ascontiguousarray(logits, np.float32)
+    counts = np.zeros(lg.size, np.uint16)
+    ids = np.zeros(lg.size, np.uint32)
+    sc = np.zeros(lg.size, np.float32)
+    so = oracle_mod.orc_sampling(o)
+    L = oracle_mod.lib()
+    n = L.orc_build_candidates(oracle_mod._p(ids), oracle_mod._p(sc), oracle_mod._p(lg), oracle_mod._p(counts),
+                               lg.size, ctypes.byref(so))
+    probs = np.zeros(max(n, 1), np.float32)
+    if n:
+        L.orc_prepare_probabilities(oracle_mod._p(probs), oracle_mod._p(sc), n, ctypes.byref(so))
+    return ids[:n], probs[:n]
+
+
+def _chain_events(probs, sums):
+    """Ties and binade crossings along the running sum: adding p_j to s_{j-1}
+    = m * u (u its binade's spacing) is a tie when p_j / u ends in exactly 1/2,
+    a crossing when the exact sum reaches the next power of two."""
+    prev = sums[:-1].astype(np.float64)
+    p = probs[1:].astype(np.float64)
+    e = np.floor(np.log2(prev))
+    u = np.exp2(e - 23)
+    x = p / u
+    ties = int(np.count_nonzero(x - np.floor(x) == 0.5))
+    crossings = int(np.count_nonzero(prev + p >= np.exp2(e + 1)))
+    return ties, crossings
+
+
+def _tie_run(vocab, z):
+    lg = np.full(vocab, np.float32(np.log1p(-2.0 ** (z - 24))), np.float32)
+    lg[vocab // 3] = 0.0
+    return lg
+
+
+MIN_TIES = {"flat_1e-4": 1, "flat_0.05": 1, "tie_run_z12": 4000, "tie_run_z13": 8000}
+
+TRACE_CASES = {
+    # name: (vocab, top_k, temperature, top_p, logits(rng, vocab))
+    "flat_1e-4": (128256, 0, 1.0, 0.95, lambda r, v: r.normal(0, 1e-4, v)),
+    "flat_0.05": (152064, 0, 0.8, 0.9, lambda r, v: r.normal(0, 0.05, v)),
+    "spread_3": (128256, 0, 0.8, 0.95, lambda r, v: r.normal(0, 3.0, v)),
+    "all_equal": (20000, 0, 1.0, 0.5, lambda r, v: np.full(v, 1.5)),
+    "quantized": (152064, 0, 1.0, 0.9, lambda r, v: np.round(r.normal(0, 2.0, v) * 8) / 8),
+    "top_k_2000": (5000, 2000, 2.0, 0.9, lambda r, v: r.normal(0, 1.0, v)),
+    # One max logit, the rest at ln(1 - 2^(z-24)): every probability but the
+    # first is 1 - 2^(z-24), whose lowest set bit is half the spacing of f32
+    # in [2^z, 2^(z+1)), so each addition while the sum is there (2^z of
+    # them, across threads and chunks) is an exact tie.
+    "tie_run_z12": (20000, 0, 1.0, 0.9, lambda r, v: _tie_run(v, 12)),
+    "tie_run_z13": (40000, 0, 1.0, 0.6, lambda r, v: _tie_run(v, 13)),
+    "finite_8192": (30000, 0, 0.7, 0.99, None),
+    "finite_8193": (30000, 0, 0.7, 0.99, None),
+    "finite_700": (30000, 0, 1.1, 0.8, None),
+}
+
+
+@pytest.mark.parametrize("name", list(TRACE_CASES))
+def test_sampler_whole_vocab_sums_bit_exact(name, oracle_mod):
+    """The whole-vocabulary path's candidate order equals the oracle's, its
+    probabilities agree with the oracle's to the two exp implementations'
+    rounding, and its running sums -- computed as integer prefix sums per
+    binade with tie corrections -- are bit-identical to adding the same
+    probabilities one after another in f32 (numpy's sequential accumulate)."""
+    vocab, top_k, temp, top_p, gen = TRACE_CASES[name]
+    rng = np.random.default_rng(sum(name.encode()))
+    if gen is None:
+        n_fin = int(name.split("_")[1])
+        logits = np.full(vocab, -np.inf, np.float32)
+        logits[rng.permutation(vocab)[:n_fin]] = rng.normal(0, 1.0, n_fin)
+    else:
+        logits = gen(rng, vocab).astype(np.float32)
+    o = opts(top_k=top_k, top_p=top_p, temperature=temp, repeat_penalty=1.0)
+    print(f"sampler trace {name} vocab={vocab}", flush=True)
+    st_gpu = R.prng_seed(77)
+    st_orc = st_gpu.copy()
+    tok, ids, probs, sums = R.sampler_trace(logits, o, st_gpu)
+    ref_ids, ref_probs = _oracle_candidates(oracle_mod, logits, o)
+    np.testing.assert_array_equal(ids, ref_ids)
+    np.testing.assert_allclose(probs, ref_probs, rtol=4e-7, atol=1e-44)
+    seq = np.add.accumulate(probs, dtype=np.float32)
+    np.testing.assert_array_equal(sums.view(np.uint32), seq.view(np.uint32))
+    ties, crossings = _chain_events(probs, sums)
+    print(f"  candidates {ids.size} ties {ties} crossings {crossings}", flush=True)
+    assert ties >= MIN_TIES.get(name, 0), "the input should exercise the tie corrections"
+    if name.startswith(("flat", "tie_run", "all_equal")):
+        assert crossings >= 10, "the sum should cross binades (restarts of the parallel chain)"
+    assert tok == oracle_mod.sampler_next(logits, [], [], o, st_orc)
+    assert np.array_equal(st_gpu, st_orc)
+
+
 def test_sampler_whole_vocab_no_finite(oracle_mod):
     """No finite candidate on the whole-vocabulary path: llm.argmax of the logits."""
     st = R.prng_seed(8)

@@ -447,6 +447,12 @@ struct SampleArgs {
     // 0 or > 1024), sample_full_bytes(vocab) bytes (nullable: such limits are
     // an error).
     void* full = nullptr;
+    // Test hook of the whole-vocabulary path (each nullable): the candidates'
+    // ids, probabilities and running sums in candidate order, and their count.
+    uint32_t* trace_ids = nullptr;
+    float* trace_probs = nullptr;
+    float* trace_sums = nullptr;
+    uint32_t* trace_count = nullptr;
 };
 size_t sample_cand_elems(uint32_t vocab);
 size_t sample_nf_elems(uint32_t vocab);

@@ -1644,6 +1644,71 @@ int vvli_gpu_generate(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prom
     return generate_sampled(m, prompt, n_prompt, max_new, eos, batched, *opts, out_tokens, n_out, stats);
 }
 
+int vvli_gpu_test_sampler_trace(const float* logits, uint32_t n, const vvli_gpu_sampling* opts,
+                                uint64_t prng_state[4], uint32_t* token_out, uint32_t* ids_out, float* probs_out,
+                                float* sums_out, uint32_t* count_out) {
+    if (!logits || !opts || !prng_state || !token_out || !ids_out || !probs_out || !sums_out || !count_out)
+        return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_test_sampler_trace");
+    if (n == 0) return set_error(VVLI_INVALID_CONFIG, "empty logits");
+    clear_error();
+    int rc = validate_sampling(*opts, n);
+    if (rc) return rc;
+    const uint32_t limit = (opts->top_k == 0 || opts->top_k > n) ? n : opts->top_k;
+    if (!(opts->temperature > 0.0f) || limit <= static_cast<uint32_t>(kMaxSampleTopK))
+        return set_error(VVLI_INVALID_CONFIG, "the trace covers the whole-vocabulary path (T > 0, over %d candidates)",
+                         kMaxSampleTopK);
+    const size_t full_bytes = sample_full_bytes(n);
+    void* d_full = nullptr;
+    float *d_logits = nullptr, *d_probs = nullptr, *d_sums = nullptr;
+    uint32_t *d_ids = nullptr, *d_result = nullptr, *d_count = nullptr;
+    unsigned long long* d_prng = nullptr;
+    hipError_t e = hipMalloc(&d_full, full_bytes);
+    if (e == hipSuccess) e = hipMalloc(&d_logits, n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d_probs, n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d_sums, n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d_ids, n * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d_result, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d_count, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d_prng, 4 * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemcpy(d_logits, logits, n * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d_prng, prng_state, 4 * sizeof(uint64_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        SampleArgs sa;
+        sa.logits = d_logits;
+        sa.vocab = n;
+        sa.temperature = opts->temperature;
+        sa.top_p = opts->top_p;
+        sa.repeat_penalty = opts->repeat_penalty;
+        sa.top_k = limit;
+        sa.repeat_last_n = opts->repeat_last_n;
+        sa.prng = d_prng;
+        sa.result = d_result;
+        sa.full = d_full;
+        sa.trace_ids = d_ids;
+        sa.trace_probs = d_probs;
+        sa.trace_sums = d_sums;
+        sa.trace_count = d_count;
+        e = launch_sample(sa, nullptr);
+    }
+    uint32_t count = 0;
+    if (e == hipSuccess) e = hipMemcpy(&count, d_count, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && count > n) e = hipErrorUnknown;
+    if (e == hipSuccess && count) e = hipMemcpy(ids_out, d_ids, count * sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && count) e = hipMemcpy(probs_out, d_probs, count * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && count) e = hipMemcpy(sums_out, d_sums, count * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(token_out, d_result, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(prng_state, d_prng, 4 * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    *count_out = count;
+    for (void* q : {static_cast<void*>(d_full), static_cast<void*>(d_logits), static_cast<void*>(d_probs),
+                    static_cast<void*>(d_sums), static_cast<void*>(d_ids), static_cast<void*>(d_result),
+                    static_cast<void*>(d_count), static_cast<void*>(d_prng)})
+        if (q) (void)hipFree(q);
+    if (e != hipSuccess)
+        return set_error(e == hipErrorOutOfMemory ? VVLI_OUT_OF_MEMORY : VVLI_HIP_ERROR, "sampler trace: %s",
+                         hipGetErrorString(e));
+    return VVLI_OK;
+}
+
 void vvli_gpu_prng_seed(uint64_t seed, uint64_t state_out[4]) {
     if (state_out) prng_seed(seed, state_out);
 }

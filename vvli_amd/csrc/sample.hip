@@ -17,15 +17,17 @@
 //
 // Whole-vocabulary candidates (limit over 1024: top_k 0, which buildCandidates
 // treats as "every finite score, sorted", :376-391, or top_k > 1024):
-// sample_full_keys_kernel writes each id's order-preserving score key (0 for
-// a non-finite score), rocPRIM's stable radix sort orders the (key, id) pairs
-// descending -- ties keep ascending ids, the order insertTopCandidate gives
-// and the oracle uses for the reference's unstable sort -- and
-// sample_full_kernel takes the first min(limit, finite) of them: the
-// probabilities in parallel, then one lane's single pass of sequential f32
+// full_keys_kernel writes each id's sort key (descending score order, the
+// non-finite ones last), four stable 8-bit radix passes (histogram + ballot-
+// ranked scatter kernels) order the (key, id) pairs -- ties keep ascending
+// ids, the order insertTopCandidate gives and the oracle uses for the
+// reference's unstable sort -- and sample_full_kernel takes the first
+// min(limit, finite) of them: the probabilities, then the sequential f32
 // prefix sums in candidate order (the running sum of prepareProbabilities'
 // total, of its top-p scan and of sampleCandidate's sums are the same
-// sequence), then the top-p cut and the pick as searches over those sums.
+// sequence), computed bit-exactly as integer prefix sums per binade of the
+// running sum, then the top-p cut and the pick as searches over those sums
+// (both predicates are monotone along the nondecreasing sums).
 //
 // Two-stage top-k (top_k <= 128, at most 64 slices, scratch of
 // sample_cand_elems keys given):
@@ -37,8 +39,6 @@
 // the global top_k is in its slice's top_k; the sampling block's first wave then merges
 // the slices' sorted lists (one list head per lane) instead of scanning the
 // vocab (one block's scan is ~1 ms at a 128K vocab).
-#include <rocprim/device/device_radix_sort.hpp>
-
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
     }
 }
 
-__device__ __noinline__ void sample_finish(const SampleArgs& a, uint32_t tok);
+__device__ __forceinline__ void sample_finish(const SampleArgs& a, uint32_t tok);
 
 __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
     __shared__ SampleShared sh;
@@ -420,37 +420,305 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
     sample_finish(a, tok);
 }
 
-// Whole-vocabulary path, pass 1: sort keys and ids (the ids in ascending
-// order, so the stable sort keeps ties by ascending id).
-__global__ __launch_bounds__(256) void sample_full_keys_kernel(SampleArgs a, uint32_t* keys, uint32_t* ids) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.vocab) return;
-    const float s = adjusted(a.logits[i], a.counts ? a.counts[i] : 0u, a.repeat_penalty);
-    keys[i] = isfinite(s) ? order_key(s) : 0u;
-    ids[i] = i;
-}
+// ---- Whole-vocabulary candidates ---------------------------------------------
+// Sort: LSD radix sort of (sort key, id) pairs, four passes of 8 bits over
+// tiles of kSortTile ids. The sort key is ~order_key(score) (0xffffffff for a
+// non-finite score), so ascending sort keys are descending scores with the
+// non-finite ones last, and the stable passes keep ties in ascending id order
+// (the ids start in ascending order), the order insertTopCandidate gives.
+// A pass is a histogram kernel (per tile and digit) and a scatter kernel; the
+// scatter ranks a tile's keys stably with wave ballots (lanes holding the
+// same digit) and per-(slot, wave) digit counts in LDS, so no atomics decide
+// an order.
+constexpr uint32_t kSortThreads = 256;
+constexpr uint32_t kSortSlots = 8;
+constexpr uint32_t kSortTile = kSortThreads * kSortSlots;          // ids per tile
+constexpr uint32_t kSortRows = kSortSlots * (kSortThreads / 64);   // (slot, wave) rows of a tile
 
-// Whole-vocabulary path, pass 3 (one block): the candidates are the first
-// min(limit, finite) sorted pairs (finite keys are >= 1, so the finite ones
-// come first).
-__global__ __launch_bounds__(kT) void sample_full_kernel(SampleArgs a, const uint32_t* keys, const uint32_t* ids,
-                                                         float* prob, float* prefix) {
-    __shared__ unsigned long long red[kT / 64];
-    __shared__ uint32_t s_n, s_cut, s_pick, s_tok;
-    const uint32_t tid = threadIdx.x, V = a.vocab;
-    // Finite count: the first zero key (binary search; keys are descending).
-    if (tid == 0) {
-        uint32_t lo = 0, hi = V;
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi) / 2;
-            if (keys[mid] != 0u) lo = mid + 1;
-            else hi = mid;
+__device__ inline uint32_t sort_key(float s) { return isfinite(s) ? ~order_key(s) : 0xffffffffu; }
+
+// Pass-0 input: each id's sort key, the ids, and the tiles' low-byte histograms.
+__global__ __launch_bounds__(kSortThreads) void full_keys_kernel(SampleArgs a, uint32_t* sk, uint32_t* ids,
+                                                                 uint32_t* hist) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const uint32_t base = blockIdx.x * kSortTile;
+    for (uint32_t s = 0; s < kSortSlots; ++s) {
+        const uint32_t i = base + s * kSortThreads + threadIdx.x;
+        if (i < a.vocab) {
+            const uint32_t k = sort_key(adjusted(a.logits[i], a.counts ? a.counts[i] : 0u, a.repeat_penalty));
+            sk[i] = k;
+            ids[i] = i;
+            atomicAdd(&h[k & 255u], 1u);
         }
-        s_n = lo;
     }
     __syncthreads();
+    hist[blockIdx.x * 256 + threadIdx.x] = h[threadIdx.x];
+}
+
+// Digit histogram of every tile for the pass at `shift`.
+__global__ __launch_bounds__(kSortThreads) void full_hist_kernel(const uint32_t* sk, uint32_t n, uint32_t shift,
+                                                                 uint32_t* hist) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const uint32_t base = blockIdx.x * kSortTile;
+    for (uint32_t s = 0; s < kSortSlots; ++s) {
+        const uint32_t i = base + s * kSortThreads + threadIdx.x;
+        if (i < n) atomicAdd(&h[(sk[i] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    hist[blockIdx.x * 256 + threadIdx.x] = h[threadIdx.x];
+}
+
+__device__ inline uint32_t wave_incl_scan_add(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(v), off, 64));
+        if (lane >= static_cast<uint32_t>(off)) v += o;
+    }
+    return v;
+}
+
+// One stable pass at `shift`: tile t (input positions t * kSortTile + s * 256
+// + thread, slot s) goes to base(digit) + (earlier tiles' count of the digit)
+// + (its rank among the tile's keys of that digit in position order).
+__global__ __launch_bounds__(kSortThreads) void full_scatter_kernel(const uint32_t* sk_in, const uint32_t* id_in,
+                                                                    uint32_t* sk_out, uint32_t* id_out, uint32_t n,
+                                                                    uint32_t shift, const uint32_t* hist,
+                                                                    uint32_t tiles) {
+    __shared__ uint32_t cnt[kSortRows][256];
+    __shared__ uint32_t base[256];
+    __shared__ uint32_t wsum[kSortThreads / 64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, t = blockIdx.x;
+    // Thread d: digit d's total and its count in tiles before t.
+    uint32_t tot = 0, before = 0;
+#pragma unroll 8
+    for (uint32_t u = 0; u < tiles; ++u) {
+        const uint32_t c = hist[u * 256 + tid];
+        tot += c;
+        before += u < t ? c : 0u;
+    }
+    const uint32_t incl = wave_incl_scan_add(tot);
+    if (lane == 63) wsum[w] = incl;
+#pragma unroll
+    for (uint32_t r = 0; r < kSortRows; ++r) cnt[r][tid] = 0;
+    __syncthreads();
+    uint32_t excl = incl - tot;
+    for (uint32_t u = 0; u < w; ++u) excl += wsum[u];
+    base[tid] = excl + before;
+
+    uint32_t key[kSortSlots], id[kSortSlots], rank[kSortSlots];
+    const uint32_t t0 = t * kSortTile + tid;
+#pragma unroll
+    for (uint32_t s = 0; s < kSortSlots; ++s) {
+        const uint32_t i = t0 + s * kSortThreads;
+        key[s] = i < n ? sk_in[i] : 0u;
+        id[s] = i < n ? id_in[i] : 0u;
+    }
+    const unsigned long long lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (uint32_t s = 0; s < kSortSlots; ++s) {
+        const bool valid = t0 + s * kSortThreads < n;
+        const uint32_t dg = (key[s] >> shift) & 255u;
+        unsigned long long same = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (dg >> b) & 1u;
+            const unsigned long long on = __ballot(bit);
+            same &= bit ? on : ~on;
+        }
+        rank[s] = static_cast<uint32_t>(__popcll(same & lt));
+        if (valid && rank[s] == 0) cnt[s * (kSortThreads / 64) + w][dg] = static_cast<uint32_t>(__popcll(same));
+    }
+    __syncthreads();
+    // Thread d: exclusive prefix of digit d's counts over the rows in order.
+    uint32_t run = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kSortRows; ++r) {
+        const uint32_t c = cnt[r][tid];
+        cnt[r][tid] = run;
+        run += c;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t s = 0; s < kSortSlots; ++s) {
+        if (t0 + s * kSortThreads >= n) continue;
+        const uint32_t dg = (key[s] >> shift) & 255u;
+        const uint32_t pos = base[dg] + cnt[s * (kSortThreads / 64) + w][dg] + rank[s];
+        sk_out[pos] = key[s];
+        id_out[pos] = id[s];
+    }
+}
+
+// p = exp((s - s_0) / T) of every sorted position (prepareProbabilities'
+// exp, src/generator.zig:436-439), 0 where it is not finite or the score is;
+// s_0 = the first sorted score.
+__global__ __launch_bounds__(kSortThreads) void full_probs_kernel(const uint32_t* sk, uint32_t n, float temperature,
+                                                                  float* prob) {
+    const float s0 = key_value(~sk[0]);
+    const float t = fmaxf(temperature, 1e-6f);
+    const uint32_t base = blockIdx.x * kSortTile;
+    for (uint32_t q = 0; q < kSortSlots; ++q) {
+        const uint32_t j = base + q * kSortThreads + threadIdx.x;
+        if (j >= n) break;
+        const uint32_t k = sk[j];
+        float v = 0.0f;
+        if (k != 0xffffffffu) {
+            v = expf(__fdiv_rn(__fsub_rn(key_value(~k), s0), t));
+            v = isfinite(v) ? v : 0.0f;
+        }
+        prob[j] = v;
+    }
+}
+
+// ---- exact sequential f32 prefix sums, computed in parallel --------------------
+// prepareProbabilities and sampleCandidate (src/generator.zig:428-463) add the
+// candidates' probabilities one after another in f32: c_j = fl(c_{j-1} + p_j).
+// While the running sum stays in one binade [2^e, 2^(e+1)), every f32 there
+// is a multiple of u = 2^(e-23), so with c = m * u (2^23 <= m < 2^24) and
+// x = p / u (exact: a power-of-two scaling),
+//   fl(c + p) = u * (m + round(x))   as long as m + x < 2^24,
+// round-to-nearest with ties to the even result. Off ties, round(x) does not
+// depend on m, and the chain is an integer prefix sum over the candidates. At
+// a tie (x = f + 1/2) the result is the even one of m + f and m + f + 1:
+// taking f tentatively (T_j = m + the tentative sums up to j) and correcting
+// by +1 where m_{j-1} + f is odd, the correction at the k-th tie is
+// parity(T at tie k) xor parity(T at tie k-1) (parity 0 before the first),
+// because after every tie the corrected sum is even; so m_j = T_j + the number
+// of parity changes along the ties up to j, also a prefix computation. The
+// first candidate whose exact sum leaves the binade (m_{j-1} + floor(x_j) >=
+// 2^24) is added as an ordinary f32 add (every thread computes it from the
+// operands the block's min passes around), and the chunk resumes after it in
+// the new binade (at most one restart per binade the sum enters, i.e. about
+// log2(vocab) in all). Every stored prefix value is bit-identical to the
+// one-after-another sum.
+// One block, candidates in chunks of kChainChunk held in registers (thread t:
+// kChainE consecutive ones); an iteration covers a window of the chunk from
+// the next candidate on (waves holding none of it skip the arithmetic), with
+// two barriers: after the (sum, ties) scan and after the min over the waves'
+// first crossings.
+constexpr int kChainE = 8;                       // candidates per thread and chunk (two float4 loads)
+constexpr uint32_t kChainChunk = kT * kChainE;   // candidates per chunk
+constexpr uint32_t kChainW0 = 1024;              // first window after a restart (grows x2 per full window)
+constexpr uint32_t kSatCap = 1u << 30;           // saturation of the integer sums (> 2^24)
+constexpr uint32_t kTieHas = 1u << 29;           // tie summary: count (bits 0-28), has, first, last parity
+
+__device__ inline uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, kSatCap); }  // a, b <= kSatCap
+
+// Summary of a run of ties' parities: (has, first, last, changes inside);
+// `a` precedes `b`; 0 is the identity.
+__device__ inline uint32_t tie_comb(uint32_t a, uint32_t b) {
+    if (!(a & kTieHas)) return b;
+    if (!(b & kTieHas)) return a;
+    const uint32_t cnt = (a & (kTieHas - 1)) + (b & (kTieHas - 1)) + ((a >> 31) != ((b >> 30) & 1u) ? 1u : 0u);
+    return cnt | kTieHas | (a & (1u << 30)) | (b & (1u << 31));
+}
+__device__ inline uint32_t tie_leaf(uint32_t parity) { return kTieHas | (parity << 30) | (parity << 31); }
+
+__device__ inline uint32_t tie_flip(uint32_t y, uint32_t par) {
+    return (par && (y & kTieHas)) ? y ^ (3u << 30) : y;
+}
+
+// Saturating-sum scans and a min with DPP (no LDS round trips): row_shr:k
+// shifts within 16-lane rows (lanes without a source read 0), row_bcast:15 /
+// :31 add the last lane of the previous row(s) into rows 1, 3 / 2, 3,
+// wave_shr:1 shifts the whole wave by one lane.
+template <int kCtrl, int kRowMask>
+__device__ inline uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xf, false));
+}
+__device__ inline uint32_t row_scan_sat(uint32_t x) {  // inclusive, within each 16-lane row
+    x = sat_add(x, dpp_u32<0x111, 0xf>(x));
+    x = sat_add(x, dpp_u32<0x112, 0xf>(x));
+    x = sat_add(x, dpp_u32<0x114, 0xf>(x));
+    return sat_add(x, dpp_u32<0x118, 0xf>(x));
+}
+__device__ inline uint32_t wave_scan_sat(uint32_t x) {  // inclusive, over the wave
+    x = row_scan_sat(x);
+    x = sat_add(x, dpp_u32<0x142, 0xa>(x));
+    return sat_add(x, dpp_u32<0x143, 0xc>(x));
+}
+__device__ inline uint32_t wave_shr1(uint32_t x) { return dpp_u32<0x138, 0xf>(x); }  // lane 0 reads 0
+__device__ inline uint32_t row_min_u32(uint32_t x) {  // every lane: its row's min
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xf, 0xf, true)));
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xf, 0xf, true)));
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xf, 0xf, true)));
+    return min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xf, 0xf, true)));
+}
+__device__ inline uint32_t wave_min_u32(uint32_t x) {
+    x = row_min_u32(x);
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 0));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 16));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 32));
+    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 48));
+    return min(min(a, b), min(c, d));
+}
+
+// A run of candidates as (integer sum, tie summary with the parities taken as
+// if the run started from an even sum); st_op(a, b) for a followed by b
+// shifts b's parities by a's sum. Associative, (0, 0) the identity, so the
+// sums and the tie corrections come out of one scan.
+struct SumTies {
+    uint32_t s, y;
+};
+__device__ inline SumTies st_op(SumTies a, SumTies b) {
+    return {sat_add(a.s, b.s), tie_comb(a.y, tie_flip(b.y, a.s & 1u))};
+}
+
+__device__ inline uint32_t block_min_u32(uint32_t v, uint32_t* lds) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v = min(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t r = lds[0];
+    for (uint32_t u = 1; u < kT / 64; ++u) r = min(r, lds[u]);
+    return r;
+}
+
+// First j in [0, n) with pred(j), for a predicate that is false then true
+// along j; n if it is false everywhere. Each round probes the last element of
+// kT equal segments (two rounds up to kT * kT elements).
+template <typename Pred>
+__device__ inline uint32_t block_first_true(uint32_t n, Pred pred, uint32_t* lds) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t lo = 0, hi = n;
+    bool first_round = true;
+    while (hi - lo > 1 || (first_round && hi > lo)) {
+        const uint32_t len = hi - lo, step = (len + kT - 1) / kT;
+        const bool in = tid * step < len;
+        const bool ok = in && pred(lo + min((tid + 1) * step, len) - 1);
+        const uint32_t seg = block_min_u32(ok ? tid : kT, lds);
+        __syncthreads();  // lds is rewritten by the next round
+        if (seg == kT) return first_round ? n : hi - 1;  // (later rounds always hold a true element)
+        const uint32_t nlo = lo + seg * step;
+        hi = min(nlo + step, hi);
+        lo = nlo;
+        first_round = false;
+    }
+    return lo;
+}
+
+// Whole-vocabulary sampling (one block): the candidates are the first
+// count = min(limit, finite) sorted pairs; their probabilities, the f32
+// prefix sums above, the top-p cut and the draw.
+__global__ __launch_bounds__(kT) void sample_full_kernel(SampleArgs a, const uint32_t* sk, const uint32_t* ids,
+                                                         const float* prob, float* prefix) {
+    __shared__ unsigned long long red[kT / 64];
+    __shared__ uint32_t l_find[kT / 64];
+    __shared__ uint2 l_scan[kT / 64];                            // waves' (sum, ties) totals
+    __shared__ uint32_t l_first[kT / 64], l_prev[kT / 64];       // waves' first crossing, m before it
+    __shared__ float l_pfirst[kT / 64];                          // and its probability
+    __shared__ float s_last;                                     // the window's last running sum
+    __shared__ uint32_t s_tok;
+    const uint32_t tid = threadIdx.x, V = a.vocab;
+    // Finite count: the first non-finite sort key (they sort last).
+    const uint32_t finite = block_first_true(V, [&](uint32_t j) { return sk[j] == 0xffffffffu; }, l_find);
     const uint32_t limit = min(a.top_k == 0 ? V : a.top_k, V);
-    const uint32_t count = min(limit, s_n);
+    const uint32_t count = min(limit, finite);
     uint32_t tok;
     if (count == 0) {
         // llm.argmax of the raw logits (:111).
@@ -469,48 +737,205 @@ __global__ __launch_bounds__(kT) void sample_full_kernel(SampleArgs a, const uin
         __syncthreads();
         tok = s_tok;
     } else {
-        const float temperature = fmaxf(a.temperature, 1e-6f);
-        const float s0 = key_value(keys[0]);
-        for (uint32_t j = tid; j < count; j += kT) {
-            const float p = expf(__fdiv_rn(__fsub_rn(key_value(keys[j]), s0), temperature));
-            prob[j] = isfinite(p) ? p : 0.0f;
-        }
-        __syncthreads();
-        if (tid == 0) {  // sequential sums in candidate order, 16 loads ahead of the adds
-            float c = 0.0f;
-            uint32_t j = 0;
-            for (; j + 16 <= count; j += 16) {
-                float v[16];
+        const uint32_t lane = tid & 63, wv = tid >> 6;
+        // Chain state, the same in every thread: the running sum, the next
+        // candidate to add and the width of the next window of candidates.
+        float c = 0.0f;
+        uint32_t pos = 0, width = kChainW0;
+        // The next chunk's probabilities, loaded a chunk ahead: two 16-byte
+        // loads from a clamped offset (the buffer holds a multiple of 64
+        // words, so the clamp stays inside it; positions at or past count are
+        // not used).
+        const uint32_t plim = (V + 63) / 64 * 64 - kChainE;
+        float pn[kChainE];
+        auto load_probs = [&](uint32_t base) {
+            const uint32_t jj = min(base + tid * kChainE, plim);
+            const float4 q0 = *reinterpret_cast<const float4*>(prob + jj);
+            const float4 q1 = *reinterpret_cast<const float4*>(prob + jj + 4);
+            pn[0] = q0.x, pn[1] = q0.y, pn[2] = q0.z, pn[3] = q0.w;
+            pn[4] = q1.x, pn[5] = q1.y, pn[6] = q1.z, pn[7] = q1.w;
+        };
+        load_probs(0);
+        for (uint32_t cbase = 0; cbase < count; cbase += kChainChunk) {
+            const uint32_t cend = min(cbase + kChainChunk, count);
+            const uint32_t j0 = cbase + tid * kChainE;
+            float p[kChainE];
 #pragma unroll
-                for (int q = 0; q < 16; ++q) v[q] = prob[j + q];
+            for (int i = 0; i < kChainE; ++i) {
+                const uint32_t j = j0 + i;
+                p[i] = j < cend ? pn[i] : 0.0f;
+                if (a.trace_probs && j < cend) a.trace_probs[j] = p[i];
+            }
+            if (cend < count) load_probs(cend);
+            while (pos < cend) {
+                // Candidates [pos, wend) in the binade of c; waves holding none
+                // of them skip the arithmetic.
+                const uint32_t wend = min(cend, pos + width);
+                const uint32_t bits = __float_as_uint(c);
+                // c >= 2^-100 keeps both power-of-two scalings below in range
+                // (in practice c >= 1: the first candidate's probability is 1).
+                const bool normal = c >= 7.88860905e-31f;
+                const int e = static_cast<int>((bits >> 23) & 255u) - 127;
+                const uint32_t m = (bits & 0x7fffffu) | 0x800000u;
+                const float scale = normal ? __uint_as_float(static_cast<uint32_t>(150 - e) << 23) : 0.0f;  // 2^(23-e)
+                const float ulp = normal ? __uint_as_float(static_cast<uint32_t>(104 + e) << 23) : 0.0f;    // 2^(e-23)
+                const uint32_t wlo = cbase + wv * 64 * kChainE;
+                const bool wact = normal && wlo < wend && wlo + 64 * kChainE > pos;  // uniform in the wave
+                uint32_t tl[kChainE], ties = 0;
+                SumTies mine = {0u, 0u};
+                if (wact) {
+                    uint32_t run = 0;
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    c = __fadd_rn(c, v[q]);
-                    prefix[j + q] = c;
+                    for (int i = 0; i < kChainE; ++i) {
+                        const uint32_t j = j0 + i;
+                        const bool act = j >= pos && j < wend;
+                        // Clamped: a larger x leaves the binade anyway (a restart).
+                        const float x = fminf(p[i] * scale, 33554432.0f);
+                        const float fl = floorf(x);
+                        const float fr = x - fl;  // exact
+                        ties |= (act && fr == 0.5f) ? (1u << i) : 0u;
+                        run = sat_add(run, act ? static_cast<uint32_t>(fl) + (fr > 0.5f ? 1u : 0u) : 0u);
+                        tl[i] = run;
+                    }
+                    uint32_t y = 0;
+                    if (__any(ties != 0u)) {
+#pragma unroll
+                        for (int i = 0; i < kChainE; ++i)
+                            if ((ties >> i) & 1u) y = tie_comb(y, tie_leaf(tl[i] & 1u));
+                    }
+                    mine = {run, y};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kChainE; ++i) tl[i] = 0u;
+                }
+                // Exclusive (sum, ties) scan over the block in candidate order:
+                // within the wave, then over the waves' totals (lanes 0-15 of
+                // every wave); sums alone where no tie is in play.
+                SumTies up = {0u, 0u};
+                if (wact) {
+                    SumTies x = mine;
+                    if (__any(mine.y != 0u)) {
+#pragma unroll
+                        for (int off = 1; off < 64; off <<= 1) {
+                            const SumTies o = {static_cast<uint32_t>(__shfl_up(static_cast<int>(x.s), off, 64)),
+                                               static_cast<uint32_t>(__shfl_up(static_cast<int>(x.y), off, 64))};
+                            if (lane >= static_cast<uint32_t>(off)) x = st_op(o, x);
+                        }
+                        up = {static_cast<uint32_t>(__shfl_up(static_cast<int>(x.s), 1, 64)),
+                              static_cast<uint32_t>(__shfl_up(static_cast<int>(x.y), 1, 64))};
+                    } else {
+                        x.s = wave_scan_sat(x.s);
+                        up = {wave_shr1(x.s), 0u};
+                    }
+                    if (lane == 63) l_scan[wv] = make_uint2(x.s, x.y);
+                } else if (lane == 63) {
+                    l_scan[wv] = make_uint2(0u, 0u);
+                }
+                __syncthreads();
+                SumTies wt = {0u, 0u};
+                if (lane < kT / 64) wt = {l_scan[lane].x, l_scan[lane].y};
+                if (__any(wt.y != 0u)) {
+#pragma unroll
+                    for (int off = 1; off < kT / 64; off <<= 1) {
+                        const SumTies o = {static_cast<uint32_t>(__shfl_up(static_cast<int>(wt.s), off, 64)),
+                                           static_cast<uint32_t>(__shfl_up(static_cast<int>(wt.y), off, 64))};
+                        if (lane >= static_cast<uint32_t>(off)) wt = st_op(o, wt);
+                    }
+                } else {
+                    wt.s = row_scan_sat(wt.s);  // lanes 0-15 are row 0
+                }
+                SumTies ex = {0u, 0u};
+                const int wsrc = __builtin_amdgcn_readfirstlane(static_cast<int>(wv)) - 1;  // uniform
+                if (wsrc >= 0)
+                    ex = {static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wt.s), wsrc)),
+                          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wt.y), wsrc))};
+                if (lane != 0) ex = st_op(ex, up);
+                // m_j for this thread's candidates, and its first one leaving the binade.
+                uint32_t mv[kChainE];
+                uint32_t first = 0xffffffffu, prev_first = 0;
+                float p_first = 0.0f;
+                if (wact) {
+                    const uint32_t yin = tie_comb(tie_leaf(0u), tie_flip(ex.y, m & 1u));
+                    uint32_t corr = yin & (kTieHas - 1), lp = yin >> 31;
+                    const uint32_t mb = sat_add(m, ex.s);
+                    uint32_t prev = sat_add(mb, corr);
+#pragma unroll
+                    for (int i = 0; i < kChainE; ++i) {
+                        const uint32_t j = j0 + i;
+                        const uint32_t t = sat_add(mb, tl[i]);
+                        if ((ties >> i) & 1u) {
+                            const uint32_t par = t & 1u;
+                            corr += par != lp ? 1u : 0u;
+                            lp = par;
+                        }
+                        mv[i] = sat_add(t, corr);
+                        const bool act = j >= pos && j < wend;
+                        const uint32_t fl = static_cast<uint32_t>(floorf(fminf(p[i] * scale, 33554432.0f)));
+                        if (act && first == 0xffffffffu && sat_add(prev, fl) >= (1u << 24)) {
+                            first = j;
+                            prev_first = prev;
+                            p_first = p[i];
+                        }
+                        if (j == wend - 1) s_last = static_cast<float>(mv[i]) * ulp;
+                        prev = mv[i];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kChainE; ++i) mv[i] = 0u;
+                }
+                if (!normal && j0 <= pos && pos < j0 + kChainE) {  // a plain f32 add
+                    first = pos;
+#pragma unroll
+                    for (int i = 0; i < kChainE; ++i) p_first = j0 + i == pos ? p[i] : p_first;
+                }
+                // The block's first crossing with its operands, to every thread.
+                const uint32_t wmin = wave_min_u32(first);
+                if (lane == 0) l_first[wv] = wmin;
+                if (first != 0xffffffffu && first == wmin) {
+                    l_prev[wv] = prev_first;
+                    l_pfirst[wv] = p_first;
+                }
+                __syncthreads();
+                const uint32_t fw = lane < kT / 64 ? l_first[lane] : 0xffffffffu;
+                const uint32_t stop =
+                    static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_min_u32(fw)), 0));
+                uint32_t prev_stop = 0;
+                float p_stop = 0.0f;
+                if (stop != 0xffffffffu) {
+                    const int u = __ffsll(static_cast<unsigned long long>(__ballot(lane < kT / 64 && fw == stop))) - 1;
+                    prev_stop = l_prev[u];
+                    p_stop = l_pfirst[u];
+                }
+                const uint32_t done = min(stop, wend);
+#pragma unroll
+                for (int i = 0; i < kChainE; ++i) {
+                    const uint32_t j = j0 + i;
+                    if (j >= pos && j < done) prefix[j] = static_cast<float>(mv[i]) * ulp;  // exact
+                }
+                if (stop < wend) {
+                    const float cp = stop == pos ? c : static_cast<float>(prev_stop) * ulp;
+                    c = __fadd_rn(cp, p_stop);
+                    if (j0 <= stop && stop < j0 + kChainE) prefix[stop] = c;
+                    width = min(max(2 * (stop - pos + 1), kChainW0), kChainChunk);
+                    pos = stop + 1;
+                } else {
+                    c = s_last;
+                    width = min(2 * width, kChainChunk);
+                    pos = wend;
                 }
             }
-            for (; j < count; ++j) {
-                c = __fadd_rn(c, prob[j]);
-                prefix[j] = c;
-            }
-            s_cut = count;
-            s_pick = 0xffffffffu;
         }
-        __syncthreads();
-        const float total = prefix[count - 1];
+        __syncthreads();  // every thread's sums are stored
+        const float total = c;  // prefix[count - 1]
         // prepareProbabilities' top-p cut: the first j with prefix[j] / total >= top_p.
         const bool bad_total = total <= 0.0f || !isfinite(total);
+        uint32_t k = bad_total ? 1u : count;
         if (!bad_total && a.top_p < 1.0f) {
-            uint32_t first = count;
-            for (uint32_t j = tid; j < count; j += kT)
-                if (__fdiv_rn(prefix[j], total) >= a.top_p) {
-                    first = j;
-                    break;
-                }
-            atomicMin(&s_cut, first == count ? count : first + 1);
+            const float top_p = a.top_p;
+            const uint32_t first =
+                block_first_true(count, [&](uint32_t j) { return __fdiv_rn(prefix[j], total) >= top_p; }, l_find);
+            k = first == count ? count : first + 1;
         }
-        __syncthreads();
-        const uint32_t k = bad_total ? 1u : s_cut;
         // sampleCandidate with one draw of Random.float(f32).
         __shared__ float s_target;
         __shared__ uint32_t s_ok;
@@ -523,27 +948,26 @@ __global__ __launch_bounds__(kT) void sample_full_kernel(SampleArgs a, const uin
             s_target = __fmul_rn(fminf(u, 0.99999994f), t2);
         }
         __syncthreads();
+        uint32_t pick = 0;
         if (s_ok) {
             const float target = s_target;
-            uint32_t first = 0xffffffffu;
-            for (uint32_t j = tid; j < k; j += kT)
-                if (target <= prefix[j]) {
-                    first = j;
-                    break;
-                }
-            atomicMin(&s_pick, first);
+            const uint32_t first = block_first_true(k, [&](uint32_t j) { return target <= prefix[j]; }, l_find);
+            pick = first == k ? k - 1 : first;
         }
-        __syncthreads();
-        const uint32_t pick = !s_ok ? 0u : (s_pick == 0xffffffffu ? k - 1 : s_pick);
         tok = ids[pick];
+        for (uint32_t j = tid; j < count; j += kT) {
+            if (a.trace_ids) a.trace_ids[j] = ids[j];
+            if (a.trace_sums) a.trace_sums[j] = prefix[j];
+        }
     }
     if (tid != 0) return;
+    if (a.trace_count) *a.trace_count = count;
     sample_finish(a, tok);
 }
 
 // Advance the step state as the greedy finish does, then the repeat window
 // (the sampling block's thread 0, with the sampled token).
-__device__ __noinline__ void sample_finish(const SampleArgs& a, uint32_t tok) {
+__device__ __forceinline__ void sample_finish(const SampleArgs& a, uint32_t tok) {
     if (a.result) *a.result = tok;
     StepState* st = a.state;
     if (!st) return;
@@ -582,23 +1006,17 @@ size_t sample_cand_elems(uint32_t vocab) {
 }
 size_t sample_nf_elems(uint32_t vocab) { return (vocab + kLocalIds - 1) / kLocalIds; }
 
-// Whole-vocabulary scratch: [keys in | keys out | ids in | ids out | prob |
-// prefix] of vocab words each (256-byte aligned), then the sort's storage.
+// Whole-vocabulary scratch: [sort keys A | sort keys B | ids A | ids B |
+// probabilities | prefix sums] of vocab words each (256-byte aligned, so each
+// holds a multiple of 64 words), then the tiles' digit histograms (256 words
+// per tile).
 namespace {
 size_t full_word_bytes(uint32_t vocab) { return ((size_t)vocab * 4 + 255) / 256 * 256; }
-size_t full_sort_bytes(uint32_t vocab) {
-    size_t bytes = 0;
-    const hipError_t e = rocprim::radix_sort_pairs_desc(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
-                                                        static_cast<uint32_t*>(nullptr),
-                                                        static_cast<const uint32_t*>(nullptr),
-                                                        static_cast<uint32_t*>(nullptr), vocab, 0, 32);
-    return e == hipSuccess ? bytes : 0;
-}
+uint32_t full_tiles(uint32_t vocab) { return (vocab + kSortTile - 1) / kSortTile; }
 }  // namespace
 
 size_t sample_full_bytes(uint32_t vocab) {
-    const size_t sort = full_sort_bytes(vocab);
-    return sort ? 6 * full_word_bytes(vocab) + sort : 0;
+    return vocab ? 6 * full_word_bytes(vocab) + (size_t)full_tiles(vocab) * 256 * sizeof(uint32_t) : 0;
 }
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
@@ -606,19 +1024,30 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
         if (!a.full) return hipErrorInvalidValue;
         const size_t wb = full_word_bytes(a.vocab);
         char* base = static_cast<char*>(a.full);
-        uint32_t* k_in = reinterpret_cast<uint32_t*>(base);
-        uint32_t* k_out = reinterpret_cast<uint32_t*>(base + wb);
-        uint32_t* i_in = reinterpret_cast<uint32_t*>(base + 2 * wb);
-        uint32_t* i_out = reinterpret_cast<uint32_t*>(base + 3 * wb);
+        uint32_t* sk[2] = {reinterpret_cast<uint32_t*>(base), reinterpret_cast<uint32_t*>(base + wb)};
+        uint32_t* id[2] = {reinterpret_cast<uint32_t*>(base + 2 * wb), reinterpret_cast<uint32_t*>(base + 3 * wb)};
         float* prob = reinterpret_cast<float*>(base + 4 * wb);
         float* prefix = reinterpret_cast<float*>(base + 5 * wb);
-        size_t sort_bytes = full_sort_bytes(a.vocab);
-        hipError_t e = vlaunch(sample_full_keys_kernel, dim3((a.vocab + 255) / 256), dim3(256), 0, s, a, k_in, i_in);
+        uint32_t* hist = reinterpret_cast<uint32_t*>(base + 6 * wb);
+        const uint32_t tiles = full_tiles(a.vocab);
+        hipError_t e = vlaunch(full_keys_kernel, dim3(tiles), dim3(kSortThreads), 0, s, a, sk[0], id[0], hist);
+        // Four stable 8-bit passes, A -> B -> A -> B -> A.
+        for (uint32_t pass = 0; pass < 4 && e == hipSuccess; ++pass) {
+            const uint32_t in = pass & 1u, shift = 8 * pass;
+            if (pass > 0)
+                e = vlaunch(full_hist_kernel, dim3(tiles), dim3(kSortThreads), 0, s,
+                            static_cast<const uint32_t*>(sk[in]), a.vocab, shift, hist);
+            if (e == hipSuccess)
+                e = vlaunch(full_scatter_kernel, dim3(tiles), dim3(kSortThreads), 0, s,
+                            static_cast<const uint32_t*>(sk[in]), static_cast<const uint32_t*>(id[in]), sk[in ^ 1u],
+                            id[in ^ 1u], a.vocab, shift, static_cast<const uint32_t*>(hist), tiles);
+        }
         if (e == hipSuccess)
-            e = rocprim::radix_sort_pairs_desc(static_cast<void*>(base + 6 * wb), sort_bytes,
-                                               static_cast<const uint32_t*>(k_in), k_out,
-                                               static_cast<const uint32_t*>(i_in), i_out, a.vocab, 0, 32, s);
-        if (e == hipSuccess) e = vlaunch(sample_full_kernel, dim3(1), dim3(kT), 0, s, a, k_out, i_out, prob, prefix);
+            e = vlaunch(full_probs_kernel, dim3(tiles), dim3(kSortThreads), 0, s, static_cast<const uint32_t*>(sk[0]),
+                        a.vocab, a.temperature, prob);
+        if (e == hipSuccess)
+            e = vlaunch(sample_full_kernel, dim3(1), dim3(kT), 0, s, a, static_cast<const uint32_t*>(sk[0]),
+                        static_cast<const uint32_t*>(id[0]), static_cast<const float*>(prob), prefix);
         return e;
     }
     SampleArgs b = a;

@@ -368,6 +368,22 @@ def sampler_next(logits: np.ndarray, prompt, generated, opts: Sampling, prng_sta
     return tok.value
 
 
+def sampler_trace(logits: np.ndarray, opts: Sampling, prng_state: np.ndarray):
+    """vvli_gpu_test_sampler_trace: the whole-vocabulary sampler's token and, in
+    candidate order, its candidates' ids, probabilities and running f32 sums."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    assert prng_state.dtype == np.uint64 and prng_state.size == 4 and prng_state.flags.c_contiguous
+    ids = np.zeros(lg.size, np.uint32)
+    probs = np.zeros(lg.size, np.float32)
+    sums = np.zeros(lg.size, np.float32)
+    tok, count = c_uint32(), c_uint32()
+    c = opts.to_c()
+    _lib.check(_lib.lib().vvli_gpu_test_sampler_trace(_ptr(lg), lg.size, byref(c), _ptr(prng_state), byref(tok),
+                                                      _ptr(ids), _ptr(probs), _ptr(sums), byref(count)))
+    n = count.value
+    return tok.value, ids[:n], probs[:n], sums[:n]
+
+
 def linear(dW: int, dX: int, dY: int, M: int, N: int, K: int, dBias: int | None = None, stream: int | None = None) -> None:
     """vvli_gpu_linear on raw device pointers (e.g. torch ``tensor.data_ptr()``)."""
     _lib.check(_lib.lib().vvli_gpu_linear(c_void_p(dW), c_void_p(dX), None if dBias is None else c_void_p(dBias),
