@@ -660,11 +660,23 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
 // same batch as the activation (into nws = xs + n). arrived() runs on every
 // thread once its share of the input is in registers, before the block-wide
 // normalisation. False: a poll failed.
-template <typename F>
+// The thread index, optionally through an empty asm: the lane-dependent
+// addresses derived from it are then formed where the phase runs instead of
+// being hoisted to the kernel's start and held (or spilled) across every
+// phase. Pinned in the variants that would otherwise spill; the hd-64 exact
+// step keeps them hoisted (no spills there, and a shorter staging path).
+template <bool kPin>
+__device__ __forceinline__ int mk_tid() {
+    int tid = threadIdx.x;
+    if constexpr (kPin) asm volatile("" : "+v"(tid));
+    return tid;
+}
+
+template <bool kPin = false, typename F>
 __device__ __forceinline__ bool mk_stage(float* xs, float* red, const tword* src, uint32_t tag,
                                          const uint16_t* src_bf16, const uint16_t* norm_w, float eps, uint32_t n,
                                          uint32_t* err, unsigned long long* tmark, F&& arrived) {
-    const int tid = threadIdx.x;
+    const int tid = mk_tid<kPin>();
     // Detail timing (profiling runs only): thread 0 records its entry, the
     // return of its first attempt, and its retry count.
     if (tmark && tid == 0) tmark[0] = __builtin_amdgcn_s_memrealtime();
@@ -807,7 +819,7 @@ struct AttnLds {
 __device__ __forceinline__ bool mk_qk_scales(const DecodeStepParams& p, uint32_t tag, float& scq, float& sck,
                                              float* qk_lds) {
     __shared__ float red2[2][kMkWaves];
-    const int tid = threadIdx.x;
+    const int tid = mk_tid<true>();  // MoE variants only
     const uint32_t nq = p.heads * p.hd, n2 = (nq + p.kvdim) / 2;  // word pairs of q | k (nq is even)
     const __amdgpu_buffer_rsrc_t r = coh_rsrc(p.tqkv, n2 * 16);
     constexpr int B = 4;
@@ -870,7 +882,8 @@ __device__ __forceinline__ bool mk_attention(const DecodeStepParams& p, uint32_t
     constexpr int TILE = LY::TILE, KS = LY::KS;
     constexpr int NP = (kMaxGroupMk * HDMAX + kMkThreads - 1) / kMkThreads;
     constexpr int NT = (TILE * HDMAX / 4 + kMkThreads - 1) / kMkThreads;  // float4 of a K (V) tile per thread
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = mk_tid<!(HDMAX == 64 && EXACT && !MOE)>();
+    const int lane = tid & 63, wave = tid >> 6;
     const int hd = EXACT ? HDMAX : (int)p.hd;
     const int half = hd / 2;
     const int vpr = hd / 4;
@@ -1628,7 +1641,7 @@ __device__ __forceinline__ bool mk_route(const DecodeStepParams& p, uint32_t lay
     }
     if (!need) return true;
     bool ok = true;
-    const int tid = threadIdx.x;
+    const int tid = mk_tid<true>();  // MoE variants only
     if ((uint32_t)tid < E) {
         tword wv = ld_a(p.trl + tid);
         ok = poll_tw(p.trl + tid, tag, wv, p.error);
@@ -1775,7 +1788,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     auto first_weights = [&]() {
                         if (!have && !gl.n && !routes) have = mk_prefetch<MOE>(g, mode, wp, buf, tile, 0, s_ex);
                     };
-                    ok = mk_stage(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
+                    ok = mk_stage<HDMAX == 128 && (MOE || !EXACT)>(smem, red, src, tag - 1, ph == 0 ? emb : nullptr, mk_norm_of(p, tb, f), p.eps,
                                   f.kind == kPhD ? p.inter : H, p.error,
                                   (p.timing && p.timing_slots == 16 && (ph + 1) * 16 <= p.timing_stride)
                                       ? p.timing + blockIdx.x * p.timing_stride + ph * 16 + 9
@@ -1852,7 +1865,7 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 b = k > b ? k : b;
             }
             b = wave_max_u64(b);
-            if (w.lane == 0) kred[tid >> 6] = b;
+            if (w.lane == 0) kred[wave] = b;
             if (__syncthreads_or(!ok)) return;
             if (tid == 0) {
                 for (int i = 0; i < kMkWaves; ++i) b = kred[i] > b ? kred[i] : b;

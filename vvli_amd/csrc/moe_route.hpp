@@ -20,7 +20,10 @@ namespace vvli {
 template <int NT>
 __device__ inline void route_block(float* logits, uint32_t E, uint32_t top_k, uint32_t* idx, float* weight,
                                    unsigned long long* keys, uint32_t* rank) {
-    const int tid = threadIdx.x;
+    // The thread index through an empty asm, so that the addresses derived
+    // from it are formed here rather than hoisted to a caller's start.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     if (tid < 64) {  // (experts walked per lane, not held in registers: the callers run near their limit)
         float mx = -INFINITY;
         for (uint32_t e = tid; e < E; e += 64) mx = fmaxf(mx, logits[e]);
