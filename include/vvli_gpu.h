@@ -2,7 +2,7 @@
  * vvli_gpu.h -- C ABI of the MI355X (gfx950) dense-decoder forward pass.
  *
  * This is the drop-in boundary for VVLI's CPU runner. A Zig host binds it with
- * @cImport (see INTEGRATION.md) and keeps its runner/generator API; the
+ * @cImport and keeps its runner/generator API; the
  * library holds the weights, the KV cache and all activations in HBM and runs
  * hand-written HIP kernels.
  *
