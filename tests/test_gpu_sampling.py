@@ -306,3 +306,27 @@ def test_generate_whole_vocab_matches_oracle(path, oracle_mod, host_threads):
         gpu.set_decode_path(path)
         got, st = gpu.generate(prompt, 40, o, batched_prefill=True)
     np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("path", ["persistent", "graph"])
+def test_generate_whole_vocab_llama_vocab(path, oracle_mod, host_threads):
+    """Sampled generation with top_k 0 over Llama-3's 128256-id vocabulary
+    (the benchmark's whole-vocabulary case, on a small model): the same tokens
+    as the oracle on both decode paths, with the repeat penalty active. Every
+    step sorts and sums all 128256 candidates; N(0, 0.6) weights spread the
+    logits (std ~10: the top ten ids hold ~99 % of the mass), so the top-p cut
+    and the pick sit in clear gaps -- with near-flat logits the ~1e-6 logit
+    differences of the two forward passes (their summation orders) move the
+    pick among ~1e5 nearly equal candidates, which says nothing about the
+    sampler (sampler_next gets identical logits on both sides above)."""
+    cfg = cfg_small(vocab_size=128256)
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=3, stddev=0.6)
+    o = opts(top_k=0, top_p=0.95, temperature=0.8, seed=5)
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab_size, 16).astype(np.uint32)
+    orc = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+    ref = orc.generate_sampled(prompt, 24, o)
+    print(f"generate whole vocab 128256 path={path}", flush=True)
+    with R.Runner(cfg, blob, 64) as gpu:
+        gpu.set_decode_path(path)
+        got, _ = gpu.generate(prompt, 24, o, batched_prefill=True)
+    np.testing.assert_array_equal(got, ref)
