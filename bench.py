@@ -755,27 +755,32 @@ def main() -> int:
         torch.cuda.synchronize()
 
     # The drop-in forwardToken boundary as a per-token caller drives it (one
-    # call per token, synchronous; with the 4 * vocab-byte logits copy to the
-    # host, or the argmax only), on the same decode path, continuing after the
-    # generated tokens. Wall clock per call.
+    # call per token, synchronous; the 4 * vocab-byte logits copied into the
+    # caller's buffer, or returned as the borrowed view of the library's
+    # pinned copy -- the reference's slice return -- or the argmax only), on
+    # the same decode path, continuing after the generated tokens. Wall clock
+    # per call.
     ft = {}
     n_ft = 32
-    if args.prompt + args.steps + 2 * n_ft <= args.ctx:
+    if args.prompt + args.steps + 3 * n_ft <= args.ctx:
         pos = args.prompt + args.steps
         tok = int(tokens[-1])
-        for kind in ("logits", "argmax"):
+        for kind in ("logits", "view", "argmax"):
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             for _ in range(n_ft):
                 if kind == "logits":
                     tok = int(np.argmax(runner.forward_token(tok, pos)))
+                elif kind == "view":
+                    tok = int(np.argmax(runner.forward_token_view(tok, pos)))
                 else:
                     tok = runner.forward_token_argmax(tok, pos)
                 pos += 1
             ft[f"us_per_call_{kind}"] = round((time.perf_counter() - t1) / n_ft * 1e6, 1)
         ft["calls"] = n_ft
-        print(f"[bench] forward_token: {ft['us_per_call_logits']} us/call with logits to host, "
-              f"{ft['us_per_call_argmax']} us/call argmax only", file=sys.stderr, flush=True)
+        print(f"[bench] forward_token: {ft['us_per_call_logits']} us/call with logits into the caller's buffer, "
+              f"{ft['us_per_call_view']} as the pinned view, {ft['us_per_call_argmax']} argmax only",
+              file=sys.stderr, flush=True)
 
     # GEMV half of the metric: the isolated op at M = 1 on the five projection
     # shapes of the model (cold weights), HBM GB/s per shape.

@@ -161,6 +161,14 @@ int vvli_gpu_set_rope_table(vvli_gpu_model* model, const float* inv_freq, uint32
  * argmax_out (llm.argmax of the logits, src/llm.zig:778-789) are optional. */
 int vvli_gpu_forward_token(vvli_gpu_model* model, uint32_t token, uint32_t pos, float* logits_out,
                            uint32_t* argmax_out);
+/* Runner.forwardToken with the reference's return convention: it returns a
+ * borrowed slice of scratch.logits, valid until the next call
+ * (src/llm.zig:702-709,729). *logits_view points at the library's pinned host
+ * copy of the vocab logits, overwritten by the next forward_token_view call
+ * on this model and freed with it (set only on success); argmax_out is
+ * optional. Same errors as vvli_gpu_forward_token. */
+int vvli_gpu_forward_token_view(vvli_gpu_model* model, uint32_t token, uint32_t pos, const float** logits_view,
+                                uint32_t* argmax_out);
 /* Runner.forwardEmbedding, src/llm.zig:711-718: embedding = hidden floats (host). */
 int vvli_gpu_forward_embedding(vvli_gpu_model* model, const float* embedding, uint32_t pos, float* logits_out,
                                uint32_t* argmax_out);
@@ -265,11 +273,12 @@ int vvli_gpu_set_prefill_path(vvli_gpu_model* model, uint32_t path);
  * persistent launch. */
 int vvli_gpu_profile_persistent(vvli_gpu_model* model, uint32_t token, uint32_t pos, uint64_t* ticks_out,
                                 uint32_t stride, uint32_t* n_blocks);
-/* Device time of the last persistent launch on this model (HIP events
+/* Device time of the last timed persistent launch on this model (HIP events
  * recorded on the model's stream right before and after the cooperative
  * launch), in milliseconds; for generate_greedy that is its decode launch,
- * for prefill its one launch. VVLI_INVALID_CONFIG if no persistent launch
- * has run. Waits for the launch to finish. */
+ * for prefill its one launch. Single-step forward_token launches are not
+ * timed. VVLI_INVALID_CONFIG if no timed persistent launch has run. Waits for
+ * the launch to finish. */
 int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
 /* Test hook for the persistent step's failure path (no reference
  * counterpart): the n-th persistent launch from now (n >= 1; 0 cancels)

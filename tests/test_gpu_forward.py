@@ -157,6 +157,43 @@ def test_persistent_steps_match_oracle(name, built, oracle_mod, host_threads):
 
 
 @pytest.mark.parametrize("path", ["graph", "persistent"])
+@pytest.mark.parametrize("name", ["qwen_small", "llama_small"])
+def test_forward_token_return_forms_match_oracle(name, path, built, oracle_mod, host_threads):
+    """The three ways a per-token caller reads a step: logits copied into its
+    buffer, the borrowed view of the library's pinned logits (the reference's
+    slice return, src/llm.zig:729), and the argmax only -- interleaved over
+    consecutive positions, each against the oracle. The view keeps its
+    address, is read-only, and holds the latest call's logits."""
+    cfg, kind, how, _ = CASES[name]
+    blob = make_blob(cfg, kind, how)
+    orc = oracle_mod.OracleRunner(cfg, blob, 128, threads=host_threads)
+    toks = np.random.default_rng(3).integers(0, cfg.vocab_size, size=30)
+    print(f"case={name} path={path} return forms", flush=True)
+    addr = None
+    with R.Runner(cfg, blob, 128) as gpu:
+        gpu.set_decode_path(path)
+        for pos, tok in enumerate(toks):
+            ref = orc.forward_token(int(tok), pos)
+            form = pos % 3
+            if form == 0:
+                got = gpu.forward_token(int(tok), pos)
+                assert rel_err(got, ref) <= TOL, f"{name} pos {pos}: logits"
+                am = gpu.last_argmax
+            elif form == 1:
+                view = gpu.forward_token_view(int(tok), pos)
+                assert not view.flags.writeable and view.size == cfg.vocab_size
+                a = view.__array_interface__["data"][0]
+                assert addr is None or a == addr, "the view moved"
+                addr = a
+                assert rel_err(view, ref) <= TOL, f"{name} pos {pos}: view logits"
+                am = gpu.last_argmax
+                assert am == R.argmax(view)
+            else:
+                am = gpu.forward_token_argmax(int(tok), pos)
+            assert am == oracle_mod.argmax(ref), f"{name} pos {pos} form {form}: argmax"
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7"])
 def test_greedy_generation_matches_oracle(name, path, built, oracle_mod, host_threads):
     cfg, kind, how, _ = CASES[name]
@@ -258,6 +295,7 @@ def test_persistent_error_flag_is_reported(built, oracle_mod, host_threads):
     lib = R._lib.lib()
     toks = [5, 77, 300, 12]
     orc = oracle_mod.OracleRunner(cfg, blob, 64, threads=host_threads)
+    orc_ref1 = None
     print("inject: forward_token", flush=True)
     with R.Runner(cfg, blob, 64) as gpu:
         gpu.set_decode_path("persistent")
@@ -269,10 +307,21 @@ def test_persistent_error_flag_is_reported(built, oracle_mod, host_threads):
         # The flag was read and cleared: the step runs again and the runner continues.
         for pos in range(len(toks)):
             ref = orc.forward_token(toks[pos], pos)
+            if pos == 1:
+                orc_ref1 = ref.copy()
             if pos == 0:
                 continue
             got = gpu.forward_token(toks[pos], pos)
             assert rel_err(got, ref) <= TOL and gpu.last_argmax == oracle_mod.argmax(ref)
+        # The same on the argmax-only and view calls (no logits copy).
+        for call in (gpu.forward_token_argmax, gpu.forward_token_view):
+            R._lib.check(lib.vvli_gpu_test_inject_step_error(gpu._h, 1))
+            with pytest.raises(VvliError) as e:
+                call(toks[1], 1)
+            assert e.value.rc == 8 and "injected" in str(e.value)
+            out = call(toks[1], 1)
+            am = out if isinstance(out, int) else gpu.last_argmax
+            assert am == oracle_mod.argmax(orc_ref1)
     print("inject: sampled generation, third per-token launch", flush=True)
     prompt = np.array(toks, dtype=np.uint32)
     opts = R.Sampling(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=7)

@@ -76,6 +76,10 @@ __device__ __forceinline__ void st_a(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void st_a(tword* p, tword v) {
     __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Pinned host memory (vector store at system scope).
+__device__ __forceinline__ void st_sys(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 __device__ __forceinline__ tword tw_make(float v, uint32_t tag) {
@@ -1685,8 +1689,22 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
         p.timing[(size_t)gridDim.x * p.timing_stride] = __builtin_amdgcn_s_memrealtime();
     const MkTables tb = mk_load_tables(p, reinterpret_cast<char*>(smem) + p.table_lds_offset);
     if (tid == 0) {
-        s_ctl[0] = ld_a(&p.state->token);
-        s_ctl[1] = ld_a(&p.state->pos);
+        if (p.init_step) {
+            s_ctl[0] = p.init_token;
+            s_ctl[1] = p.init_pos;
+            if (blockIdx.x == 0) {  // the same thread finishes the step and reads these back
+                st_a(&p.state->token, p.init_token);
+                st_a(&p.state->pos, p.init_pos);
+                st_a(&p.state->n_out, 0u);
+                st_a(&p.state->counting, 0u);
+                st_a(&p.state->argmax, 0u);
+                st_a(&p.state->prompt_len, 0u);
+                st_a(&p.state->stop, 0u);
+            }
+        } else {
+            s_ctl[0] = ld_a(&p.state->token);
+            s_ctl[1] = ld_a(&p.state->pos);
+        }
         s_ctl[3] = ld_a(p.error);
     }
     __syncthreads();
@@ -1889,6 +1907,15 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 if (step + 1 < p.n_steps) st_a(p.step_word, tw_make_u(stop ? 0xffffffffu : next_tok, e0 + nps - 1));
             }
         }
+    }
+    // The thread that finished every step (or saw the stop or the error flag)
+    // reports to the host; the step state holds its own last writes.
+    if (p.host_out && blockIdx.x == 0 && tid == 0) {
+        HostStepOut* h = p.host_out;
+        st_sys(&h->argmax, ld_a(&p.state->argmax));
+        st_sys(&h->stop, ld_a(&p.state->stop));
+        st_sys(&h->error, ld_a(p.error));
+        st_sys(&h->seq, p.host_seq);
     }
 }
 

@@ -153,7 +153,20 @@ struct DecodeGemv {
 
 // Values of DecodeStepParams::error: a poll passed its spin limit, the step
 // state was out of range, or the host raised it before the launch (test hook).
+// The word is zero at a launch's start unless an earlier launch of an
+// unchecked sequence failed; the host clears it once it has reported it.
 enum : uint32_t { kDecodeErrTimeout = 1, kDecodeErrState = 2, kDecodeErrInjected = 3 };
+
+// What the persistent step's finishing thread leaves in pinned host memory at
+// the end of its last step: the argmax, the stop flag, the device error word
+// as it read it, then the launch's sequence number (the host compares it with
+// the one it passed: a launch whose blocks left early never writes it).
+struct HostStepOut {
+    uint32_t seq;
+    uint32_t argmax;
+    uint32_t stop;
+    uint32_t error;
+};
 
 // Activations of the persistent step are arrays of tagged 64-bit words: the
 // f32 value (or u32) in the low half, the epoch of the phase that wrote it in
@@ -214,6 +227,13 @@ struct DecodeStepParams {
     // `inter` is then top_k * the expert width (the down phase's staged input).
     uint32_t experts, top_k;
     unsigned long long* trl;
+    // Single-step calls (init_step != 0): the token and position come from
+    // here instead of the step state, which block 0's first thread then
+    // initialises (no prompt, no counting) before any phase.
+    uint32_t init_step, init_token, init_pos;
+    // Nullable pinned host memory, written at the end of the last step.
+    HostStepOut* host_out;
+    uint32_t host_seq;
 };
 
 // LDS bytes of one gate/up tile (gate row + up row of K bf16 weights, in

@@ -70,8 +70,11 @@ struct vvli_gpu_model {
     uint32_t* h_err = nullptr;    // pinned
     bool mk_pending = false;      // a persistent launch ran since the last error check
     uint32_t mk_inject = 0;       // test hook: the mk_inject-th next persistent launch starts flagged
-    hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last persistent launch
+    hipEvent_t mk_ev0 = nullptr, mk_ev1 = nullptr;  // around the last timed persistent launch
     bool mk_timed = false;
+    HostStepOut* h_out = nullptr;  // pinned: result of the last single-step launch
+    float* h_logits = nullptr;     // pinned [vocab]: forward_token_view's logits (allocated on first use)
+    uint32_t mk_host_seq = 0;      // sequence number of the last single-step launch
     // Mixture-of-experts model (vvli_gpu_moe_model_create).
     bool moe = false;
     MoeLayout moe_layout;
@@ -453,8 +456,14 @@ TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t b
     return t;
 }
 
+// One step of a single-step call (forward_token): its token and position go
+// in the launch arguments, and the result comes back in m->h_out.
+struct SingleStep {
+    uint32_t token, pos;
+};
+
 int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned long long* timing = nullptr,
-                   uint32_t timing_stride = 0, float* hidden_dbg = nullptr) {
+                   uint32_t timing_stride = 0, float* hidden_dbg = nullptr, const SingleStep* single = nullptr) {
     const vvli_gpu_config& c = m->cfg;
     // Epochs only grow; before they would wrap, clear every tag (stale words
     // then carry epoch 0, which no phase uses).
@@ -515,29 +524,40 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.g_lds_park = m->mk_glds_park;
     p.hidden_dbg = hidden_dbg;
     if (m->moe) p.experts = c.num_experts, p.top_k = c.experts_per_tok, p.trl = m->mk_tw + tl.rl;
+    if (single) {
+        p.init_step = 1;
+        p.init_token = single->token;
+        p.init_pos = single->pos;
+        p.host_out = m->h_out;
+        p.host_seq = ++m->mk_host_seq;
+        if (p.host_seq == 0) p.host_seq = m->mk_host_seq = 1;  // 0 is what h_out holds before any launch
+    }
     m->mk_epoch += static_cast<uint32_t>(need);
-    // The error word is cleared only once the host has read it: a launch
-    // that follows an unchecked one (the sampled generation loop) keeps a
-    // raised flag -- its blocks leave at once -- and the loop's final check
-    // reports it.
-    if (!m->mk_pending) HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
+    // The error word is zero here unless a launch of an unchecked sequence
+    // (the sampled generation loop) failed: its blocks then leave at once, and
+    // the check that reports the flag clears it (persistent_error_rc).
     if (m->mk_inject && --m->mk_inject == 0)
         HIP_TRY(hipMemsetAsync(m->mk_err, kDecodeErrInjected, 1, m->stream));
-    HIP_TRY(hipEventRecord(m->mk_ev0, m->stream));
+    // Single steps go untimed: the two event records cost a per-token caller
+    // about 8 us per call.
+    if (!single) HIP_TRY(hipEventRecord(m->mk_ev0, m->stream));
     HIP_TRY(launch_decode_step(p, m->mk_blocks, m->mk_lds, m->stream));
-    HIP_TRY(hipEventRecord(m->mk_ev1, m->stream));
+    if (!single) HIP_TRY(hipEventRecord(m->mk_ev1, m->stream));
     m->mk_pending = true;
-    m->mk_timed = true;
+    if (!single) m->mk_timed = true;
     return VVLI_OK;
 }
 
 // The device error word of the last persistent launch, once it is in h_err.
-static int persistent_error_rc(uint32_t e) {
-    if (e != 0)
-        return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (%s)", e,
-                         e == kDecodeErrTimeout ? "input wait timed out"
-                                                : (e == kDecodeErrState ? "invalid step state" : "injected by test hook"));
-    return VVLI_OK;
+// A raised flag is reported once and cleared, so the next launch starts
+// with it down.
+static int persistent_error_rc(vvli_gpu_model* m, uint32_t e) {
+    if (e == 0) return VVLI_OK;
+    HIP_TRY(hipMemsetAsync(m->mk_err, 0, sizeof(uint32_t), m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return set_error(VVLI_HIP_ERROR, "persistent decode step stopped: device error %u (%s)", e,
+                     e == kDecodeErrTimeout ? "input wait timed out"
+                                            : (e == kDecodeErrState ? "invalid step state" : "injected by test hook"));
 }
 
 int check_persistent_error(vvli_gpu_model* m) {
@@ -546,7 +566,27 @@ int check_persistent_error(vvli_gpu_model* m) {
     HIP_TRY(hipMemcpyAsync(m->h_err, m->mk_err, sizeof(uint32_t),
                            hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
-    return persistent_error_rc(*m->h_err);
+    return persistent_error_rc(m, *m->h_err);
+}
+
+// Outputs of a single-step persistent launch: the argmax (and error word)
+// from pinned host memory, which the step's finishing thread wrote -- no
+// copy -- and the logits when asked for, behind one synchronisation.
+int read_single(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
+    if (logits_out)
+        HIP_TRY(hipMemcpyAsync(logits_out, m->logits, static_cast<size_t>(m->cfg.vocab) * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    const volatile HostStepOut* h = m->h_out;
+    if (h->seq == m->mk_host_seq && h->error == 0) {
+        m->mk_pending = false;
+        if (argmax_out) *argmax_out = h->argmax;
+        return VVLI_OK;
+    }
+    // The blocks left before the end of the step: the device word says why.
+    const int rc = check_persistent_error(m);
+    if (rc) return rc;
+    return set_error(VVLI_HIP_ERROR, "persistent decode step ended without its result");
 }
 
 // The step's outputs. Without logits, the argmax and (after a persistent
@@ -566,7 +606,7 @@ int read_outputs(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
     HIP_TRY(hipStreamSynchronize(m->stream));
     if (merged) {
         m->mk_pending = false;
-        const int rc = persistent_error_rc(*m->h_err);
+        const int rc = persistent_error_rc(m, *m->h_err);
         if (rc) return rc;
     } else {
         const int rc = check_persistent_error(m);
@@ -848,6 +888,8 @@ void free_model(vvli_gpu_model* m) {
         if (b) (void)hipFree(b);
     if (m->h_state) (void)hipHostFree(m->h_state);
     if (m->h_err) (void)hipHostFree(m->h_err);
+    if (m->h_out) (void)hipHostFree(m->h_out);
+    if (m->h_logits) (void)hipHostFree(m->h_logits);
     if (m->mk_ev0) (void)hipEventDestroy(m->mk_ev0);
     if (m->mk_ev1) (void)hipEventDestroy(m->mk_ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -983,6 +1025,11 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
                           hipSuccess
                       ? 0
                       : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
+        TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_out), sizeof(HostStepOut), hipHostMallocDefault) ==
+                          hipSuccess
+                      ? 0
+                      : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
+        std::memset(m->h_out, 0, sizeof(HostStepOut));
     }
     TRY_ALLOC(dmalloc(&m->state, 1));
     TRY_ALLOC(dmalloc(&m->prompt, max_seq_len));
@@ -1404,16 +1451,35 @@ int vvli_gpu_forward_token(vvli_gpu_model* m, uint32_t token, uint32_t pos, floa
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
     if (use_persistent(m)) {
-        HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
-        int rc = run_persistent(m, 1, -1);
+        const SingleStep one{token, pos};
+        int rc = run_persistent(m, 1, -1, nullptr, 0, nullptr, &one);
         if (rc) return rc;
-        return read_outputs(m, logits_out, argmax_out);
+        return read_single(m, logits_out, argmax_out);
     }
     int rc = ensure_graph(m);
     if (rc) return rc;
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
     HIP_TRY(hipGraphLaunch(m->graph, m->stream));
     return read_outputs(m, logits_out, argmax_out);
+}
+
+int vvli_gpu_forward_token_view(vvli_gpu_model* m, uint32_t token, uint32_t pos, const float** logits_view,
+                                uint32_t* argmax_out) {
+    if (!m || !logits_view) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_forward_token_view");
+    if (!m->h_logits) {
+        HIP_TRY(hipSetDevice(m->device));
+        if (hipHostMalloc(reinterpret_cast<void**>(&m->h_logits), static_cast<size_t>(m->cfg.vocab) * sizeof(float),
+                          hipHostMallocDefault) != hipSuccess) {
+            m->h_logits = nullptr;
+            return set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc of the logits view failed");
+        }
+    }
+    // A copy into pinned memory is a direct DMA (measured per call at
+    // Llama-1B: 793-803 against 817-855 us into pageable memory).
+    const int rc = vvli_gpu_forward_token(m, token, pos, m->h_logits, argmax_out);
+    if (rc) return rc;
+    *logits_view = m->h_logits;
+    return VVLI_OK;
 }
 
 int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
@@ -1523,7 +1589,7 @@ int vvli_gpu_profile_persistent(vvli_gpu_model* m, uint32_t token, uint32_t pos,
 
 int vvli_gpu_last_launch_time(vvli_gpu_model* m, float* ms_out) {
     if (!m || !ms_out) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_last_launch_time");
-    if (!m->mk_timed) return set_error(VVLI_INVALID_CONFIG, "no persistent launch has run on this model");
+    if (!m->mk_timed) return set_error(VVLI_INVALID_CONFIG, "no timed persistent launch has run on this model");
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(hipEventSynchronize(m->mk_ev1));
     HIP_TRY(hipEventElapsedTime(ms_out, m->mk_ev0, m->mk_ev1));

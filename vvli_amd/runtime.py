@@ -219,6 +219,19 @@ class Runner:
         self.last_argmax = am.value
         return self.logits
 
+    def forward_token_view(self, token_id: int, position: int) -> np.ndarray:
+        """Runner.forwardToken with its borrowed-slice return (src/llm.zig:729):
+        a read-only array over the library's pinned logits, overwritten by the
+        next forward_token_view call and invalid once the runner is closed."""
+        view = c_void_p()
+        am = c_uint32()
+        _lib.check(_lib.lib().vvli_gpu_forward_token_view(self._h, token_id, position, byref(view), byref(am)))
+        self.last_argmax = am.value
+        buf = (ctypes.c_float * self.cfg.vocab_size).from_address(view.value)
+        out = np.frombuffer(buf, dtype=np.float32)
+        out.flags.writeable = False
+        return out
+
     def forward_token_argmax(self, token_id: int, position: int) -> int:
         am = c_uint32()
         _lib.check(_lib.lib().vvli_gpu_forward_token(self._h, token_id, position, None, byref(am)))
