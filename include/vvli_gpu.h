@@ -287,6 +287,14 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* model, float* ms_out);
  * for it returns VVLI_HIP_ERROR; the flag is cleared once the host has read
  * it. */
 int vvli_gpu_test_inject_step_error(vvli_gpu_model* model, uint32_t n);
+/* Test hook of the batched prefill (no reference counterpart): the launch
+ * form of its flash attention for every later prefill in the process -- -1
+ * chosen by the prompt's size (the default), 0 blocks of 128 query vectors,
+ * 1 the same with two key groups per block, 2 blocks of 64 query vectors with
+ * two key groups -- so that each form can be compared with the token loop.
+ * Form 2 needs heads / kv_heads <= 64 (else the prefill returns
+ * VVLI_HIP_ERROR). Values outside -1..2 -> VVLI_INVALID_CONFIG. */
+int vvli_gpu_test_set_prefill_attention_form(int32_t form);
 /* Test hook of the whole-vocabulary sampler (no reference counterpart):
  * Sampler.next as vvli_gpu_sampler_next with no repeat history, restricted to
  * candidate lists over 1024 (temperature > 0, top_k 0 or > 1024; else

@@ -65,6 +65,71 @@ def built():
     return True
 
 
+# Attention-form cases, by the default choice on 256 CUs: 32 kv heads put a
+# 600-row prompt on 128-vector blocks with two key groups (160 blocks; the
+# 64-vector form would need 320), 64 kv heads a 1100-row prompt on the
+# one-group form (576 blocks, more than two rounds).
+FORM_CASES = {
+    "kv32_two_groups": (cfg_small(vocab_size=500, hidden_size=2048, intermediate_size=512, num_attention_heads=32,
+                                  num_key_value_heads=32, qkv_bias=False), "synth", [600]),
+    "kv64_one_group": (cfg_small(vocab_size=300, hidden_size=4096, intermediate_size=256, num_attention_heads=64,
+                                 num_key_value_heads=64, qkv_bias=False, num_hidden_layers=1), "synth", [1100]),
+}
+
+
+def _check_prefill(name, cfg, parts, oracle_mod, host_threads):
+    total = sum(parts)
+    max_seq = total + 8
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02)
+    orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
+    toks = np.random.default_rng(11).integers(0, cfg.vocab_size, size=total).astype(np.uint32)
+    with R.Runner(cfg, blob, max_seq) as gpu:
+        gpu.set_prefill_path("batched")
+        start = 0
+        for n in parts:
+            logits, am = gpu.prefill(toks[start:start + n], start)
+            logits = logits.copy()
+            for i in range(start, start + n):
+                ref = orc.forward_token(int(toks[i]), i)
+            e = rel_err(logits, ref)
+            assert e <= TOL, f"{name} prefill [{start}, {start + n}): logits rel err {e:.3e}"
+            assert am == oracle_mod.argmax(ref)
+            start += n
+        for layer in range(cfg.num_hidden_layers):
+            for pos in sorted({0, 1, total // 3, total // 2, total - 2, total - 1}):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"{name} kv layer {layer} pos {pos}"
+        # The next token step continues from the prefilled state.
+        nxt = int(toks[0])
+        e = rel_err(gpu.forward_token(nxt, total), orc.forward_token(nxt, total))
+        assert e <= TOL, f"{name} step after prefill: {e:.3e}"
+
+
+@pytest.mark.parametrize("form", [0, 1, 2])
+@pytest.mark.parametrize("name", ["qwen_small_split", "llama_small", "hd128_split", "hd32_g1"])
+def test_attention_forms_match_token_loop(name, form, built, oracle_mod, host_threads):
+    """Every launch form of the prefill attention (blocks of 128 query
+    vectors with one or two key groups, blocks of 64 with two), forced through
+    the test hook, against the token loop: ragged tiles, start_pos > 0,
+    head_dim 32 / 64 / 128, groups 1 / 2 / 4 / 7."""
+    cfg, how, parts = CASES[name]
+    lib = R._lib.lib()
+    print(f"case={name} parts={parts} attention form {form}", flush=True)
+    R._lib.check(lib.vvli_gpu_test_set_prefill_attention_form(form))
+    try:
+        _check_prefill(name, cfg, parts, oracle_mod, host_threads)
+    finally:
+        R._lib.check(lib.vvli_gpu_test_set_prefill_attention_form(-1))
+
+
+@pytest.mark.parametrize("name", list(FORM_CASES))
+def test_attention_default_forms_match_token_loop(name, built, oracle_mod, host_threads):
+    cfg, how, parts = FORM_CASES[name]
+    print(f"case={name} parts={parts}", flush=True)
+    _check_prefill(name, cfg, parts, oracle_mod, host_threads)
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_batched_prefill_matches_token_loop(name, built, oracle_mod, host_threads):
     cfg, how, parts = CASES[name]
@@ -120,6 +185,9 @@ def test_generate_with_batched_prefill(name, path, built, oracle_mod, host_threa
 
 
 def test_prefill_paths_and_errors(built):
+    lib = R._lib.lib()
+    assert lib.vvli_gpu_test_set_prefill_attention_form(3) == 1
+    assert lib.vvli_gpu_test_set_prefill_attention_form(-2) == 1
     tiny = C.tiny_test()  # head_dim 4: the token loop serves it
     with R.Runner(tiny, R.deterministic_blob(tiny, C.WEIGHT_BF16), 16) as gpu:
         with pytest.raises(VvliError):

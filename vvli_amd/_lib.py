@@ -138,6 +138,7 @@ PROTOTYPES = {
     "vvli_gpu_profile_persistent": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, POINTER(c_uint32)]),
     "vvli_gpu_last_launch_time": (c_int, [c_void_p, POINTER(ctypes.c_float)]),
     "vvli_gpu_test_inject_step_error": (c_int, [c_void_p, c_uint32]),
+    "vvli_gpu_test_set_prefill_attention_form": (c_int, [ctypes.c_int32]),
     "vvli_gpu_test_sampler_trace": (
         c_int, [c_void_p, c_uint32, POINTER(CSampling), c_void_p, POINTER(c_uint32), c_void_p, c_void_p, c_void_p,
                 POINTER(c_uint32)]),

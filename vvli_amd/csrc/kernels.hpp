@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <utility>
 #include <vector>
 
@@ -383,6 +384,10 @@ size_t prefill_kv_pack_bytes(uint32_t keys, uint32_t kv_heads, uint32_t hd);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_t s);
 // false (default): the MFMA flash-attention kernel; true: the f32 vector kernel.
 extern bool prefill_attn_vector;
+// Form of the MFMA flash-attention launch: -1 chosen by the prompt (default),
+// 0 blocks of 128 query vectors, 1 the same with two key groups, 2 blocks of
+// 64 query vectors with two key groups (group size up to 64).
+extern std::atomic<int> prefill_fa_form;
 
 // ---------------------------------------------------------------------------
 // Mixture-of-experts step pieces (moe.hip).

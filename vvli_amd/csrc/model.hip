@@ -1602,6 +1602,12 @@ int vvli_gpu_test_inject_step_error(vvli_gpu_model* m, uint32_t n) {
     return VVLI_OK;
 }
 
+int vvli_gpu_test_set_prefill_attention_form(int32_t form) {
+    if (form < -1 || form > 2) return set_error(VVLI_INVALID_CONFIG, "attention form %d not in -1..2", form);
+    prefill_fa_form.store(form, std::memory_order_relaxed);
+    return VVLI_OK;
+}
+
 int vvli_gpu_kv_read(vvli_gpu_model* m, uint32_t layer, uint32_t pos, float* k_out, float* v_out) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     if (layer >= m->cfg.layers || pos >= m->max_seq)

@@ -26,6 +26,7 @@
 // precision the reference computes with, where one bf16 rounding of the
 // activations would cost about 2^-9.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -773,16 +774,15 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
 // f32: the row max over the lane's 8 values and two xor shuffles; the row sum
 // stays per lane until the end. v_mfma_f32_16x16x32_bf16 layout as the GEMM's.
 // ---------------------------------------------------------------------------
-constexpr int kFaThreads = 256;
-constexpr int kFaVecs = 128;  // query vectors per block
+constexpr int kFaQueryWaves = 4;  // query waves (32 vectors each) of the one-group blocks
+constexpr int kFaVecs = 128;      // their query vectors per block
 
 template <int HD>
 struct FaShape {
     static constexpr int TK = HD == 128 ? 32 : 64;  // keys per tile
     static constexpr int Plane = TK * HD * 2;       // bytes of one bf16 plane
     static constexpr int Stage = 4 * Plane;         // K hi | K lo | V^T hi | V^T lo
-    static constexpr int DmaPerWave = Stage / 1024 / (kFaThreads / 64);
-    static_assert(Stage % (1024 * (kFaThreads / 64)) == 0, "whole 1 KiB copies per wave");
+    static_assert(Stage % (1024 * 4) == 0, "whole 1 KiB copies per wave for 2 or 4 waves");
 };
 
 // Chunk position of 16-byte chunk c of row r in a plane of `chunks` chunks per row.
@@ -855,19 +855,29 @@ __device__ __forceinline__ void fa_lds_wait(bf16x8 (&f)[4]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
 }
 
-template <int HD>
-__global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fa_kernel(
+// A block holds QW * 32 query vectors (QW query waves). KS = 2 (prompts
+// whose blocks would leave CUs idle or alone on them): two groups of QW waves
+// take the block's key tiles in turn (group 1 the odd tiles), each through
+// its own two stages, and group 0 merges group 1's running max, sum and
+// outputs at the end (flash-decoding's merge of two splits): half the tiles
+// on the longest block.
+template <int HD, int QW, int KS>
+__global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fa_kernel(
     PrefillAttnArgs a) {
     using S = FaShape<HD>;
     constexpr int TK = S::TK, DS = HD / 32, NT = HD / 16, SUB = TK / 32;
     constexpr int KCH = HD / 8, VCH = TK / 8;
+    constexpr int DMA = S::Stage / 1024 / QW;  // 1 KiB copies per wave per tile
     static_assert(HD % 32 == 0 && (DS + NT / 2) % 2 == 0, "head_dim 32, 64 or 128");
-    __shared__ __attribute__((aligned(1024))) char lds[2 * S::Stage];
+    static_assert((KS == 1 || KS == 2) && (QW == 2 || QW == 4), "one or two key groups of 2 or 4 waves");
+    __shared__ __attribute__((aligned(1024))) char lds[KS * 2 * S::Stage];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = (tid >> 6) % QW;  // query wave within the key group
+    const int kg = (tid >> 6) / QW;    // key group: tiles kg, kg + KS, ...
     const int fr = lane & 15, fq = lane >> 4;
     const uint32_t G = a.heads / a.kv_heads;
-    const uint32_t rows_per_block = kFaVecs / G;
+    const uint32_t rows_per_block = (32 * QW) / G;
     const uint32_t row_groups = (a.rows + rows_per_block - 1) / rows_per_block;
     const uint32_t kvh = blockIdx.x % a.kv_heads;
     const uint32_t r0 = (row_groups - 1 - blockIdx.x / a.kv_heads) * rows_per_block;  // longest first
@@ -916,14 +926,15 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
         for (int n = 0; n < NT; ++n) o[gi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
 
-    // Copies: wave w moves bytes [w, w + 1) * DmaPerWave KiB of each tile image.
+    // Copies: wave w moves bytes [w, w + 1) * DMA KiB of each tile image of
+    // its key group, into the group's two stages.
     const char* src0 = static_cast<const char*>(a.kv_pack) + static_cast<size_t>(kvh) * a.kv_tiles * S::Stage +
-                       wave * S::DmaPerWave * 1024 + lane * 16;
-    char* dst0 = lds + wave * S::DmaPerWave * 1024;
+                       wave * DMA * 1024 + lane * 16;
+    char* dst0 = lds + kg * 2 * S::Stage + wave * DMA * 1024;
     auto issue = [&](uint32_t t, int st) {
         const char* src = src0 + static_cast<size_t>(t) * S::Stage;
 #pragma unroll
-        for (int i = 0; i < S::DmaPerWave; ++i) gemm_dma16(src + i * 1024, dst0 + st * S::Stage + i * 1024);
+        for (int i = 0; i < DMA; ++i) gemm_dma16(src + i * 1024, dst0 + st * S::Stage + i * 1024);
     };
     // Fragment offsets: K row 16u + l%16 of a 32-key step, chunk 4s + l/16;
     // V^T row 16n + l%16, chunk 4ks + l/16 (both swizzled by the row).
@@ -1005,15 +1016,19 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float m_new = fmaxf(m_run[gi], mx);  // finite: key 0 is in the first step
+                // Finite with one key group: key 0 is in its first step. The
+                // second group's first tiles can hide every key from a
+                // vector: the max then stays -inf and p = 0, corr = 0.
+                const float m_new = fmaxf(m_run[gi], mx);
+                const float m_sub = KS == 1 || m_new != -INFINITY ? m_new : 0.f;
                 grew |= m_new != m_run[gi];
-                corr[gi] = __builtin_amdgcn_exp2f(m_run[gi] - m_new);
+                corr[gi] = __builtin_amdgcn_exp2f(m_run[gi] - m_sub);
                 float sum = 0.f;
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const float p = __builtin_amdgcn_exp2f(sacc[gi][u][j] - m_new);
+                        const float p = __builtin_amdgcn_exp2f(sacc[gi][u][j] - m_sub);
                         sum += p;
                         const __bf16 hb = static_cast<__bf16>(p);
                         ph[gi][4 * u + j] = hb;
@@ -1056,17 +1071,53 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
         }
     };
 
-    issue(0, 0);
-    for (uint32_t it = 0; it < n_tiles; ++it) {
+    if (static_cast<uint32_t>(kg) < n_tiles) issue(kg, 0);
+    const uint32_t n_it = (n_tiles + KS - 1) / KS;
+    for (uint32_t it = 0; it < n_it; ++it) {
         const int st = it & 1;
-        gemm_wait_vm(0);  // this wave's copies of tile it
+        const uint32_t t = it * KS + kg;
+        gemm_wait_vm(0);  // this wave's copies of tile t
         gemm_barrier();   // every wave's copies landed; stage st ^ 1 is no longer read
-        if (it + 1 < n_tiles) issue(it + 1, st ^ 1);
-        const uint32_t j0 = it * TK;
+        if (t + KS < n_tiles) issue(t + KS, st ^ 1);
+        if (t >= n_tiles) continue;
+        const uint32_t j0 = t * TK;
         if (j0 > pos_last) continue;  // every key of the tile is masked for this wave
-        const uint32_t sb = lds0 + st * S::Stage;
+        const uint32_t sb = lds0 + (kg * 2 + st) * S::Stage;
         if (j0 + TK - 1 <= pos_first) tile(sb, j0, std::false_type{});
         else tile(sb, j0, std::true_type{});
+    }
+    if constexpr (KS == 2) {
+        // Group 1's state through LDS (field f of lane l of query wave w at
+        // [w][f][l]); group 0 combines in group order: M = max(m0, m1),
+        // O = O0 2^(m0 - M) + O1 2^(m1 - M), the same for the sums.
+        constexpr int F = 4 + 8 * NT;
+        static_assert(QW * F * 64 * 4 <= KS * 2 * S::Stage, "the merge fits the stages");
+        float* xs = reinterpret_cast<float*>(lds) + static_cast<size_t>(wave) * F * 64 + lane;
+        __syncthreads();  // both groups are done with their stages
+        if (kg == 1) {
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                xs[(2 * gi) * 64] = m_run[gi];
+                xs[(2 * gi + 1) * 64] = l_run[gi];
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xs[(4 + (gi * NT + n) * 4 + e) * 64] = o[gi][n][e];
+            }
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+            const float m1 = xs[(2 * gi) * 64], l1 = xs[(2 * gi + 1) * 64];
+            const float m = fmaxf(m_run[gi], m1);  // finite: group 0 saw key 0
+            const float c0 = __builtin_amdgcn_exp2f(m_run[gi] - m), c1 = __builtin_amdgcn_exp2f(m1 - m);
+            l_run[gi] = l_run[gi] * c0 + l1 * c1;
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[gi][n][e] = o[gi][n][e] * c0 + xs[(4 + (gi * NT + n) * 4 + e) * 64] * c1;
+        }
     }
     // out[row][(kvh G + g) HD + d] = O / l: lane l holds dims 16n + 4(l/16) .. +3 of vector l%16.
 #pragma unroll
@@ -1103,6 +1154,8 @@ __global__ __launch_bounds__(kFaThreads) __attribute__((amdgpu_waves_per_eu(2)))
 }
 
 }  // namespace
+
+std::atomic<int> prefill_fa_form{-1};
 
 // VVLI_PREFILL_ATTN=vector selects the f32 vector kernel (A/B measurement).
 bool prefill_attn_vector = [] {
@@ -1322,19 +1375,41 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_
         if (a.out_hl && a.out_plane < static_cast<size_t>(a.rows) * a.heads * hd) return hipErrorInvalidValue;
         PrefillAttnArgs b = a;
         b.kv_tiles = (keys + fa_tile_keys(hd) - 1) / fa_tile_keys(hd);
-        const uint32_t rows_per_block = kFaVecs / G;
-        const dim3 pack(b.kv_tiles, a.kv_heads), grid((a.rows + rows_per_block - 1) / rows_per_block * a.kv_heads);
+        // Blocks of 64 query vectors with two key groups while they fit one
+        // round of the CUs (one block of 4 waves per CU), else blocks of 128
+        // with two key groups up to two rounds, else one key group (two
+        // blocks per CU). Measured at Llama-3.2-1B / Qwen2.5-7B, whole
+        // prefill against one key group throughout: 512 rows -2.0 / -1.3 %,
+        // 1024 rows -2.0 %, 2048 rows -1.4 / -1.4 %.
+        const uint32_t cus = gemm_cus();
+        const uint32_t blocks4 = (a.rows + kFaVecs / G - 1) / (kFaVecs / G) * a.kv_heads;
+        const uint32_t rows2 = 64 / G;
+        const uint32_t blocks2 = rows2 ? (a.rows + rows2 - 1) / rows2 * a.kv_heads : 0;
+        const int forced = prefill_fa_form.load(std::memory_order_relaxed);
+        const int f = forced >= 0 ? forced : (rows2 && blocks2 <= cus ? 2 : (blocks4 <= 2 * cus ? 1 : 0));
+        if (f == 2 && !rows2) return hipErrorInvalidValue;
+        const dim3 pack(b.kv_tiles, a.kv_heads);
+        const dim3 grid(f == 2 ? blocks2 : blocks4), blk(f == 0 ? 256 : 512);
         hipError_t e;
         switch (hd) {
             case 32:
                 e = vlaunch(prefill_kv_pack_kernel<32>, pack, dim3(256), 0, s, b);
-                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<32>, grid, dim3(kFaThreads), 0, s, b);
+                if (e != hipSuccess) return e;
+                if (f == 0) return vlaunch(prefill_fa_kernel<32, 4, 1>, grid, blk, 0, s, b);
+                if (f == 1) return vlaunch(prefill_fa_kernel<32, 4, 2>, grid, dim3(512), 0, s, b);
+                return vlaunch(prefill_fa_kernel<32, 2, 2>, grid, dim3(256), 0, s, b);
             case 64:
                 e = vlaunch(prefill_kv_pack_kernel<64>, pack, dim3(256), 0, s, b);
-                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<64>, grid, dim3(kFaThreads), 0, s, b);
+                if (e != hipSuccess) return e;
+                if (f == 0) return vlaunch(prefill_fa_kernel<64, 4, 1>, grid, blk, 0, s, b);
+                if (f == 1) return vlaunch(prefill_fa_kernel<64, 4, 2>, grid, dim3(512), 0, s, b);
+                return vlaunch(prefill_fa_kernel<64, 2, 2>, grid, dim3(256), 0, s, b);
             case 128:
                 e = vlaunch(prefill_kv_pack_kernel<128>, pack, dim3(256), 0, s, b);
-                return e != hipSuccess ? e : vlaunch(prefill_fa_kernel<128>, grid, dim3(kFaThreads), 0, s, b);
+                if (e != hipSuccess) return e;
+                if (f == 0) return vlaunch(prefill_fa_kernel<128, 4, 1>, grid, blk, 0, s, b);
+                if (f == 1) return vlaunch(prefill_fa_kernel<128, 4, 2>, grid, dim3(512), 0, s, b);
+                return vlaunch(prefill_fa_kernel<128, 2, 2>, grid, dim3(256), 0, s, b);
             default: return hipErrorInvalidValue;
         }
     }
