@@ -109,6 +109,7 @@ def lib() -> ctypes.CDLL:
             "orc_prefill": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
             "orc_forward_embedding": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
             "orc_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+            "orc_kv_write": (c_int, [c_void_p, c_uint32, c_uint32, c_uint32, c_void_p, c_void_p]),
             "orc_generate_greedy": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_int64, c_void_p, P(c_uint32),
                                             P(OrcStats)]),
             "orc_moe_layout": (c_size_t, [P(OrcMoeConfig), c_void_p, P(c_size_t), P(c_size_t), P(c_size_t)]),
@@ -328,6 +329,14 @@ class OracleRunner:
         v = np.zeros(kv, dtype=np.float32)
         _check(lib().orc_kv_read(self._h, layer, pos, _p(k), _p(v)))
         return k, v
+
+    def kv_write(self, layer: int, pos: int, k: np.ndarray, v: np.ndarray):
+        """Overwrite cache rows pos .. pos + len(k) - 1 of one layer ([n, kv] f32 each)."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        if k.shape != v.shape or k.ndim != 2:
+            raise ValueError("k and v must both be [n, kv]")
+        _check(lib().orc_kv_write(self._h, layer, pos, k.shape[0], _p(k), _p(v)))
 
     def kv_clear(self):
         lib().orc_kv_clear(self._h)

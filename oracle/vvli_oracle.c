@@ -857,6 +857,18 @@ int orc_kv_read(const orc_runner* r, uint32_t layer, uint32_t pos, float* k_out,
     return ORC_OK;
 }
 
+/* Overwrite n consecutive cache rows pos.. of one layer (k, v: n * kv floats
+ * each), so that a test can continue from another implementation's cache. */
+int orc_kv_write(orc_runner* r, uint32_t layer, uint32_t pos, uint32_t n, const float* k, const float* v) {
+    if (!r || !k || !v) return ORC_NULL_ARG;
+    if (layer >= r->c.layers || pos > r->max_seq || n > r->max_seq - pos) return ORC_INVALID_CONFIG;
+    size_t kv = kv_dim(&r->c);
+    size_t off = ((size_t)layer * r->max_seq + pos) * kv;
+    memcpy(r->keys + off, k, (size_t)n * kv * sizeof(float));
+    memcpy(r->values + off, v, (size_t)n * kv * sizeof(float));
+    return ORC_OK;
+}
+
 /* ------------------------------------------------------------------------ */
 /* generator: src/generator.zig:142-175, 221-293                             */
 /* ------------------------------------------------------------------------ */

@@ -136,6 +136,9 @@ int orc_forward_embedding(orc_runner* r, const float* embedding, uint32_t pos, f
  * calls (checked by tests/test_oracle.py). */
 int orc_prefill(orc_runner* r, const uint32_t* tokens, uint32_t n, uint32_t start_pos, float* logits_out);
 int orc_kv_read(const orc_runner* r, uint32_t layer, uint32_t pos, float* k_out, float* v_out);
+/* Overwrite n cache rows pos.. of one layer (tests continuing from another
+ * implementation's cache; not part of the reference's API). */
+int orc_kv_write(orc_runner* r, uint32_t layer, uint32_t pos, uint32_t n, const float* k, const float* v);
 
 /* ---- generator: src/generator.zig:142-175, 221-293 ---- */
 typedef struct orc_stats {

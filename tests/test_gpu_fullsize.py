@@ -129,3 +129,57 @@ def test_llama1b_workload_as_benched(oracle_mod, host_threads, tmp_path):
             worst = max(rel_err(hidden[l], ref_hidden[l]) for l in range(cfg.num_hidden_layers))
             assert worst <= TOL, f"pos {pos}: hidden rel err {worst:.3e}"
             assert rel_err(logits, ref_logits) <= TOL, f"pos {pos}: logits"
+
+
+def test_qwen7b_long_context_full_size(oracle_mod, host_threads):
+    """The Qwen2.5-7B workload's decode at its real length: a 4096-token
+    batched prefill at ctx 8192 (two 2048-row chunks) on the GPU; the
+    oracle's prompt pass over the first 128 tokens (their K/V rows at the
+    32-key tile edges compared in every layer); then the oracle continues
+    from the GPU's cache (all 4096 rows of every layer copied in) through
+    eight persistent decode steps at positions 4096-4103: every layer's
+    residual, the logits, the argmax and
+    the new K/V rows against the oracle. At these positions each kv head has
+    43 attention splits (spread merge, matrix-core tiles), and the down phase
+    stages the 18944-wide SwiGLU vector. The full prompt pass is out of the
+    oracle's reach (about 60 TFLOP on the host), hence the copied cache."""
+    cfg = C.qwen25_7b()
+    ctx, n_prompt, n_head, n_steps = 8192, 4096, 128, 8
+    L_, kv = cfg.num_hidden_layers, cfg.kv_dim()
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=0, stddev=0.02, threads=host_threads)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, n_prompt).astype(np.uint32)
+    orc = oracle_mod.OracleRunner(cfg, blob, ctx, threads=host_threads)
+    print("case=qwen2.5-7b long context: 4096-token prefill", flush=True)
+    with R.Runner(cfg, blob, ctx) as gpu:
+        gpu.set_prefill_path("batched")
+        gpu.set_decode_path("persistent")
+        _, am = gpu.prefill(prompt, 0)
+        print(f"case=qwen2.5-7b long context: oracle prompt pass over {n_head} tokens", flush=True)
+        orc.prefill(prompt[:n_head], 0)
+        for layer in range(L_):
+            for pos in (0, 31, 32, 63, 64, 95, 96, n_head - 1):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"kv layer {layer} pos {pos}"
+        print("case=qwen2.5-7b long context: cache copied to the oracle", flush=True)
+        k = np.empty((n_prompt, kv), np.float32)
+        v = np.empty((n_prompt, kv), np.float32)
+        for layer in range(L_):
+            for pos in range(n_prompt):
+                k[pos], v[pos] = gpu.kv_read(layer, pos)
+            orc.kv_write(layer, 0, k, v)
+        tok = int(am)
+        for step in range(n_steps):
+            pos = n_prompt + step
+            print(f"case=qwen2.5-7b long context: step at pos {pos}", flush=True)
+            ref_logits, ref_hidden = orc.forward_token(tok, pos, want_hidden=True)
+            logits, hidden = gpu.forward_token_debug(tok, pos)
+            worst = max(rel_err(hidden[l], ref_hidden[l]) for l in range(L_))
+            assert worst <= TOL, f"pos {pos}: hidden rel err {worst:.3e}"
+            assert rel_err(logits, ref_logits) <= TOL, f"pos {pos}: logits"
+            assert R.argmax(logits) == oracle_mod.argmax(ref_logits), f"pos {pos}: argmax"
+            for layer in (0, L_ // 2, L_ - 1):
+                gk, gv = gpu.kv_read(layer, pos)
+                rk, rv = orc.kv_read(layer, pos)
+                assert rel_err(gk, rk) <= TOL and rel_err(gv, rv) <= TOL, f"new kv row layer {layer} pos {pos}"
+            tok = oracle_mod.argmax(ref_logits)

@@ -405,6 +405,36 @@ def test_prefill_pass_equals_token_loop(oracle_mod, case):
                           loop.forward_token(nxt, len(toks)).view(np.uint32))
 
 
+def test_kv_write_continues_like_the_computed_cache(oracle_mod):
+    """orc_kv_write (the setter the full-size long-context GPU test uses to
+    continue from the GPU's cache): a runner whose cache rows are copied from
+    another's continues with bit-identical logits and rows; a wrong row
+    changes the next step; out-of-range rows are rejected."""
+    kw = dict(vocab_size=300, hidden_size=128, intermediate_size=192, num_hidden_layers=2, num_attention_heads=4,
+              num_key_value_heads=2, max_position_embeddings=64, rope_theta=1e6, rms_norm_eps=1e-6,
+              tie_word_embeddings=True, architecture="qwen2", qkv_bias=True, rope_layout=C.ROPE_SPLIT_HALF)
+    cfg = C.Config(**kw)
+    blob = R.synthetic_blob(cfg, C.WEIGHT_BF16, seed=3)
+    toks = np.random.default_rng(4).integers(0, cfg.vocab_size, size=12)
+    a = oracle_mod.OracleRunner(cfg, blob, 32, threads=2)
+    for pos, t in enumerate(toks[:10]):
+        a.forward_token(int(t), pos)
+    b = oracle_mod.OracleRunner(cfg, blob, 32, threads=2)
+    for layer in range(cfg.num_hidden_layers):
+        rows = [a.kv_read(layer, pos) for pos in range(10)]
+        b.kv_write(layer, 0, np.stack([r[0] for r in rows]), np.stack([r[1] for r in rows]))
+    want = a.forward_token(int(toks[10]), 10)
+    got = b.forward_token(int(toks[10]), 10)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for layer in range(cfg.num_hidden_layers):
+        assert np.array_equal(a.kv_read(layer, 10)[0].view(np.uint32), b.kv_read(layer, 10)[0].view(np.uint32))
+    k, v = b.kv_read(0, 3)
+    b.kv_write(0, 3, (k + 0.5)[None], v[None])
+    assert not np.array_equal(b.forward_token(int(toks[11]), 11), a.forward_token(int(toks[11]), 11))
+    with pytest.raises(oracle_mod.OracleError):
+        b.kv_write(0, 31, np.zeros((2, cfg.kv_dim()), np.float32), np.zeros((2, cfg.kv_dim()), np.float32))
+
+
 def test_llama3_rope_table_matches_hf_fixture(oracle_mod):
     """Llama-3 RoPE scaling (no reference counterpart): the oracle's table and
     the library's vvli_host_llama3_inv_freq against Hugging Face's

@@ -774,8 +774,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
 // f32: the row max over the lane's 8 values and two xor shuffles; the row sum
 // stays per lane until the end. v_mfma_f32_16x16x32_bf16 layout as the GEMM's.
 // ---------------------------------------------------------------------------
-constexpr int kFaQueryWaves = 4;  // query waves (32 vectors each) of the one-group blocks
-constexpr int kFaVecs = 128;      // their query vectors per block
+constexpr int kFaVecs = 128;  // query vectors (4 waves of 32) per block of the first two forms
 
 template <int HD>
 struct FaShape {
@@ -861,8 +860,10 @@ __device__ __forceinline__ void fa_lds_wait(bf16x8 (&f)[4]) {
 // its own two stages, and group 0 merges group 1's running max, sum and
 // outputs at the end (flash-decoding's merge of two splits): half the tiles
 // on the longest block.
+// (Two waves per SIMD where the LDS lets two blocks or two groups share a CU.)
 template <int HD, int QW, int KS>
-__global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fa_kernel(
+__global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(QW * KS == 4 && KS == 2 ? 1 : 2)))
+void prefill_fa_kernel(
     PrefillAttnArgs a) {
     using S = FaShape<HD>;
     constexpr int TK = S::TK, DS = HD / 32, NT = HD / 16, SUB = TK / 32;
