@@ -357,6 +357,12 @@ struct PrefillRopeArgs {
     // K into a partial-sum buffer: summed into qkv first.
     const float* part = nullptr;
     uint32_t splits = 0;
+    // The MFMA attention's packed K/V tiles (prefill_kv_pack_bytes(start +
+    // rows, ..)): the new rows' images are written here too, and the last
+    // tile's rows past them zeroed; the attention launch then packs only the
+    // tiles of rows before start (PrefillAttnArgs::new_rows_packed).
+    void* kv_pack = nullptr;
+    size_t kv_pack_bytes = 0;
 };
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s);
 
@@ -377,6 +383,9 @@ struct PrefillAttnArgs {
     // gemm_kp(heads * head_dim), out_plane elements apart) instead of out.
     uint16_t* out_hl = nullptr;
     size_t out_plane = 0;
+    // The RoPE / KV pass already wrote the images of rows start .. start +
+    // rows - 1 (and the last tile's padding) into kv_pack.
+    bool new_rows_packed = false;
 };
 // Bytes of the packed K/V tiles the MFMA attention kernel reads for `keys`
 // cache rows (0 for an unsupported head_dim).

@@ -808,12 +808,13 @@ int enqueue_prefill_batched(vvli_gpu_model* m, uint32_t start, uint32_t n, uint3
                                m->rope_cs, kc, vc};
             if (q_splits > 1) ra.part = m->pf_part, ra.splits = q_splits;
             if (L.q_norm != kNone) ra.q_norm = w16(L.q_norm), ra.k_norm = w16(L.k_norm), ra.norm_eps = c.rms_eps;
+            // The MFMA attention writes o_proj's split planes itself (heads * hd = H, a multiple of 32).
+            const bool fused_o = !prefill_attn_vector;
+            if (fused_o) ra.kv_pack = m->pf_kvp, ra.kv_pack_bytes = m->pf_kvp_bytes;
             LAUNCH(launch_prefill_rope_kv(ra, s));
             PrefillAttnArgs aa{m->pf_qkv, ldqkv, kc, vc, m->pf_attn, H, P, pos0, c.heads, c.kv_heads, kv,
                                1.0f / sqrtf(static_cast<float>(hd))};
-            aa.kv_pack = m->pf_kvp, aa.kv_pack_bytes = m->pf_kvp_bytes;
-            // The MFMA attention writes o_proj's split planes itself (heads * hd = H, a multiple of 32).
-            const bool fused_o = !prefill_attn_vector;
+            aa.kv_pack = m->pf_kvp, aa.kv_pack_bytes = m->pf_kvp_bytes, aa.new_rows_packed = fused_o;
             if (fused_o) aa.out_hl = reinterpret_cast<uint16_t*>(m->pf_ahl2), aa.out_plane = m->pf_rows * gemm_kp(H);
             LAUNCH(launch_prefill_attn(aa, hd, s));
             // x += attn . Wo^T

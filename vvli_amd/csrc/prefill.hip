@@ -544,6 +544,73 @@ __global__ __launch_bounds__(kRowThreads) void prefill_embed_kernel(const uint16
     x[static_cast<size_t>(t) * n + i] = from_bf16(embed[static_cast<size_t>(tokens[t]) * n + i]);
 }
 
+// ---------------------------------------------------------------------------
+// Packed K/V tile images of the MFMA attention (prefill_kv_pack_kernel writes
+// them from the cache rows; the RoPE / KV pass writes a prompt's new rows
+// directly): per (kv head, tile of TK keys) [K hi | K lo | V^T hi | V^T lo],
+// K planes TK rows of head_dim bf16, V^T planes head_dim rows of TK bf16,
+// 16-byte chunks swizzled by the row (fa_swz), V^T positions permuted within
+// each 32-key group (fa_pos_key).
+// ---------------------------------------------------------------------------
+template <int HD>
+struct FaShape {
+    static constexpr int TK = HD == 128 ? 32 : 64;  // keys per tile
+    static constexpr int Plane = TK * HD * 2;       // bytes of one bf16 plane
+    static constexpr int Stage = 4 * Plane;         // K hi | K lo | V^T hi | V^T lo
+    static_assert(Stage % (1024 * 4) == 0, "whole 1 KiB copies per wave for 2 or 4 waves");
+};
+
+// Chunk position of 16-byte chunk c of row r in a plane of `chunks` chunks per row.
+__device__ __forceinline__ uint32_t fa_swz(uint32_t r, uint32_t c, uint32_t chunks) {
+    return chunks >= 16 ? c ^ (r & 15u) : chunks == 8 ? c ^ (r & 7u) : c ^ ((r >> 1) & (chunks - 1u));
+}
+// Key (within the tile) held at V^T position p.
+__device__ __forceinline__ uint32_t fa_pos_key(uint32_t p) {
+    return (p & ~31u) | (((p >> 2) & 1u) << 4) | (((p >> 3) & 3u) << 2) | (p & 3u);
+}
+// V^T position of key k (within the tile): the inverse of fa_pos_key.
+__device__ __forceinline__ uint32_t fa_key_pos(uint32_t k) {
+    return (k & ~31u) | (((k >> 2) & 3u) << 3) | (((k >> 4) & 1u) << 2) | (k & 3u);
+}
+
+__device__ inline void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+    hi = to_bf16_rne(v);
+    lo = to_bf16_rne(v - from_bf16(hi));
+}
+
+// Byte offsets of element d of key row r in a tile image (head_dim hd).
+struct FaImage {
+    uint32_t hd, tk, plane, stage, tiles;
+    __device__ FaImage(uint32_t head_dim, uint32_t n_keys)
+        : hd(head_dim), tk(head_dim == 128 ? 32u : 64u), plane(tk * head_dim * 2), stage(4 * plane),
+          tiles((n_keys + tk - 1) / tk) {}
+    __device__ size_t tile(uint32_t h, uint32_t key) const { return (static_cast<size_t>(h) * tiles + key / tk) * stage; }
+    __device__ uint32_t k_off(uint32_t r, uint32_t d) const {
+        return r * (2 * hd) + fa_swz(r, d / 8, hd / 8) * 16 + (d % 8) * 2;
+    }
+    __device__ uint32_t v_off(uint32_t r, uint32_t d) const {
+        const uint32_t p = fa_key_pos(r);
+        return 2 * plane + d * (2 * tk) + fa_swz(d, p / 8, tk / 8) * 16 + (p % 8) * 2;
+    }
+};
+// Key row `key` of head h: k and v values of dimension d, split hi / lo.
+__device__ __forceinline__ void fa_image_put(char* img, const FaImage& f, uint32_t h, uint32_t key, uint32_t d,
+                                             const float* k, const float* v) {
+    char* t = img + f.tile(h, key);
+    const uint32_t r = key % f.tk;
+    uint16_t hi, lo;
+    if (k) {
+        split_bf16(*k, hi, lo);
+        *reinterpret_cast<uint16_t*>(t + f.k_off(r, d)) = hi;
+        *reinterpret_cast<uint16_t*>(t + f.plane + f.k_off(r, d)) = lo;
+    }
+    if (v) {
+        split_bf16(*v, hi, lo);
+        *reinterpret_cast<uint16_t*>(t + f.v_off(r, d)) = hi;
+        *reinterpret_cast<uint16_t*>(t + f.plane + f.v_off(r, d)) = lo;
+    }
+}
+
 // One block per token row t (position start + t): rotate its q heads in place
 // and its k head vectors (after the QK-norm when the model has one), then
 // write k and v to the cache rows of that position.
@@ -565,6 +632,11 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
     const uint32_t qpairs = a.heads * half, kpairs = a.kv_heads * half;
     float* kc = a.kcache + static_cast<size_t>(pos) * a.kvdim;
     float* vc = a.vcache + static_cast<size_t>(pos) * a.kvdim;
+    // With kv_pack: the new rows' tile images too (the attention's pack pass
+    // then covers only the tiles of earlier rows).
+    char* const img = static_cast<char*>(a.kv_pack);
+    const uint32_t n_keys = a.start + a.rows;
+    const FaImage fi(a.hd, n_keys);
     float scq = 1.f, sck = 1.f;
     if (a.q_norm) {
         __shared__ float red[2][kRowThreads / 64];
@@ -630,11 +702,24 @@ __global__ __launch_bounds__(kRowThreads) void prefill_rope_kv_kernel(PrefillRop
             if (!is_q) {
                 kc[h * a.hd + f] = r0;
                 kc[h * a.hd + sidx] = r1;
+                if (img) {
+                    fa_image_put(img, fi, h, pos, f, &r0, nullptr);
+                    fa_image_put(img, fi, h, pos, sidx, &r1, nullptr);
+                }
             }
         }
     }
     const float* vsrc = row + (a.heads + a.kv_heads) * a.hd;
-    for (uint32_t i = threadIdx.x; i < a.kvdim; i += kRowThreads) vc[i] = vsrc[i];
+    for (uint32_t i = threadIdx.x; i < a.kvdim; i += kRowThreads) {
+        vc[i] = vsrc[i];
+        if (img) fa_image_put(img, fi, i / a.hd, pos, i % a.hd, nullptr, vsrc + i);
+    }
+    if (img) {  // the last tile's rows past the prompt's keys: zeros (the pack kernel's padding)
+        const float zero = 0.f;
+        for (uint32_t key = n_keys + t; key < fi.tiles * fi.tk; key += a.rows)
+            for (uint32_t i = threadIdx.x; i < a.kvdim; i += kRowThreads)
+                fa_image_put(img, fi, i / a.hd, key, i % a.hd, &zero, &zero);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -776,27 +861,6 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attn_kernel(PrefillAttnA
 // ---------------------------------------------------------------------------
 constexpr int kFaVecs = 128;  // query vectors (4 waves of 32) per block of the first two forms
 
-template <int HD>
-struct FaShape {
-    static constexpr int TK = HD == 128 ? 32 : 64;  // keys per tile
-    static constexpr int Plane = TK * HD * 2;       // bytes of one bf16 plane
-    static constexpr int Stage = 4 * Plane;         // K hi | K lo | V^T hi | V^T lo
-    static_assert(Stage % (1024 * 4) == 0, "whole 1 KiB copies per wave for 2 or 4 waves");
-};
-
-// Chunk position of 16-byte chunk c of row r in a plane of `chunks` chunks per row.
-__device__ __forceinline__ uint32_t fa_swz(uint32_t r, uint32_t c, uint32_t chunks) {
-    return chunks >= 16 ? c ^ (r & 15u) : chunks == 8 ? c ^ (r & 7u) : c ^ ((r >> 1) & (chunks - 1u));
-}
-// Key (within the tile) held at V^T position p.
-__device__ __forceinline__ uint32_t fa_pos_key(uint32_t p) {
-    return (p & ~31u) | (((p >> 2) & 1u) << 4) | (((p >> 3) & 3u) << 2) | (p & 3u);
-}
-
-__device__ inline void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
-    hi = to_bf16_rne(v);
-    lo = to_bf16_rne(v - from_bf16(hi));
-}
 
 // One block per (key tile, kv head): K chunks straight to the K planes, the V
 // tile through LDS to the transposed planes.
@@ -1361,6 +1425,9 @@ hipError_t launch_prefill_embed(const uint16_t* embed, const uint32_t* tokens, u
 
 hipError_t launch_prefill_rope_kv(const PrefillRopeArgs& a, hipStream_t s) {
     if ((a.q_norm == nullptr) != (a.k_norm == nullptr)) return hipErrorInvalidValue;
+    if (a.kv_pack && (a.kv_pack_bytes < prefill_kv_pack_bytes(a.start + a.rows, a.kv_heads, a.hd) ||
+                      prefill_kv_pack_bytes(a.start + a.rows, a.kv_heads, a.hd) == 0 || a.kvdim != a.kv_heads * a.hd))
+        return hipErrorInvalidValue;
     if (a.part && (a.splits < 2 || a.splits > kMaxPartSplits || a.ld % 4 != 0)) return hipErrorInvalidValue;
     return vlaunch(prefill_rope_kv_kernel, dim3(a.rows), dim3(kRowThreads), 0, s, a);
 }
@@ -1389,24 +1456,27 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs& a, uint32_t hd, hipStream_
         const int forced = prefill_fa_form.load(std::memory_order_relaxed);
         const int f = forced >= 0 ? forced : (rows2 && blocks2 <= cus ? 2 : (blocks4 <= 2 * cus ? 1 : 0));
         if (f == 2 && !rows2) return hipErrorInvalidValue;
-        const dim3 pack(b.kv_tiles, a.kv_heads);
+        // Tiles holding rows before `start` (all tiles unless the RoPE / KV
+        // pass wrote the new rows' images).
+        const uint32_t tk = fa_tile_keys(hd);
+        const dim3 pack(a.new_rows_packed ? (a.start + tk - 1) / tk : b.kv_tiles, a.kv_heads);
         const dim3 grid(f == 2 ? blocks2 : blocks4), blk(f == 0 ? 256 : 512);
         hipError_t e;
         switch (hd) {
             case 32:
-                e = vlaunch(prefill_kv_pack_kernel<32>, pack, dim3(256), 0, s, b);
+                e = pack.x ? vlaunch(prefill_kv_pack_kernel<32>, pack, dim3(256), 0, s, b) : hipSuccess;
                 if (e != hipSuccess) return e;
                 if (f == 0) return vlaunch(prefill_fa_kernel<32, 4, 1>, grid, blk, 0, s, b);
                 if (f == 1) return vlaunch(prefill_fa_kernel<32, 4, 2>, grid, dim3(512), 0, s, b);
                 return vlaunch(prefill_fa_kernel<32, 2, 2>, grid, dim3(256), 0, s, b);
             case 64:
-                e = vlaunch(prefill_kv_pack_kernel<64>, pack, dim3(256), 0, s, b);
+                e = pack.x ? vlaunch(prefill_kv_pack_kernel<64>, pack, dim3(256), 0, s, b) : hipSuccess;
                 if (e != hipSuccess) return e;
                 if (f == 0) return vlaunch(prefill_fa_kernel<64, 4, 1>, grid, blk, 0, s, b);
                 if (f == 1) return vlaunch(prefill_fa_kernel<64, 4, 2>, grid, dim3(512), 0, s, b);
                 return vlaunch(prefill_fa_kernel<64, 2, 2>, grid, dim3(256), 0, s, b);
             case 128:
-                e = vlaunch(prefill_kv_pack_kernel<128>, pack, dim3(256), 0, s, b);
+                e = pack.x ? vlaunch(prefill_kv_pack_kernel<128>, pack, dim3(256), 0, s, b) : hipSuccess;
                 if (e != hipSuccess) return e;
                 if (f == 0) return vlaunch(prefill_fa_kernel<128, 4, 1>, grid, blk, 0, s, b);
                 if (f == 1) return vlaunch(prefill_fa_kernel<128, 4, 2>, grid, dim3(512), 0, s, b);
