@@ -185,7 +185,8 @@ def gemv_sweep(shapes, ms, log=True) -> list:
     Time per call, two ways: `us` -- a HIP graph of `reps` back-to-back calls
     (one per weight copy in turn), HIP events around its replay, so the GPU
     runs the kernels back to back without waiting for the host (the op's
-    device time including the gap between launches); `us_host_loop` -- the
+    device time including the gap between launches; the median of five
+    replays); `us_host_loop` -- the
     same calls issued one by one from Python through ctypes, HIP events
     around the loop (bounded below by the host's per-call cost, about 3 us
     here). The graph is captured on a stream whose scratch the warm-up calls
@@ -224,14 +225,17 @@ def gemv_sweep(shapes, ms, log=True) -> list:
             with torch.cuda.graph(g, stream=stream):
                 for i in range(reps):
                     call(i)
+            samples = []
             with torch.cuda.stream(stream):
                 g.replay()
                 stream.synchronize()
-                e0.record(stream)
-                g.replay()
-                e1.record(stream)
-            e1.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / reps
+                for _ in range(5):  # the median of five timed replays: one slow replay does not set the figure
+                    e0.record(stream)
+                    g.replay()
+                    e1.record(stream)
+                    e1.synchronize()
+                    samples.append(e0.elapsed_time(e1) * 1e3 / reps)
+            us = sorted(samples)[len(samples) // 2]
             del g
             nbytes = 2 * n * k + 4 * m * k + 4 * m * n
             rows.append({"N": n, "K": k, "M": m, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
@@ -791,7 +795,7 @@ def main() -> int:
         agg = (sum(2 * r["N"] * r["K"] + 4 * r["K"] + 4 * r["N"] for r in gemv_rows) / sum(r["us"] for r in gemv_rows)
                / 1e3)
         gemv["all_shapes"] = {"gbs": round(agg, 1), "frac": round(agg / HBM_PEAK_GBS, 4),
-                              "timing": "per shape: HIP graph of back-to-back calls over >= 1 GiB of weight copies"}
+                              "timing": "per shape: HIP graph of back-to-back calls over >= 1 GiB of weight copies, median of 5 replays"}
         print("[bench] gemv M=1: " + ", ".join(f"{k} {v['gbs']:.0f}GB/s" for k, v in gemv.items()), file=sys.stderr,
               flush=True)
 
