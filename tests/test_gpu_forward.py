@@ -194,6 +194,30 @@ def test_forward_token_return_forms_match_oracle(name, path, built, oracle_mod, 
 
 
 @pytest.mark.parametrize("path", ["graph", "persistent"])
+def test_forward_token_up_to_the_last_position(path, built, oracle_mod, host_threads):
+    """Single steps at every position up to max_seq_len - 1 (the step at the
+    last position also marks the cache full), then ContextFull
+    (src/llm.zig:706-707) at max_seq_len; the argmax-only form at the last
+    position."""
+    cfg, kind, how, _ = CASES["qwen_small"]
+    max_seq = 48
+    blob = make_blob(cfg, kind, how)
+    orc = oracle_mod.OracleRunner(cfg, blob, max_seq, threads=host_threads)
+    toks = np.random.default_rng(8).integers(0, cfg.vocab_size, size=max_seq)
+    with R.Runner(cfg, blob, max_seq) as gpu:
+        gpu.set_decode_path(path)
+        for pos in range(max_seq - 1):
+            ref = orc.forward_token(int(toks[pos]), pos)
+            got = gpu.forward_token(int(toks[pos]), pos)
+            assert rel_err(got, ref) <= TOL and gpu.last_argmax == oracle_mod.argmax(ref), f"pos {pos}"
+        ref = orc.forward_token(int(toks[-1]), max_seq - 1)
+        assert gpu.forward_token_argmax(int(toks[-1]), max_seq - 1) == oracle_mod.argmax(ref)
+        with pytest.raises(VvliError) as e:
+            gpu.forward_token(int(toks[0]), max_seq)
+        assert e.value.rc == 4
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
 @pytest.mark.parametrize("name", ["tiny_bf16", "qwen_small", "llama_small", "hd128_g7"])
 def test_greedy_generation_matches_oracle(name, path, built, oracle_mod, host_threads):
     cfg, kind, how, _ = CASES[name]
