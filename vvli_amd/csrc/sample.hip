@@ -33,12 +33,14 @@
 // sample_cand_elems keys given):
 // sample_local_kernel cuts the vocab into slices of 4096 ids, one block each,
 // and writes a slice's top_k keys (score key << 32 | ~id; 0 for a non-finite
-// score), descending, with its finite count: each wave takes the top_k of its
-// 256 ids (top_k rounds of a wave max over keys held in registers) and the
-// first wave merges the 16 lists. The keys are distinct, so every member of
-// the global top_k is in its slice's top_k; the sampling block's first wave then merges
-// the slices' sorted lists (one list head per lane) instead of scanning the
-// vocab (one block's scan is ~1 ms at a 128K vocab).
+// score), descending, with its finite count: each wave sorts its 256 ids'
+// keys in registers (a bitonic network, lanes exchanged by DPP and shuffles)
+// and the block tree-merges the 16 waves' first 128. The keys are distinct,
+// so every member of the global top_k is in its slice's top_k; the sampling
+// block then tree-merges the slices' lists (up to 32; more: its first wave
+// merges them, one list head per lane) instead of scanning the vocab (one
+// block's scan is ~1 ms at a 128K vocab), and its first wave forms the
+// candidates' running sums, from which the top-p cut and the pick follow.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -155,13 +157,128 @@ __device__ inline void wave_merge(const unsigned long long* lists, uint32_t n_li
     }
 }
 
+// ---- Wave-level bitonic networks over 64-bit keys held in registers ----
+// Element e = lane * R + r of a wave's 64 R keys lives in v[r] of lane
+// `lane`; a compare-exchange at distance d < R stays in the lane's
+// registers, d >= R pairs lane with lane ^ (d / R): DPP moves within a row
+// of 16 lanes (xor 1, 2 as quad permutes; xor 4, 8 as a row shift each way
+// and a select), shuffles through the LDS crossbar for xor 16 and 32 (the
+// crossbar's throughput, shared by the block's 16 waves, bounds the shuffle
+// form: 25 us for the slice top-k with shuffles at every distance).
+template <int LX>
+__device__ inline uint32_t xor_lane32(uint32_t x, uint32_t lane) {
+    const int xi = static_cast<int>(x);
+    if constexpr (LX == 1) {
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(xi, 0xB1, 0xf, 0xf, true));  // quad_perm [1,0,3,2]
+    } else if constexpr (LX == 2) {
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(xi, 0x4E, 0xf, 0xf, true));  // quad_perm [2,3,0,1]
+    } else if constexpr (LX == 4 || LX == 8) {
+        const int up = __builtin_amdgcn_mov_dpp(xi, 0x100 + LX, 0xf, 0xf, true);  // row_shl: lane + LX
+        const int dn = __builtin_amdgcn_mov_dpp(xi, 0x110 + LX, 0xf, 0xf, true);  // row_shr: lane - LX
+        return static_cast<uint32_t>((lane & LX) ? dn : up);
+    } else {
+        return static_cast<uint32_t>(__shfl_xor(xi, LX, 64));
+    }
+}
+template <int LX>
+__device__ inline unsigned long long xor_lane64(unsigned long long x, uint32_t lane) {
+    const uint32_t lo = xor_lane32<LX>(static_cast<uint32_t>(x), lane);
+    const uint32_t hi = xor_lane32<LX>(static_cast<uint32_t>(x >> 32), lane);
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ inline unsigned long long shfl_xor64(unsigned long long x, uint32_t lx, uint32_t lane) {
+    switch (lx) {
+        case 1: return xor_lane64<1>(x, lane);
+        case 2: return xor_lane64<2>(x, lane);
+        case 4: return xor_lane64<4>(x, lane);
+        case 8: return xor_lane64<8>(x, lane);
+        case 16: return xor_lane64<16>(x, lane);
+        default: return xor_lane64<32>(x, lane);
+    }
+}
+// One stage at distance d of a bitonic network; `size` picks each element's
+// direction (descending where (e & size) == 0); size = 0: all descending.
+template <int R>
+__device__ inline void wave_cx(unsigned long long (&v)[R], uint32_t lane, uint32_t size, uint32_t d) {
+    if (d < static_cast<uint32_t>(R)) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int q = r ^ static_cast<int>(d);
+            if (q > r) {
+                const bool desc = ((lane * R + r) & size) == 0;
+                const unsigned long long a = v[r], b = v[q];
+                const bool sw = desc ? a < b : a > b;
+                v[r] = sw ? b : a;
+                v[q] = sw ? a : b;
+            }
+        }
+    } else {
+        const uint32_t lx = d / R;
+        const bool lower = (lane & lx) == 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const unsigned long long o = shfl_xor64(v[r], lx, lane);
+            const bool desc = ((lane * R + r) & size) == 0;
+            v[r] = (lower == desc) ? (v[r] > o ? v[r] : o) : (v[r] < o ? v[r] : o);
+        }
+    }
+}
+// The wave's 64 R keys sorted descending (element order e = lane * R + r).
+// (Unrolled, so every stage's distance is a constant and its DPP form fixed.)
+template <int R>
+__device__ inline void wave_sort_desc(unsigned long long (&v)[R], uint32_t lane) {
+#pragma unroll
+    for (uint32_t size = 2; size <= 64u * R; size <<= 1)
+#pragma unroll
+        for (uint32_t d = size >> 1; d > 0; d >>= 1) wave_cx<R>(v, lane, size, d);
+}
+// A bitonic sequence of 64 R keys (descending, then ascending) sorted descending.
+template <int R>
+__device__ inline void wave_merge_desc(unsigned long long (&v)[R], uint32_t lane) {
+#pragma unroll
+    for (uint32_t d = 32u * R; d > 0; d >>= 1) wave_cx<R>(v, lane, 0u, d);
+}
+// Tree merge of n (a power of two, <= 2 * waves of the block) descending
+// lists of kFastTopK keys, buf[0][i] (i < n), keeping the first kFastTopK:
+// at each level wave w merges lists 2w and 2w + 1 (list 2w, then 2w + 1
+// reversed: a bitonic sequence of 2 kFastTopK keys) into buf[other][w].
+// Every thread of the block calls it; returns the buffer holding the result
+// in its list 0.
+__device__ inline int block_tree_merge(unsigned long long (*buf)[32][kFastTopK], uint32_t n) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int cur = 0;
+    for (uint32_t nl = n; nl > 1; nl >>= 1) {
+        if (wave < nl / 2) {
+            const unsigned long long* A = buf[cur][2 * wave];
+            const unsigned long long* B = buf[cur][2 * wave + 1];
+            unsigned long long v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t e = lane * 4 + r;
+                v[r] = e < static_cast<uint32_t>(kFastTopK) ? A[e] : B[2 * kFastTopK - 1 - e];
+            }
+            wave_merge_desc<4>(v, lane);
+            if (lane < static_cast<uint32_t>(kFastTopK) / 4)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) buf[cur ^ 1][wave][lane * 4 + r] = v[r];
+        }
+        __syncthreads();
+        cur ^= 1;
+    }
+    return cur;
+}
+static_assert(kFastTopK == 128, "the tree merge holds 2 x 128 keys as 4 per lane");
+
 struct SampleShared {
     uint32_t hist[256];
     unsigned long long cand[kMaxCand];  // (score key << 32) | ~id, sorted descending
     float prob[kMaxCand];
     uint32_t scan_gt[kT], scan_eq[kT];
     unsigned long long red[kT / 64];
-    unsigned long long surv[kSurvivors];  // two-stage path: the slices' lists
+    union {
+        unsigned long long surv[kSurvivors];          // two-stage path: the slices' lists (more than 32)
+        unsigned long long tree[2][32][kFastTopK];    // ... up to 32 lists: the tree merge's buffers
+    } u;
     uint32_t prefix, remaining, n_finite, token;
 };
 
@@ -191,10 +308,15 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* buf) {
 }
 
 // One slice of kLocalIds ids per block: its top_k keys and its finite count.
+// Each wave sorts its 256 keys (a register bitonic network) and the block
+// tree-merges the 16 waves' first 128; the first top_k are the slice's list.
+// (k rounds of a wave max per wave and a one-wave merge of the wave lists,
+// the earlier form, took 5 + 0.53 k us: 26 us at top_k 40.)
 __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
     constexpr int R = kLocalIds / kT;  // keys per lane
     constexpr int W = kT / 64;
-    __shared__ unsigned long long lists[W * kFastTopK];
+    static_assert(R == 4 && W == 16, "256 keys per wave, 16 waves");
+    __shared__ unsigned long long lists[2][32][kFastTopK];
     __shared__ uint32_t nred[W];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t base = blockIdx.x * kLocalIds + wave * (64 * R), k = a.top_k;
@@ -212,27 +334,20 @@ __global__ __launch_bounds__(kT) void sample_local_kernel(SampleArgs a) {
             }
         }
     }
-    // The wave's top k, descending: k rounds of a wave max, the owner zeroing its copy.
-    for (uint32_t i = 0; i < k; ++i) {
-        unsigned long long mx = v[0];
+    wave_sort_desc<R>(v, lane);  // keys are distinct (ids in the low half); zeros last
+    if (lane < static_cast<uint32_t>(kFastTopK) / R)
 #pragma unroll
-        for (int r = 1; r < R; ++r) mx = v[r] > mx ? v[r] : mx;
-        const unsigned long long b = wave_max_dpp(mx);
-        if (lane == 0) lists[wave * k + i] = b;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (v[r] == b) v[r] = 0ull;
-    }
+        for (int r = 0; r < R; ++r) lists[0][wave][lane * R + r] = v[r];
     for (int off = 32; off > 0; off >>= 1) nf += __shfl_xor(nf, off, 64);
     if (lane == 0) nred[wave] = nf;
     __syncthreads();
-    if (wave == 0) {
-        wave_merge(lists, W, k, k, a.cand_buf + static_cast<size_t>(blockIdx.x) * k);
-        if (lane == 0) {
-            uint32_t total = 0;
-            for (int w = 0; w < W; ++w) total += nred[w];
-            a.cand_nf[blockIdx.x] = total;
-        }
+    const int cur = block_tree_merge(lists, W);
+    unsigned long long* out = a.cand_buf + static_cast<size_t>(blockIdx.x) * k;
+    for (uint32_t i = tid; i < k; i += kT) out[i] = lists[cur][0][i];
+    if (tid == 0) {
+        uint32_t total = 0;
+        for (int w = 0; w < W; ++w) total += nred[w];
+        a.cand_nf[blockIdx.x] = total;
     }
 }
 
@@ -294,17 +409,31 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
             tok = sh.token;
         } else {
           if (two_stage) {
-            // The slices' lists (each top_k keys, descending, zero padded): the
-            // first wave merges them, lane s holding list s's head; the top
-            // count heads taken are the candidates, in order.
-            // Lists staged in LDS when they fit, else merged from the scratch.
-            const uint32_t total = slices * a.top_k;
-            const bool staged = total <= static_cast<uint32_t>(kSurvivors);
-            if (staged)
-                for (uint32_t j = tid; j < total; j += kT) sh.surv[j] = a.cand_buf[j];
+            // The slices' lists (each top_k keys, descending, zero padded).
+            // Up to 32 lists: a tree merge of the lists padded to 128 keys
+            // (and to a power of two of lists with zero lists); more: the
+            // first wave merges them, lane s holding list s's head, staged
+            // in LDS when they fit, else from the scratch. The top count keys
+            // are the candidates, in order.
             for (uint32_t j = tid; j < static_cast<uint32_t>(kMaxCand); j += kT) sh.cand[j] = 0ull;
-            __syncthreads();
-            if (tid < 64) wave_merge(staged ? sh.surv : a.cand_buf, slices, a.top_k, count, sh.cand);
+            if (slices <= 32) {
+                uint32_t n = 1;
+                while (n < slices) n <<= 1;
+                for (uint32_t j = tid; j < n * kFastTopK; j += kT) {
+                    const uint32_t sl = j / kFastTopK, i = j % kFastTopK;
+                    sh.u.tree[0][sl][i] = (sl < slices && i < a.top_k) ? a.cand_buf[sl * a.top_k + i] : 0ull;
+                }
+                __syncthreads();
+                const int cur = block_tree_merge(sh.u.tree, n);
+                for (uint32_t j = tid; j < count; j += kT) sh.cand[j] = sh.u.tree[cur][0][j];
+            } else {
+                const uint32_t total = slices * a.top_k;
+                const bool staged = total <= static_cast<uint32_t>(kSurvivors);
+                if (staged)
+                    for (uint32_t j = tid; j < total; j += kT) sh.u.surv[j] = a.cand_buf[j];
+                __syncthreads();
+                if (tid < 64) wave_merge(staged ? sh.u.surv : a.cand_buf, slices, a.top_k, count, sh.cand);
+            }
             __syncthreads();
           } else {
             // Radix select: the key of the count-th largest finite score.
@@ -375,7 +504,56 @@ __global__ __launch_bounds__(kT) void sample_kernel(SampleArgs a) {
                 sh.prob[j] = isfinite(p) ? p : 0.0f;
             }
             __syncthreads();
-            if (tid == 0) {
+            if (count <= 128) {
+                // prepareProbabilities' total, its top-p scan and sampleCandidate's
+                // sums are one sequence of running sums P_j = P_{j-1} + p_j in
+                // candidate order: the first wave forms it (lane l holds P_l and
+                // P_{l+64}), then the cut and the pick are ballots over it.
+                if (tid < 64) {
+                    const uint32_t lane = tid;
+                    const float q0 = lane < count ? sh.prob[lane] : 0.0f;
+                    const float q1 = lane + 64 < count ? sh.prob[lane + 64] : 0.0f;
+                    float run = 0.0f, P0 = 0.0f, P1 = 0.0f;
+                    for (uint32_t j = 0; j < count; ++j) {
+                        const float pj = __int_as_float(
+                            __builtin_amdgcn_readlane(__float_as_int(j < 64 ? q0 : q1), static_cast<int>(j & 63)));
+                        run = __fadd_rn(run, pj);
+                        if (lane == (j & 63)) {
+                            if (j < 64) P0 = run;
+                            else P1 = run;
+                        }
+                    }
+                    const float total = run;
+                    uint32_t k = count;
+                    if (total <= 0.0f || !isfinite(total)) {
+                        k = 1;
+                    } else if (a.top_p < 1.0f) {
+                        const unsigned long long c0 = __ballot(lane < count && __fdiv_rn(P0, total) >= a.top_p);
+                        const unsigned long long c1 = __ballot(lane + 64 < count && __fdiv_rn(P1, total) >= a.top_p);
+                        if (c0) k = __ffsll(static_cast<long long>(c0));
+                        else if (c1) k = 64 + __ffsll(static_cast<long long>(c1));
+                    }
+                    // sampleCandidate with one draw of Random.float(f32) (every lane
+                    // draws the same value from the same state; lane 0 stores it).
+                    uint64_t st[4] = {a.prng[0], a.prng[1], a.prng[2], a.prng[3]};
+                    const float u = prng_float(st);
+                    __builtin_amdgcn_wave_barrier();
+                    if (lane == 0)
+                        for (int q = 0; q < 4; ++q) a.prng[q] = st[q];
+                    const uint32_t kl = k - 1;
+                    const float t2 = __int_as_float(
+                        __builtin_amdgcn_readlane(__float_as_int(kl < 64 ? P0 : P1), static_cast<int>(kl & 63)));
+                    uint32_t pick = 0;
+                    if (t2 > 0.0f && isfinite(t2)) {
+                        const float target = __fmul_rn(fminf(u, 0.99999994f), t2);
+                        const unsigned long long c0 = __ballot(lane < k && target <= P0);
+                        const unsigned long long c1 = __ballot(lane + 64 < k && target <= P1);
+                        pick = c0 ? __ffsll(static_cast<long long>(c0)) - 1
+                                  : (c1 ? 64 + __ffsll(static_cast<long long>(c1)) - 1 : k - 1);
+                    }
+                    if (lane == 0) sh.token = 0xffffffffu - static_cast<uint32_t>(sh.cand[pick] & 0xffffffffull);
+                }
+            } else if (tid == 0) {
                 float total = 0.0f;
                 for (uint32_t j = 0; j < count; ++j) total = __fadd_rn(total, sh.prob[j]);
                 uint32_t k = count;
