@@ -8,10 +8,12 @@
 //            to the lower id (buildCandidates + insertTopCandidate), found by
 //            a 4-pass radix select on order-preserving score keys, gathered
 //            and bitonic-sorted in LDS (top_k <= 1024);
-//            p_i = exp((s_i - s_0) / T) in parallel, then one thread sums
-//            them in candidate order, applies the top_p cut (:428-449), draws
+//            p_i = exp((s_i - s_0) / T) in parallel, then the running sums
+//            in candidate order (up to 128 candidates formed once by the
+//            first wave, with the cut and the pick as ballots over them;
+//            more by one thread), the top_p cut (:428-449), one draw of
 //            u = Random.float(f32) from Zig's DefaultPrng (xoshiro256++,
-//            state in device memory) and walks the cumulative sum
+//            state in device memory) and the walk of the cumulative sum
 //            (sampleCandidate, :451-463).
 // Sequential f32 sums in candidate order keep the reference's rounding.
 //
