@@ -764,27 +764,37 @@ def main() -> int:
     # pinned copy -- the reference's slice return -- or the argmax only), on
     # the same decode path, continuing after the generated tokens. Wall clock
     # per call.
+    # Then the same with resident single steps (vvli_gpu_set_resident: the
+    # launch stays and takes the next call's token through pinned memory).
     ft = {}
     n_ft = 32
-    if args.prompt + args.steps + 3 * n_ft <= args.ctx:
+    resident = persistent
+    if args.prompt + args.steps + (6 if resident else 3) * n_ft <= args.ctx:
         pos = args.prompt + args.steps
         tok = int(tokens[-1])
-        for kind in ("logits", "view", "argmax"):
-            torch.cuda.synchronize()
-            t1 = time.perf_counter()
-            for _ in range(n_ft):
-                if kind == "logits":
-                    tok = int(np.argmax(runner.forward_token(tok, pos)))
-                elif kind == "view":
-                    tok = int(np.argmax(runner.forward_token_view(tok, pos)))
-                else:
-                    tok = runner.forward_token_argmax(tok, pos)
-                pos += 1
-            ft[f"us_per_call_{kind}"] = round((time.perf_counter() - t1) / n_ft * 1e6, 1)
+        for suffix in ("", "_resident") if resident else ("",):
+            runner.set_resident(2000 if suffix else 0)
+            for kind in ("logits", "view", "argmax"):
+                torch.cuda.synchronize()
+                t1 = time.perf_counter()
+                for _ in range(n_ft):
+                    if kind == "logits":
+                        tok = int(np.argmax(runner.forward_token(tok, pos)))
+                    elif kind == "view":
+                        tok = int(np.argmax(runner.forward_token_view(tok, pos)))
+                    else:
+                        tok = runner.forward_token_argmax(tok, pos)
+                    pos += 1
+                ft[f"us_per_call_{kind}{suffix}"] = round((time.perf_counter() - t1) / n_ft * 1e6, 1)
+        runner.set_resident(0)
         ft["calls"] = n_ft
         print(f"[bench] forward_token: {ft['us_per_call_logits']} us/call with logits into the caller's buffer, "
               f"{ft['us_per_call_view']} as the pinned view, {ft['us_per_call_argmax']} argmax only",
               file=sys.stderr, flush=True)
+        if resident:
+            print(f"[bench] forward_token, resident steps: {ft['us_per_call_logits_resident']} / "
+                  f"{ft['us_per_call_view_resident']} / {ft['us_per_call_argmax_resident']} us/call",
+                  file=sys.stderr, flush=True)
 
     # GEMV half of the metric: the isolated op at M = 1 on the five projection
     # shapes of the model (cold weights), HBM GB/s per shape.

@@ -165,10 +165,23 @@ int vvli_gpu_forward_token(vvli_gpu_model* model, uint32_t token, uint32_t pos, 
  * borrowed slice of scratch.logits, valid until the next call
  * (src/llm.zig:702-709,729). *logits_view points at the library's pinned host
  * copy of the vocab logits, overwritten by the next forward_token_view call
- * on this model and freed with it (set only on success); argmax_out is
+ * on this model (and, with resident steps, by the next forward_token call
+ * that returns logits) and freed with it (set only on success); argmax_out is
  * optional. Same errors as vvli_gpu_forward_token. */
 int vvli_gpu_forward_token_view(vvli_gpu_model* model, uint32_t token, uint32_t pos, const float** logits_view,
                                 uint32_t* argmax_out);
+/* Resident single steps for callers that drive the model one token at a time
+ * (the forwardToken loop of src/generator.zig:243-293 run from the host). No
+ * counterpart in the reference, which has no launches: with linger_us > 0, a
+ * forward_token / forward_token_view call on the persistent decode path
+ * leaves its launch running for up to linger_us of idle time, and the next
+ * call hands it (token, pos) through pinned host memory instead of
+ * launching again; the step writes the logits straight to pinned host memory
+ * when the call returns them. Results are those of separate launches. While
+ * such a launch waits it occupies every CU, so other work on the GPU waits up
+ * to linger_us; every other entry point on the model ends it first. 0 (the
+ * default) turns it off; linger_us over 100000 -> VVLI_INVALID_CONFIG. */
+int vvli_gpu_set_resident(vvli_gpu_model* model, uint32_t linger_us);
 /* Runner.forwardEmbedding, src/llm.zig:711-718: embedding = hidden floats (host). */
 int vvli_gpu_forward_embedding(vvli_gpu_model* model, const float* embedding, uint32_t pos, float* logits_out,
                                uint32_t* argmax_out);

@@ -115,6 +115,7 @@ PROTOTYPES = {
     "vvli_gpu_set_rope_table": (c_int, [c_void_p, c_void_p, c_uint32]),
     "vvli_gpu_forward_token": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, POINTER(c_uint32)]),
     "vvli_gpu_forward_token_view": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_void_p), POINTER(c_uint32)]),
+    "vvli_gpu_set_resident": (c_int, [c_void_p, c_uint32]),
     "vvli_gpu_forward_embedding": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, POINTER(c_uint32)]),
     "vvli_gpu_forward_token_debug": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
     "vvli_gpu_kv_read": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),

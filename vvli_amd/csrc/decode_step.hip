@@ -61,6 +61,9 @@ constexpr uint32_t kSpinLimit = 1u << 22;  // polls of one word (each after a sh
 
 typedef unsigned long long tword;
 
+__device__ __forceinline__ float ld_a(const float* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t ld_a(const uint32_t* p) {
     return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -79,6 +82,12 @@ __device__ __forceinline__ void st_a(tword* p, tword v) {
 // Pinned host memory (vector store at system scope).
 __device__ __forceinline__ void st_sys(uint32_t* p, uint32_t v) {
     __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_sys(float* p, float v) {
+    __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t ld_sys(const uint32_t* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
@@ -473,12 +482,15 @@ __device__ __forceinline__ void mk_glds_compute(const GLds& gl, const MkGemv& g,
 // loads and stores share one completion counter, so a store per tile would
 // make every following weight wait for that store's acknowledgement. Each lane
 // also loads its tile's addend (residual row or bias) when the batch opens and
-// checks the residual's tag only when it writes.
+// checks the residual's tag only when it writes. dbg (nullable): a second
+// destination of the outputs -- the residual rows after the layer (parity
+// dumps) -- or, in the logits phase with WT, a flag: the logits are written
+// through (every block then copies a slice of them to host memory).
 // MOE down phase (g.moe == 2): a tile (one output row) has an item per pair
 // of slots (and chunk of the row); slots s, s + 1 multiply their experts'
 // rows with xs + s * K and xs + (s + 1) * K and add wsl[s], wsl[s + 1] times
 // the dot products, per lane, before the wave sum.
-template <bool MOE = false>
+template <bool MOE = false, bool WT = false>
 __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* xs, const MkWave& w,
                                         uint4 (&bufA)[2][kNJC], MkTile& tA, bool have, unsigned long long& best,
                                         uint32_t tag, const MkResid& rs, uint32_t t0, const float* park,
@@ -538,8 +550,13 @@ __device__ __forceinline__ bool mk_gemv(const MkGemv& g, int mode, const float* 
         auto flush = [&]() {
             if ((uint32_t)lane < pending) {
                 if (mode == kGemvLogits) {
-                    if (va) *as_global(g.plain + ra) = oa;
-                    if (vb) *as_global(g.plain + rb) = ob;
+                    if (WT && dbg) {  // written through, for the copy to host memory (resident single steps)
+                        if (va) st_a(g.plain + ra, oa);
+                        if (vb) st_a(g.plain + rb, ob);
+                    } else {
+                        if (va) *as_global(g.plain + ra) = oa;
+                        if (vb) *as_global(g.plain + rb) = ob;
+                    }
                 } else {
                     if (mode == kGemvResid && !rs.bf16) {
                         ok = ok && poll_tw(rs.src + ra, rs.tag, wa, err) && poll_tw(rs.src + rb, rs.tag, wb, err);
@@ -1657,7 +1674,9 @@ __device__ __forceinline__ bool mk_route(const DecodeStepParams& p, uint32_t lay
     return true;
 }
 
-template <int HDMAX, bool EXACT, bool MOE = false>
+// RES: the resident single-step form (p.mbox set); its code is compiled only
+// into those instances, so the other launches run exactly the plain step.
+template <int HDMAX, bool EXACT, bool MOE = false, bool RES = false>
 __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParams p) {
     extern __shared__ float smem[];
     __shared__ float red[kMkWaves];
@@ -1691,7 +1710,8 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     if (tid == 0) {
         if (p.init_step) {
             s_ctl[0] = p.init_token;
-            s_ctl[1] = p.init_pos;
+            // (bit 31, resident steps: this step writes its logits to host memory)
+            s_ctl[1] = p.init_pos | ((RES && p.host_logits && p.init_logits) ? 0x80000000u : 0u);
             if (blockIdx.x == 0) {  // the same thread finishes the step and reads these back
                 st_a(&p.state->token, p.init_token);
                 st_a(&p.state->pos, p.init_pos);
@@ -1712,7 +1732,11 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
     // or the host raised it): leave before any phase.
     if (s_ctl[3] != 0) return;
     uint32_t token = s_ctl[0];
-    const uint32_t pos0 = s_ctl[1];
+    const uint32_t pos0 = s_ctl[1] & 0x7fffffffu;
+    // Resident single steps carry their own position (and whether to write
+    // the logits to host memory, bit 31) in a second step word, kept in
+    // s_ctl[1] for the step (read where needed, not held in registers).
+    auto host_lg = [&]() { return RES && p.host_logits && (s_ctl[1] >> 31); };
     bool have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
     // The o phases leave out blocks [0, kv_heads) -- they run the attention
     // units that append the K/V row and merge, the last to finish the
@@ -1725,17 +1749,24 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
 
     for (uint32_t step = 0; step < p.n_steps; ++step) {
         const uint32_t e0 = p.epoch0 + step * nps;  // epoch of this step's phase 0
-        const uint32_t pos = pos0 + step;
-        if (step > 0) {  // next token from the previous step's argmax
+        if (step > 0) {  // next token from the previous step's argmax (or the host's request)
             __syncthreads();
             if (tid == 0) {
                 tword wv = ld_a(p.step_word);
                 s_ctl[2] = poll_tw(p.step_word, e0 - 1, wv, p.error) ? (uint32_t)wv : 0xfffffffeu;
+                if (RES && s_ctl[2] < 0xfffffffeu) {
+                    tword wp = ld_a(p.step_word + 1);
+                    if (poll_tw(p.step_word + 1, e0 - 1, wp, p.error)) s_ctl[1] = (uint32_t)wp;
+                    else s_ctl[2] = 0xfffffffeu;
+                }
             }
             __syncthreads();
             token = s_ctl[2];
-            if (token >= 0xfffffffeu) break;  // stop (EOS / context full) or error
+            if (token >= 0xfffffffeu) break;  // stop (EOS / context full / no request) or error
         }
+        // (Block-uniform: read into a scalar register.)
+        const uint32_t pos =
+            RES ? (uint32_t)__builtin_amdgcn_readfirstlane((int)(s_ctl[1] & 0x7fffffffu)) : pos0 + step;
         if (pos >= p.max_seq || token >= p.vocab) {  // host validated; defensive stop
             if (blockIdx.x == 0 && tid == 0) st_a(p.error, kDecodeErrState);
             return;
@@ -1832,15 +1863,20 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                         have = mk_prefetch(g, mode, w, buf, tile, gl.n);
                         mk_glds_compute(gl, g, smem, reinterpret_cast<char*>(smem), p.g_lds_park, w);
                     }
-                    ok = ok && mk_gemv<MOE>(g, mode, smem, wp, buf, tile, have, best, tag, rs, gl.n,
+                    ok = ok && mk_gemv<MOE, RES>(g, mode, smem, wp, buf, tile, have, best, tag, rs, gl.n,
                                             reinterpret_cast<const float*>(reinterpret_cast<const char*>(smem) +
                                                                            p.g_lds_park),
                                             n_lds ? (blockIdx.x - gl.first_block) * gl.per_block + w.wave : 0,
                                             n_lds, p.error,
                                             (f.kind == kPhD && p.hidden_dbg) ? p.hidden_dbg + (size_t)f.layer * H
+                                            : (f.logits && host_lg())         ? p.host_logits
                                                                              : nullptr,
                                             s_ex, s_w);
                 }
+                // The wave's written-through logits are complete before its
+                // key is published (the blocks copy them to host memory once
+                // every key is there).
+                if (f.logits && host_lg()) wait_all_mem();
                 if (f.logits && w.lane == 0) {
                     st_a(p.tkeys + 2 * w.wid, tw_make_u((uint32_t)(best >> 32), tag));
                     st_a(p.tkeys + 2 * w.wid + 1, tw_make_u((uint32_t)best, tag));
@@ -1865,10 +1901,31 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                     mk_glds(p, units, ng).n > 0)
                     have = false;
                 else have = false;
-            } else if (step + 1 < p.n_steps) {
+            } else if (!RES && step + 1 < p.n_steps) {
                 have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
             }
             if (tid == 0) mk_mark(p, ph, 13);
+        }
+
+        // ---- resident step that returns its logits: every block copies a
+        // slice of them to host memory once every wave's key shows that its
+        // (written-through) logits are complete, then marks its slice copied.
+        if (host_lg()) {
+            constexpr bool kPin = HDMAX == 128 && (MOE || !EXACT);  // (as the staging: no hoisted addresses)
+            const uint32_t ktag = e0 + logits_ph;
+            bool ok = true;
+            for (uint32_t i = mk_tid<kPin>(); i < w.nw; i += kMkThreads) {
+                tword hi = ld_a(p.tkeys + 2 * i), lo = ld_a(p.tkeys + 2 * i + 1);
+                ok = ok && poll_tw2(p.tkeys + 2 * i, p.tkeys + 2 * i + 1, ktag, hi, lo, p.error);
+            }
+            if (__syncthreads_or(!ok)) return;
+            const uint32_t per = (p.vocab + gridDim.x - 1) / gridDim.x;
+            const uint32_t end = min(p.vocab, (blockIdx.x + 1) * per);
+            for (uint32_t i = blockIdx.x * per + mk_tid<kPin>(); i < end; i += kMkThreads)
+                st_sys(p.host_logits + i, ld_a(p.logits + i));
+            wait_all_mem();
+            __syncthreads();
+            if (tid == 0) st_a(p.tcopied + blockIdx.x, tw_make_u(0u, ktag));
         }
 
         // ---- argmax + step advance (block 0) ----
@@ -1885,7 +1942,55 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
             b = wave_max_u64(b);
             if (w.lane == 0) kred[wave] = b;
             if (__syncthreads_or(!ok)) return;
-            if (tid == 0) {
+            if (host_lg()) {  // every block's slice of the logits is in host memory
+                const uint32_t ktag = e0 + logits_ph;
+                for (uint32_t bl = mk_tid<HDMAX == 128 && (MOE || !EXACT)>(); bl < gridDim.x; bl += kMkThreads) {
+                    tword cw = ld_a(p.tcopied + bl);
+                    ok = ok && poll_tw(p.tcopied + bl, ktag, cw, p.error);
+                }
+                if (__syncthreads_or(!ok)) return;
+            }
+            if constexpr (RES) {
+                if (tid == 0) {
+                    for (int i = 0; i < kMkWaves; ++i) b = kred[i] > b ? kred[i] : b;
+                    const uint32_t tok = argmax_key_index(b);  // llm.argmax, src/llm.zig:778-789
+                    st_a(&p.state->argmax, tok);
+                    // Resident single steps: report this one, then wait for the
+                    // host's next request (bounded by the linger time).
+                    // (The report goes to coherent host memory: each store is
+                    // complete before the sequence number is issued, and every
+                    // block's logits stores were complete before its mark.)
+                    HostStepOut* h = p.host_out;
+                    st_sys(&h->argmax, tok);
+                    st_sys(&h->stop, 0u);
+                    st_sys(&h->error, 0u);
+                    wait_all_mem();
+                    st_sys(&h->seq, p.host_seq + step);
+                    if (step + 1 < p.n_steps) {
+                        const uint32_t want = p.host_seq + step + 1;
+                        uint32_t next_tok = 0xffffffffu, next_pos = 0;
+                        const unsigned long long deadline = __builtin_amdgcn_s_memrealtime() + p.linger_ticks;
+                        for (uint32_t spins = 0;; ++spins) {
+                            if (ld_sys(&p.mbox->seq) == want) {
+                                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");  // the request's fields after its number
+                                if (ld_sys(&p.mbox->cmd) == 0) {
+                                    next_tok = ld_sys(&p.mbox->token);
+                                    next_pos = ld_sys(&p.mbox->pos);
+                                }
+                                break;
+                            }
+                            if ((spins & 15u) == 15u && __builtin_amdgcn_s_memrealtime() > deadline) break;
+                            __builtin_amdgcn_s_sleep(2);
+                        }
+                        if (next_tok != 0xffffffffu) {
+                            st_a(&p.state->token, next_tok);
+                            st_a(&p.state->pos, next_pos & 0x7fffffffu);
+                            st_a(p.step_word + 1, tw_make_u(next_pos, e0 + nps - 1));
+                        }
+                        st_a(p.step_word, tw_make_u(next_tok, e0 + nps - 1));
+                    }
+                }
+            } else if (tid == 0) {
                 for (int i = 0; i < kMkWaves; ++i) b = kred[i] > b ? kred[i] : b;
                 const uint32_t tok = argmax_key_index(b);  // llm.argmax, src/llm.zig:778-789
                 const uint32_t next_pos = pos + 1;
@@ -1907,10 +2012,14 @@ __global__ __launch_bounds__(kMkThreads) void decode_step_kernel(DecodeStepParam
                 if (step + 1 < p.n_steps) st_a(p.step_word, tw_make_u(stop ? 0xffffffffu : next_tok, e0 + nps - 1));
             }
         }
+        // (Resident steps: the next step's first weights after block 0's
+        // argmax, report and copy, so that none is held in registers across
+        // that code.)
+        if (RES && step + 1 < p.n_steps) have = mk_prefetch(tb.gemv[0], kGemvPlain, w, buf, tile);
     }
     // The thread that finished every step (or saw the stop or the error flag)
     // reports to the host; the step state holds its own last writes.
-    if (p.host_out && blockIdx.x == 0 && tid == 0) {
+    if (!RES && p.host_out && blockIdx.x == 0 && tid == 0) {
         HostStepOut* h = p.host_out;
         st_sys(&h->argmax, ld_a(&p.state->argmax));
         st_sys(&h->stop, ld_a(&p.state->stop));
@@ -1965,23 +2074,34 @@ uint32_t decode_step_glds_plan(uint32_t hidden, uint32_t inter, uint32_t hd, siz
 
 bool decode_step_moe_supported(uint32_t hd) { return hd == 64 || hd == 128; }
 
-static const void* decode_step_fn(uint32_t hd, bool moe) {
+template <bool RES>
+static const void* decode_step_fn_t(uint32_t hd, bool moe) {
     if (moe) {
-        if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true, true>);
-        return reinterpret_cast<const void*>(&decode_step_kernel<128, true, true>);
+        if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true, true, RES>);
+        return reinterpret_cast<const void*>(&decode_step_kernel<128, true, true, RES>);
     }
-    if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true>);
-    if (hd == 128) return reinterpret_cast<const void*>(&decode_step_kernel<128, true>);
-    if (hd <= 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, false>);
-    return reinterpret_cast<const void*>(&decode_step_kernel<128, false>);
+    if (hd == 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, true, false, RES>);
+    if (hd == 128) return reinterpret_cast<const void*>(&decode_step_kernel<128, true, false, RES>);
+    if (hd <= 64) return reinterpret_cast<const void*>(&decode_step_kernel<64, false, false, RES>);
+    return reinterpret_cast<const void*>(&decode_step_kernel<128, false, false, RES>);
+}
+static const void* decode_step_fn(uint32_t hd, bool moe, bool resident = false) {
+    return resident ? decode_step_fn_t<true>(hd, moe) : decode_step_fn_t<false>(hd, moe);
 }
 
 hipError_t decode_step_max_blocks(uint32_t hd, size_t lds, int* blocks_per_cu, bool moe) {
     if (moe && !decode_step_moe_supported(hd)) return hipErrorInvalidValue;
     const void* f = decode_step_fn(hd, moe);
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(decode_step_fn(hd, moe, true), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kMkThreads, lds);
+    int res_blocks = 0;  // the resident form fits as many blocks
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&res_blocks, decode_step_fn(hd, moe, true), kMkThreads, lds);
+    if (e != hipSuccess) return e;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kMkThreads, lds);
+    if (e == hipSuccess && res_blocks < *blocks_per_cu) *blocks_per_cu = res_blocks;
+    return e;
 }
 
 // The launch is cooperative (the runtime guarantees that all blocks are
@@ -2001,8 +2121,10 @@ hipError_t launch_decode_step(const DecodeStepParams& p, uint32_t blocks, size_t
     if (moe && (!decode_step_moe_supported(p.hd) || p.experts > 256 || p.top_k == 0 || p.top_k > kMaxTopK ||
                 p.top_k > p.experts || p.hidden % 8 != 0))
         return hipErrorInvalidValue;
-    if (plain) return hipLaunchKernel(decode_step_fn(p.hd, moe), dim3(blocks), dim3(kMkThreads), args, lds, s);
-    return hipLaunchCooperativeKernel(decode_step_fn(p.hd, moe), dim3(blocks), dim3(kMkThreads), args, (unsigned)lds,
+    if (p.mbox && (!p.host_out || !p.init_step)) return hipErrorInvalidValue;
+    const void* f = decode_step_fn(p.hd, moe, p.mbox != nullptr);
+    if (plain) return hipLaunchKernel(f, dim3(blocks), dim3(kMkThreads), args, lds, s);
+    return hipLaunchCooperativeKernel(f, dim3(blocks), dim3(kMkThreads), args, (unsigned)lds,
                                       s);
 }
 

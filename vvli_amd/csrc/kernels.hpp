@@ -169,6 +169,17 @@ struct HostStepOut {
     uint32_t error;
 };
 
+// Pinned host memory through which the host hands a resident launch its next
+// single step: the host writes token, pos (bit 31: write the step's logits to
+// host memory) and cmd (0 step, 1 leave), then seq; the launch takes request
+// seq == (its first step's sequence number) + (steps done).
+struct HostMailbox {
+    uint32_t seq;
+    uint32_t token;
+    uint32_t pos;
+    uint32_t cmd;
+};
+
 // Activations of the persistent step are arrays of tagged 64-bit words: the
 // f32 value (or u32) in the low half, the epoch of the phase that wrote it in
 // the high half.
@@ -190,6 +201,7 @@ struct DecodeStepParams {
     unsigned long long* tpart_ml;   // attention partials: (max, sum) [kv_heads][nsplit][group][2]
     unsigned long long* tpart_acc;  // attention partials: unnormalised out [kv_heads][nsplit][group][hd]
     unsigned long long* tkeys;      // argmax key of every wave: [waves][2] (high, low half)
+    unsigned long long* tcopied;    // resident steps with logits: block b's slice copied to the host [blocks]
     unsigned long long* step_word;  // next token (0xffffffff: stop) published by the argmax
     float* logits;                  // [vocab]
     StepState* state;
@@ -235,6 +247,17 @@ struct DecodeStepParams {
     // Nullable pinned host memory, written at the end of the last step.
     HostStepOut* host_out;
     uint32_t host_seq;
+    // Resident single steps (mbox != nullptr, with init_step and host_out):
+    // after each step the finishing thread reports it in host_out (sequence
+    // number host_seq + step) and waits up to linger_ticks (100 MHz clock)
+    // for the next request in mbox, which the other blocks take from the step
+    // words; no request in time, a leave command or n_steps reached: the
+    // launch ends. host_logits: where a step that asks for them writes its
+    // logits (pinned host memory); init_logits: whether the first step does.
+    HostMailbox* mbox;
+    uint32_t linger_ticks;
+    float* host_logits;
+    uint32_t init_logits;
 };
 
 // LDS bytes of one gate/up tile (gate row + up row of K bf16 weights, in

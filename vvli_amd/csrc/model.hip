@@ -13,6 +13,7 @@
 // the token and position from `state`, so it is captured once into a HIP
 // graph and replayed; generation chains the steps on the device.
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -74,7 +75,14 @@ struct vvli_gpu_model {
     bool mk_timed = false;
     HostStepOut* h_out = nullptr;  // pinned: result of the last single-step launch
     float* h_logits = nullptr;     // pinned [vocab]: forward_token_view's logits (allocated on first use)
-    uint32_t mk_host_seq = 0;      // sequence number of the last single-step launch
+    uint32_t mk_host_seq = 0;      // sequence number of the last single step (launch or resident request)
+    // Resident single steps (vvli_gpu_set_resident): the launch stays on the
+    // stream between forward_token calls and takes the next request from
+    // h_mbox, for up to res_linger_us of idle time.
+    HostMailbox* h_mbox = nullptr;  // pinned (allocated on first use)
+    uint32_t res_linger_us = 0;     // 0: off
+    bool res_active = false;        // a resident launch may still be running
+    uint32_t res_left = 0;          // requests it can still take
     // Mixture-of-experts model (vvli_gpu_moe_model_create).
     bool moe = false;
     MoeLayout moe_layout;
@@ -126,6 +134,11 @@ namespace {
     } while (0)
 
 #define LAUNCH(expr) HIP_TRY(expr)
+#define RESIDENT_STOP(m)                       \
+    do {                                       \
+        const int rs_ = resident_stop(m);      \
+        if (rs_) return rs_;                   \
+    } while (0)
 
 const void* wslice(const vvli_gpu_model* m, size_t off) {
     return off == kNone ? nullptr : static_cast<const void*>(m->blob + off * m->ebytes);
@@ -432,7 +445,7 @@ uint32_t mk_ff_width(const vvli_gpu_config& c) { return c.num_experts ? c.expert
 
 // Offsets (in words) of the tagged activation arrays inside mk_tw.
 struct TaggedLayout {
-    size_t tx, tqkv, tattn, tff, ml, acc, keys, step, rl, total;
+    size_t tx, tqkv, tattn, tff, ml, acc, keys, copied, step, rl, total;
 };
 TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t blocks) {
     const size_t H = c.hidden, kv = kv_dim(c), G = c.heads / c.kv_heads, hd = head_dim(c);
@@ -450,6 +463,7 @@ TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t b
     t.ml = take(static_cast<size_t>(c.kv_heads) * nsplit * G * 2);
     t.acc = take(static_cast<size_t>(c.kv_heads) * nsplit * G * hd);
     t.keys = take(static_cast<size_t>(blocks) * 8 * 2);
+    t.copied = take(blocks);
     t.step = take(1);
     t.rl = take(c.num_experts);  // MoE router logits
     t.total = cur;
@@ -460,7 +474,14 @@ TaggedLayout tagged_layout(const vvli_gpu_config& c, uint32_t nsplit, uint32_t b
 // in the launch arguments, and the result comes back in m->h_out.
 struct SingleStep {
     uint32_t token, pos;
+    bool resident = false;  // stay for the next requests (h_mbox)
+    bool logits = false;    // resident: the first step writes its logits to h_logits
 };
+// Steps one resident launch can take (its epochs are reserved at launch), and
+// the longest idle wait between requests (well inside the other blocks'
+// bounded step-word polls, which last seconds).
+constexpr uint32_t kResidentSteps = 4096;
+constexpr uint32_t kMaxResidentLingerUs = 100000;
 
 int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned long long* timing = nullptr,
                    uint32_t timing_stride = 0, float* hidden_dbg = nullptr, const SingleStep* single = nullptr) {
@@ -501,6 +522,7 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
     p.tpart_ml = m->mk_tw + tl.ml;
     p.tpart_acc = m->mk_tw + tl.acc;
     p.tkeys = m->mk_tw + tl.keys;
+    p.tcopied = m->mk_tw + tl.copied;
     p.step_word = m->mk_tw + tl.step;
     p.logits = m->logits;
     p.state = m->state;
@@ -531,6 +553,12 @@ int run_persistent(vvli_gpu_model* m, uint32_t n_steps, int64_t eos, unsigned lo
         p.host_out = m->h_out;
         p.host_seq = ++m->mk_host_seq;
         if (p.host_seq == 0) p.host_seq = m->mk_host_seq = 1;  // 0 is what h_out holds before any launch
+        if (single->resident) {
+            p.mbox = m->h_mbox;
+            p.linger_ticks = m->res_linger_us * 100u;  // s_memrealtime runs at 100 MHz
+            p.host_logits = m->h_logits;
+            p.init_logits = single->logits ? 1u : 0u;
+        }
     }
     m->mk_epoch += static_cast<uint32_t>(need);
     // The error word is zero here unless a launch of an unchecked sequence
@@ -587,6 +615,102 @@ int read_single(vvli_gpu_model* m, float* logits_out, uint32_t* argmax_out) {
     const int rc = check_persistent_error(m);
     if (rc) return rc;
     return set_error(VVLI_HIP_ERROR, "persistent decode step ended without its result");
+}
+
+// ---------------------------------------------------------------------------
+// Resident single steps. forward_token hands the running launch its request
+// through pinned host memory (token, position, whether to write the logits,
+// then the sequence number) and spins on the step's report in h_out; the
+// step writes its logits straight to h_logits when asked. A launch that has
+// ended (no request within the linger time, kResidentSteps taken, or an
+// error) is found by a stream query: after an error the device word says
+// why, else the request goes out with a new launch.
+// ---------------------------------------------------------------------------
+// Coherent (fine-grained) pinned memory: the device's stores reach it while
+// its launch runs, and its loads see the host's stores.
+static int alloc_pinned(void** p, size_t bytes) {
+    if (*p) return VVLI_OK;
+    if (hipHostMalloc(p, bytes, hipHostMallocCoherent) != hipSuccess) {
+        *p = nullptr;
+        return set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc of %zu bytes failed", bytes);
+    }
+    std::memset(*p, 0, bytes);
+    return VVLI_OK;
+}
+
+// Ends a resident launch that may still be waiting for a request (every
+// other entry point calls this before it touches the stream or the model).
+int resident_stop(vvli_gpu_model* m) {
+    if (!m->res_active) return VVLI_OK;
+    m->res_active = false;
+    volatile HostMailbox* mb = m->h_mbox;
+    mb->cmd = 1;
+    std::atomic_thread_fence(std::memory_order_release);
+    mb->seq = ++m->mk_host_seq;  // the request it waits for: leave
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return check_persistent_error(m);
+}
+
+static int resident_launch(vvli_gpu_model* m, uint32_t token, uint32_t pos, bool logits) {
+    SingleStep one{token, pos};
+    one.resident = true;
+    one.logits = logits;
+    const int rc = run_persistent(m, kResidentSteps, -1, nullptr, 0, nullptr, &one);
+    if (rc) return rc;
+    m->res_active = true;
+    m->res_left = kResidentSteps - 1;
+    return VVLI_OK;
+}
+
+static int forward_resident(vvli_gpu_model* m, uint32_t token, uint32_t pos, float* logits_out,
+                            uint32_t* argmax_out) {
+    const vvli_gpu_config& c = m->cfg;
+    int rc = alloc_pinned(reinterpret_cast<void**>(&m->h_mbox), sizeof(HostMailbox));
+    if (rc) return rc;
+    const bool want = logits_out != nullptr;
+    // Every resident launch gets the logits buffer, so any request can ask for them.
+    if ((rc = alloc_pinned(reinterpret_cast<void**>(&m->h_logits), static_cast<size_t>(c.vocab) * sizeof(float))))
+        return rc;
+    if (m->mk_host_seq >= 0xfffffff0u) {  // sequence numbers restart (0 is never a request's)
+        if ((rc = resident_stop(m))) return rc;
+        m->mk_host_seq = 0;
+        m->h_out->seq = 0;
+    }
+    bool sent = false;
+    if (m->res_active && m->res_left > 0) {
+        volatile HostMailbox* mb = m->h_mbox;
+        mb->token = token;
+        mb->pos = pos | (want ? 0x80000000u : 0u);
+        mb->cmd = 0;
+        std::atomic_thread_fence(std::memory_order_release);
+        mb->seq = ++m->mk_host_seq;
+        --m->res_left;
+        sent = true;
+    } else {
+        if ((rc = resident_stop(m))) return rc;  // a launch with no requests left
+        if ((rc = resident_launch(m, token, pos, want))) return rc;
+    }
+    const volatile HostStepOut* h = m->h_out;
+    // (m->mk_host_seq: the request's number; a relaunch below gives it a new one.)
+    for (uint32_t spins = 1; h->seq != m->mk_host_seq; ++spins) {
+        if ((spins & 255u) != 0) continue;
+        const hipError_t q = hipStreamQuery(m->stream);
+        if (q == hipErrorNotReady) continue;
+        if (q != hipSuccess) HIP_TRY(q);
+        if (h->seq == m->mk_host_seq) break;
+        // The launch has ended without this step's report.
+        m->res_active = false;
+        if ((rc = check_persistent_error(m))) return rc;
+        if (!sent) return set_error(VVLI_HIP_ERROR, "persistent decode step ended without its result");
+        // It left before taking the request: a new launch carries it.
+        if ((rc = resident_launch(m, token, pos, want))) return rc;
+        sent = false;
+    }
+    std::atomic_thread_fence(std::memory_order_acquire);
+    if (argmax_out) *argmax_out = h->argmax;
+    if (logits_out && logits_out != m->h_logits)
+        std::memcpy(logits_out, m->h_logits, static_cast<size_t>(c.vocab) * sizeof(float));
+    return VVLI_OK;
 }
 
 // The step's outputs. Without logits, the argmax and (after a persistent
@@ -890,6 +1014,7 @@ void free_model(vvli_gpu_model* m) {
     if (m->h_state) (void)hipHostFree(m->h_state);
     if (m->h_err) (void)hipHostFree(m->h_err);
     if (m->h_out) (void)hipHostFree(m->h_out);
+    if (m->h_mbox) (void)hipHostFree(m->h_mbox);
     if (m->h_logits) (void)hipHostFree(m->h_logits);
     if (m->mk_ev0) (void)hipEventDestroy(m->mk_ev0);
     if (m->mk_ev1) (void)hipEventDestroy(m->mk_ev1);
@@ -1026,7 +1151,7 @@ int create_impl(const vvli_gpu_config* cfg, uint32_t max_seq_len, const void* ho
                           hipSuccess
                       ? 0
                       : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
-        TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_out), sizeof(HostStepOut), hipHostMallocDefault) ==
+        TRY_ALLOC(hipHostMalloc(reinterpret_cast<void**>(&m->h_out), sizeof(HostStepOut), hipHostMallocCoherent) ==
                           hipSuccess
                       ? 0
                       : set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc failed"));
@@ -1405,6 +1530,7 @@ int vvli_gpu_read_weights(vvli_gpu_model* m, uint64_t elem_offset, uint64_t n, v
                          static_cast<unsigned long long>(elem_offset), static_cast<unsigned long long>(n),
                          m->layout.total);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     HIP_TRY(hipMemcpy(out, m->blob + elem_offset * m->ebytes, n * m->ebytes, hipMemcpyDeviceToHost));
     return VVLI_OK;
 }
@@ -1418,6 +1544,7 @@ int vvli_gpu_moe_model_create(const vvli_gpu_config* cfg, uint32_t max_seq_len, 
 int vvli_gpu_model_destroy(vvli_gpu_model* model) {
     if (!model) return set_error(VVLI_NULL_ARG, "model is NULL");
     (void)hipSetDevice(model->device);
+    (void)resident_stop(model);
     (void)hipStreamSynchronize(model->stream);
     free_model(model);
     return VVLI_OK;
@@ -1426,6 +1553,7 @@ int vvli_gpu_model_destroy(vvli_gpu_model* model) {
 int vvli_gpu_kv_clear(vvli_gpu_model* m) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     const size_t kvlen = static_cast<size_t>(m->cfg.layers) * m->max_seq * kv_dim(m->cfg);
     HIP_TRY(hipMemsetAsync(m->kcache, 0, kvlen * sizeof(float), m->stream));
     HIP_TRY(hipMemsetAsync(m->vcache, 0, kvlen * sizeof(float), m->stream));
@@ -1436,6 +1564,7 @@ int vvli_gpu_kv_clear(vvli_gpu_model* m) {
 int vvli_gpu_set_rope_table(vvli_gpu_model* m, const float* inv_freq, uint32_t n) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     const uint32_t half = head_dim(m->cfg) / 2;
     if (inv_freq && n != half) return set_error(VVLI_INVALID_CONFIG, "rope table needs %u entries, got %u", half, n);
     if (inv_freq)
@@ -1452,6 +1581,7 @@ int vvli_gpu_forward_token(vvli_gpu_model* m, uint32_t token, uint32_t pos, floa
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
     if (use_persistent(m)) {
+        if (m->res_linger_us) return forward_resident(m, token, pos, logits_out, argmax_out);
         const SingleStep one{token, pos};
         int rc = run_persistent(m, 1, -1, nullptr, 0, nullptr, &one);
         if (rc) return rc;
@@ -1470,7 +1600,7 @@ int vvli_gpu_forward_token_view(vvli_gpu_model* m, uint32_t token, uint32_t pos,
     if (!m->h_logits) {
         HIP_TRY(hipSetDevice(m->device));
         if (hipHostMalloc(reinterpret_cast<void**>(&m->h_logits), static_cast<size_t>(m->cfg.vocab) * sizeof(float),
-                          hipHostMallocDefault) != hipSuccess) {
+                          hipHostMallocCoherent) != hipSuccess) {
             m->h_logits = nullptr;
             return set_error(VVLI_OUT_OF_MEMORY, "hipHostMalloc of the logits view failed");
         }
@@ -1488,7 +1618,19 @@ int vvli_gpu_set_decode_path(vvli_gpu_model* m, uint32_t path) {
     if (path > 2) return set_error(VVLI_INVALID_CONFIG, "decode path %u not in 0..2", path);
     if (path == 2 && !m->mk_ok)
         return set_error(VVLI_INVALID_CONFIG, "persistent decode step unavailable (bf16 weights, fits one CU)");
+    HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     m->path = path;
+    return VVLI_OK;
+}
+
+int vvli_gpu_set_resident(vvli_gpu_model* m, uint32_t linger_us) {
+    if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    if (linger_us > kMaxResidentLingerUs)
+        return set_error(VVLI_INVALID_CONFIG, "linger %u us over %u", linger_us, kMaxResidentLingerUs);
+    HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
+    m->res_linger_us = linger_us;
     return VVLI_OK;
 }
 
@@ -1506,6 +1648,7 @@ int vvli_gpu_forward_embedding(vvli_gpu_model* m, const float* embedding, uint32
     if (!m || !embedding) return set_error(VVLI_NULL_ARG, "NULL argument to vvli_gpu_forward_embedding");
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     HIP_TRY(hipMemcpyAsync(m->x, embedding, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(launch_set_state(m->state, 0, pos, 0, 0, m->stream));
     int rc = enqueue_body(m, m->stream, nullptr);
@@ -1519,6 +1662,7 @@ int vvli_gpu_forward_token_debug(vvli_gpu_model* m, uint32_t token, uint32_t pos
     if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
     // The path forward_token takes: the persistent step's down-projection
     // phases write the residual rows, or the per-kernel step runs eagerly.
@@ -1536,6 +1680,7 @@ int vvli_gpu_profile_step(vvli_gpu_model* m, uint32_t token, uint32_t pos, float
     if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     HIP_TRY(launch_set_state(m->state, token, pos, 0, 0, m->stream));
     std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
     g_launch_events = &evs;
@@ -1568,6 +1713,7 @@ int vvli_gpu_profile_persistent(vvli_gpu_model* m, uint32_t token, uint32_t pos,
     if (token >= m->cfg.vocab) return set_error(VVLI_INVALID_TOKEN, "token %u >= vocab %u", token, m->cfg.vocab);
     if (pos >= m->max_seq) return set_error(VVLI_CONTEXT_FULL, "pos %u >= max_seq_len %u", pos, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     const size_t n = static_cast<size_t>(m->mk_blocks + 1) * stride;
     unsigned long long* d = nullptr;
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&d), n * sizeof(unsigned long long)));
@@ -1599,6 +1745,8 @@ int vvli_gpu_last_launch_time(vvli_gpu_model* m, float* ms_out) {
 
 int vvli_gpu_test_inject_step_error(vvli_gpu_model* m, uint32_t n) {
     if (!m) return set_error(VVLI_NULL_ARG, "model is NULL");
+    HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);  // the flag is raised before the next launch
     m->mk_inject = n;
     return VVLI_OK;
 }
@@ -1614,6 +1762,7 @@ int vvli_gpu_kv_read(vvli_gpu_model* m, uint32_t layer, uint32_t pos, float* k_o
     if (layer >= m->cfg.layers || pos >= m->max_seq)
         return set_error(VVLI_INVALID_CONFIG, "layer %u / pos %u out of range", layer, pos);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     const size_t kv = kv_dim(m->cfg);
     const size_t off = (static_cast<size_t>(layer) * m->max_seq + pos) * kv;
     if (k_out)
@@ -1633,6 +1782,7 @@ int vvli_gpu_prefill(vvli_gpu_model* m, const uint32_t* tokens, uint32_t n, uint
     if (static_cast<uint64_t>(start_pos) + n > m->max_seq)
         return set_error(VVLI_CONTEXT_FULL, "prefill end %u > max_seq_len %u", start_pos + n, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     // Prompt tokens live at their absolute positions in `prompt`.
     HIP_TRY(hipMemcpyAsync(m->prompt + start_pos, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
     if (use_batched_prefill(m)) {
@@ -1663,6 +1813,7 @@ int vvli_gpu_generate_greedy(vvli_gpu_model* m, const uint32_t* prompt, uint32_t
         return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
     const bool batched = (flags & VVLI_GEN_BATCHED_PREFILL) && use_batched_prefill(m);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     if (use_persistent(m))
         return generate_persistent(m, prompt, n_prompt, max_new, eos, batched, out_tokens, n_out, stats);
     int rc = ensure_graph(m);
@@ -1732,6 +1883,7 @@ int vvli_gpu_generate(vvli_gpu_model* m, const uint32_t* prompt, uint32_t n_prom
     if (n_prompt > m->max_seq)
         return set_error(VVLI_CONTEXT_FULL, "prompt of %u tokens > max_seq_len %u", n_prompt, m->max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    RESIDENT_STOP(m);
     const bool batched = (flags & VVLI_GEN_BATCHED_PREFILL) && use_batched_prefill(m);
     return generate_sampled(m, prompt, n_prompt, max_new, eos, batched, *opts, out_tokens, n_out, stats);
 }

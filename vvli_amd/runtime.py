@@ -222,7 +222,8 @@ class Runner:
     def forward_token_view(self, token_id: int, position: int) -> np.ndarray:
         """Runner.forwardToken with its borrowed-slice return (src/llm.zig:729):
         a read-only array over the library's pinned logits, overwritten by the
-        next forward_token_view call and invalid once the runner is closed."""
+        next forward_token_view call (with resident steps, by the next call
+        that returns logits) and invalid once the runner is closed."""
         view = c_void_p()
         am = c_uint32()
         _lib.check(_lib.lib().vvli_gpu_forward_token_view(self._h, token_id, position, byref(view), byref(am)))
@@ -287,6 +288,13 @@ class Runner:
         ms = ctypes.c_float()
         _lib.check(_lib.lib().vvli_gpu_last_launch_time(self._h, ctypes.byref(ms)))
         return float(ms.value)
+
+    def set_resident(self, linger_us: int) -> None:
+        """Resident single steps: forward_token calls on the persistent path
+        hand their (token, position) to a launch that stays running for up to
+        linger_us of idle time (0 turns it off). Same results as separate
+        launches; other work on the GPU waits while such a launch idles."""
+        _lib.check(_lib.lib().vvli_gpu_set_resident(self._h, linger_us))
 
     def set_decode_path(self, path: str) -> None:
         """'auto', 'graph' (per-kernel HIP graph) or 'persistent' (one launch per step)."""
