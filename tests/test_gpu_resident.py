@@ -13,10 +13,11 @@ import time
 import numpy as np
 import pytest
 
+from vvli_amd import config as C
 from vvli_amd import runtime as R
 from vvli_amd._lib import VvliError
 
-from test_gpu_forward import CASES, make_blob, rel_err
+from test_gpu_forward import CASES, cfg_small, make_blob, rel_err
 from test_gpu_moe import CASES as MOE_CASES
 from test_gpu_moe import moe_blob
 
@@ -35,9 +36,14 @@ def _call(gpu, form, tok, pos):
     return None, gpu.forward_token_argmax(tok, pos)
 
 
-@pytest.mark.parametrize("name", ["qwen_small", "llama_small", "hd128_g7"])
+# Every resident kernel instance: head_dim 64 and 128 (exact), 32 and 96
+# (the general instances); the MoE instances below.
+RES_CASES = dict(CASES, hd32_g4=(cfg_small(num_attention_heads=8, num_key_value_heads=2), C.WEIGHT_BF16, "synth", 0))
+
+
+@pytest.mark.parametrize("name", ["qwen_small", "llama_small", "hd128_g7", "hd32_g4", "hd96_g4"])
 def test_resident_steps_equal_separate_launches(name, oracle_mod, host_threads):
-    cfg, kind, how, _ = CASES[name]
+    cfg, kind, how, _ = RES_CASES[name]
     blob = make_blob(cfg, kind, how)
     max_seq = 96
     rng = np.random.default_rng(11)
@@ -121,10 +127,12 @@ def test_resident_error_is_reported(oracle_mod, host_threads):
                 assert rel_err(got, refs[pos]) <= TOL
 
 
-def test_resident_moe_steps_equal_separate_launches(oracle_mod):
-    cfg, _ = MOE_CASES["olmoe_small"]
+@pytest.mark.parametrize("name,n", [("olmoe_small", 20), ("olmoe_1b_7b_2layers", 6)])
+def test_resident_moe_steps_equal_separate_launches(name, n, oracle_mod):
+    """MoE instances: head_dim 64 (the small case) and 128 (OLMoE-1B-7B layers)."""
+    cfg, _ = MOE_CASES[name]
     blob = moe_blob(oracle_mod, cfg)
-    toks = np.random.default_rng(4).integers(0, cfg.vocab_size, size=20)
+    toks = np.random.default_rng(4).integers(0, cfg.vocab_size, size=n)
     with R.MoeRunner(cfg, blob, 64) as ref:
         ref.set_decode_path("persistent")
         refs = [_call(ref, 0, int(tok), pos) for pos, tok in enumerate(toks)]
