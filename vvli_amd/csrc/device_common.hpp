@@ -48,8 +48,12 @@ __device__ __forceinline__ VVLI_GLOBAL T* as_global(T* p) {
 }
 typedef unsigned int vvli_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int vvli_u32x2 __attribute__((ext_vector_type(2)));
+// Weights are streamed once per use: nontemporal loads (the nt cache policy)
+// keep them from displacing what is reused in the caches -- the tagged
+// activation words, the K/V rows, x (measured on the persistent decode step:
+// 1340 -> 1354 tok/s at Llama-3.2-1B, 1298 -> 1308 at Qwen2.5-0.5B).
 __device__ inline uint4 load_unit(const void* p) {
-    const vvli_u32x4 v = *as_global(reinterpret_cast<const vvli_u32x4*>(p));
+    const vvli_u32x4 v = __builtin_nontemporal_load(as_global(reinterpret_cast<const vvli_u32x4*>(p)));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ inline float4 load_f32x4(const float* p) {
