@@ -329,7 +329,9 @@ int vvli_gpu_test_sampler_trace(const float* logits, uint32_t n, const vvli_gpu_
  * pointers; K must be a multiple of 8; dY must be device memory (hipMalloc:
  * the K-split paths publish partials with write-through stores). stream:
  * hipStream_t or NULL for the null stream. Asynchronous: returns after the
- * launch. M < 4 runs one GEMV per row; 4 <= M <= 64 one skinny MFMA kernel (W
+ * launch. M <= 3 (and M = 4 when W has few row tiles) runs the
+ * GEMV kernel, one launch for all rows of X (one per row when they do not fit
+ * its LDS); otherwise 4 <= M <= 64 one skinny MFMA kernel (W
  * read once, X split into two bf16 halves in registers so the products keep
  * about 16 bits of each f32 activation; few row tiles split K across blocks
  * and the last block of a tile sums the partials in a fixed order); M > 64 one

@@ -166,11 +166,15 @@ def test_linear_benchmark_shapes(N, K, M, oracle_mod):
     (2, 1, 2048, True),     # a single output row
     (3, 512, 16384, False), # 3 x 64 KiB of x exceeds LDS: one launch per row
     (1, 300, 40960, False), # the largest K whose x fits LDS
+    (4, 300, 2048, True),   # M = 4 where the skinny row tiles leave CUs idle: four rows of x in one launch
+    (4, 1000, 10240, False),  # M = 4, the largest K whose four x rows fit LDS
+    (4, 700, 10248, True),  # M = 4 past that: the skinny kernel
 ])
 def test_linear_gemv_shapes(M, N, K, has_bias, oracle_mod):
-    """The M <= 3 GEMV kernel (one launch for up to three rows of x staged in
-    LDS, whole-row wave tiles walked in items of 1-4 units per lane): ragged
-    rows and tiles, bias, and the per-row fallback, against the oracle."""
+    """The GEMV kernel (M <= 3, and M = 4 where the skinny kernel's row tiles
+    leave CUs idle: one launch for up to four rows of x staged in LDS, whole-row wave tiles
+    walked in items of 1-4 units per lane): ragged rows and tiles, bias, and
+    the per-row fallback, against the oracle."""
     import torch
 
     rng = np.random.default_rng(M * 31 + N * 17 + K)

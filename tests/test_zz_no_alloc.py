@@ -67,9 +67,11 @@ def test_noalloc_linear_matches_linear(oracle_mod):
     assert 4 * 512 * 8192 == LIMIT
     print("noalloc call 1: M=512 N=2048 K=8192", flush=True)
     run_case(512, 2048, 8192, False, oracle_mod, 1)
-    # Second call, smaller: stale planes of the first call remain beyond its rows.
-    print("noalloc call 2: M=64 N=512 K=2048 bias", flush=True)
-    run_case(64, 512, 2048, True, oracle_mod, 2)
+    # Second call, smaller: stale planes of the first call remain beyond its
+    # rows; the skinny kernel with K split across blocks (32 row tiles, 2
+    # splits): its counters and partials in the same scratch.
+    print("noalloc call 2: M=64 N=512 K=4096 bias", flush=True)
+    run_case(64, 512, 4096, True, oracle_mod, 2)
     print("noalloc call 3: M=130 N=1000 K=896 bias (ragged tiles)", flush=True)
     run_case(130, 1000, 896, True, oracle_mod, 3)
     print("noalloc call 4: M=2 N=2048 K=2048 (GEMV path)", flush=True)

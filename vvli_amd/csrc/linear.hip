@@ -20,13 +20,14 @@ using namespace vvli;
 namespace {
 
 // Rows from which one MFMA kernel replaces the GEMV kernel (linear_gemv.hpp,
-// up to 3 rows of x in one launch); up to kSkinnyMaxRows the skinny kernel
+// up to 4 rows of x in one launch: 4 only where the skinny kernel would split
+// K across blocks, linear_uses_gemv); up to kSkinnyMaxRows the skinny kernel
 // below, beyond it the prefill GEMM.
 constexpr uint32_t kLinearGemmMinRows = 4;
 constexpr uint32_t kSkinnyMaxRows = 64;
 
 // ---------------------------------------------------------------------------
-// GEMV plan (M <= 3): one wave per row tile (RW = 1), UL units of 16 bytes per
+// GEMV plan (M <= 4): one wave per row tile (RW = 1), UL units of 16 bytes per
 // lane per item (4, i.e. 4 KiB rows in one item at K = 2048; fewer when rows
 // are short), one block of four waves per CU. Measured on the Llama-3.2-1B
 // shapes (per-dispatch time, cold weights): more waves per CU or two-row
@@ -50,7 +51,7 @@ hipError_t launch_gemv_t(const uint16_t* dW, const float* dX, const uint16_t* dB
     return vlaunch(linear_gemv_kernel<MR, 1, UL>, dim3(blocks), dim3(kLgThreads), lds, s, dW, dX, dBias, dY, M, N, K);
 }
 
-// One launch for up to 3 rows of x (x staged in LDS: MR * K * 4 bytes).
+// One launch for up to 4 rows of x (x staged in LDS: MR * K * 4 bytes).
 hipError_t launch_gemv_rows(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M,
                             uint32_t N, uint32_t K, hipStream_t s) {
     const uint32_t ul = gemv_ul(K);
@@ -60,7 +61,8 @@ hipError_t launch_gemv_rows(const uint16_t* dW, const float* dX, const uint16_t*
                      : launch_gemv_t<MR_, 1>(dW, dX, dBias, dY, M, N, K, s);
     if (M == 1) VVLI_GEMV_MR(1)
     if (M == 2) VVLI_GEMV_MR(2)
-    VVLI_GEMV_MR(3)
+    if (M == 3) VVLI_GEMV_MR(3)
+    VVLI_GEMV_MR(4)
 #undef VVLI_GEMV_MR
 }
 
@@ -247,16 +249,24 @@ __global__ __launch_bounds__(kSkinnyThreads) void linear_skinny_kernel(const uin
 // gives a block per CU, 64 for very tall W (fewer re-reads of X), else 16.
 uint32_t skinny_nt(uint32_t N) { return N >= 32768 ? 4 : (N >= 256 * 32 ? 2 : 1); }
 
+// Row tiles of the skinny kernel at N rows of W.
+uint32_t skinny_tiles(uint32_t N) { return (N + skinny_nt(N) * 16 - 1) / (skinny_nt(N) * 16); }
+
 // K splits, only when the row tiles leave CUs idle (measured: at 256 tiles of
 // 8192 x 2048 a split of 2 costs 4 us -- the partials' write-through and the
 // last block's sum -- and gains nothing): enough blocks for two per CU, each
-// wave keeping >= 4 K steps, at most 8 splits.
+// wave keeping >= 8 K steps, at most 8 splits. The hand-off (write-through
+// partials, counter, the last block's acquire and ordered sum) costs several
+// microseconds, which only long K repays (one session: 2048 x 8192 at
+// M = 16 / 32 23.5 / 30.5 us with 4 splits against 25.3 / 38.4 without; 2048 x
+// 2048 at M = 16 / 32 8.4 / 12.4 us unsplit against 14.3 / 16.4 with 2 splits
+// of 4 steps per wave).
 uint32_t skinny_splits(uint32_t N, uint32_t K) {
-    const uint32_t tiles = (N + skinny_nt(N) * 16 - 1) / (skinny_nt(N) * 16);
+    const uint32_t tiles = skinny_tiles(N);
     if (tiles >= 256) return 1;
     const uint32_t S = (K + 31) / 32;
     uint32_t ks = (512 + tiles - 1) / tiles;
-    ks = std::min(ks, S / (4 * kSkinnyWaves));
+    ks = std::min(ks, S / (8 * kSkinnyWaves));
     ks = std::min(ks, 8u);
     return ks < 1 ? 1 : ks;
 }
@@ -319,7 +329,10 @@ int linear_setup() {
                               reinterpret_cast<const void*>(&linear_gemv_kernel<2, 1, 4>),
                               reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 1>),
                               reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 2>),
-                              reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 4>)};
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<3, 1, 4>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<4, 1, 1>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<4, 1, 2>),
+                              reinterpret_cast<const void*>(&linear_gemv_kernel<4, 1, 4>)};
         for (const void* k : gemv)
             if (err == hipSuccess) err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds);
         // Skinny variants keep up to 128 KiB of wave partials in LDS.
@@ -352,8 +365,21 @@ int check_linear_args(const void* dW, const void* dX, const void* dY, uint32_t M
 }
 
 // Payload bytes a call needs beyond the counters (0 and no counters: none).
+// M = 4 takes the GEMV kernel where the skinny kernel's row tiles leave CUs
+// idle (fewer than 256: the GEMV spreads whole rows over every CU and reads
+// the four x rows from LDS; one session: 2048 x 2048 5.7 against 6.4 us
+// unsplit and 13.3 split, 512 x 2048 4.8 against 6.1 and 7.4, 2048 x 8192 13.3
+// against 17.0 and 19.4). On tall W the skinny kernel stays: 8192 x 2048 11.7
+// against 13.0 us, 128256 x 2048 117.9 against 148.9 (the x reads from LDS
+// bound the GEMV there).
+bool linear_uses_gemv(uint32_t M, uint32_t N, uint32_t K) {
+    if (M < kLinearGemmMinRows) return true;
+    return M == 4 && skinny_tiles(N) < 256 && (size_t)M * K * sizeof(float) <= kGemvMaxLds;
+}
+
 size_t linear_payload_bytes(uint32_t M, uint32_t N, uint32_t K) {
     if (M > kSkinnyMaxRows) return gemm_split_elems(M, K) * sizeof(uint16_t);
+    if (linear_uses_gemv(M, N, K)) return 0;
     if (M >= kLinearGemmMinRows) {
         const uint32_t ks = skinny_splits(N, K);
         return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
@@ -365,7 +391,7 @@ size_t linear_payload_bytes(uint32_t M, uint32_t N, uint32_t K) {
 // device memory laid out as above, or null when the payload is 0.
 int linear_enqueue(const uint16_t* dW, const float* dX, const uint16_t* dBias, float* dY, uint32_t M, uint32_t N,
                    uint32_t K, hipStream_t s, char* scratch_mem) {
-    if (M >= kLinearGemmMinRows && M <= kSkinnyMaxRows) {
+    if (M >= kLinearGemmMinRows && M <= kSkinnyMaxRows && !linear_uses_gemv(M, N, K)) {
         float* ws = scratch_mem ? reinterpret_cast<float*>(scratch_mem + kCounterBytes) : nullptr;
         uint32_t* cnt = reinterpret_cast<uint32_t*>(scratch_mem);
         HIP_TRY(launch_skinny(dW, dX, dBias, dY, M, N, K, ws, cnt, s));
@@ -382,7 +408,7 @@ int linear_enqueue(const uint16_t* dW, const float* dX, const uint16_t* dBias, f
         HIP_TRY(launch_gemm_bf16(kGemmPlain, g, s));
         return VVLI_OK;
     }
-    // M <= 3: one GEMV launch for all rows when their x fits LDS, else one per row.
+    // M <= 4: one GEMV launch for all rows when their x fits LDS, else one per row.
     if ((size_t)M * K * sizeof(float) <= kGemvMaxLds) {
         HIP_TRY(launch_gemv_rows(dW, dX, dBias, dY, M, N, K, s));
         return VVLI_OK;

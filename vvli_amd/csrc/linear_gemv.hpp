@@ -1,4 +1,4 @@
-// linear_gemv.hpp -- the isolated op at M <= 3 (one to three GEMVs over the
+// linear_gemv.hpp -- the isolated op at M <= 4 (one to four GEMVs over the
 // same weights): linearInto / dotBf16 (src/llm.zig:1228-1275, 1445-1466),
 // y[m][n] = sum_k bf16 W[n,k] * x[m][k] (+ bias[n]), f32 accumulation.
 //
